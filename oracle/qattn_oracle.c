@@ -1,0 +1,433 @@
+/*
+ * CPU restatement of the reference's SageAttention-2 quantized-attention math.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, and only as the checker (or as the
+ * timed "reference CPU path" baseline).  The product path never calls it.
+ *
+ * Reference files followed (paths relative to the TeleFuser tree):
+ *   tf-kernel/csrc/sageattn2/fused/fused.cu:59-194      QuantInt8Kernel (per-block INT8 quantizer)
+ *   tf-kernel/csrc/sageattn2/fused/fused.cu:332-445     MeanScaleKernel (per-channel FP8 V quantizer)
+ *   tf-kernel/csrc/sageattn2/numeric_conversion.cuh:47-58,147-151  rounding semantics
+ *        (cvt.rn.satfinite.e4m3x2.f32, cvt.rni.sat.s8.f32)
+ *   tf-kernel/tf_kernel/triton/quant_per_block.py:22-166  Triton per-block quantizer
+ *   tf-kernel/csrc/sageattn2/qattn/qk_int_sv_f8_cuda_sm89.cuh:136-470,711-840  attention main loop
+ *   tf-kernel/csrc/sageattn2/qattn/attn_utils.cuh:35,316-452,469-534,711-875  update_mdo / RS_32_to_8 /
+ *        accumulate_d / normalize_d
+ *   tf-kernel/tf_kernel/triton/attn_qk_int8_per_block.py:46-101  Triton inner loop (bf16/fp16 P.V mode)
+ *
+ * Parity pins (see tests/test_oracle_kat.py): every function here is checked against closed-form
+ * known-answer cases, torch's float8_e4m3fn / bfloat16 casts, brute-force float64 attention and
+ * softmax invariances.  The reference ships no golden vectors for this path.
+ *
+ * Build: oracle/Makefile (gcc -O3 -fopenmp, no -ffast-math: IEEE division and rounding are part
+ * of the bit-exact contract).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ------------------------------------------------------------------------------------------ */
+/* scalar conversions                                                                          */
+/* ------------------------------------------------------------------------------------------ */
+
+static inline float u32_as_f32(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+static inline uint32_t f32_as_u32(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+
+float oq_bf16_to_f32(uint16_t h) { return u32_as_f32(((uint32_t)h) << 16); }
+
+float oq_f16_to_f32(uint16_t h) {
+  uint32_t s = (h >> 15) & 1, e = (h >> 10) & 0x1f, m = h & 0x3ff;
+  float v;
+  if (e == 0) v = ldexpf((float)m, -24);
+  else if (e == 31) v = m ? NAN : INFINITY;
+  else v = ldexpf((float)(m | 0x400), (int)e - 25);
+  return s ? -v : v;
+}
+
+/* round-to-nearest-even fp32 -> bf16 (NaN kept quiet) */
+uint16_t oq_f32_to_bf16(float f) {
+  uint32_t u = f32_as_u32(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  uint32_t lsb = (u >> 16) & 1u;
+  u += 0x7fffu + lsb;
+  return (uint16_t)(u >> 16);
+}
+
+/* OCP E4M3FN decode: 1-4-3, bias 7, no infinities, 0x7f/0xff are NaN, max 448 */
+float oq_e4m3_to_f32(uint8_t b) {
+  int s = b >> 7, e = (b >> 3) & 0xf, m = b & 7;
+  float v;
+  if (e == 0xf && m == 7) return NAN;
+  if (e == 0) v = ldexpf((float)m, -9);
+  else v = ldexpf((float)(8 + m), e - 10);
+  return s ? -v : v;
+}
+
+/* fp32 -> E4M3FN, round-to-nearest-even, saturate finite values to +-448 (PTX
+ * cvt.rn.satfinite.e4m3x2.f32 semantics, numeric_conversion.cuh:47-58).  NaN -> 0x7f.
+ * Bit-level: normals keep 3 mantissa bits with RNE on the 20 dropped bits; values below 2^-6
+ * are multiples of 2^-9 (a*512 is exact, rintf is RNE; n == 8 encodes 2^-6 correctly). */
+uint8_t oq_f32_to_e4m3(float f) {
+  if (isnan(f)) return 0x7f;
+  uint32_t u = f32_as_u32(f);
+  uint8_t sign = (u >> 31) ? 0x80 : 0;
+  float a = fabsf(f);
+  if (a >= 448.f) return sign | 0x7e;
+  if (a < 0.015625f) return sign | (uint8_t)(int)rintf(a * 512.f);
+  uint32_t ua = u & 0x7fffffffu;
+  int e4 = (int)(ua >> 23) - 127 + 7;
+  uint32_t man = ua & 0x7fffffu;
+  uint32_t m = man >> 20, rem = man & 0xfffffu;
+  if (rem > 0x80000u || (rem == 0x80000u && (m & 1u))) m++;
+  if (m == 8) { m = 0; e4++; }
+  return sign | (uint8_t)((e4 << 3) | m);
+}
+
+/* fp32 -> IEEE half bits, round-to-nearest-even (used for the Triton fp16 K - km rounding) */
+uint16_t oq_f32_to_f16(float f) {
+  uint32_t u = f32_as_u32(f);
+  uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+  uint32_t ua = u & 0x7fffffffu;
+  if (ua > 0x7f800000u) return sign | 0x7e00;
+  if (ua >= 0x477ff000u) return sign | 0x7c00; /* >= 65520 rounds to inf */
+  float a = fabsf(f);
+  if (a < 6.103515625e-05f) return sign | (uint16_t)(int)rintf(a * 16777216.f); /* subnormal: 2^-24 steps */
+  int e5 = (int)(ua >> 23) - 127 + 15;
+  uint32_t man = ua & 0x7fffffu;
+  uint32_t m = man >> 13, rem = man & 0x1fffu;
+  if (rem > 0x1000u || (rem == 0x1000u && (m & 1u))) m++;
+  if (m == 0x400u) { m = 0; e5++; }
+  return sign | (uint16_t)((e5 << 10) | m);
+}
+
+/* cvt.rni.sat.s8.f32: round to nearest even, saturate to [-128, 127]; NaN -> 0 */
+int8_t oq_f32_to_s8_rne_sat(float x) {
+  if (isnan(x)) return 0;
+  float r = rintf(x); /* default FE_TONEAREST = RNE */
+  if (r > 127.f) r = 127.f;
+  if (r < -128.f) r = -128.f;
+  return (int8_t)r;
+}
+
+/* Triton: x += 0.5*sign(x>=0 ? 1 : -1); x.to(int8) = truncation toward zero.  NaN -> 0. */
+int8_t oq_f32_to_s8_half_away(float x) {
+  if (isnan(x)) return 0;
+  float t = x + (x >= 0.f ? 0.5f : -0.5f);
+  float r = truncf(t);
+  if (r > 127.f) r = 127.f;
+  if (r < -128.f) r = -128.f;
+  return (int8_t)r;
+}
+
+static inline float load_h(const uint16_t* p, int is_fp16) {
+  return is_fp16 ? oq_f16_to_f32(*p) : oq_bf16_to_f32(*p);
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* per-block INT8 quantizers                                                                   */
+/* ------------------------------------------------------------------------------------------ */
+
+/*
+ * CUDA QuantInt8Kernel semantics (fused.cu:59-194, launchers :447-696):
+ *   x = float(in); if km: x -= float(km[d]); if has_sm_scale: x *= sm_scale   (fp32, in that order)
+ *   tail rows (token >= L) are x = 0 and are not stored
+ *   amax = max(1e-7f, max|x|); scale = amax / 127.f (IEEE); inv = 127.f / amax (IEEE)
+ *   q = cvt.rni.sat.s8(x * inv)
+ * Layout: element (b, l, h, d) at in[b*sb + l*sl + h*sh + d]; scale is contiguous [B, H, nblk].
+ */
+void oq_quant_per_block_int8(const uint16_t* in, int is_fp16, int64_t B, int64_t L, int64_t H, int64_t D,
+                             int64_t sb, int64_t sl, int64_t sh, const uint16_t* km, int64_t kmb, int64_t kmh,
+                             float sm_scale, int has_sm_scale, int64_t blk, int8_t* out, int64_t ob, int64_t ol,
+                             int64_t oh, float* scale) {
+  int64_t nblk = (L + blk - 1) / blk;
+#pragma omp parallel for collapse(3) schedule(static)
+  for (int64_t b = 0; b < B; b++)
+    for (int64_t h = 0; h < H; h++)
+      for (int64_t n = 0; n < nblk; n++) {
+        float* xs = (float*)malloc(sizeof(float) * blk * D);
+        float amax = 0.0000001f;
+        for (int64_t r = 0; r < blk; r++) {
+          int64_t l = n * blk + r;
+          for (int64_t d = 0; d < D; d++) {
+            float x = 0.f;
+            if (l < L) {
+              x = load_h(in + b * sb + l * sl + h * sh + d, is_fp16);
+              if (km) x -= load_h(km + b * kmb + h * kmh + d, is_fp16);
+              if (has_sm_scale) x *= sm_scale;
+            }
+            xs[r * D + d] = x;
+            amax = fmaxf(amax, fabsf(x));
+          }
+        }
+        volatile float a = amax;
+        float sc = a / 127.0f;
+        float inv = 127.0f / a;
+        scale[(b * H + h) * nblk + n] = sc;
+        for (int64_t r = 0; r < blk; r++) {
+          int64_t l = n * blk + r;
+          if (l >= L) break;
+          for (int64_t d = 0; d < D; d++) {
+            volatile float p = xs[r * D + d] * inv;
+            out[b * ob + l * ol + h * oh + d] = oq_f32_to_s8_rne_sat(p);
+          }
+        }
+        free(xs);
+      }
+}
+
+/*
+ * Triton quant_per_block_int8_kernel semantics (triton/quant_per_block.py:22-166):
+ *   K path: k = k - km is a torch op on half tensors -> fp32 difference rounded to the input dtype
+ *   x = float(x) * sm_scale (sm_scale = 1.0 for K); masked tail rows load as 0
+ *   scale = max|x| / 127 (no floor: an all-zero block gives scale 0 and q = 0 here)
+ *   q = trunc(x/scale + 0.5*sign)   (round half away from zero)
+ */
+void oq_quant_per_block_int8_triton(const uint16_t* in, int is_fp16, int64_t B, int64_t L, int64_t H, int64_t D,
+                                    int64_t sb, int64_t sl, int64_t sh, const uint16_t* km, int64_t kmb,
+                                    int64_t kmh, float sm_scale, int64_t blk, int8_t* out, int64_t ob, int64_t ol,
+                                    int64_t oh, float* scale) {
+  int64_t nblk = (L + blk - 1) / blk;
+#pragma omp parallel for collapse(3) schedule(static)
+  for (int64_t b = 0; b < B; b++)
+    for (int64_t h = 0; h < H; h++)
+      for (int64_t n = 0; n < nblk; n++) {
+        float* xs = (float*)malloc(sizeof(float) * blk * D);
+        float amax = 0.f;
+        for (int64_t r = 0; r < blk; r++) {
+          int64_t l = n * blk + r;
+          for (int64_t d = 0; d < D; d++) {
+            float x = 0.f;
+            if (l < L) {
+              x = load_h(in + b * sb + l * sl + h * sh + d, is_fp16);
+              if (km) {
+                float diff = x - load_h(km + b * kmb + h * kmh + d, is_fp16);
+                if (is_fp16) {
+                  x = oq_f16_to_f32(oq_f32_to_f16(diff));
+                } else {
+                  x = oq_bf16_to_f32(oq_f32_to_bf16(diff));
+                }
+              }
+              volatile float xm = x * sm_scale;
+              x = xm;
+            }
+            xs[r * D + d] = x;
+            amax = fmaxf(amax, fabsf(x));
+          }
+        }
+        volatile float a = amax;
+        float sc = a / 127.0f;
+        scale[(b * H + h) * nblk + n] = sc;
+        for (int64_t r = 0; r < blk; r++) {
+          int64_t l = n * blk + r;
+          if (l >= L) break;
+          for (int64_t d = 0; d < D; d++) {
+            volatile float t = xs[r * D + d] / sc;
+            out[b * ob + l * ol + h * oh + d] = oq_f32_to_s8_half_away(t);
+          }
+        }
+        free(xs);
+      }
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* per-channel FP8 V quantizer                                                                 */
+/* ------------------------------------------------------------------------------------------ */
+
+/*
+ * MeanScaleKernel<_, sub_mean=false> semantics (fused.cu:332-445):
+ *   per (b, h, d): amax = max(|max_l v|, |min_l v|) over all tokens (padding zeros never change it)
+ *   v_scale = amax / scale_max; recp = scale_max / amax; v8 = e4m3_rn_satfinite(v * recp)
+ *   (no floor: an all-zero channel yields 0/0 = NaN, as in the reference)
+ * Output here is the plain transposed layout v8[b][h][d][l] with Lpad >= L columns (pad = 0x00);
+ * the device kernel's in-tile key permutation is a storage detail undone by the tests.
+ */
+void oq_per_channel_fp8(const uint16_t* in, int is_fp16, int64_t B, int64_t L, int64_t H, int64_t D, int64_t sb,
+                        int64_t sl, int64_t sh, float scale_max, uint8_t* v8, int64_t Lpad, float* v_scale) {
+#pragma omp parallel for collapse(3) schedule(static)
+  for (int64_t b = 0; b < B; b++)
+    for (int64_t h = 0; h < H; h++)
+      for (int64_t d = 0; d < D; d++) {
+        float mx = -1000000.0f, mn = 1000000.0f;
+        for (int64_t l = 0; l < L; l++) {
+          float x = load_h(in + b * sb + l * sl + h * sh + d, is_fp16);
+          mx = fmaxf(mx, x);
+          mn = fminf(mn, x);
+        }
+        if (Lpad > L) { /* the reference reduces over zero padding up to a multiple of 16 */
+          mx = fmaxf(mx, 0.f);
+          mn = fminf(mn, 0.f);
+        }
+        volatile float amax = fmaxf(fabsf(mx), fabsf(mn));
+        v_scale[(b * H + h) * D + d] = amax / scale_max;
+        volatile float recp = scale_max / amax;
+        uint8_t* row = v8 + ((b * H + h) * D + d) * Lpad;
+        for (int64_t l = 0; l < Lpad; l++) {
+          float x = l < L ? load_h(in + b * sb + l * sl + h * sh + d, is_fp16) : 0.f;
+          volatile float y = x * recp;
+          row[l] = oq_f32_to_e4m3(y);
+        }
+      }
+}
+
+/* ------------------------------------------------------------------------------------------ */
+/* quantized attention forward                                                                 */
+/* ------------------------------------------------------------------------------------------ */
+
+#define OQ_FP8_OFFSET 8.807 /* attn_utils.cuh:35 S_FP8_OFFSET */
+
+/*
+ * Quantized attention with the reference's tile structure (qk_int_sv_f8_cuda_sm89.cuh:342-840):
+ *   for each 64-key tile (blkk):  s = float(Q8.K8^T) * (q_scale * k_scale) * qk_mult
+ *     m_new = max(m, rowmax(s) - offset);  p = exp2(s - m_new);  d = d*exp2(m - m_new) + sum(p)
+ *     pv_mode 0: O = O*exp2(m-m_new) + e4m3(p) . e4m3(V)   (offset = 8.807, V per-channel fp8)
+ *     pv_mode 1: O = O*exp2(m-m_new) + bf16(p) . Vh         (offset = 0, V = bf16/fp16 input values)
+ *   end: O /= d; pv_mode 0: O *= v_scale[d]
+ * Everything not rounded by the reference is carried in double.
+ *
+ * q8: element (b,l,h,d) at q8[b*qsb + l*qsl + h*qsh + d]; k8 likewise with ks*; q_scale [B,Hq,nQB]
+ * with block blkq; k_scale [B,Hkv,nKB] with block blkk (one scale per key tile, blkk = tile).
+ * pv_mode 0: v8 is the plain transposed [B,Hkv,D,Lpad] e4m3 tensor, v_scale [B,Hkv,D].
+ * pv_mode 1: vh is (b,l,h,d) at vh[b*vsb + l*vsl + h*vsh + d] (bf16 or fp16 bits).
+ * kv_valid: per-batch number of valid keys (NULL = Lk); causal: top-left aligned kv > q + q_offset masked.
+ * out: float [B, Lq, Hq, D] contiguous; lse2 (optional): log2-domain row LSE [B, Hq, Lq] of the
+ * quantized logits (log2(d) + m).
+ * If qrows_limit > 0 only the first qrows_limit query rows of every (b, h) are computed (CPU timing).
+ */
+void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const float* q_scale, int64_t blkq,
+                  const int8_t* k8, int64_t ksb, int64_t ksl, int64_t ksh, const float* k_scale, int64_t blkk,
+                  const uint8_t* v8, int64_t Lpad, const float* v_scale, const uint16_t* vh, int is_fp16,
+                  int64_t vsb, int64_t vsl, int64_t vsh, int64_t B, int64_t Lq, int64_t Lk, int64_t Hq,
+                  int64_t Hkv, int64_t D, double qk_mult, int pv_mode, int causal, int64_t q_offset,
+                  const int32_t* kv_valid, int64_t h_begin, int64_t h_end, int64_t qrows_limit, float* out,
+                  float* lse2) {
+  int64_t nQB = (Lq + blkq - 1) / blkq;
+  int64_t nKB = (Lk + blkk - 1) / blkk;
+  int64_t group = Hq / Hkv;
+  int64_t rows = qrows_limit > 0 && qrows_limit < Lq ? qrows_limit : Lq;
+  if (h_end <= 0 || h_end > Hq) h_end = Hq;
+  double offset = pv_mode == 0 ? OQ_FP8_OFFSET : 0.0;
+#pragma omp parallel for collapse(3) schedule(dynamic, 4)
+  for (int64_t b = 0; b < B; b++)
+    for (int64_t h = h_begin; h < h_end; h++)
+      for (int64_t i = 0; i < rows; i++) {
+        int64_t hk = h / group;
+        int64_t valid = kv_valid ? kv_valid[b] : Lk;
+        if (valid > Lk) valid = Lk;
+        int64_t last = valid; /* exclusive */
+        if (causal) {
+          int64_t lim = i + q_offset + 1;
+          if (lim < last) last = lim;
+        }
+        double* o = (double*)calloc((size_t)D, sizeof(double));
+        double s[64 * 8];
+        double m = -5000000.0, dsum = 0.0;
+        int has = 0;
+        const int8_t* qrow = q8 + b * qsb + i * qsl + h * qsh;
+        double qs = q_scale[(b * Hq + h) * nQB + i / blkq];
+        for (int64_t t = 0; t < nKB && t * blkk < last; t++) {
+          int64_t k0 = t * blkk, k1 = k0 + blkk < last ? k0 + blkk : last;
+          double ks = k_scale[(b * Hkv + hk) * nKB + t];
+          double c = qs * ks * qk_mult;
+          double mx = -1e300;
+          for (int64_t j = k0; j < k1; j++) {
+            const int8_t* krow = k8 + b * ksb + j * ksl + hk * ksh;
+            int32_t acc = 0;
+            for (int64_t d = 0; d < D; d++) acc += (int32_t)qrow[d] * (int32_t)krow[d];
+            s[j - k0] = (double)acc * c;
+            if (s[j - k0] > mx) mx = s[j - k0];
+          }
+          double m_new = mx - offset > m ? mx - offset : m;
+          double alpha = has ? exp2(m - m_new) : 0.0;
+          dsum *= alpha;
+          for (int64_t d = 0; d < D; d++) o[d] *= alpha;
+          m = m_new;
+          has = 1;
+          for (int64_t j = k0; j < k1; j++) {
+            double p = exp2(s[j - k0] - m);
+            dsum += p;
+            double pr;
+            if (pv_mode == 0) {
+              pr = oq_e4m3_to_f32(oq_f32_to_e4m3((float)p));
+              const uint8_t* vcol = v8 + ((b * Hkv + hk) * D) * Lpad + j;
+              for (int64_t d = 0; d < D; d++) o[d] += pr * (double)oq_e4m3_to_f32(vcol[d * Lpad]);
+            } else {
+              pr = oq_bf16_to_f32(oq_f32_to_bf16((float)p));
+              const uint16_t* vrow = vh + b * vsb + j * vsl + hk * vsh;
+              for (int64_t d = 0; d < D; d++) o[d] += pr * (double)load_h(vrow + d, is_fp16);
+            }
+          }
+        }
+        float* orow = out + ((b * Lq + i) * Hq + h) * D;
+        for (int64_t d = 0; d < D; d++) {
+          double v = has && dsum > 0 ? o[d] / dsum : 0.0;
+          if (pv_mode == 0) v *= (double)v_scale[(b * Hkv + hk) * D + d];
+          orow[d] = (float)v;
+        }
+        if (lse2) lse2[(b * Hq + h) * Lq + i] = has && dsum > 0 ? (float)(log2(dsum) + m) : -INFINITY;
+        free(o);
+      }
+}
+
+/* float64 exact softmax attention on half inputs (the unquantized truth), same layouts as above. */
+void oq_attn_fp64(const uint16_t* q, const uint16_t* k, const uint16_t* v, int is_fp16, int64_t B, int64_t Lq,
+                  int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, double sm_scale, int causal, int64_t q_offset,
+                  const int32_t* kv_valid, float* out) {
+  int64_t group = Hq / Hkv;
+#pragma omp parallel for collapse(3) schedule(dynamic, 4)
+  for (int64_t b = 0; b < B; b++)
+    for (int64_t h = 0; h < Hq; h++)
+      for (int64_t i = 0; i < Lq; i++) {
+        int64_t hk = h / group;
+        int64_t last = kv_valid ? kv_valid[b] : Lk;
+        if (last > Lk) last = Lk;
+        if (causal && i + q_offset + 1 < last) last = i + q_offset + 1;
+        double* s = (double*)malloc(sizeof(double) * (Lk > 0 ? Lk : 1));
+        double* o = (double*)calloc((size_t)D, sizeof(double));
+        double mx = -1e300;
+        for (int64_t j = 0; j < last; j++) {
+          double acc = 0;
+          for (int64_t d = 0; d < D; d++)
+            acc += (double)load_h(q + ((b * Lq + i) * Hq + h) * D + d, is_fp16) *
+                   (double)load_h(k + ((b * Lk + j) * Hkv + hk) * D + d, is_fp16);
+          s[j] = acc * sm_scale;
+          if (s[j] > mx) mx = s[j];
+        }
+        double den = 0;
+        for (int64_t j = 0; j < last; j++) {
+          double p = exp(s[j] - mx);
+          den += p;
+          for (int64_t d = 0; d < D; d++) o[d] += p * (double)load_h(v + ((b * Lk + j) * Hkv + hk) * D + d, is_fp16);
+        }
+        for (int64_t d = 0; d < D; d++) out[((b * Lq + i) * Hq + h) * D + d] = last > 0 ? (float)(o[d] / den) : 0.f;
+        free(s);
+        free(o);
+      }
+}
+
+int oq_num_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+/* Element-wise conversions over an array (kind 0: e4m3 bytes, 1: bf16 bits, 2: s8 RNE-sat,
+ * 3: s8 half-away (Triton), 4: fp16 bits).  Lets tests sweep millions of values in one call. */
+void oq_cvt_array(const float* x, int64_t n, int kind, void* out) {
+  for (int64_t i = 0; i < n; i++) {
+    switch (kind) {
+      case 0: ((uint8_t*)out)[i] = oq_f32_to_e4m3(x[i]); break;
+      case 1: ((uint16_t*)out)[i] = oq_f32_to_bf16(x[i]); break;
+      case 2: ((int8_t*)out)[i] = oq_f32_to_s8_rne_sat(x[i]); break;
+      case 3: ((int8_t*)out)[i] = oq_f32_to_s8_half_away(x[i]); break;
+      default: ((uint16_t*)out)[i] = oq_f32_to_f16(x[i]); break;
+    }
+  }
+}

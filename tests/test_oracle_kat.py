@@ -1,0 +1,368 @@
+"""Pins the CPU oracle before anything is checked against it.
+
+The reference ships no golden vectors for this path (its only test compares against fp attention
+at rtol/atol 0.1-0.15, tf-kernel/tests/test_sageattn2.py:127-244), so every oracle function is
+pinned here by closed-form known answers, by torch's own casts, by an independent float32 numpy
+restatement, by brute-force float64 attention and by softmax invariances.  Each check is chosen so
+that a plausible slip (RNE vs half-away rounding, a missing amax floor, km applied in the wrong
+precision, a dropped sm_scale, a transposed operand, a wrong tile max) fails at least one of them.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from tests.inputs import bf16_bits, cosine, qkv
+
+LOG2E = 1.44269504
+
+
+def _bits(vals, shape):
+    return bf16_bits(torch.tensor(vals, dtype=torch.float32).reshape(shape))
+
+
+# ------------------------------------------------------------------------------------------------
+# scalar conversions
+# ------------------------------------------------------------------------------------------------
+
+def _float_sweep():
+    """Every fp32 whose low 16 bits are one of a set of tie / near-tie patterns, plus randoms."""
+    hi = np.arange(0, 1 << 16, dtype=np.uint32)
+    lows = np.array([0, 1, 0x7FFF, 0x8000, 0x8001, 0xFFFF, 0x1234], np.uint32)
+    u = (hi[:, None] << 16 | lows[None, :]).ravel()
+    f = u.view(np.float32)
+    f = f[np.isfinite(f)]
+    rng = np.random.default_rng(1)
+    return np.concatenate([f, rng.standard_normal(1 << 18).astype(np.float32) * 50])
+
+
+def test_e4m3_matches_torch_cast_in_range(oracle):
+    x = _float_sweep()
+    x = x[np.abs(x) < 448.0]
+    got = oracle.cvt_array(x, "e4m3")
+    want = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(got, want)
+
+
+def test_e4m3_known_answers_and_satfinite(oracle):
+    cases = {
+        0.0: 0x00, 448.0: 0x7E, 447.99: 0x7E, 460.0: 0x7E, 1e9: 0x7E, float("inf"): 0x7E, -1e9: 0xFE,
+        -448.0: 0xFE, 1.0: 0x38, 1.0625: 0x38, 1.1875: 0x3A, 2 ** -9: 0x01, 2 ** -10: 0x00,
+        3 * 2 ** -10: 0x02, 2 ** -6: 0x08, 240.0: 0x77, 2 ** 8.807: 0x7E,
+    }
+    for x, b in cases.items():
+        assert oracle.lib().oq_f32_to_e4m3(x) == b, (x, hex(b))
+    # decode round trip of every finite code
+    codes = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], np.uint8)
+    vals = oracle.e4m3_to_f32(codes)
+    assert np.array_equal(oracle.cvt_array(vals, "e4m3")[codes != 0x80], codes[codes != 0x80])
+    assert vals.max() == 448.0 and vals[vals > 0].min() == 2 ** -9
+
+
+def test_bf16_rne_matches_torch(oracle):
+    x = _float_sweep()
+    got = oracle.cvt_array(x, "bf16")
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def test_f16_rne_matches_torch(oracle):
+    x = _float_sweep()
+    got = oracle.cvt_array(x, "f16")
+    want = torch.from_numpy(x).to(torch.float16).view(torch.int16).numpy().view(np.uint16)
+    finite = np.isfinite(torch.from_numpy(x).to(torch.float16).numpy())
+    assert np.array_equal(got[finite], want[finite])
+
+
+def test_s8_rounding_kats(oracle):
+    x = np.array([2.5, -2.5, 3.5, -3.5, 0.5, -0.5, 126.5, 127.4, 127.6, 200, -129, -127.5, 1.49999],
+                 np.float32)
+    rne = oracle.cvt_array(x, "s8_rne")
+    away = oracle.cvt_array(x, "s8_half_away")
+    assert rne.tolist() == [2, -2, 4, -4, 0, 0, 126, 127, 127, 127, -128, -128, 1]
+    assert away.tolist() == [3, -3, 4, -4, 1, -1, 127, 127, 127, 127, -128, -128, 1]
+
+
+# ------------------------------------------------------------------------------------------------
+# per-block INT8 quantizer (CUDA QuantInt8Kernel semantics)
+# ------------------------------------------------------------------------------------------------
+
+def test_quant_all_zero_block_uses_amax_floor(oracle):
+    x = np.zeros((1, 64, 1, 128), np.uint16)
+    q, s = oracle.quant_per_block_int8(x, blk=64)
+    assert np.all(q == 0)
+    assert s[0, 0, 0] == np.float32(np.float32(1e-7) / np.float32(127.0))
+
+
+def test_quant_ties_are_round_half_even(oracle):
+    vals = np.zeros((64, 128), np.float32)
+    vals[0, 0] = 127.0  # amax 127 -> inv = 1 exactly
+    vals[0, 1:9] = [2.5, -2.5, 3.5, -3.5, 0.5, -0.5, -127.0, 1.5]
+    q, s = oracle.quant_per_block_int8(_bits(vals, (1, 64, 1, 128)), blk=64)
+    assert s[0, 0, 0] == np.float32(1.0)
+    assert q[0, 0, 0, :9].tolist() == [127, 2, -2, 4, -4, 0, 0, -127, 2]
+
+
+def test_quant_triton_variant_ties_away_and_no_floor(oracle):
+    vals = np.zeros((64, 128), np.float32)
+    vals[0, 0] = 127.0
+    vals[0, 1:5] = [2.5, -2.5, 0.5, -0.5]
+    q, s = oracle.quant_per_block_int8(_bits(vals, (1, 64, 1, 128)), blk=64, variant="triton")
+    assert q[0, 0, 0, :5].tolist() == [127, 3, -3, 1, -1]
+    z, sz = oracle.quant_per_block_int8(np.zeros((1, 64, 1, 128), np.uint16), blk=64, variant="triton")
+    assert sz[0, 0, 0] == 0.0 and np.all(z == 0)
+
+
+def test_quant_ragged_tail_rows_excluded(oracle):
+    L = 130
+    vals = np.ones((L, 128), np.float32)
+    vals[:128] *= 0.25
+    vals[128:] = 4.0
+    vals[129, 3] = -8.0
+    q, s = oracle.quant_per_block_int8(_bits(vals, (1, L, 1, 128)), blk=128)
+    assert s.shape == (1, 1, 2)
+    assert s[0, 0, 0] == np.float32(0.25) / np.float32(127)
+    assert s[0, 0, 1] == np.float32(8.0) / np.float32(127)
+    assert q[0, 129, 0, 3] == -127 and q[0, 128, 0, 0] == 64  # 4*127/8 = 63.5 -> 64 (RNE, even)
+
+
+def test_quant_km_subtracted_in_fp32(oracle):
+    # x - km is not bf16-representable: the CUDA path keeps the fp32 difference, Triton rounds it
+    x = np.full((64, 128), 1.0078125, np.float32)
+    km = np.full((1, 1, 128), 2 ** -9, np.float32)
+    xb, kb = _bits(x, (1, 64, 1, 128)), _bits(km, (1, 1, 128))
+    _, s_cuda = oracle.quant_per_block_int8(xb, km_bits=kb, blk=64)
+    _, s_tri = oracle.quant_per_block_int8(xb, km_bits=kb, blk=64, variant="triton")
+    assert s_cuda[0, 0, 0] == np.float32(1.005859375) / np.float32(127)
+    assert s_tri[0, 0, 0] == np.float32(1.0078125) / np.float32(127)
+
+
+def test_quant_sm_scale_is_fp32_of_the_python_double(oracle):
+    D = 128
+    sm = D ** -0.5 * LOG2E
+    vals = np.zeros((128, D), np.float32)
+    vals[0, 0] = 3.0
+    vals[5, 7] = 1.0
+    q, s = oracle.quant_per_block_int8(_bits(vals, (1, 128, 1, D)), sm_scale=sm, blk=128)
+    f = np.float32(sm)
+    amax = np.float32(3.0) * f
+    assert s[0, 0, 0] == amax / np.float32(127)
+    inv = np.float32(127) / amax
+    assert q[0, 5, 0, 7] == np.rint(np.float32(np.float32(1.0) * f) * inv)  # 42.333 -> 42
+
+
+def _numpy_quant(xf, kmf, sm, blk):
+    """Independent vectorised float32 restatement (numpy's float32 ops are IEEE-rounded)."""
+    B, L, H, D = xf.shape
+    n = (L + blk - 1) // blk
+    x = xf.astype(np.float32)
+    if kmf is not None:
+        x = (x - kmf[:, None, :, :].astype(np.float32)).astype(np.float32)
+    if sm is not None:
+        x = (x * np.float32(sm)).astype(np.float32)
+    pad = np.zeros((B, n * blk, H, D), np.float32)
+    pad[:, :L] = x
+    blocks = pad.reshape(B, n, blk, H, D)
+    amax = np.maximum(np.abs(blocks).max(axis=(2, 4)), np.float32(1e-7)).astype(np.float32)  # [B, n, H]
+    scale = (amax / np.float32(127)).astype(np.float32)
+    inv = (np.float32(127) / amax).astype(np.float32)
+    qv = np.clip(np.rint((blocks * inv[:, :, None, :, None]).astype(np.float32)), -128, 127).astype(np.int8)
+    return qv.reshape(B, n * blk, H, D)[:, :L], scale.transpose(0, 2, 1)
+
+
+@pytest.mark.parametrize("L,blk,with_km,with_sm", [(1000, 128, False, True), (777, 64, True, False),
+                                                   (64, 64, True, False), (300, 128, False, False)])
+def test_quant_random_matches_numpy_restatement(oracle, L, blk, with_km, with_sm):
+    q, k, _ = qkv(2, L, L, 3, 3, seed=7, k_offset_std=0.5)
+    x = k if with_km else q
+    xb = bf16_bits(x)
+    xf = oracle.bf16_bits_to_f32(xb)
+    kmb = oracle.k_mean_bits(xb) if with_km else None
+    kmf = oracle.bf16_bits_to_f32(kmb) if with_km else None
+    sm = 128 ** -0.5 * LOG2E if with_sm else None
+    got_q, got_s = oracle.quant_per_block_int8(xb, km_bits=kmb, sm_scale=sm, blk=blk)
+    want_q, want_s = _numpy_quant(xf, kmf, sm, blk)
+    assert np.array_equal(got_s, want_s)
+    assert np.array_equal(got_q, want_q)
+
+
+def test_quant_hnd_layout_equals_nhd(oracle):
+    q, _, _ = qkv(1, 200, 200, 2, 2, seed=3)
+    nhd = bf16_bits(q)
+    hnd = np.ascontiguousarray(nhd.transpose(0, 2, 1, 3))
+    a, sa = oracle.quant_per_block_int8(nhd, blk=64, layout="NHD")
+    b, sb = oracle.quant_per_block_int8(hnd, blk=64, layout="HND")
+    assert np.array_equal(sa, sb)
+    assert np.array_equal(a, b.transpose(0, 2, 1, 3))
+
+
+# ------------------------------------------------------------------------------------------------
+# per-channel FP8 V quantizer
+# ------------------------------------------------------------------------------------------------
+
+def test_v_fp8_known_answers(oracle):
+    v = np.zeros((70, 128), np.float32)
+    v[:, 0] = 1.0
+    v[3, 0] = 2.0
+    v[:, 1] = -0.5
+    v[:, 2] = np.linspace(-3, 1, 70)
+    v8, vs = oracle.per_channel_fp8(_bits(v, (1, 70, 1, 128)))
+    assert v8.shape == (1, 1, 128, 128)
+    assert vs[0, 0, 0] == np.float32(2.0) / np.float32(448)
+    assert v8[0, 0, 0, 3] == 0x7E and v8[0, 0, 0, 0] == oracle.lib().oq_f32_to_e4m3(224.0)
+    assert v8[0, 0, 1, 0] == 0xFE  # -0.5 is the channel's amax -> -448
+    assert np.all(v8[0, 0, :3, 70:] == 0)  # padding of live channels (dead channels are NaN codes)
+    assert np.all(v8[0, 0, 5] == 0x7F)
+    assert vs[0, 0, 5] == 0.0  # all-zero channel: scale 0, recp = inf, codes NaN (as the reference)
+
+
+def test_v_fp8_random_matches_torch_cast(oracle):
+    _, _, v = qkv(2, 333, 333, 3, 3, seed=11)
+    vb = bf16_bits(v)
+    v8, vs = oracle.per_channel_fp8(vb)
+    vf = oracle.bf16_bits_to_f32(vb).transpose(0, 2, 3, 1)  # B H D L
+    amax = np.abs(vf).max(axis=-1).astype(np.float32)
+    assert np.array_equal(vs, (amax / np.float32(448)).astype(np.float32))
+    recp = (np.float32(448) / amax).astype(np.float32)
+    y = (vf * recp[..., None]).astype(np.float32)
+    want = torch.from_numpy(np.clip(y, -448, 448)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(v8[..., :333], want)
+
+
+# ------------------------------------------------------------------------------------------------
+# attention
+# ------------------------------------------------------------------------------------------------
+
+def _numpy_attn(qf, kf, vf, scale, mask=None):
+    s = np.einsum("bqhd,bkhd->bhqk", qf.astype(np.float64), kf.astype(np.float64)) * scale
+    if mask is not None:
+        s = np.where(mask, s, -np.inf)
+    s = s - s.max(-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(-1, keepdims=True)
+    return np.einsum("bhqk,bkhd->bqhd", p, vf.astype(np.float64))
+
+
+def test_fp64_truth_matches_numpy(oracle):
+    q, k, v = qkv(1, 70, 90, 2, 2, seed=5)
+    qb, kb, vb = bf16_bits(q), bf16_bits(k), bf16_bits(v)
+    got = oracle.attn_fp64(qb, kb, vb, 128 ** -0.5)
+    f = oracle.bf16_bits_to_f32
+    want = _numpy_attn(f(qb), f(kb), f(vb), 128 ** -0.5)
+    assert np.abs(got - want).max() < 1e-6
+    # causal (top-left) and key padding
+    got_c = oracle.attn_fp64(qb, kb, vb, 128 ** -0.5, causal=True, kv_valid=[60])
+    qi, ki = np.arange(70)[:, None], np.arange(90)[None, :]
+    mask = (ki <= qi) & (ki < 60)
+    want_c = _numpy_attn(f(qb), f(kb), f(vb), 128 ** -0.5, mask[None, None])
+    assert np.abs(got_c - want_c).max() < 1e-6
+
+
+def _pipeline(oracle, q, k, v, smooth=True, pv_mode=0, blkk=64, **kw):
+    D = q.shape[-1]
+    sm = D ** -0.5
+    qb, kb, vb = bf16_bits(q), bf16_bits(k), bf16_bits(v)
+    kmb = oracle.k_mean_bits(kb) if smooth else None
+    q8, qs = oracle.quant_per_block_int8(qb, sm_scale=sm * LOG2E, blk=128)
+    k8, ks = oracle.quant_per_block_int8(kb, km_bits=kmb, blk=blkk)
+    if pv_mode == 0:
+        v8, vs = oracle.per_channel_fp8(vb, pad=blkk)
+        return oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, blkk=blkk, **kw)
+    return oracle.qattn_fwd(q8, qs, k8, ks, vh_bits=vb, pv_mode=1, blkk=blkk, **kw)
+
+
+def test_quantized_pipeline_close_to_truth_c1(oracle):
+    # B=1, H=2, L=1024, D=128, k offset N(0, 0.5)
+    q, k, v = qkv(1, 1024, 1024, 2, 2, seed=20250101, k_offset_std=0.5)
+    truth = oracle.attn_fp64(bf16_bits(q), bf16_bits(k), bf16_bits(v), 128 ** -0.5)
+    o8 = _pipeline(oracle, q, k, v, pv_mode=0)
+    o16 = _pipeline(oracle, q, k, v, pv_mode=1)
+    assert cosine(o8, truth) >= 0.999
+    assert cosine(o16, truth) >= 0.999
+    assert cosine(o16, truth) > cosine(o8, truth)  # fp8 P/V rounding costs accuracy
+
+
+def test_dequantized_two_pass_agrees_with_tile_order(oracle):
+    """pv_mode 1 differs from exact softmax on the dequantized int8 logits only by bf16 P rounding."""
+    q, k, v = qkv(1, 200, 333, 2, 2, seed=9, k_offset_std=1.0)
+    qb, kb, vb = bf16_bits(q), bf16_bits(k), bf16_bits(v)
+    sm = 128 ** -0.5
+    kmb = oracle.k_mean_bits(kb)
+    q8, qs = oracle.quant_per_block_int8(qb, sm_scale=sm * LOG2E, blk=128)
+    k8, ks = oracle.quant_per_block_int8(kb, km_bits=kmb, blk=64)
+    got = oracle.qattn_fwd(q8, qs, k8, ks, vh_bits=vb, pv_mode=1)
+    qd = q8.astype(np.float64) * np.repeat(qs.transpose(0, 2, 1), 128, axis=1)[:, :200, :, None]
+    kd = k8.astype(np.float64) * np.repeat(ks.transpose(0, 2, 1), 64, axis=1)[:, :333, :, None]
+    want = _numpy_attn(qd, kd, oracle.bf16_bits_to_f32(vb), math.log(2))  # exp2(s) == exp(s ln2)
+    assert cosine(got, want) > 0.99999
+    assert np.abs(got - want).max() < 2e-2
+
+
+def test_smoothing_invariance(oracle):
+    """Adding a constant vector to every key leaves softmax unchanged; with K smoothing the
+    quantized pipeline output is (nearly) unchanged too, without it accuracy collapses."""
+    q, k, v = qkv(1, 256, 512, 1, 1, seed=13)
+    shift = torch.randn((1, 1, 1, 128), generator=torch.Generator().manual_seed(2)) * 8.0
+    k2 = (k.float() + shift).to(torch.bfloat16)
+    truth = oracle.attn_fp64(bf16_bits(q), bf16_bits(k2), bf16_bits(v), 128 ** -0.5)
+    smooth = _pipeline(oracle, q, k2, v, smooth=True)
+    raw = _pipeline(oracle, q, k2, v, smooth=False)
+    assert cosine(smooth, truth) >= 0.999
+    assert cosine(smooth, truth) > cosine(raw, truth)
+
+
+def test_uniform_v_and_single_key(oracle):
+    q, k, v = qkv(1, 128, 300, 1, 1, seed=17)
+    row = torch.linspace(-2, 2, 128).to(torch.bfloat16)
+    vu = row.expand(1, 300, 1, 128).contiguous()
+    o = _pipeline(oracle, q, k, vu)
+    assert np.abs(o - row.float().numpy()).max() < 0.05 * 2  # fp8 P sum vs fp32 d: ~1% relative
+    o1 = _pipeline(oracle, q, k[:, :1], v[:, :1])
+    v0 = v[0, 0, 0].float().numpy()
+    # single key: p = 2^8.807 -> 448, O = 448/2^8.807 * fp8(V0) * v_scale
+    assert np.abs(o1[0, :, 0] - v0[None]).max() <= np.abs(v0).max() * (2 ** -4) + 1e-6
+
+
+def test_masks_in_quantized_oracle(oracle):
+    q, k, v = qkv(1, 192, 192, 2, 2, seed=19)
+    qb, kb, vb = bf16_bits(q), bf16_bits(k), bf16_bits(v)
+    truth = oracle.attn_fp64(qb, kb, vb, 128 ** -0.5, causal=True)
+    o = _pipeline(oracle, q, k, v, causal=True)
+    assert cosine(o, truth) >= 0.999
+    truth_p = oracle.attn_fp64(qb, kb, vb, 128 ** -0.5, kv_valid=[100])
+    o_p = _pipeline(oracle, q, k, v, kv_valid=[100])
+    assert cosine(o_p, truth_p) >= 0.999
+    # on the same quantized tensors, the padding mask equals truncating K/V to the valid keys
+    q8, qs = oracle.quant_per_block_int8(qb, sm_scale=128 ** -0.5 * LOG2E, blk=128)
+    k8, ks = oracle.quant_per_block_int8(kb, blk=64)
+    v8, vs = oracle.per_channel_fp8(vb)
+    masked = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, kv_valid=[100])
+    trunc = oracle.qattn_fwd(q8, qs, k8[:, :100], ks[:, :, :2], np.ascontiguousarray(v8[..., :128]), vs)
+    assert np.array_equal(masked, trunc)
+
+
+def test_gqa_heads_map_to_kv_groups(oracle):
+    q, k, v = qkv(1, 128, 128, 4, 2, seed=23)
+    qb, kb, vb = bf16_bits(q), bf16_bits(k), bf16_bits(v)
+    truth = oracle.attn_fp64(qb, kb, vb, 128 ** -0.5)
+    o = _pipeline(oracle, q, k, v)
+    assert cosine(o, truth) >= 0.999
+    # head 3 must use kv head 1: swapping kv heads breaks it
+    kb2 = kb[:, :, ::-1].copy()
+    assert cosine(oracle.attn_fp64(qb, kb2, vb, 128 ** -0.5), truth) < 0.9
+
+
+def test_lse_matches_logsumexp(oracle):
+    q, k, v = qkv(1, 128, 256, 1, 1, seed=29)
+    qb, kb, vb = bf16_bits(q), bf16_bits(k), bf16_bits(v)
+    q8, qs = oracle.quant_per_block_int8(qb, sm_scale=128 ** -0.5 * LOG2E, blk=128)
+    k8, ks = oracle.quant_per_block_int8(kb, blk=64)
+    v8, vs = oracle.per_channel_fp8(vb)
+    _, lse2 = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, want_lse=True)
+    qd = q8[0, :, 0].astype(np.float64) * qs[0, 0, 0]
+    kd = k8[0, :, 0].astype(np.float64) * np.repeat(ks[0, 0], 64)[:, None]
+    s = qd @ kd.T  # log2 domain
+    want = np.log2(np.exp2(s - s.max(1, keepdims=True)).sum(1)) + s.max(1)
+    assert np.abs(lse2[0, 0] - want).max() < 1e-4
