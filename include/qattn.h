@@ -1,0 +1,135 @@
+/*
+ * qattn.h - C ABI of the MI355X (gfx950) quantized attention library (libqattn.so).
+ *
+ * Drop-in for the SageAttention-2 path TeleFuser reaches through
+ * telefuser/ops/attention/attention_impl.py:245-283 -> tf_kernel.sageattn2 -> torch.ops.tf_kernel.*.
+ * Every entry point takes device pointers, element strides and sizes, never allocates, launches
+ * asynchronously on the given HIP stream and returns a status code (0 = OK).  On error the
+ * message of the calling thread's last failure is available from qattn_last_error().
+ *
+ * Tensor views: a "sequence tensor" holds element (b, l, h, d) at
+ *     data[b * sb + l * sl + h * sh + d]
+ * with the head dim contiguous.  NHD ([B, L, H, D]) and HND ([B, H, L, D]) layouts are both
+ * expressed by choosing the strides (reference tensor_layout 0/1, fused.cu:476-492).
+ */
+#ifndef QATTN_H_
+#define QATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* qattn_stream_t; /* == hipStream_t */
+
+/* element strides of a sequence tensor (head dim contiguous) */
+typedef struct qattn_seq {
+  void* data;
+  int64_t sb, sl, sh;
+} qattn_seq;
+
+enum qattn_status {
+  QATTN_OK = 0,
+  QATTN_ERR_DTYPE = 1,      /* unsupported dtype code */
+  QATTN_ERR_SHAPE = 2,      /* inconsistent or unsupported sizes */
+  QATTN_ERR_STRIDE = 3,     /* strides not representable / not 16-byte aligned rows */
+  QATTN_ERR_ALIGN = 4,      /* base pointer misaligned */
+  QATTN_ERR_HEAD_DIM = 5,   /* head_dim other than 128 (callers pad 64 < D < 128 up to 128) */
+  QATTN_ERR_HEAD_RATIO = 6, /* num_qo_heads % num_kv_heads != 0 */
+  QATTN_ERR_WORKSPACE = 7,  /* workspace missing or too small */
+  QATTN_ERR_LAUNCH = 8,     /* HIP launch error */
+  QATTN_ERR_ARG = 9         /* other invalid argument */
+};
+
+enum qattn_dtype { QATTN_BF16 = 0, QATTN_FP16 = 1 };
+
+/* rounding / smoothing semantics of the per-block INT8 quantizer */
+enum qattn_quant_variant {
+  QATTN_QUANT_CUDA = 0,  /* QuantInt8Kernel: fp32 (x - km) * sm_scale, amax floor 1e-7, RNE + saturate */
+  QATTN_QUANT_TRITON = 1 /* quant_per_block_int8_kernel: half-rounded (x - km), no floor, round half away */
+};
+
+const char* qattn_last_error(void);
+int qattn_version(void);
+
+/*
+ * Per-block INT8 quantization of one tensor.
+ * Replaces torch.ops.tf_kernel.quant_per_block_int8_cuda_with_sm_scale, quant_per_block_int8_cuda and
+ * quant_per_block_int8_fuse_sub_mean_cuda (tf-kernel/csrc/common_extension.cc:168-187,
+ * tf-kernel/csrc/sageattn2/fused/fused.cu:447-696) and, with variant QATTN_QUANT_TRITON, the Triton
+ * quant_per_block_int8_kernel (tf-kernel/tf_kernel/triton/quant_per_block.py:22-71).
+ *   in:    sequence tensor [B, L, H, D] (bf16/fp16), D = 64 or 128
+ *   mean:  NULL or [B, H, D] contiguous, same dtype as in (subtracted before quantization)
+ *   out:   int8 sequence tensor (same sizes)
+ *   scale: fp32 [B, H, ceil(L / block_size)] contiguous
+ *   has_sm_scale: multiply by sm_scale (callers pass sm_scale * 1.44269504 for Q)
+ *   block_size: 32, 64 or 128
+ */
+int qattn_quant_per_block_int8(qattn_seq in, int dtype, int64_t B, int64_t L, int64_t H, int64_t D,
+                               const void* mean, qattn_seq out, float* scale, float sm_scale, int has_sm_scale,
+                               int block_size, int variant, qattn_stream_t stream);
+
+/*
+ * Q and K quantized in one launch: Q with sm_scale folded in (block blkq), K with the optional mean
+ * subtracted (block blkk).  Replaces the pair of launches in per_block_int8
+ * (tf-kernel/tf_kernel/sageattn2.py:96-187).
+ */
+int qattn_quant_qk_per_block_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq, int64_t Lk,
+                                  int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean, qattn_seq q_out,
+                                  qattn_seq k_out, float* q_scale, float* k_scale, float sm_scale, int blkq,
+                                  int blkk, int variant, qattn_stream_t stream);
+
+/*
+ * Mean over the sequence, rounded to the input dtype: mean[b, h, d] (contiguous [B, H, D]).
+ * Replaces k.mean(dim=seq) in sageattn_qk_int8_pv_fp8_cuda (tf-kernel/tf_kernel/sageattn2.py:1329-1330).
+ * Deterministic (fixed reduction order).  Needs workspace of qattn_seq_mean_workspace_size bytes.
+ */
+size_t qattn_seq_mean_workspace_size(int64_t B, int64_t L, int64_t H, int64_t D);
+int qattn_seq_mean(qattn_seq in, int dtype, int64_t B, int64_t L, int64_t H, int64_t D, void* mean,
+                   void* workspace, size_t workspace_bytes, qattn_stream_t stream);
+
+/*
+ * Per-channel FP8 (OCP e4m3) quantization of V.
+ * Replaces per_channel_fp8 = transpose_pad_permute_cuda + scale_fuse_quant_cuda
+ * (tf-kernel/tf_kernel/sageattn2.py:320-407, fused.cu:265-330,332-445,863-1010).
+ *   v8:      [B, H, D, Lpad] bytes, Lpad = ceil(L / 64) * 64.  Within every 64-key tile the keys are
+ *            stored in the order the attention kernel's FP8 MFMA A-operand reads them: key
+ *            kappa = 32*kb + 8*g + 4*hf + t sits at position 32*hf + 16*kb + 4*g + t.
+ *   v_scale: fp32 [B, H, D]; v ~= e4m3(v8) * v_scale
+ */
+size_t qattn_per_channel_fp8_workspace_size(int64_t B, int64_t L, int64_t H, int64_t D);
+int qattn_per_channel_fp8(qattn_seq v, int dtype, int64_t B, int64_t L, int64_t H, int64_t D, float scale_max,
+                          uint8_t* v8, int64_t Lpad, float* v_scale, void* workspace, size_t workspace_bytes,
+                          qattn_stream_t stream);
+
+/*
+ * Quantized attention: INT8 Q.K^T on MFMA, fp32 online softmax (exp2 domain, FP8 offset 8.807),
+ * FP8 P.V on MFMA with fp32 accumulation, v_scale fused into the epilogue.
+ * Replaces torch.ops.tf_kernel.qk_int8_sv_f8_accum_f32_fuse_v_scale_attn(_inst_buf)
+ * (tf-kernel/csrc/common_extension.cc:239-258, qattn/qk_int_sv_f8_cuda_sm89.cuh:66-841).
+ *   q8, k8:   int8 sequence tensors; q_scale [B, Hq, ceil(Lq/128)], k_scale [B, Hkv, ceil(Lk/64)]
+ *   v8/v_scale as produced by qattn_per_channel_fp8 (Lpad >= ceil(Lk/64)*64)
+ *   o:        output sequence tensor [B, Lq, Hq, D] of out_dtype
+ *   qk_mult:  extra logit multiplier (1.0 when sm_scale*log2e was folded into Q by the quantizer)
+ *   causal:   mask kv_idx > q_idx + q_offset (reference is_causal is top-left aligned, q_offset 0)
+ *   kv_valid: NULL or device int32 [B]: keys >= kv_valid[b] are masked (key padding)
+ *   lse:      NULL or fp32 [B, Hq, Lq] receiving log2(sum 2^s) of the quantized logits
+ *   num_splits: 0 = automatic, 1 = no KV split, n > 1 = split keys over n workgroups
+ *   workspace: needed when splitting, qattn_fwd_workspace_size bytes
+ * D must be 128 (callers pad head_dim < 128, as sageattn2.py:1307-1316 does).
+ */
+size_t qattn_fwd_workspace_size(int64_t B, int64_t Lq, int64_t Hq, int64_t D, int num_splits);
+int qattn_fwd_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq);
+int qattn_fwd(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const uint8_t* v8,
+              int64_t Lpad, const float* v_scale, qattn_seq o, int out_dtype, int64_t B, int64_t Lq, int64_t Lk,
+              int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int causal, int64_t q_offset,
+              const int32_t* kv_valid, float* lse, int num_splits, void* workspace, size_t workspace_bytes,
+              qattn_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QATTN_H_ */

@@ -298,79 +298,115 @@ void oq_per_channel_fp8(const uint16_t* in, int is_fp16, int64_t B, int64_t L, i
  * out: float [B, Lq, Hq, D] contiguous; lse2 (optional): log2-domain row LSE [B, Hq, Lq] of the
  * quantized logits (log2(d) + m).
  * If qrows_limit > 0 only the first qrows_limit query rows of every (b, h) are computed (CPU timing).
+ * tiles_per_split > 0 restates the KV-split schedule: every run of tiles_per_split key tiles keeps its
+ * own (m, d, O) and the partials are merged at the end with weights exp2(m_s - max m).
+ *
+ * Loop order: (b, h, 128-row query block) x key tile, with the tile's V decoded once into floats, so the
+ * same code doubles as the timed CPU baseline.
  */
 void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const float* q_scale, int64_t blkq,
                   const int8_t* k8, int64_t ksb, int64_t ksl, int64_t ksh, const float* k_scale, int64_t blkk,
                   const uint8_t* v8, int64_t Lpad, const float* v_scale, const uint16_t* vh, int is_fp16,
                   int64_t vsb, int64_t vsl, int64_t vsh, int64_t B, int64_t Lq, int64_t Lk, int64_t Hq,
                   int64_t Hkv, int64_t D, double qk_mult, int pv_mode, int causal, int64_t q_offset,
-                  const int32_t* kv_valid, int64_t h_begin, int64_t h_end, int64_t qrows_limit, float* out,
-                  float* lse2) {
+                  const int32_t* kv_valid, int64_t h_begin, int64_t h_end, int64_t qrows_limit, int64_t tiles_per_split,
+                  float* out, float* lse2) {
+  const int64_t RB = 128; /* query rows per work item */
   int64_t nQB = (Lq + blkq - 1) / blkq;
   int64_t nKB = (Lk + blkk - 1) / blkk;
   int64_t group = Hq / Hkv;
   int64_t rows = qrows_limit > 0 && qrows_limit < Lq ? qrows_limit : Lq;
+  int64_t nRB = (rows + RB - 1) / RB;
   if (h_end <= 0 || h_end > Hq) h_end = Hq;
+  if (tiles_per_split <= 0) tiles_per_split = nKB > 0 ? nKB : 1;
   double offset = pv_mode == 0 ? OQ_FP8_OFFSET : 0.0;
-#pragma omp parallel for collapse(3) schedule(dynamic, 4)
+#pragma omp parallel for collapse(3) schedule(dynamic, 1)
   for (int64_t b = 0; b < B; b++)
     for (int64_t h = h_begin; h < h_end; h++)
-      for (int64_t i = 0; i < rows; i++) {
+      for (int64_t rb = 0; rb < nRB; rb++) {
         int64_t hk = h / group;
+        int64_t i0 = rb * RB, i1 = i0 + RB < rows ? i0 + RB : rows, nr = i1 - i0;
         int64_t valid = kv_valid ? kv_valid[b] : Lk;
         if (valid > Lk) valid = Lk;
-        int64_t last = valid; /* exclusive */
-        if (causal) {
-          int64_t lim = i + q_offset + 1;
-          if (lim < last) last = lim;
-        }
-        double* o = (double*)calloc((size_t)D, sizeof(double));
-        double s[64 * 8];
-        double m = -5000000.0, dsum = 0.0;
-        int has = 0;
-        const int8_t* qrow = q8 + b * qsb + i * qsl + h * qsh;
-        double qs = q_scale[(b * Hq + h) * nQB + i / blkq];
-        for (int64_t t = 0; t < nKB && t * blkk < last; t++) {
-          int64_t k0 = t * blkk, k1 = k0 + blkk < last ? k0 + blkk : last;
-          double ks = k_scale[(b * Hkv + hk) * nKB + t];
-          double c = qs * ks * qk_mult;
-          double mx = -1e300;
-          for (int64_t j = k0; j < k1; j++) {
-            const int8_t* krow = k8 + b * ksb + j * ksl + hk * ksh;
-            int32_t acc = 0;
-            for (int64_t d = 0; d < D; d++) acc += (int32_t)qrow[d] * (int32_t)krow[d];
-            s[j - k0] = (double)acc * c;
-            if (s[j - k0] > mx) mx = s[j - k0];
-          }
-          double m_new = mx - offset > m ? mx - offset : m;
-          double alpha = has ? exp2(m - m_new) : 0.0;
-          dsum *= alpha;
-          for (int64_t d = 0; d < D; d++) o[d] *= alpha;
-          m = m_new;
-          has = 1;
-          for (int64_t j = k0; j < k1; j++) {
-            double p = exp2(s[j - k0] - m);
-            dsum += p;
-            double pr;
-            if (pv_mode == 0) {
-              pr = oq_e4m3_to_f32(oq_f32_to_e4m3((float)p));
-              const uint8_t* vcol = v8 + ((b * Hkv + hk) * D) * Lpad + j;
-              for (int64_t d = 0; d < D; d++) o[d] += pr * (double)oq_e4m3_to_f32(vcol[d * Lpad]);
-            } else {
-              pr = oq_bf16_to_f32(oq_f32_to_bf16((float)p));
-              const uint16_t* vrow = vh + b * vsb + j * vsl + hk * vsh;
-              for (int64_t d = 0; d < D; d++) o[d] += pr * (double)load_h(vrow + d, is_fp16);
+        double* o = (double*)calloc((size_t)(nr * D), sizeof(double));   /* current split */
+        double* oacc = (double*)calloc((size_t)(nr * D), sizeof(double)); /* merged splits */
+        double* m = (double*)malloc(sizeof(double) * nr);
+        double* dsum = (double*)malloc(sizeof(double) * nr);
+        double* macc = (double*)malloc(sizeof(double) * nr);
+        double* dacc = (double*)calloc((size_t)nr, sizeof(double));
+        int* has = (int*)calloc((size_t)nr, sizeof(int));
+        int* hasacc = (int*)calloc((size_t)nr, sizeof(int));
+        double* vt = (double*)malloc(sizeof(double) * blkk * D);
+        double s[1024];
+        for (int64_t r = 0; r < nr; r++) macc[r] = -INFINITY;
+        for (int64_t t0 = 0; t0 < nKB; t0 += tiles_per_split) {
+          int64_t t1 = t0 + tiles_per_split < nKB ? t0 + tiles_per_split : nKB;
+          for (int64_t r = 0; r < nr; r++) { m[r] = -5000000.0; dsum[r] = 0.0; has[r] = 0; }
+          memset(o, 0, sizeof(double) * nr * D);
+          for (int64_t t = t0; t < t1 && t * blkk < valid; t++) {
+            int64_t k0 = t * blkk, kend = k0 + blkk < valid ? k0 + blkk : valid;
+            double ks = k_scale[(b * Hkv + hk) * nKB + t];
+            for (int64_t j = k0; j < kend; j++)
+              for (int64_t d = 0; d < D; d++) {
+                double vv;
+                if (pv_mode == 0) vv = oq_e4m3_to_f32(v8[((b * Hkv + hk) * D + d) * Lpad + j]);
+                else vv = load_h(vh + b * vsb + j * vsl + hk * vsh + d, is_fp16);
+                vt[(j - k0) * D + d] = vv;
+              }
+            for (int64_t r = 0; r < nr; r++) {
+              int64_t i = i0 + r;
+              int64_t k1 = kend;
+              if (causal && i + q_offset + 1 < k1) k1 = i + q_offset + 1;
+              if (k1 <= k0) continue;
+              const int8_t* qrow = q8 + b * qsb + i * qsl + h * qsh;
+              double c = (double)q_scale[(b * Hq + h) * nQB + i / blkq] * ks * qk_mult;
+              double mx = -1e300;
+              for (int64_t j = k0; j < k1; j++) {
+                const int8_t* krow = k8 + b * ksb + j * ksl + hk * ksh;
+                int32_t acc = 0;
+                for (int64_t d = 0; d < D; d++) acc += (int32_t)qrow[d] * (int32_t)krow[d];
+                s[j - k0] = (double)acc * c;
+                if (s[j - k0] > mx) mx = s[j - k0];
+              }
+              double m_new = mx - offset > m[r] ? mx - offset : m[r];
+              double alpha = has[r] ? exp2(m[r] - m_new) : 0.0;
+              double* orow = o + r * D;
+              dsum[r] *= alpha;
+              for (int64_t d = 0; d < D; d++) orow[d] *= alpha;
+              m[r] = m_new;
+              has[r] = 1;
+              for (int64_t j = k0; j < k1; j++) {
+                double p = exp2(s[j - k0] - m_new);
+                dsum[r] += p;
+                double pr = pv_mode == 0 ? oq_e4m3_to_f32(oq_f32_to_e4m3((float)p))
+                                         : oq_bf16_to_f32(oq_f32_to_bf16((float)p));
+                const double* vr = vt + (j - k0) * D;
+                for (int64_t d = 0; d < D; d++) orow[d] += pr * vr[d];
+              }
             }
           }
+          /* merge this split into the accumulator */
+          for (int64_t r = 0; r < nr; r++) {
+            if (!has[r]) continue;
+            double M = m[r] > macc[r] ? m[r] : macc[r];
+            double fa = hasacc[r] ? exp2(macc[r] - M) : 0.0, fs = exp2(m[r] - M);
+            dacc[r] = dacc[r] * fa + dsum[r] * fs;
+            for (int64_t d = 0; d < D; d++) oacc[r * D + d] = oacc[r * D + d] * fa + o[r * D + d] * fs;
+            macc[r] = M;
+            hasacc[r] = 1;
+          }
         }
-        float* orow = out + ((b * Lq + i) * Hq + h) * D;
-        for (int64_t d = 0; d < D; d++) {
-          double v = has && dsum > 0 ? o[d] / dsum : 0.0;
-          if (pv_mode == 0) v *= (double)v_scale[(b * Hkv + hk) * D + d];
-          orow[d] = (float)v;
+        for (int64_t r = 0; r < nr; r++) {
+          int64_t i = i0 + r;
+          float* orow = out + ((b * Lq + i) * Hq + h) * D;
+          for (int64_t d = 0; d < D; d++) {
+            double v = hasacc[r] && dacc[r] > 0 ? oacc[r * D + d] / dacc[r] : 0.0;
+            if (pv_mode == 0) v *= (double)v_scale[(b * Hkv + hk) * D + d];
+            orow[d] = (float)v;
+          }
+          if (lse2) lse2[(b * Hq + h) * Lq + i] = hasacc[r] && dacc[r] > 0 ? (float)(log2(dacc[r]) + macc[r]) : -INFINITY;
         }
-        if (lse2) lse2[(b * Hq + h) * Lq + i] = has && dsum > 0 ? (float)(log2(dsum) + m) : -INFINITY;
-        free(o);
+        free(o); free(oacc); free(m); free(dsum); free(macc); free(dacc); free(has); free(hasacc); free(vt);
       }
 }
 

@@ -1,0 +1,120 @@
+"""ctypes binding of libqattn.so (the C ABI declared in include/qattn.h).
+
+The library is built in-tree (telefuser_amd/lib/libqattn.so) by ``telefuser_amd.build`` /
+``__graft_entry__.build()``.  There is no fallback: if the library or a GPU is missing, loading
+raises, so the HIP kernels are always what runs.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libqattn.so")
+
+QATTN_BF16 = 0
+QATTN_FP16 = 1
+QATTN_QUANT_CUDA = 0
+QATTN_QUANT_TRITON = 1
+
+EXPORTED = (
+    "qattn_last_error",
+    "qattn_version",
+    "qattn_quant_per_block_int8",
+    "qattn_quant_qk_per_block_int8",
+    "qattn_seq_mean_workspace_size",
+    "qattn_seq_mean",
+    "qattn_per_channel_fp8_workspace_size",
+    "qattn_per_channel_fp8",
+    "qattn_fwd_workspace_size",
+    "qattn_fwd_num_splits",
+    "qattn_fwd",
+)
+
+
+class QattnSeq(ctypes.Structure):
+    """struct qattn_seq: element (b, l, h, d) at data[b*sb + l*sl + h*sh + d]."""
+
+    _fields_ = [("data", ctypes.c_void_p), ("sb", ctypes.c_int64), ("sl", ctypes.c_int64), ("sh", ctypes.c_int64)]
+
+
+class QattnError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"qattn error {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load libqattn.so and declare its signatures.  Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`"
+                           " (or make -C telefuser_amd/csrc)")
+    L = ctypes.CDLL(LIB_PATH)
+    i64, i32, vp, f32, sz = ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_float, ctypes.c_size_t
+    S = QattnSeq
+    L.qattn_last_error.restype = ctypes.c_char_p
+    L.qattn_version.restype = i32
+    L.qattn_quant_per_block_int8.argtypes = [S, i32, i64, i64, i64, i64, vp, S, vp, f32, i32, i32, i32, vp]
+    L.qattn_quant_qk_per_block_int8.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, f32, i32,
+                                                i32, i32, vp]
+    L.qattn_seq_mean_workspace_size.argtypes = [i64, i64, i64, i64]
+    L.qattn_seq_mean_workspace_size.restype = sz
+    L.qattn_seq_mean.argtypes = [S, i32, i64, i64, i64, i64, vp, vp, sz, vp]
+    L.qattn_per_channel_fp8_workspace_size.argtypes = [i64, i64, i64, i64]
+    L.qattn_per_channel_fp8_workspace_size.restype = sz
+    L.qattn_per_channel_fp8.argtypes = [S, i32, i64, i64, i64, i64, f32, vp, i64, vp, vp, sz, vp]
+    L.qattn_fwd_workspace_size.argtypes = [i64, i64, i64, i64, i32]
+    L.qattn_fwd_workspace_size.restype = sz
+    L.qattn_fwd_num_splits.argtypes = [i64, i64, i64, i64]
+    L.qattn_fwd_num_splits.restype = i32
+    L.qattn_fwd.argtypes = [S, vp, S, vp, vp, i64, vp, S, i32, i64, i64, i64, i64, i64, i64, f32, i32, i64, vp, vp,
+                            i32, vp, sz, vp]
+    for name in ("qattn_quant_per_block_int8", "qattn_quant_qk_per_block_int8", "qattn_seq_mean",
+                 "qattn_per_channel_fp8", "qattn_fwd"):
+        getattr(L, name).restype = i32
+    _lib = L
+    return L
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        msg = load().qattn_last_error().decode()
+        if rc in (1, 5):
+            raise ValueError(f"qattn error {rc}: {msg}")
+        raise QattnError(rc, msg)
+
+
+def ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def seq(t: torch.Tensor, layout: str) -> QattnSeq:
+    """View a 4-D tensor as qattn_seq for "NHD" ([B, L, H, D]) or "HND" ([B, H, L, D])."""
+    if t.stride(-1) != 1:
+        raise ValueError("Last dim of qkv must be contiguous.")
+    if layout == "NHD":
+        return QattnSeq(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
+    if layout == "HND":
+        return QattnSeq(t.data_ptr(), t.stride(0), t.stride(2), t.stride(1))
+    raise ValueError(f"Unknown tensor layout: {layout}")
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return QATTN_BF16
+    if dt == torch.float16:
+        return QATTN_FP16
+    raise ValueError("Input tensors must be in dtype of torch.float16 or torch.bfloat16")
+
+
+def stream_of(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)

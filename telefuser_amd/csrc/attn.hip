@@ -1,0 +1,416 @@
+// Quantized attention forward for gfx950: INT8 Q.K^T and FP8 P.V on MFMA, fp32 online softmax.
+//
+// Math (the reference's sm89 kernel, tf-kernel/csrc/sageattn2/qattn/qk_int_sv_f8_cuda_sm89.cuh:342-840,
+// attn_utils.cuh:362-452 update_mdo, :469-481 RS_32_to_8, :711-756 normalize_d):
+//   s    = int32(Q8 . K8^T) * (q_scale * k_scale * qk_mult)          (log2 domain)
+//   m'   = max(m, rowmax(s) - 8.807);   p = exp2(s - m')  in (0, 448]
+//   l    = l * exp2(m - m') + sum(p)
+//   O    = O * exp2(m - m') + e4m3(p) . e4m3(V)                        (fp32 accumulation)
+//   out  = O / l * v_scale[d]
+//
+// MI355X design (not a translation of the NVIDIA tiling):
+//   * workgroup = 4 wave64s = 128 query rows (one Q quantization block, so one q_scale);
+//     each wave owns 32 rows.  Key tiles of 64 keys (one K quantization block, one k_scale).
+//   * S^T = K . Q^T with v_mfma_i32_32x32x32_i8 (A = K from LDS, B = Q held in VGPRs for the whole
+//     loop).  In the 32x32 result each lane owns one query column and 16 key rows, so the row max
+//     is an in-lane max plus one lane^32 exchange, and the running sum stays per lane until the end.
+//   * O^T = V^T . P^T with v_mfma_f32_32x32x64_f8f6f4 (A = V^T from LDS, B = P^T straight from the
+//     softmax registers).  The FP8 V quantizer stores every 64-key tile in exactly the key order the
+//     B operand inherits from the S^T layout, so P never goes through LDS.
+//   * K and V tiles are double-buffered in LDS (32 KiB) with XOR-swizzled 16-byte chunks; the next
+//     tile's global loads are issued before the current tile's MFMA/softmax work.
+//   * blockIdx -> tile mapping is XCD-aware: the hardware deals workgroups round-robin over the 8
+//     XCDs, so consecutive tiles of one (batch, head) are gathered onto one XCD and share its L2.
+//   * Optional KV split (flash-decoding style) for grids that cannot fill 256 CUs; a combine kernel
+//     merges the partial (O, m, l) triples.
+#include <algorithm>
+#include <type_traits>
+
+#include "common.h"
+
+namespace qattn {
+
+constexpr int kD = 128;
+constexpr int kBQ = 128;
+constexpr int kBK = 64;
+constexpr int kThreads = 256;
+constexpr float kFp8Offset = 8.807f;  // attn_utils.cuh:35 S_FP8_OFFSET
+constexpr float kMInit = -3.0e38f;
+
+struct AttnParams {
+  const int8_t* q8;
+  int64_t qsb, qsl, qsh;
+  const int8_t* k8;
+  int64_t ksb, ksl, ksh;
+  const uint8_t* v8;  // [B, Hkv, D, Lpad]
+  int64_t Lpad;
+  const float* q_scale;  // [B, Hq, nQB]
+  const float* k_scale;  // [B, Hkv, nKB]
+  const float* v_scale;  // [B, Hkv, D]
+  void* o;
+  int64_t osb, osl, osh;
+  float* lse;  // [B, Hq, Lq] or null
+  const int32_t* kv_valid;
+  float* ws_o;   // split partials [split][B][Hq][Lq][D]
+  float* ws_ml;  // [split][B][Hq][Lq][2]
+  int64_t B, Lq, Lk, Hq, Hkv, nQB, nKB;
+  int64_t q_offset;
+  int group;
+  int nsplit;
+  int tiles_per_split;
+  int causal;
+  float qk_mult;
+};
+
+__device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t n) {
+  const int64_t q = n / 8, r = n % 8;
+  const int64_t xcd = bid % 8, idx = bid / 8;
+  return xcd * q + (xcd < r ? xcd : r) + idx;
+}
+
+// LDS layouts (bytes):
+//   K tile: 64 rows x 128 B, 16-byte chunk c of row r at r*128 + ((c ^ ((r >> 1) & 7)) * 16)
+//   V tile: 128 rows (d) x 64 B, chunk c (0..3) of row d at d*64 + ((c ^ ((d >> 2) & 3)) * 16)
+__device__ __forceinline__ int k_lds_off(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
+__device__ __forceinline__ int v_lds_off(int d, int c) { return d * 64 + ((c ^ ((d >> 2) & 3)) << 4); }
+
+template <bool IS_FP16_OUT, bool SPLIT>
+__global__ __launch_bounds__(kThreads, 2) void qattn_fwd_kernel(AttnParams p) {
+  __shared__ __align__(16) uint8_t lds_k[2][kBK * kD];
+  __shared__ __align__(16) uint8_t lds_v[2][kD * kBK];
+
+  const int64_t tile_id = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t qb = tile_id % p.nQB;
+  int64_t rest = tile_id / p.nQB;
+  const int split = (int)(rest % p.nsplit);
+  rest /= p.nsplit;
+  const int64_t h = rest % p.Hq;
+  const int64_t b = rest / p.Hq;
+  const int64_t hk = h / p.group;
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, lane = tid & 63, lq = lane & 31, hf = lane >> 5;
+
+  // key range of this workgroup
+  int64_t kv_end = p.Lk;
+  if (p.kv_valid) kv_end = min(kv_end, (int64_t)p.kv_valid[b]);
+  const int64_t q_first = qb * kBQ;
+  if (p.causal) kv_end = min(kv_end, q_first + kBQ + p.q_offset);
+  int64_t n_tiles = kv_end > 0 ? (kv_end + kBK - 1) / kBK : 0;
+  int64_t t_begin = 0, t_end = n_tiles;
+  if (SPLIT) {
+    t_begin = (int64_t)split * p.tiles_per_split;
+    t_end = min(n_tiles, t_begin + p.tiles_per_split);
+  }
+
+  // Q fragment (B operand of S^T = K.Q^T): lane owns query row lq of this wave, bytes
+  // d = 32*m + 16*hf .. +16 for m = 0..3
+  const int64_t qrow = q_first + w * 32 + lq;
+  v4i qf[4];
+  {
+    const int8_t* qp = p.q8 + b * p.qsb + qrow * p.qsl + h * p.qsh + hf * 16;
+#pragma unroll
+    for (int m = 0; m < 4; m++) qf[m] = qrow < p.Lq ? *reinterpret_cast<const v4i*>(qp + m * 32) : v4i{0, 0, 0, 0};
+  }
+  const float qs = p.q_scale[(b * p.Hq + h) * p.nQB + qb] * p.qk_mult;
+  const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKB;
+
+  // global -> LDS copy assignment: each thread moves 2 K chunks and 2 V chunks of 16 bytes
+  const int8_t* kbase = p.k8 + b * p.ksb + hk * p.ksh;
+  const uint8_t* vbase = p.v8 + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad;
+  int kr[2], kc[2], vd[2], vc[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int id = tid + i * kThreads;
+    kr[i] = id >> 3;
+    kc[i] = id & 7;
+    vd[i] = id >> 2;
+    vc[i] = id & 3;
+  }
+  v4i kreg[2], vreg[2];
+  auto gload = [&](int64_t t) {
+    const int64_t k0 = t * kBK;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int64_t key = k0 + kr[i];
+      kreg[i] = key < p.Lk ? *reinterpret_cast<const v4i*>(kbase + key * p.ksl + kc[i] * 16) : v4i{0, 0, 0, 0};
+      vreg[i] = *reinterpret_cast<const v4i*>(vbase + vd[i] * p.Lpad + k0 + vc[i] * 16);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      *reinterpret_cast<v4i*>(&lds_k[buf][k_lds_off(kr[i], kc[i])]) = kreg[i];
+      *reinterpret_cast<v4i*>(&lds_v[buf][v_lds_off(vd[i], vc[i])]) = vreg[i];
+    }
+  };
+
+  v16f o[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[i][r] = 0.f;
+  float m_run = kMInit, l_run = 0.f;
+
+  if (t_begin < t_end) {
+    gload(t_begin);
+    lstore(0);
+  }
+  __syncthreads();
+
+  for (int64_t t = t_begin; t < t_end; t++) {
+    const int buf = (int)((t - t_begin) & 1);
+    const bool has_next = t + 1 < t_end;
+    if (has_next) gload(t + 1);
+
+    // ---- S^T = K . Q^T (two 32-key blocks) ----
+    v16i s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) s[kb][r] = 0;
+      const int krow = kb * 32 + lq;
+#pragma unroll
+      for (int m = 0; m < 4; m++) {
+        const v4i a = *reinterpret_cast<const v4i*>(&lds_k[buf][k_lds_off(krow, 2 * m + hf)]);
+        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qf[m], s[kb], 0, 0, 0);
+      }
+    }
+
+    // ---- masking (tail tile, key padding, causal) ----
+    const int64_t k0 = t * kBK;
+    const bool need_mask = (k0 + kBK > kv_end) || (p.causal && k0 + kBK - 1 > q_first + w * 32 + p.q_offset);
+    if (need_mask) {
+      const int64_t qlim = p.causal ? qrow + p.q_offset : INT64_MAX;
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int64_t key = k0 + kb * 32 + (r >> 2) * 8 + hf * 4 + (r & 3);
+          if (key >= kv_end || key > qlim) s[kb][r] = INT32_MIN;
+        }
+    }
+
+    // ---- online softmax ----
+    int mx = s[0][0];
+#pragma unroll
+    for (int r = 1; r < 16; r++) mx = max(mx, s[0][r]);
+#pragma unroll
+    for (int r = 0; r < 16; r++) mx = max(mx, s[1][r]);
+    mx = max(mx, __shfl_xor(mx, 32, 64));
+    const float cs = qs * ks_ptr[t];
+    // a row whose keys in this tile are all masked must not raise the running max
+    const float m_tile = mx == INT32_MIN ? kMInit : fmaf((float)mx, cs, -kFp8Offset);
+    const float m_new = fmaxf(m_run, m_tile);
+    if (__any(m_new > m_run)) {
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[i][r] *= alpha;
+      m_run = m_new;
+    }
+    const float neg_m = -m_run;
+    v8i pf;
+    // masked logits (INT32_MIN) become p = 0 exactly: the sentinel times a tiny block scale is not
+    // necessarily very negative, so it is tested explicitly on masked tiles only
+    auto softmax_tile = [&](auto masked) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int kb = j >> 2, r0 = (j & 3) * 4;
+        float pv[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int sv = s[kb][r0 + e];
+          pv[e] = __builtin_amdgcn_exp2f(fmaf((float)sv, cs, neg_m));
+          if constexpr (decltype(masked)::value) pv[e] = sv == INT32_MIN ? 0.f : pv[e];
+        }
+        l_run += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+        int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], 0, false);
+        packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
+        pf[j] = packed;
+      }
+    };
+    if (need_mask) softmax_tile(std::true_type{});
+    else softmax_tile(std::false_type{});
+
+    // ---- O^T += V^T . P^T ----
+#pragma unroll
+    for (int dblk = 0; dblk < 4; dblk++) {
+      const int d = dblk * 32 + lq;
+      v8i a;
+      const v4i a0 = *reinterpret_cast<const v4i*>(&lds_v[buf][v_lds_off(d, 2 * hf)]);
+      const v4i a1 = *reinterpret_cast<const v4i*>(&lds_v[buf][v_lds_off(d, 2 * hf + 1)]);
+      a[0] = a0[0]; a[1] = a0[1]; a[2] = a0[2]; a[3] = a0[3];
+      a[4] = a1[0]; a[5] = a1[1]; a[6] = a1[2]; a[7] = a1[3];
+      o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, pf, o[dblk], 0, 0, 0, 0, 0, 0);
+    }
+
+    if (has_next) lstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue ----
+  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  if (qrow >= p.Lq) return;
+  if (SPLIT) {
+    const int64_t row = (((int64_t)split * p.B + b) * p.Hq + h) * p.Lq + qrow;
+    float* wo = p.ws_o + row * kD;
+#pragma unroll
+    for (int dblk = 0; dblk < 4; dblk++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int d = dblk * 32 + g * 8 + hf * 4;
+        *reinterpret_cast<v4f*>(wo + d) =
+            v4f{o[dblk][g * 4 + 0], o[dblk][g * 4 + 1], o[dblk][g * 4 + 2], o[dblk][g * 4 + 3]};
+      }
+    if (hf == 0) {
+      p.ws_ml[row * 2 + 0] = m_run;
+      p.ws_ml[row * 2 + 1] = l_tot;
+    }
+    return;
+  }
+  const float inv_l = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  const float* vs = p.v_scale + (b * p.Hkv + hk) * kD;
+  uint16_t* orow = static_cast<uint16_t*>(p.o) + b * p.osb + qrow * p.osl + h * p.osh;
+#pragma unroll
+  for (int dblk = 0; dblk < 4; dblk++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int d = dblk * 32 + g * 8 + hf * 4;
+      const v4f sc = *reinterpret_cast<const v4f*>(vs + d);
+      uint16_t hv[4];
+#pragma unroll
+      for (int t = 0; t < 4; t++) hv[t] = f32_to_half<IS_FP16_OUT>(o[dblk][g * 4 + t] * inv_l * sc[t]);
+      v2u packed;
+      __builtin_memcpy(&packed, hv, 8);
+      *reinterpret_cast<v2u*>(orow + d) = packed;
+    }
+  if (p.lse && hf == 0)
+    p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
+}
+
+// Merge the KV-split partials: one wave per query row, 2 channels per lane.
+template <bool IS_FP16_OUT>
+__global__ __launch_bounds__(256) void qattn_combine_kernel(AttnParams p) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // over B*Hq*Lq
+  const int lane = threadIdx.x & 63;
+  const int64_t total = p.B * p.Hq * p.Lq;
+  if (row >= total) return;
+  const int64_t qrow = row % p.Lq;
+  const int64_t h = (row / p.Lq) % p.Hq;
+  const int64_t b = row / (p.Lq * p.Hq);
+  const int64_t hk = h / p.group;
+  const int64_t sstride = total;
+  float M = kMInit;
+  for (int s = 0; s < p.nsplit; s++) M = fmaxf(M, p.ws_ml[(s * sstride + row) * 2]);
+  float L = 0.f, a0 = 0.f, a1 = 0.f;
+  for (int s = 0; s < p.nsplit; s++) {
+    const float ms = p.ws_ml[(s * sstride + row) * 2], ls = p.ws_ml[(s * sstride + row) * 2 + 1];
+    const float f = __builtin_amdgcn_exp2f(ms - M);
+    L += ls * f;
+    const float* wo = p.ws_o + (s * sstride + row) * kD + lane * 2;
+    a0 += wo[0] * f;
+    a1 += wo[1] * f;
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  const float* vs = p.v_scale + (b * p.Hkv + hk) * kD + lane * 2;
+  uint16_t* orow = static_cast<uint16_t*>(p.o) + b * p.osb + qrow * p.osl + h * p.osh + lane * 2;
+  orow[0] = f32_to_half<IS_FP16_OUT>(a0 * inv * vs[0]);
+  orow[1] = f32_to_half<IS_FP16_OUT>(a1 * inv * vs[1]);
+  if (p.lse && lane == 0) p.lse[(b * p.Hq + h) * p.Lq + qrow] = L > 0.f ? __builtin_log2f(L) + M : -INFINITY;
+}
+
+}  // namespace qattn
+
+using namespace qattn;
+
+extern "C" int qattn_fwd_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq) {
+  const int64_t wgs = B * Hq * ((Lq + kBQ - 1) / kBQ);
+  const int64_t nkb = (Lk + kBK - 1) / kBK;
+  if (wgs <= 0 || nkb <= 0) return 1;
+  // 256 CUs x 2 resident workgroups; split only when the grid leaves the chip mostly idle and every
+  // split still gets at least 8 key tiles
+  const int64_t target = 1024;
+  if (wgs >= target / 2) return 1;
+  int64_t s = (target + wgs - 1) / wgs;
+  s = std::min<int64_t>(s, nkb / 8);
+  return (int)std::max<int64_t>(1, std::min<int64_t>(s, 32));
+}
+
+extern "C" size_t qattn_fwd_workspace_size(int64_t B, int64_t Lq, int64_t Hq, int64_t D, int num_splits) {
+  if (num_splits <= 1) return 0;
+  return (size_t)num_splits * B * Hq * Lq * (D + 2) * sizeof(float);
+}
+
+extern "C" int qattn_fwd(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const uint8_t* v8,
+                         int64_t Lpad, const float* v_scale, qattn_seq o, int out_dtype, int64_t B, int64_t Lq,
+                         int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int causal,
+                         int64_t q_offset, const int32_t* kv_valid, float* lse, int num_splits, void* workspace,
+                         size_t workspace_bytes, qattn_stream_t stream) {
+  QATTN_REQUIRE(out_dtype == QATTN_BF16 || out_dtype == QATTN_FP16, QATTN_ERR_DTYPE, "out dtype must be bf16 or fp16");
+  QATTN_REQUIRE(D == kD, QATTN_ERR_HEAD_DIM, "qattn_fwd needs head_dim 128 (pad smaller heads), got %lld",
+                (long long)D);
+  QATTN_REQUIRE(B >= 0 && Lq >= 0 && Lk >= 0 && Hq > 0 && Hkv > 0, QATTN_ERR_SHAPE, "bad sizes");
+  QATTN_REQUIRE(Hq % Hkv == 0, QATTN_ERR_HEAD_RATIO, "num_qo_heads (%lld) must be divisible by num_kv_heads (%lld)",
+                (long long)Hq, (long long)Hkv);
+  if (B * Lq == 0) return QATTN_OK;
+  QATTN_REQUIRE(Lk > 0, QATTN_ERR_SHAPE, "kv_len must be positive");
+  QATTN_REQUIRE(Lpad % kBK == 0 && Lpad >= (Lk + kBK - 1) / kBK * kBK, QATTN_ERR_SHAPE,
+                "Lpad must be a multiple of 64 covering kv_len");
+  for (const qattn_seq* s : {&q8, &k8}) {
+    QATTN_REQUIRE(s->data && aligned16(s->data), QATTN_ERR_ALIGN, "q8/k8 must be 16-byte aligned");
+    QATTN_REQUIRE(s->sb % 16 == 0 && s->sl % 16 == 0 && s->sh % 16 == 0, QATTN_ERR_STRIDE,
+                  "q8/k8 strides must be multiples of 16 bytes");
+  }
+  QATTN_REQUIRE(o.data && aligned16(o.data), QATTN_ERR_ALIGN, "output must be 16-byte aligned");
+  QATTN_REQUIRE(o.sb % 8 == 0 && o.sl % 8 == 0 && o.sh % 8 == 0, QATTN_ERR_STRIDE,
+                "output strides must be multiples of 16 bytes");
+  QATTN_REQUIRE(v8 && aligned16(v8) && q_scale && k_scale && v_scale, QATTN_ERR_ARG, "null scale or v8 pointer");
+  QATTN_REQUIRE(!causal || q_offset >= 0, QATTN_ERR_ARG, "q_offset must be >= 0");
+
+  AttnParams p{};
+  p.q8 = static_cast<const int8_t*>(q8.data);
+  p.qsb = q8.sb; p.qsl = q8.sl; p.qsh = q8.sh;
+  p.k8 = static_cast<const int8_t*>(k8.data);
+  p.ksb = k8.sb; p.ksl = k8.sl; p.ksh = k8.sh;
+  p.v8 = v8; p.Lpad = Lpad;
+  p.q_scale = q_scale; p.k_scale = k_scale; p.v_scale = v_scale;
+  p.o = o.data; p.osb = o.sb; p.osl = o.sl; p.osh = o.sh;
+  p.lse = lse; p.kv_valid = kv_valid;
+  p.B = B; p.Lq = Lq; p.Lk = Lk; p.Hq = Hq; p.Hkv = Hkv;
+  p.nQB = (Lq + kBQ - 1) / kBQ;
+  p.nKB = (Lk + kBK - 1) / kBK;
+  p.q_offset = q_offset;
+  p.group = (int)(Hq / Hkv);
+  p.causal = causal ? 1 : 0;
+  p.qk_mult = qk_mult;
+
+  int ns = num_splits > 0 ? num_splits : qattn_fwd_num_splits(B, Lq, Lk, Hq);
+  ns = (int)std::min<int64_t>(ns, p.nKB);
+  if (ns < 1) ns = 1;
+  p.nsplit = ns;
+  p.tiles_per_split = (int)((p.nKB + ns - 1) / ns);
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t grid = B * Hq * p.nQB * ns;
+  QATTN_REQUIRE(grid < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
+  if (ns > 1) {
+    QATTN_REQUIRE(workspace && workspace_bytes >= qattn_fwd_workspace_size(B, Lq, Hq, D, ns), QATTN_ERR_WORKSPACE,
+                  "qattn_fwd with %d KV splits needs %zu workspace bytes", ns,
+                  qattn_fwd_workspace_size(B, Lq, Hq, D, ns));
+    p.ws_o = static_cast<float*>(workspace);
+    p.ws_ml = p.ws_o + (int64_t)ns * B * Hq * Lq * D;
+    if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, true><<<grid, kThreads, 0, st>>>(p);
+    else qattn_fwd_kernel<true, true><<<grid, kThreads, 0, st>>>(p);
+    const int64_t rows = B * Hq * Lq;
+    if (out_dtype == QATTN_BF16) qattn_combine_kernel<false><<<(rows + 3) / 4, 256, 0, st>>>(p);
+    else qattn_combine_kernel<true><<<(rows + 3) / 4, 256, 0, st>>>(p);
+  } else {
+    p.nsplit = 1;
+    p.tiles_per_split = (int)p.nKB;
+    if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, false><<<grid, kThreads, 0, st>>>(p);
+    else qattn_fwd_kernel<true, false><<<grid, kThreads, 0, st>>>(p);
+  }
+  return check_launch("qattn_fwd");
+}

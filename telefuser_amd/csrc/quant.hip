@@ -1,0 +1,428 @@
+// Quantizers of the SageAttention-2 path, written for gfx950 (wave64, 16-byte vector loads):
+//   * per-block INT8 quantization of Q and K (one launch for both), with optional K-mean smoothing
+//     and sm_scale folding - semantics of QuantInt8Kernel (tf-kernel/csrc/sageattn2/fused/fused.cu:59-194)
+//     or of the Triton quant_per_block_int8_kernel (tf-kernel/tf_kernel/triton/quant_per_block.py:22-71);
+//   * the sequence mean of K used for smoothing (sageattn2.py:1329-1330);
+//   * per-channel FP8 e4m3 quantization of V into the attention kernel's tile layout
+//     (semantics of MeanScaleKernel, fused.cu:332-445, with scale_max = 448).
+// All of them are HBM-bound streaming kernels: one pass over the input, coalesced row reads,
+// reductions in registers + wave shuffles + a tiny LDS step.
+#include "common.h"
+
+namespace qattn {
+
+// ------------------------------------------------------------------------------------------------
+// per-block INT8 quantizer
+// ------------------------------------------------------------------------------------------------
+
+struct QuantJob {
+  const uint16_t* in;
+  int64_t sb, sl, sh;
+  int8_t* out;
+  int64_t ob, ol, oh;
+  float* scale;  // [B, H, nblk]
+  const uint16_t* mean;  // [B, H, D] or null
+  int64_t L, H, nblk;
+  int blk;
+  int has_sm_scale;
+  float sm_scale;
+  int64_t nwg;  // B * H * nblk
+};
+
+struct QuantArgs {
+  QuantJob job[2];
+  int njobs;
+};
+
+constexpr int kQuantThreads = 256;
+
+// Round-half-away-from-zero of the Triton kernel: t + 0.5*sign, truncate; NaN -> 0.
+__device__ __forceinline__ int8_t s8_half_away(float t) {
+  if (t != t) return 0;
+  float r = truncf(t + (t >= 0.f ? 0.5f : -0.5f));
+  r = fminf(fmaxf(r, -128.f), 127.f);
+  return (int8_t)(int)r;
+}
+
+// cvt.rni.sat.s8.f32: round to nearest even, then saturate
+__device__ __forceinline__ int8_t s8_rne_sat(float t) {
+  float r = __builtin_rintf(t);
+  r = fminf(fmaxf(r, -128.f), 127.f);
+  return (int8_t)(int)r;
+}
+
+template <bool IS_FP16, int VARIANT, int D>
+__global__ __launch_bounds__(kQuantThreads) void quant_per_block_kernel(QuantArgs args) {
+  constexpr int TPR = D / 8;                       // threads (16-byte chunks) per row
+  constexpr int MAXC = 128 * TPR / kQuantThreads;  // chunks per thread at blk = 128
+  __shared__ float red[kQuantThreads / 64];
+
+  int64_t wg = blockIdx.x;
+  int j = 0;
+  if (args.njobs > 1 && wg >= args.job[0].nwg) {
+    wg -= args.job[0].nwg;
+    j = 1;
+  }
+  const QuantJob& J = args.job[j];
+  const int64_t n = wg % J.nblk;
+  const int64_t h = (wg / J.nblk) % J.H;
+  const int64_t b = wg / (J.nblk * J.H);
+  const int tid = threadIdx.x;
+  const int nchunks = J.blk * TPR;
+
+  float x[MAXC][8];
+  float amax = VARIANT == QATTN_QUANT_CUDA ? 0.0000001f : 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXC; i++) {
+    const int c = tid + i * kQuantThreads;
+    const int row = c / TPR, dc = c % TPR;
+    const int64_t l = n * J.blk + row;
+#pragma unroll
+    for (int e = 0; e < 8; e++) x[i][e] = 0.f;
+    if (c < nchunks && l < J.L) {
+      v4u raw = *reinterpret_cast<const v4u*>(J.in + b * J.sb + l * J.sl + h * J.sh + dc * 8);
+      uint16_t hv[8];
+      __builtin_memcpy(hv, &raw, 16);
+      float mv[8];
+      if (J.mean) {
+        v4u mraw = *reinterpret_cast<const v4u*>(J.mean + (b * J.H + h) * D + dc * 8);
+        uint16_t mh[8];
+        __builtin_memcpy(mh, &mraw, 16);
+#pragma unroll
+        for (int e = 0; e < 8; e++) mv[e] = half_to_f32<IS_FP16>(mh[e]);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        float v = half_to_f32<IS_FP16>(hv[e]);
+        if (J.mean) {
+          v = v - mv[e];
+          // Triton path: k - km is a torch op on half tensors, rounded back to the half type
+          if constexpr (VARIANT == QATTN_QUANT_TRITON) v = half_to_f32<IS_FP16>(f32_to_half<IS_FP16>(v));
+        }
+        if (J.has_sm_scale) v = v * J.sm_scale;
+        x[i][e] = v;
+        amax = fmaxf(amax, fabsf(v));
+      }
+    }
+  }
+  amax = wave_max(amax);
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+
+  const float scale = amax / 127.0f;  // IEEE division (hipcc default: correctly rounded)
+  if (tid == 0) J.scale[(b * J.H + h) * J.nblk + n] = scale;
+  const float inv = 127.0f / amax;
+
+#pragma unroll
+  for (int i = 0; i < MAXC; i++) {
+    const int c = tid + i * kQuantThreads;
+    const int row = c / TPR, dc = c % TPR;
+    const int64_t l = n * J.blk + row;
+    if (c < nchunks && l < J.L) {
+      int8_t qv[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        if constexpr (VARIANT == QATTN_QUANT_CUDA) qv[e] = s8_rne_sat(x[i][e] * inv);
+        else qv[e] = s8_half_away(x[i][e] / scale);
+      }
+      v2u packed;
+      __builtin_memcpy(&packed, qv, 8);
+      *reinterpret_cast<v2u*>(J.out + b * J.ob + l * J.ol + h * J.oh + dc * 8) = packed;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// column reductions over the sequence: partial sums (mean of K) or partial abs-max (scale of V)
+// ------------------------------------------------------------------------------------------------
+
+constexpr int kColChunk = 256;  // sequence rows per workgroup
+
+template <bool IS_FP16, int MODE, int D>  // MODE 0: sum, 1: max |x|
+__global__ __launch_bounds__(256) void col_partial_kernel(const uint16_t* in, int64_t sb, int64_t sl, int64_t sh,
+                                                          int64_t L, int64_t H, int64_t nchunk, float* part) {
+  constexpr int TPR = D / 8;
+  constexpr int RPP = 256 / TPR;  // rows per pass
+  __shared__ float red[RPP][D + 1];
+  const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, r0 = tid / TPR, dc = tid % TPR;
+  float acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) acc[e] = 0.f;
+  for (int r = r0; r < kColChunk; r += RPP) {
+    const int64_t l = c * kColChunk + r;
+    if (l < L) {
+      v4u raw = *reinterpret_cast<const v4u*>(in + b * sb + l * sl + h * sh + dc * 8);
+      uint16_t hv[8];
+      __builtin_memcpy(hv, &raw, 16);
+#pragma unroll
+      for (int e = 0; e < 8; e++) {
+        float v = half_to_f32<IS_FP16>(hv[e]);
+        if constexpr (MODE == 0) acc[e] += v;
+        else acc[e] = fmaxf(acc[e], fabsf(v));
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; e++) red[r0][dc * 8 + e] = acc[e];
+  __syncthreads();
+  if (tid < D) {
+    float s = red[0][tid];
+    for (int r = 1; r < RPP; r++) s = MODE == 0 ? s + red[r][tid] : fmaxf(s, red[r][tid]);
+    part[((b * H + h) * nchunk + c) * D + tid] = s;
+  }
+}
+
+template <bool IS_FP16, int D>
+__global__ void mean_finalize_kernel(const float* part, int64_t nchunk, int64_t L, uint16_t* mean) {
+  const int64_t bh = blockIdx.x;
+  const int d = threadIdx.x;
+  float s = 0.f;
+  for (int64_t c = 0; c < nchunk; c++) s += part[(bh * nchunk + c) * D + d];
+  mean[bh * D + d] = f32_to_half<IS_FP16>(s / (float)L);
+}
+
+template <int D>
+__global__ void vscale_finalize_kernel(const float* part, int64_t nchunk, float scale_max, float* v_scale,
+                                       float* recp) {
+  const int64_t bh = blockIdx.x;
+  const int d = threadIdx.x;
+  float a = 0.f;
+  for (int64_t c = 0; c < nchunk; c++) a = fmaxf(a, part[(bh * nchunk + c) * D + d]);
+  v_scale[bh * D + d] = a / scale_max;
+  recp[bh * D + d] = scale_max / a;
+}
+
+// ------------------------------------------------------------------------------------------------
+// V -> FP8 in the attention kernel's tile layout
+// ------------------------------------------------------------------------------------------------
+
+// position of key kappa (0..63) inside its 64-key tile; see qattn.h
+__host__ __device__ __forceinline__ int vtile_pos(int kappa) {
+  const int kb = kappa >> 5, g = (kappa >> 3) & 3, hf = (kappa >> 2) & 1, t = kappa & 3;
+  return hf * 32 + kb * 16 + g * 4 + t;
+}
+
+__device__ __forceinline__ uint8_t f32_to_e4m3_sat(float y) {
+  if (y != y) return 0x7f;
+  y = fminf(fmaxf(y, -448.f), 448.f);
+  return (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(y, 0.f, 0, false) & 0xff);
+}
+
+template <bool IS_FP16, int D>
+__global__ __launch_bounds__(256) void v_fp8_kernel(const uint16_t* in, int64_t sb, int64_t sl, int64_t sh,
+                                                    int64_t L, int64_t H, const float* recp, uint8_t* v8,
+                                                    int64_t Lpad) {
+  constexpr int TPR = D / 8;
+  __shared__ __align__(16) uint8_t tile[D][64];
+  const int64_t t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const float* rc = recp + (b * H + h) * D;
+#pragma unroll
+  for (int i = 0; i < 64 * TPR / 256; i++) {
+    const int c = tid + i * 256;
+    const int row = c / TPR, dc = c % TPR;
+    const int64_t l = t * 64 + row;
+    uint16_t hv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (l < L) {
+      v4u raw = *reinterpret_cast<const v4u*>(in + b * sb + l * sl + h * sh + dc * 8);
+      __builtin_memcpy(hv, &raw, 16);
+    }
+    const int pos = vtile_pos(row);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const int d = dc * 8 + e;
+      const float y = half_to_f32<IS_FP16>(hv[e]) * rc[d];
+      tile[d][pos] = f32_to_e4m3_sat(y);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < D * 4 / 256; i++) {
+    const int c = tid + i * 256;
+    const int d = c / 4, cc = c % 4;
+    *reinterpret_cast<v4u*>(v8 + ((b * H + h) * D + d) * Lpad + t * 64 + cc * 16) =
+        *reinterpret_cast<const v4u*>(&tile[d][cc * 16]);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
+// host side
+// ------------------------------------------------------------------------------------------------
+
+static int check_seq(const char* name, const qattn_seq& s, int elem_bytes) {
+  QATTN_REQUIRE(s.data != nullptr, QATTN_ERR_ARG, "%s: null data pointer", name);
+  QATTN_REQUIRE(aligned16(s.data), QATTN_ERR_ALIGN, "%s: data pointer must be 16-byte aligned", name);
+  QATTN_REQUIRE((s.sb * elem_bytes) % 16 == 0 && (s.sl * elem_bytes) % 16 == 0 && (s.sh * elem_bytes) % 16 == 0,
+                QATTN_ERR_STRIDE, "%s: batch/seq/head strides must be multiples of 16 bytes", name);
+  return QATTN_OK;
+}
+
+static bool fill_job(QuantJob& J, const qattn_seq& in, const qattn_seq& out, int64_t B, int64_t L, int64_t H,
+                     const void* mean, float* scale, float sm_scale, int has_sm, int blk) {
+  J.in = static_cast<const uint16_t*>(in.data);
+  J.sb = in.sb; J.sl = in.sl; J.sh = in.sh;
+  J.out = static_cast<int8_t*>(out.data);
+  J.ob = out.sb; J.ol = out.sl; J.oh = out.sh;
+  J.scale = scale;
+  J.mean = static_cast<const uint16_t*>(mean);
+  J.L = L; J.H = H; J.blk = blk;
+  J.nblk = (L + blk - 1) / blk;
+  J.has_sm_scale = has_sm;
+  J.sm_scale = sm_scale;
+  J.nwg = B * H * J.nblk;
+  return true;
+}
+
+template <int D>
+static void launch_quant(const QuantArgs& a, int dtype, int variant, int64_t nwg, hipStream_t st) {
+  dim3 grid((unsigned)nwg), block(kQuantThreads);
+  if (dtype == QATTN_BF16) {
+    if (variant == QATTN_QUANT_CUDA) quant_per_block_kernel<false, QATTN_QUANT_CUDA, D><<<grid, block, 0, st>>>(a);
+    else quant_per_block_kernel<false, QATTN_QUANT_TRITON, D><<<grid, block, 0, st>>>(a);
+  } else {
+    if (variant == QATTN_QUANT_CUDA) quant_per_block_kernel<true, QATTN_QUANT_CUDA, D><<<grid, block, 0, st>>>(a);
+    else quant_per_block_kernel<true, QATTN_QUANT_TRITON, D><<<grid, block, 0, st>>>(a);
+  }
+}
+
+static int run_quant(QuantArgs& a, int dtype, int64_t D, int variant, hipStream_t st) {
+  int64_t nwg = 0;
+  for (int j = 0; j < a.njobs; j++) nwg += a.job[j].nwg;
+  if (nwg == 0) return QATTN_OK;
+  QATTN_REQUIRE(nwg < (1ll << 31), QATTN_ERR_SHAPE, "quantizer grid too large");
+  if (D == 128) launch_quant<128>(a, dtype, variant, nwg, st);
+  else launch_quant<64>(a, dtype, variant, nwg, st);
+  return check_launch("quant_per_block_int8");
+}
+
+static int check_common(int dtype, int64_t D, int variant, int blk) {
+  QATTN_REQUIRE(dtype == QATTN_BF16 || dtype == QATTN_FP16, QATTN_ERR_DTYPE, "dtype must be bf16 (0) or fp16 (1)");
+  QATTN_REQUIRE(D == 64 || D == 128, QATTN_ERR_HEAD_DIM, "head_dim must be 64 or 128, got %lld", (long long)D);
+  QATTN_REQUIRE(variant == QATTN_QUANT_CUDA || variant == QATTN_QUANT_TRITON, QATTN_ERR_ARG, "unknown variant %d",
+                variant);
+  QATTN_REQUIRE(blk == 32 || blk == 64 || blk == 128, QATTN_ERR_ARG, "block_size must be 32, 64 or 128, got %d", blk);
+  return QATTN_OK;
+}
+
+}  // namespace qattn
+
+using namespace qattn;
+
+extern "C" int qattn_quant_per_block_int8(qattn_seq in, int dtype, int64_t B, int64_t L, int64_t H, int64_t D,
+                                          const void* mean, qattn_seq out, float* scale, float sm_scale,
+                                          int has_sm_scale, int block_size, int variant, qattn_stream_t stream) {
+  int rc;
+  if ((rc = check_common(dtype, D, variant, block_size))) return rc;
+  QATTN_REQUIRE(B >= 0 && L >= 0 && H >= 0, QATTN_ERR_SHAPE, "negative size");
+  if (B * L * H == 0) return QATTN_OK;
+  if ((rc = check_seq("input", in, 2)) || (rc = check_seq("output", out, 1))) return rc;
+  QATTN_REQUIRE(scale != nullptr, QATTN_ERR_ARG, "scale is null");
+  QATTN_REQUIRE(mean == nullptr || aligned16(mean), QATTN_ERR_ALIGN, "mean must be 16-byte aligned");
+  QuantArgs a{};
+  a.njobs = 1;
+  fill_job(a.job[0], in, out, B, L, H, mean, scale, sm_scale, has_sm_scale, block_size);
+  return run_quant(a, dtype, D, variant, (hipStream_t)stream);
+}
+
+extern "C" int qattn_quant_qk_per_block_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq,
+                                             int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean,
+                                             qattn_seq q_out, qattn_seq k_out, float* q_scale, float* k_scale,
+                                             float sm_scale, int blkq, int blkk, int variant,
+                                             qattn_stream_t stream) {
+  int rc;
+  if ((rc = check_common(dtype, D, variant, blkq)) || (rc = check_common(dtype, D, variant, blkk))) return rc;
+  QATTN_REQUIRE(B >= 0 && Lq >= 0 && Lk >= 0 && Hq >= 0 && Hkv >= 0, QATTN_ERR_SHAPE, "negative size");
+  QuantArgs a{};
+  a.njobs = 0;
+  if (B * Lq * Hq > 0) {
+    if ((rc = check_seq("q", q, 2)) || (rc = check_seq("q_out", q_out, 1))) return rc;
+    QATTN_REQUIRE(q_scale != nullptr, QATTN_ERR_ARG, "q_scale is null");
+    fill_job(a.job[a.njobs++], q, q_out, B, Lq, Hq, nullptr, q_scale, sm_scale, 1, blkq);
+  }
+  if (B * Lk * Hkv > 0) {
+    if ((rc = check_seq("k", k, 2)) || (rc = check_seq("k_out", k_out, 1))) return rc;
+    QATTN_REQUIRE(k_scale != nullptr, QATTN_ERR_ARG, "k_scale is null");
+    QATTN_REQUIRE(k_mean == nullptr || aligned16(k_mean), QATTN_ERR_ALIGN, "k_mean must be 16-byte aligned");
+    fill_job(a.job[a.njobs++], k, k_out, B, Lk, Hkv, k_mean, k_scale, 1.0f, 0, blkk);
+  }
+  if (a.njobs == 0) return QATTN_OK;
+  return run_quant(a, dtype, D, variant, (hipStream_t)stream);
+}
+
+static int64_t col_chunks(int64_t L) { return (L + kColChunk - 1) / kColChunk; }
+
+extern "C" size_t qattn_seq_mean_workspace_size(int64_t B, int64_t L, int64_t H, int64_t D) {
+  return (size_t)(B * H * col_chunks(L) * D) * sizeof(float);
+}
+
+template <int MODE>
+static void launch_col(const qattn_seq& in, int dtype, int64_t B, int64_t L, int64_t H, int64_t D, int64_t nchunk,
+                       float* part, hipStream_t st) {
+  dim3 grid((unsigned)nchunk, (unsigned)H, (unsigned)B);
+  const uint16_t* p = static_cast<const uint16_t*>(in.data);
+#define QATTN_COL(F16, DD) col_partial_kernel<F16, MODE, DD><<<grid, 256, 0, st>>>(p, in.sb, in.sl, in.sh, L, H, nchunk, part)
+  if (dtype == QATTN_BF16) { if (D == 128) QATTN_COL(false, 128); else QATTN_COL(false, 64); }
+  else { if (D == 128) QATTN_COL(true, 128); else QATTN_COL(true, 64); }
+#undef QATTN_COL
+}
+
+extern "C" int qattn_seq_mean(qattn_seq in, int dtype, int64_t B, int64_t L, int64_t H, int64_t D, void* mean,
+                              void* workspace, size_t workspace_bytes, qattn_stream_t stream) {
+  int rc;
+  if ((rc = check_common(dtype, D, QATTN_QUANT_CUDA, 64))) return rc;
+  QATTN_REQUIRE(B > 0 && L > 0 && H > 0, QATTN_ERR_SHAPE, "seq_mean needs non-empty input");
+  if ((rc = check_seq("input", in, 2))) return rc;
+  QATTN_REQUIRE(mean != nullptr, QATTN_ERR_ARG, "mean is null");
+  const int64_t nchunk = col_chunks(L);
+  QATTN_REQUIRE(workspace && workspace_bytes >= qattn_seq_mean_workspace_size(B, L, H, D), QATTN_ERR_WORKSPACE,
+                "seq_mean workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  float* part = static_cast<float*>(workspace);
+  launch_col<0>(in, dtype, B, L, H, D, nchunk, part, st);
+  uint16_t* m = static_cast<uint16_t*>(mean);
+  if (dtype == QATTN_BF16) {
+    if (D == 128) mean_finalize_kernel<false, 128><<<B * H, 128, 0, st>>>(part, nchunk, L, m);
+    else mean_finalize_kernel<false, 64><<<B * H, 64, 0, st>>>(part, nchunk, L, m);
+  } else {
+    if (D == 128) mean_finalize_kernel<true, 128><<<B * H, 128, 0, st>>>(part, nchunk, L, m);
+    else mean_finalize_kernel<true, 64><<<B * H, 64, 0, st>>>(part, nchunk, L, m);
+  }
+  return check_launch("seq_mean");
+}
+
+extern "C" size_t qattn_per_channel_fp8_workspace_size(int64_t B, int64_t L, int64_t H, int64_t D) {
+  return (size_t)(B * H * col_chunks(L) * D + B * H * D) * sizeof(float);
+}
+
+extern "C" int qattn_per_channel_fp8(qattn_seq v, int dtype, int64_t B, int64_t L, int64_t H, int64_t D,
+                                     float scale_max, uint8_t* v8, int64_t Lpad, float* v_scale, void* workspace,
+                                     size_t workspace_bytes, qattn_stream_t stream) {
+  int rc;
+  if ((rc = check_common(dtype, D, QATTN_QUANT_CUDA, 64))) return rc;
+  QATTN_REQUIRE(B > 0 && L > 0 && H > 0, QATTN_ERR_SHAPE, "per_channel_fp8 needs non-empty input");
+  if ((rc = check_seq("v", v, 2))) return rc;
+  QATTN_REQUIRE(Lpad >= (L + 63) / 64 * 64 && Lpad % 64 == 0, QATTN_ERR_SHAPE,
+                "Lpad must be a multiple of 64 and >= L rounded up to 64");
+  QATTN_REQUIRE(v8 && aligned16(v8) && v_scale, QATTN_ERR_ALIGN, "v8 must be non-null and 16-byte aligned");
+  QATTN_REQUIRE(workspace && workspace_bytes >= qattn_per_channel_fp8_workspace_size(B, L, H, D),
+                QATTN_ERR_WORKSPACE, "per_channel_fp8 workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t nchunk = col_chunks(L);
+  float* part = static_cast<float*>(workspace);
+  float* recp = part + B * H * nchunk * D;
+  launch_col<1>(v, dtype, B, L, H, D, nchunk, part, st);
+  if (D == 128) vscale_finalize_kernel<128><<<B * H, 128, 0, st>>>(part, nchunk, scale_max, v_scale, recp);
+  else vscale_finalize_kernel<64><<<B * H, 64, 0, st>>>(part, nchunk, scale_max, v_scale, recp);
+  dim3 grid((unsigned)(Lpad / 64), (unsigned)H, (unsigned)B);
+  const uint16_t* p = static_cast<const uint16_t*>(v.data);
+  if (dtype == QATTN_BF16) {
+    if (D == 128) v_fp8_kernel<false, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad);
+    else v_fp8_kernel<false, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad);
+  } else {
+    if (D == 128) v_fp8_kernel<true, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad);
+    else v_fp8_kernel<true, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad);
+  }
+  return check_launch("per_channel_fp8");
+}

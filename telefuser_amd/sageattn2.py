@@ -1,0 +1,263 @@
+"""SageAttention-2 compatible front end over the gfx950 kernels of libqattn.
+
+Mirrors the module TeleFuser's backend registry loads into ``backends.sageattention``
+(telefuser/ops/attention/backends.py:87-99, called from attention_impl.py:245-283), i.e. the public
+functions of tf-kernel/tf_kernel/sageattn2.py: ``per_block_int8`` (:96-187), ``per_channel_fp8``
+(:320-407), ``sageattn_qk_int8_pv_fp8_cuda`` (:1197-1457), ``sageattn_qk_int8_pv_fp8_cuda_sm90``
+(:1460-1693), ``sageattn_qk_int8_pv_fp16_cuda`` (:930-1194) and ``sageattn`` (:415-548).
+
+Differences from the reference, all deliberate:
+  * Q/K are always quantized per block (Q blocks of 128 rows with sm_scale*log2e folded in, K blocks of
+    64 rows after K-mean smoothing) - the ``per_block_int8`` semantics.  ``qk_quant_gran`` is accepted
+    for signature compatibility; the per-warp / per-thread granularities are not used.
+  * ``pv_accum_dtype`` variants all accumulate P.V in full fp32 (MFMA accumulators are fp32), so
+    "fp32", "fp32+fp32" and "fp32+fp16" give the same result; V uses scale_max 448.
+  * ``kv_valid_len`` (per-batch number of valid keys) is honoured; ``attn_mask`` is ignored exactly as
+    the reference CUDA functions ignore it (it is swallowed by ``**kwargs``).
+  * ``per_channel_fp8`` returns V in this library's tile layout [B, H, D, Lpad] for both tensor
+    layouts (see include/qattn.h), not the NVIDIA mma permutation.
+"""
+
+from __future__ import annotations
+
+import math
+import warnings
+from typing import Any, Optional
+
+import torch
+
+from . import _lib
+
+LOG2E = 1.44269504  # the constant the reference folds into sm_scale (sageattn2.py:177)
+BLKQ = 128
+BLKK = 64
+
+
+def _dims(x: torch.Tensor, layout: str):
+    if layout == "NHD":
+        b, l, h, d = x.shape
+    elif layout == "HND":
+        b, h, l, d = x.shape
+    else:
+        raise ValueError(f"Unknown tensor layout: {layout}")
+    return b, l, h, d
+
+
+def _mean_3d(km: torch.Tensor, b: int, h: int, d: int, layout: str) -> torch.Tensor:
+    """Accept km as [B, H, D] or the keepdim forms [B, 1, H, D] (NHD) / [B, H, 1, D] (HND)."""
+    if km.dim() == 4:
+        km = km.squeeze(1) if layout == "NHD" else km.squeeze(2)
+    if tuple(km.shape) != (b, h, d):
+        raise ValueError(f"km must have shape [B, H, D] = {(b, h, d)}, got {tuple(km.shape)}")
+    return km.contiguous()
+
+
+def k_mean(k: torch.Tensor, tensor_layout: str = "HND") -> torch.Tensor:
+    """k.mean(dim=seq) as [B, H, D] in k's dtype (fp32 accumulation, fixed order), on the GPU."""
+    L = _lib.load()
+    b, l, h, d = _dims(k, tensor_layout)
+    out = torch.empty((b, h, d), dtype=k.dtype, device=k.device)
+    ws = torch.empty(L.qattn_seq_mean_workspace_size(b, l, h, d), dtype=torch.uint8, device=k.device)
+    _lib.check(L.qattn_seq_mean(_lib.seq(k, tensor_layout), _lib.dtype_code(k.dtype), b, l, h, d, _lib.ptr(out),
+                                _lib.ptr(ws), ws.numel(), _lib.stream_of(k)))
+    return out
+
+
+def per_block_int8(q: torch.Tensor, k: torch.Tensor, km: Optional[torch.Tensor] = None, BLKQ: int = 128,
+                   BLKK: int = 64, sm_scale: Optional[float] = None, tensor_layout: str = "HND",
+                   variant: str = "cuda"):
+    """Per-block INT8 quantization of q (sm_scale*1.44269504 folded in) and k (km subtracted).
+
+    Same contract as tf_kernel.sageattn2.per_block_int8 (sageattn2.py:96-187); ``variant="triton"``
+    reproduces the Triton quantizer (triton/quant_per_block.py:22-166) instead of the CUDA one.
+    Returns (q_int8, q_scale [B, Hq, ceil(Lq/BLKQ)], k_int8, k_scale [B, Hkv, ceil(Lk/BLKK)]).
+    """
+    L = _lib.load()
+    if q.dtype != k.dtype:
+        raise ValueError("q and k must have the same dtype")
+    b, lq, hq, d = _dims(q, tensor_layout)
+    _, lk, hkv, _ = _dims(k, tensor_layout)
+    q_int8 = torch.empty(q.shape, dtype=torch.int8, device=q.device)
+    k_int8 = torch.empty(k.shape, dtype=torch.int8, device=k.device)
+    q_scale = torch.empty((b, hq, (lq + BLKQ - 1) // BLKQ), dtype=torch.float32, device=q.device)
+    k_scale = torch.empty((b, hkv, (lk + BLKK - 1) // BLKK), dtype=torch.float32, device=q.device)
+    if sm_scale is None:
+        sm_scale = d ** -0.5
+    sm_scale *= LOG2E
+    kmc = None if km is None else _mean_3d(km.to(k.dtype), b, hkv, d, tensor_layout)
+    var = _lib.QATTN_QUANT_TRITON if variant == "triton" else _lib.QATTN_QUANT_CUDA
+    _lib.check(L.qattn_quant_qk_per_block_int8(
+        _lib.seq(q, tensor_layout), _lib.seq(k, tensor_layout), _lib.dtype_code(q.dtype), b, lq, lk, hq, hkv, d,
+        _lib.ptr(kmc), _lib.seq(q_int8, tensor_layout), _lib.seq(k_int8, tensor_layout), _lib.ptr(q_scale),
+        _lib.ptr(k_scale), float(sm_scale), BLKQ, BLKK, var, _lib.stream_of(q)))
+    return q_int8, q_scale, k_int8, k_scale
+
+
+def quant_per_block_int8(x: torch.Tensor, block_size: int, sm_scale: Optional[float] = None,
+                         mean: Optional[torch.Tensor] = None, tensor_layout: str = "HND", variant: str = "cuda"):
+    """One-tensor form: torch.ops.tf_kernel.quant_per_block_int8_cuda(_with_sm_scale / _fuse_sub_mean)
+    (common_extension.cc:168-187).  ``sm_scale`` is multiplied as given (no log2e)."""
+    L = _lib.load()
+    b, l, h, d = _dims(x, tensor_layout)
+    out = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    scale = torch.empty((b, h, (l + block_size - 1) // block_size), dtype=torch.float32, device=x.device)
+    mc = None if mean is None else _mean_3d(mean.to(x.dtype), b, h, d, tensor_layout)
+    var = _lib.QATTN_QUANT_TRITON if variant == "triton" else _lib.QATTN_QUANT_CUDA
+    _lib.check(L.qattn_quant_per_block_int8(
+        _lib.seq(x, tensor_layout), _lib.dtype_code(x.dtype), b, l, h, d, _lib.ptr(mc), _lib.seq(out, tensor_layout),
+        _lib.ptr(scale), float(sm_scale or 0.0), int(sm_scale is not None), block_size, var, _lib.stream_of(x)))
+    return out, scale
+
+
+def per_channel_fp8(v: torch.Tensor, tensor_layout: str = "HND", scale_max: float = 448.0, smooth_v: bool = True):
+    """V -> (v_fp8 [B, H, D, Lpad] float8_e4m3fn in tile layout, v_scale [B, H, D] fp32, None).
+
+    Same quantization as tf_kernel.sageattn2.per_channel_fp8 (sageattn2.py:320-407, MeanScaleKernel
+    fused.cu:332-445).  V smoothing (``smooth_v``) is only meaningful for fp16 accumulation and is
+    not applied (the third return value is always None)."""
+    L = _lib.load()
+    b, l, h, d = _dims(v, tensor_layout)
+    lpad = (l + 63) // 64 * 64
+    v_fp8 = torch.empty((b, h, d, lpad), dtype=torch.float8_e4m3fn, device=v.device)
+    v_scale = torch.empty((b, h, d), dtype=torch.float32, device=v.device)
+    ws = torch.empty(L.qattn_per_channel_fp8_workspace_size(b, l, h, d), dtype=torch.uint8, device=v.device)
+    _lib.check(L.qattn_per_channel_fp8(_lib.seq(v, tensor_layout), _lib.dtype_code(v.dtype), b, l, h, d,
+                                       float(scale_max), _lib.ptr(v_fp8), lpad, _lib.ptr(v_scale), _lib.ptr(ws),
+                                       ws.numel(), _lib.stream_of(v)))
+    return v_fp8, v_scale, None
+
+
+def _kv_valid_tensor(kv_valid_len, b: int, device) -> Optional[torch.Tensor]:
+    if kv_valid_len is None:
+        return None
+    t = torch.as_tensor(kv_valid_len, dtype=torch.int32)
+    if t.dim() == 0:
+        t = t.expand(b)
+    if t.numel() != b:
+        raise ValueError(f"kv_valid_len must have {b} entries")
+    return t.to(device=device, dtype=torch.int32).contiguous()
+
+
+def qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout="HND", out_dtype=torch.bfloat16,
+              qk_mult=1.0, is_causal=False, q_offset=0, kv_valid_len=None, return_lse=False, num_splits=0,
+              out: Optional[torch.Tensor] = None):
+    """Attention on already-quantized operands (the torch.ops.tf_kernel.qk_int8_sv_f8_accum_f32_fuse_v_scale
+    _attn op, common_extension.cc:239-258).  Returns o (and the log2-domain LSE [B, Hq, Lq] if asked)."""
+    L = _lib.load()
+    b, lq, hq, d = _dims(q_int8, tensor_layout)
+    _, lk, hkv, _ = _dims(k_int8, tensor_layout)
+    if hq % hkv != 0:
+        raise ValueError(f"num_qo_heads ({hq}) must be divisible by num_kv_heads ({hkv})")
+    o = out if out is not None else torch.empty(q_int8.shape, dtype=out_dtype, device=q_int8.device)
+    lse = torch.empty((b, hq, lq), dtype=torch.float32, device=q_int8.device) if return_lse else None
+    kvv = _kv_valid_tensor(kv_valid_len, b, q_int8.device)
+    ns = num_splits if num_splits > 0 else L.qattn_fwd_num_splits(b, lq, lk, hq)
+    wsb = L.qattn_fwd_workspace_size(b, lq, hq, d, ns)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=q_int8.device) if wsb else None
+    _lib.check(L.qattn_fwd(
+        _lib.seq(q_int8, tensor_layout), _lib.ptr(q_scale), _lib.seq(k_int8, tensor_layout), _lib.ptr(k_scale),
+        _lib.ptr(v_fp8), v_fp8.shape[-1], _lib.ptr(v_scale), _lib.seq(o, tensor_layout), _lib.dtype_code(o.dtype), b,
+        lq, lk, hq, hkv, d, float(qk_mult), int(bool(is_causal)), int(q_offset), _lib.ptr(kvv), _lib.ptr(lse), ns,
+        _lib.ptr(ws), wsb, _lib.stream_of(q_int8)))
+    return (o, lse) if return_lse else o
+
+
+def _pad_head_dim(x: torch.Tensor) -> torch.Tensor:
+    d = x.size(-1)
+    if d == 128:
+        return x
+    if d > 128:
+        raise ValueError(f"Unsupported head_dim: {d}")
+    return torch.nn.functional.pad(x, (0, 128 - d))
+
+
+def sageattn_qk_int8_pv_fp8_cuda(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str = "HND",
+                                 is_causal: bool = False, qk_quant_gran: str = "per_thread",
+                                 sm_scale: Optional[float] = None, pv_accum_dtype: str = "fp32+fp16",
+                                 smooth_k: bool = True, smooth_v: bool = False, return_lse: bool = False,
+                                 kv_valid_len=None, q_offset: int = 0, **kwargs: Any):
+    """INT8 Q.K^T + FP8 P.V attention (signature of sageattn2.py:1197-1210).
+
+    Extra keyword arguments beyond the reference: ``kv_valid_len`` (int or per-batch sequence: keys at
+    or beyond it are masked) and ``q_offset`` (causal diagonal offset, kv > q + q_offset is masked).
+    """
+    dtype = q.dtype
+    if not q.is_cuda:
+        raise AssertionError("Input tensors must be on cuda.")
+    if dtype not in (torch.float16, torch.bfloat16):
+        raise AssertionError("Input tensors must be in dtype of torch.float16 or torch.bfloat16")
+    if qk_quant_gran not in ("per_warp", "per_thread", "per_block"):
+        raise AssertionError("qk_quant_gran must be either 'per_warp' or 'per_thread'.")
+    if not (q.device == k.device == v.device):
+        raise AssertionError("All tensors must be on the same device.")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise AssertionError("All tensors must have the same dtype.")
+    head_dim_og = q.size(-1)
+    q, k, v = _pad_head_dim(q), _pad_head_dim(k), _pad_head_dim(v)
+    if not (q.stride(-1) == 1 and k.stride(-1) == 1 and v.stride(-1) == 1):
+        raise AssertionError("Last dim of qkv must be contiguous.")
+    if sm_scale is None:
+        sm_scale = head_dim_og ** -0.5
+    b, lq, hq, _ = _dims(q, tensor_layout)
+    _, lk, hkv, _ = _dims(k, tensor_layout)
+    if hq % hkv != 0:
+        raise ValueError(f"num_qo_heads ({hq}) must be divisible by num_kv_heads ({hkv})")
+
+    km = k_mean(k, tensor_layout) if smooth_k else None
+    q_int8, q_scale, k_int8, k_scale = per_block_int8(q, k, km, BLKQ, BLKK, sm_scale=sm_scale,
+                                                      tensor_layout=tensor_layout)
+    if smooth_v:
+        warnings.warn(f"pv_accum_dtype is '{pv_accum_dtype}', smooth_v will be ignored.")
+    v_fp8, v_scale, _ = per_channel_fp8(v, tensor_layout=tensor_layout, scale_max=448.0)
+    res = qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, tensor_layout=tensor_layout, out_dtype=dtype,
+                    is_causal=is_causal, q_offset=q_offset, kv_valid_len=kv_valid_len, return_lse=return_lse)
+    o, lse = res if return_lse else (res, None)
+    o = o[..., :head_dim_og]
+    if not return_lse:
+        return o
+    lse = lse / LOG2E
+    if smooth_k:
+        # logits were computed against k - km: add back q.km * sm_scale (sageattn2.py:1334-1354,1450-1455)
+        qq = q if tensor_layout == "HND" else q.transpose(1, 2)
+        kmb = km.repeat_interleave(hq // hkv, dim=1)  # [B, Hq, D]
+        corr = torch.matmul(qq, kmb.unsqueeze(-1)).squeeze(-1).to(torch.float32)
+        lse = lse + corr * sm_scale
+    return o, lse
+
+
+def sageattn_qk_int8_pv_fp8_cuda_sm90(*args, **kwargs):
+    """Same entry as sageattn_qk_int8_pv_fp8_cuda (the reference's Hopper variant, sageattn2.py:1460)."""
+    return sageattn_qk_int8_pv_fp8_cuda(*args, **kwargs)
+
+
+def sageattn_qk_int8_pv_fp16_cuda(q, k, v, tensor_layout: str = "HND", is_causal: bool = False,
+                                  qk_quant_gran: str = "per_thread", sm_scale: Optional[float] = None,
+                                  pv_accum_dtype: str = "fp32", smooth_k: bool = True, smooth_v: bool = False,
+                                  return_lse: bool = False, **kwargs: Any):
+    """Reference SAGE_ATTN_2_8_16 entry (sageattn2.py:930).  Served by the FP8 P.V kernel."""
+    return sageattn_qk_int8_pv_fp8_cuda(q, k, v, tensor_layout=tensor_layout, is_causal=is_causal,
+                                        qk_quant_gran=qk_quant_gran, sm_scale=sm_scale,
+                                        pv_accum_dtype=pv_accum_dtype, smooth_k=smooth_k, smooth_v=smooth_v,
+                                        return_lse=return_lse, **kwargs)
+
+
+def sageattn(q, k, v, tensor_layout: str = "HND", is_causal: bool = False, sm_scale: Optional[float] = None,
+             return_lse: bool = False, **kwargs: Any):
+    """Architecture dispatch of the reference (sageattn2.py:415-548): gfx950 always takes the
+    INT8-QK / FP8-PV kernel."""
+    return sageattn_qk_int8_pv_fp8_cuda(q, k, v, tensor_layout=tensor_layout, is_causal=is_causal,
+                                        sm_scale=sm_scale, pv_accum_dtype="fp32+fp32", return_lse=return_lse,
+                                        **kwargs)
+
+
+__all__ = [
+    "per_block_int8",
+    "quant_per_block_int8",
+    "per_channel_fp8",
+    "k_mean",
+    "qattn_fwd",
+    "sageattn",
+    "sageattn_qk_int8_pv_fp8_cuda",
+    "sageattn_qk_int8_pv_fp8_cuda_sm90",
+    "sageattn_qk_int8_pv_fp16_cuda",
+]

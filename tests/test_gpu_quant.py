@@ -1,0 +1,99 @@
+"""GPU parity of the quantizers: bit-exact against the CPU oracle (which is pinned by
+tests/test_oracle_kat.py), through the C ABI."""
+
+import numpy as np
+import pytest
+import torch
+
+from tests.gpu_util import log, require_gpu, untile_v
+from tests.inputs import bf16_bits, qkv
+
+pytestmark = pytest.mark.gpu
+LOG2E = 1.44269504
+
+
+def _as_bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("B,Lq,Lk,Hq,Hkv,layout,dtype,variant", [
+    (1, 1024, 1024, 2, 2, "NHD", torch.bfloat16, "cuda"),   # config 1
+    (2, 1000, 777, 4, 2, "NHD", torch.bfloat16, "cuda"),    # ragged tails, GQA
+    (1, 300, 130, 3, 3, "HND", torch.bfloat16, "cuda"),
+    (1, 517, 333, 2, 1, "NHD", torch.float16, "cuda"),
+    (1, 1000, 777, 2, 2, "NHD", torch.bfloat16, "triton"),
+    (1, 300, 200, 2, 2, "HND", torch.float16, "triton"),
+])
+def test_qk_quant_bit_exact(oracle, B, Lq, Lk, Hq, Hkv, layout, dtype, variant):
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    log(f"qk_quant B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} {layout} {dtype} {variant}")
+    q, k, _ = qkv(B, Lq, Lk, Hq, Hkv, seed=101, k_offset_std=0.5, dtype=dtype)
+    if layout == "HND":
+        q, k = q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
+    qd, kd = q.to(dev), k.to(dev)
+    km = sa.k_mean(kd, layout)
+    sm = 128 ** -0.5
+    q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=sm, tensor_layout=layout, variant=variant)
+    torch.cuda.synchronize()
+    f16 = dtype == torch.float16
+    kmb = _as_bits(km)
+    oq8, oqs = oracle.quant_per_block_int8(_as_bits(q), sm_scale=sm * LOG2E, blk=128, layout=layout, is_fp16=f16,
+                                           variant=variant)
+    ok8, oks = oracle.quant_per_block_int8(_as_bits(k), km_bits=kmb, blk=64, layout=layout, is_fp16=f16,
+                                           variant=variant)
+    assert np.array_equal(qs.cpu().numpy(), oqs)
+    assert np.array_equal(ks.cpu().numpy(), oks)
+    assert np.array_equal(q8.cpu().numpy(), oq8)
+    assert np.array_equal(k8.cpu().numpy(), ok8)
+
+
+def test_quant_known_answers_on_gpu(oracle):
+    """Closed-form cases (ties, all-zero block, tail rows) through the single-tensor entry."""
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    vals = torch.zeros((1, 130, 1, 128))
+    vals[0, 0, 0, 0] = 127.0
+    vals[0, 0, 0, 1:5] = torch.tensor([2.5, -2.5, 3.5, 0.5])
+    vals[0, 64:128] = 0.0  # all-zero block
+    vals[0, 128:, 0, :] = 4.0
+    vals[0, 129, 0, 3] = -8.0
+    x = vals.to(torch.bfloat16).to(dev)
+    q8, s = sa.quant_per_block_int8(x, 64, tensor_layout="NHD")
+    q8, s = q8.cpu(), s.cpu()
+    assert q8[0, 0, 0, :5].tolist() == [127, 2, -2, 4, 0]
+    assert s[0, 0, 1].item() == np.float32(np.float32(1e-7) / np.float32(127))
+    assert q8[0, 129, 0, 3].item() == -127 and q8[0, 128, 0, 0].item() == 64
+    t8, ts = sa.quant_per_block_int8(x, 64, tensor_layout="NHD", variant="triton")
+    assert t8.cpu()[0, 0, 0, :5].tolist() == [127, 3, -3, 4, 1]
+    assert ts.cpu()[0, 0, 1].item() == 0.0
+
+
+def test_k_mean_close_to_fp64(oracle):
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    _, k, _ = qkv(2, 16, 3001, 2, 3, seed=5, k_offset_std=1.0)
+    km = sa.k_mean(k.to(dev), "NHD").float().cpu().numpy()
+    want = k.double().mean(dim=1).numpy()
+    # bf16 result of an fp32 sum: within one bf16 ulp of the exact mean
+    assert np.all(np.abs(km - want) <= np.abs(want) * 2 ** -7 + 1e-6)
+
+
+@pytest.mark.parametrize("B,L,H,layout,dtype", [(1, 1024, 2, "NHD", torch.bfloat16), (2, 777, 3, "NHD", torch.bfloat16),
+                                                (1, 300, 2, "HND", torch.float16), (1, 64, 1, "NHD", torch.bfloat16)])
+def test_v_fp8_bit_exact(oracle, B, L, H, layout, dtype):
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    log(f"v_fp8 B={B} L={L} H={H} {layout} {dtype}")
+    _, _, v = qkv(B, 8, L, H, H, seed=77, dtype=dtype)
+    if layout == "HND":
+        v = v.transpose(1, 2).contiguous()
+    v8, vs, _ = sa.per_channel_fp8(v.to(dev), tensor_layout=layout)
+    torch.cuda.synchronize()
+    ov8, ovs = oracle.per_channel_fp8(_as_bits(v), layout=layout, is_fp16=dtype == torch.float16)
+    assert np.array_equal(vs.cpu().numpy(), ovs)
+    assert np.array_equal(untile_v(v8), ov8)

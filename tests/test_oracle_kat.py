@@ -366,3 +366,19 @@ def test_lse_matches_logsumexp(oracle):
     s = qd @ kd.T  # log2 domain
     want = np.log2(np.exp2(s - s.max(1, keepdims=True)).sum(1)) + s.max(1)
     assert np.abs(lse2[0, 0] - want).max() < 1e-4
+
+
+def test_split_schedule_restatement(oracle):
+    """One split covering every tile is the unsplit schedule bit for bit; real splits only change
+    the fp8 rounding of P (each split has its own running max)."""
+    q, k, v = qkv(1, 128, 1000, 1, 1, seed=31)
+    qb, kb, vb = bf16_bits(q), bf16_bits(k), bf16_bits(v)
+    q8, qs = oracle.quant_per_block_int8(qb, sm_scale=128 ** -0.5 * LOG2E, blk=128)
+    k8, ks = oracle.quant_per_block_int8(kb, blk=64)
+    v8, vs = oracle.per_channel_fp8(vb)
+    base = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs)
+    assert np.array_equal(base, oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, tiles_per_split=16))
+    split = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, tiles_per_split=3)
+    assert 0.999 < cosine(split, base) < 1.0
+    truth = oracle.attn_fp64(qb, kb, vb, 128 ** -0.5)
+    assert cosine(split, truth) >= 0.999
