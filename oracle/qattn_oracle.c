@@ -298,6 +298,9 @@ void oq_per_channel_fp8(const uint16_t* in, int is_fp16, int64_t B, int64_t L, i
  * out: float [B, Lq, Hq, D] contiguous; lse2 (optional): log2-domain row LSE [B, Hq, Lq] of the
  * quantized logits (log2(d) + m).
  * If qrows_limit > 0 only the first qrows_limit query rows of every (b, h) are computed (CPU timing).
+ * lazy_tau >= 0 restates the lazy running-max rule of the device kernel: m moves to rowmax(s) -
+ * (offset - tau) only when that exceeds the current m by more than tau (p stays <= 2^offset);
+ * lazy_tau < 0 is the reference rule m = max(m, rowmax(s) - offset) of update_mdo.
  * tiles_per_split > 0 restates the KV-split schedule: every run of tiles_per_split key tiles keeps its
  * own (m, d, O) and the partials are merged at the end with weights exp2(m_s - max m).
  *
@@ -310,7 +313,7 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
                   int64_t vsb, int64_t vsl, int64_t vsh, int64_t B, int64_t Lq, int64_t Lk, int64_t Hq,
                   int64_t Hkv, int64_t D, double qk_mult, int pv_mode, int causal, int64_t q_offset,
                   const int32_t* kv_valid, int64_t h_begin, int64_t h_end, int64_t qrows_limit, int64_t tiles_per_split,
-                  float* out, float* lse2) {
+                  double lazy_tau, float* out, float* lse2) {
   const int64_t RB = 128; /* query rows per work item */
   int64_t nQB = (Lq + blkq - 1) / blkq;
   int64_t nKB = (Lk + blkk - 1) / blkk;
@@ -368,7 +371,13 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
                 s[j - k0] = (double)acc * c;
                 if (s[j - k0] > mx) mx = s[j - k0];
               }
-              double m_new = mx - offset > m[r] ? mx - offset : m[r];
+              double m_new;
+              if (lazy_tau < 0) {
+                m_new = mx - offset > m[r] ? mx - offset : m[r];
+              } else { /* lazy rule: move m only when the tile max exceeds it by more than tau */
+                double mt = mx - (offset - lazy_tau);
+                m_new = (!has[r] || mt > m[r] + lazy_tau) ? mt : m[r];
+              }
               double alpha = has[r] ? exp2(m[r] - m_new) : 0.0;
               double* orow = o + r * D;
               dsum[r] *= alpha;

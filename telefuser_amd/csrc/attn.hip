@@ -4,6 +4,8 @@
 // attn_utils.cuh:362-452 update_mdo, :469-481 RS_32_to_8, :711-756 normalize_d):
 //   s    = int32(Q8 . K8^T) * (q_scale * k_scale * qk_mult)          (log2 domain)
 //   m'   = max(m, rowmax(s) - 8.807);   p = exp2(s - m')  in (0, 448]
+//          (here with a lazy update rule: m' = rowmax(s) - 7.807 only if that exceeds m by > 1, which
+//          keeps p <= 448 and skips the O rescale on almost every tile; oracle/ restates the rule)
 //   l    = l * exp2(m - m') + sum(p)
 //   O    = O * exp2(m - m') + e4m3(p) . e4m3(V)                        (fp32 accumulation)
 //   out  = O / l * v_scale[d]
@@ -17,8 +19,9 @@
 //   * O^T = V^T . P^T with v_mfma_f32_32x32x64_f8f6f4 (A = V^T from LDS, B = P^T straight from the
 //     softmax registers).  The FP8 V quantizer stores every 64-key tile in exactly the key order the
 //     B operand inherits from the S^T layout, so P never goes through LDS.
-//   * K and V tiles are double-buffered in LDS (32 KiB) with XOR-swizzled 16-byte chunks; the next
-//     tile's global loads are issued before the current tile's MFMA/softmax work.
+//   * K tiles are double-buffered and V tiles triple-buffered in LDS (40 KiB) with XOR-swizzled 16-byte chunks; the next
+//     tile is fetched by LDS DMA (global_load_lds_dwordx4) issued before the current tile's
+//     MFMA/softmax work, so staging costs neither VGPRs nor VALU slots.
 //   * blockIdx -> tile mapping is XCD-aware: the hardware deals workgroups round-robin over the 8
 //     XCDs, so consecutive tiles of one (batch, head) are gathered onto one XCD and share its L2.
 //   * Optional KV split (flash-decoding style) for grids that cannot fill 256 CUs; a combine kernel
@@ -31,11 +34,16 @@
 namespace qattn {
 
 constexpr int kD = 128;
-constexpr int kBQ = 128;
+constexpr int kBQ = 128;  // query quantization block
+constexpr int kWavesPerSimd = 2;  // occupancy target: 2 workgroups of 4 waves per CU
+constexpr int kPrefetch = 2;      // K/V tiles in flight ahead of the one being computed
+constexpr int kNBuf = kPrefetch + 1;
+constexpr int kMaxTilesPerSplit = 2048;  // key tiles per workgroup (k_scales staged in LDS)
 constexpr int kBK = 64;
 constexpr int kThreads = 256;
 constexpr float kFp8Offset = 8.807f;  // attn_utils.cuh:35 S_FP8_OFFSET
 constexpr float kMInit = -3.0e38f;
+constexpr float kLazyTau = 1.0f;  // lazy-rescale threshold (log2 units), see the softmax below
 
 struct AttnParams {
   const int8_t* q8;
@@ -74,10 +82,27 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t n) {
 __device__ __forceinline__ int k_lds_off(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
 __device__ __forceinline__ int v_lds_off(int d, int c) { return d * 64 + ((c ^ ((d >> 2) & 3)) << 4); }
 
+// One 16-byte-per-lane global -> LDS DMA (global_load_lds_dwordx4): lane j's 16 bytes land at
+// lds_base + 16 j.  Issued through inline asm so the compiler does not treat every later LDS read
+// as a possible alias of the in-flight DMA (it would otherwise put an s_waitcnt vmcnt(0) in front of
+// them and serialise the prefetch); completion is tracked with explicit vmcnt waits instead.
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
+  const uint32_t lds =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_base);
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(src), "s"(lds)
+      : "memory", "m0");
+}
+
 template <bool IS_FP16_OUT, bool SPLIT>
-__global__ __launch_bounds__(kThreads, 2) void qattn_fwd_kernel(AttnParams p) {
-  __shared__ __align__(16) uint8_t lds_k[2][kBK * kD];
-  __shared__ __align__(16) uint8_t lds_v[2][kD * kBK];
+__global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(AttnParams p) {
+  __shared__ __align__(16) uint8_t lds_k[kNBuf][kBK * kD];
+  __shared__ __align__(16) uint8_t lds_v[kNBuf][kD * kBK];
+  __shared__ float lds_ks[kMaxTilesPerSplit];  // k_scale of this workgroup's key tiles
 
   const int64_t tile_id = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t qb = tile_id % p.nQB;
@@ -92,11 +117,11 @@ __global__ __launch_bounds__(kThreads, 2) void qattn_fwd_kernel(AttnParams p) {
   const int w = tid >> 6, lane = tid & 63, lq = lane & 31, hf = lane >> 5;
 
   // key range of this workgroup
+  const int64_t q_first = qb * kBQ;
   int64_t kv_end = p.Lk;
   if (p.kv_valid) kv_end = min(kv_end, (int64_t)p.kv_valid[b]);
-  const int64_t q_first = qb * kBQ;
   if (p.causal) kv_end = min(kv_end, q_first + kBQ + p.q_offset);
-  int64_t n_tiles = kv_end > 0 ? (kv_end + kBK - 1) / kBK : 0;
+  const int64_t n_tiles = kv_end > 0 ? (kv_end + kBK - 1) / kBK : 0;
   int64_t t_begin = 0, t_end = n_tiles;
   if (SPLIT) {
     t_begin = (int64_t)split * p.tiles_per_split;
@@ -105,43 +130,53 @@ __global__ __launch_bounds__(kThreads, 2) void qattn_fwd_kernel(AttnParams p) {
 
   // Q fragment (B operand of S^T = K.Q^T): lane owns query row lq of this wave, bytes
   // d = 32*m + 16*hf .. +16 for m = 0..3
-  const int64_t qrow = q_first + w * 32 + lq;
+  const int64_t wrow0 = q_first + w * 32;
+  const int64_t qrow = wrow0 + lq;
   v4i qf[4];
   {
     const int8_t* qp = p.q8 + b * p.qsb + qrow * p.qsl + h * p.qsh + hf * 16;
 #pragma unroll
     for (int m = 0; m < 4; m++) qf[m] = qrow < p.Lq ? *reinterpret_cast<const v4i*>(qp + m * 32) : v4i{0, 0, 0, 0};
+    // consume the loads here: otherwise the compiler's wait for them lands at their first use inside
+    // the key loop, where it becomes a full vmcnt(0) drain of the K/V prefetch on every iteration
+#pragma unroll
+    for (int m = 0; m < 4; m++) asm volatile("" ::"v"(qf[m]));
   }
   const float qs = p.q_scale[(b * p.Hq + h) * p.nQB + qb] * p.qk_mult;
   const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKB;
 
-  // global -> LDS copy assignment: each thread moves 2 K chunks and 2 V chunks of 16 bytes
+  // global -> LDS copies go through the LDS-DMA path (global_load_lds_dwordx4): lane j of a wave
+  // writes the 16 bytes at LDS slot (wave base + 16 j), so the XOR swizzle is applied on the global
+  // side: the lane that owns LDS slot (row, chunk c') fetches global chunk c = c' ^ swizzle(row).
+  // Each wave moves 2 x 1 KiB of K and 2 x 1 KiB of V per tile; no VGPRs are spent on staging.
   const int8_t* kbase = p.k8 + b * p.ksb + hk * p.ksh;
   const uint8_t* vbase = p.v8 + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad;
-  int kr[2], kc[2], vd[2], vc[2];
+  // per-lane DMA source offsets relative to the tile start (first K row / first V column)
+  int64_t koff[2];
+  int voff[2];
+  int kr[2];
 #pragma unroll
   for (int i = 0; i < 2; i++) {
-    const int id = tid + i * kThreads;
-    kr[i] = id >> 3;
-    kc[i] = id & 7;
-    vd[i] = id >> 2;
-    vc[i] = id & 3;
+    const int slot = (i * 4 + w) * 64 + lane;
+    kr[i] = slot >> 3;
+    const int kc = (slot & 7) ^ ((kr[i] >> 1) & 7);
+    const int vd = slot >> 2;
+    const int vc = (slot & 3) ^ ((vd >> 2) & 3);
+    koff[i] = kr[i] * p.ksl + kc * 16;
+    voff[i] = (int)(vd * p.Lpad + vc * 16);
   }
-  v4i kreg[2], vreg[2];
-  auto gload = [&](int64_t t) {
-    const int64_t k0 = t * kBK;
+  const int64_t k_step = (int64_t)kBK * p.ksl;
+  auto dma_tile = [&](int64_t t, int buf) {
+    const int8_t* kt = kbase + t * k_step;
+    const uint8_t* vt = vbase + t * kBK;
+    const bool clamp = t * kBK + kBK > p.Lk;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
-      const int64_t key = k0 + kr[i];
-      kreg[i] = key < p.Lk ? *reinterpret_cast<const v4i*>(kbase + key * p.ksl + kc[i] * 16) : v4i{0, 0, 0, 0};
-      vreg[i] = *reinterpret_cast<const v4i*>(vbase + vd[i] * p.Lpad + k0 + vc[i] * 16);
-    }
-  };
-  auto lstore = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      *reinterpret_cast<v4i*>(&lds_k[buf][k_lds_off(kr[i], kc[i])]) = kreg[i];
-      *reinterpret_cast<v4i*>(&lds_v[buf][v_lds_off(vd[i], vc[i])]) = vreg[i];
+      // rows past Lk (last tile only) are clamped onto the last key; they are masked out anyway
+      const int8_t* src = kt + koff[i];
+      if (clamp) src = kbase + min(t * kBK + kr[i], p.Lk - 1) * p.ksl + (koff[i] - kr[i] * p.ksl);
+      lds_dma16(src, &lds_k[buf][(i * 4 + w) * 1024]);
+      lds_dma16(vt + voff[i], &lds_v[buf][(i * 4 + w) * 1024]);
     }
   };
 
@@ -152,35 +187,41 @@ __global__ __launch_bounds__(kThreads, 2) void qattn_fwd_kernel(AttnParams p) {
     for (int r = 0; r < 16; r++) o[i][r] = 0.f;
   float m_run = kMInit, l_run = 0.f;
 
-  if (t_begin < t_end) {
-    gload(t_begin);
-    lstore(0);
-  }
+  // K/V tiles run kPrefetch tiles ahead of the compute through kNBuf = kPrefetch + 1 LDS buffers:
+  // iteration t issues tile t + kPrefetch into buffer (t + kPrefetch) % kNBuf, which was last read in
+  // iteration t - 1.  The k_scales of all tiles are staged in LDS once, so the only VMEM traffic in the
+  // loop is the 4 DMA instructions per tile and the vmcnt accounting below is exact.
+  for (int64_t t = t_begin + tid; t < t_end; t += kThreads) lds_ks[t - t_begin] = ks_ptr[t];
+#pragma unroll
+  for (int d = 0; d < kPrefetch; d++)
+    if (t_begin + d < t_end) dma_tile(t_begin + d, d);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
+  int buf = 0;
   for (int64_t t = t_begin; t < t_end; t++) {
-    const int buf = (int)((t - t_begin) & 1);
-    const bool has_next = t + 1 < t_end;
-    if (has_next) gload(t + 1);
+    const bool issue = t + kPrefetch < t_end;
+    if (issue) dma_tile(t + kPrefetch, buf == 0 ? kNBuf - 1 : buf - 1);
+    const float ks_cur = lds_ks[t - t_begin];
 
-    // ---- S^T = K . Q^T (two 32-key blocks) ----
+    // ---- S^T = K . Q^T: two 32-key blocks x 4 MFMAs over D = 128; K fragments streamed from LDS ----
     v16i s[2];
+    {
+      v4i kf[8];  // all K fragments first: the LDS latency is paid once per tile
 #pragma unroll
-    for (int kb = 0; kb < 2; kb++) {
+      for (int j = 0; j < 8; j++)
+        kf[j] = *reinterpret_cast<const v4i*>(&lds_k[buf][k_lds_off((j & 1) * 32 + lq, 2 * (j >> 1) + hf)]);
 #pragma unroll
-      for (int r = 0; r < 16; r++) s[kb][r] = 0;
-      const int krow = kb * 32 + lq;
-#pragma unroll
-      for (int m = 0; m < 4; m++) {
-        const v4i a = *reinterpret_cast<const v4i*>(&lds_k[buf][k_lds_off(krow, 2 * m + hf)]);
-        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, qf[m], s[kb], 0, 0, 0);
+      for (int j = 0; j < 8; j++) {
+        const int m = j >> 1, kb = j & 1;
+        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j], qf[m], m == 0 ? v16i{} : s[kb], 0, 0, 0);
       }
     }
 
-    // ---- masking (tail tile, key padding, causal) ----
+    // ---- masking (tail tile, key padding, causal diagonal) ----
     const int64_t k0 = t * kBK;
-    const bool need_mask = (k0 + kBK > kv_end) || (p.causal && k0 + kBK - 1 > q_first + w * 32 + p.q_offset);
-    if (need_mask) {
+    const bool masked = (k0 + kBK > kv_end) || (p.causal && k0 + kBK - 1 > wrow0 + p.q_offset);
+    if (masked) {
       const int64_t qlim = p.causal ? qrow + p.q_offset : INT64_MAX;
 #pragma unroll
       for (int kb = 0; kb < 2; kb++)
@@ -192,17 +233,25 @@ __global__ __launch_bounds__(kThreads, 2) void qattn_fwd_kernel(AttnParams p) {
     }
 
     // ---- online softmax ----
-    int mx = s[0][0];
+    int mx = max(s[0][0], s[0][1]);
 #pragma unroll
-    for (int r = 1; r < 16; r++) mx = max(mx, s[0][r]);
+    for (int r = 2; r < 16; r++) mx = max(mx, s[0][r]);
 #pragma unroll
     for (int r = 0; r < 16; r++) mx = max(mx, s[1][r]);
-    mx = max(mx, __shfl_xor(mx, 32, 64));
-    const float cs = qs * ks_ptr[t];
-    // a row whose keys in this tile are all masked must not raise the running max
-    const float m_tile = mx == INT32_MIN ? kMInit : fmaf((float)mx, cs, -kFp8Offset);
-    const float m_new = fmaxf(m_run, m_tile);
-    if (__any(m_new > m_run)) {
+    {  // lanes l and l^32 hold the two key halves of the same query row
+      const auto sw = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);
+      mx = max((int)sw[0], (int)sw[1]);
+    }
+    const float cs = qs * ks_cur;
+    // Lazy rescale: the running max m is only moved when the tile max exceeds it by more than
+    // kLazyTau (log2 units), per row.  With the offset lowered by the same tau, p = exp2(s - m) stays
+    // <= 2^8.807 = 448 (the e4m3 maximum), so the FP8 range is honoured while the O rescale (64
+    // multiplies per lane) is skipped on almost every tile.  A row whose keys in this tile are all
+    // masked never moves m.
+    const float m_tile = mx == INT32_MIN ? kMInit : fmaf((float)mx, cs, -(kFp8Offset - kLazyTau));
+    const bool grow = m_tile > m_run + kLazyTau;
+    if (__any(grow)) {
+      const float m_new = grow ? m_tile : m_run;
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       l_run *= alpha;
 #pragma unroll
@@ -213,9 +262,10 @@ __global__ __launch_bounds__(kThreads, 2) void qattn_fwd_kernel(AttnParams p) {
     }
     const float neg_m = -m_run;
     v8i pf;
-    // masked logits (INT32_MIN) become p = 0 exactly: the sentinel times a tiny block scale is not
-    // necessarily very negative, so it is tested explicitly on masked tiles only
-    auto softmax_tile = [&](auto masked) {
+    // p = exp2(s * cs - m), packed to e4m3; masked logits (INT32_MIN) become p = 0 exactly (the
+    // sentinel times a tiny block scale is not necessarily very negative)
+    auto body = [&](auto mk) {
+      float lsum = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; j++) {
         const int kb = j >> 2, r0 = (j & 3) * 4;
@@ -224,35 +274,46 @@ __global__ __launch_bounds__(kThreads, 2) void qattn_fwd_kernel(AttnParams p) {
         for (int e = 0; e < 4; e++) {
           const int sv = s[kb][r0 + e];
           pv[e] = __builtin_amdgcn_exp2f(fmaf((float)sv, cs, neg_m));
-          if constexpr (decltype(masked)::value) pv[e] = sv == INT32_MIN ? 0.f : pv[e];
+          if constexpr (decltype(mk)::value) pv[e] = sv == INT32_MIN ? 0.f : pv[e];
         }
-        l_run += (pv[0] + pv[1]) + (pv[2] + pv[3]);
-        int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], 0, false);
-        packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
-        pf[j] = packed;
+        lsum += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+        const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], 0, false);
+        pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
       }
+      l_run += lsum;
     };
-    if (need_mask) softmax_tile(std::true_type{});
-    else softmax_tile(std::false_type{});
+    if (masked) body(std::true_type{});
+    else body(std::false_type{});
 
-    // ---- O^T += V^T . P^T ----
+    // ---- O^T += V^T . P^T; V^T fragments streamed from LDS ----
+    {
+      auto load_v1 = [&](int dblk) -> v8i {
+        const int d = dblk * 32 + lq;
+        const v4i a0 = *reinterpret_cast<const v4i*>(&lds_v[buf][v_lds_off(d, 2 * hf)]);
+        const v4i a1 = *reinterpret_cast<const v4i*>(&lds_v[buf][v_lds_off(d, 2 * hf + 1)]);
+        return v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+      };
+      v8i vf[4];
 #pragma unroll
-    for (int dblk = 0; dblk < 4; dblk++) {
-      const int d = dblk * 32 + lq;
-      v8i a;
-      const v4i a0 = *reinterpret_cast<const v4i*>(&lds_v[buf][v_lds_off(d, 2 * hf)]);
-      const v4i a1 = *reinterpret_cast<const v4i*>(&lds_v[buf][v_lds_off(d, 2 * hf + 1)]);
-      a[0] = a0[0]; a[1] = a0[1]; a[2] = a0[2]; a[3] = a0[3];
-      a[4] = a1[0]; a[5] = a1[1]; a[6] = a1[2]; a[7] = a1[3];
-      o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, pf, o[dblk], 0, 0, 0, 0, 0, 0);
+      for (int dblk = 0; dblk < 4; dblk++) vf[dblk] = load_v1(dblk);
+#pragma unroll
+      for (int dblk = 0; dblk < 4; dblk++)
+        o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, o[dblk], 0, 0, 0, 0, 0, 0);
     }
 
-    if (has_next) lstore(buf ^ 1);
+    // tile t+1 must have landed; the DMAs of the tiles after it may stay in flight
+    if (issue) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (kPrefetch - 1)) : "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    buf = buf + 1 == kNBuf ? 0 : buf + 1;
   }
 
   // ---- epilogue ----
-  const float l_tot = l_run + __shfl_xor(l_run, 32, 64);
+  float l_tot;
+  {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+    l_tot = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+  }
   if (qrow >= p.Lq) return;
   if (SPLIT) {
     const int64_t row = (((int64_t)split * p.B + b) * p.Hq + h) * p.Lq + qrow;
@@ -282,7 +343,7 @@ __global__ __launch_bounds__(kThreads, 2) void qattn_fwd_kernel(AttnParams p) {
       const v4f sc = *reinterpret_cast<const v4f*>(vs + d);
       uint16_t hv[4];
 #pragma unroll
-      for (int t = 0; t < 4; t++) hv[t] = f32_to_half<IS_FP16_OUT>(o[dblk][g * 4 + t] * inv_l * sc[t]);
+      for (int e = 0; e < 4; e++) hv[e] = f32_to_half<IS_FP16_OUT>(o[dblk][g * 4 + e] * inv_l * sc[e]);
       v2u packed;
       __builtin_memcpy(&packed, hv, 8);
       *reinterpret_cast<v2u*>(orow + d) = packed;
@@ -333,10 +394,11 @@ extern "C" int qattn_fwd_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t H
   // 256 CUs x 2 resident workgroups; split only when the grid leaves the chip mostly idle and every
   // split still gets at least 8 key tiles
   const int64_t target = 1024;
-  if (wgs >= target / 2) return 1;
+  const int64_t min_s = (nkb + kMaxTilesPerSplit - 1) / kMaxTilesPerSplit;
+  if (wgs >= target / 2) return (int)min_s;
   int64_t s = (target + wgs - 1) / wgs;
   s = std::min<int64_t>(s, nkb / 8);
-  return (int)std::max<int64_t>(1, std::min<int64_t>(s, 32));
+  return (int)std::max<int64_t>(min_s, std::min<int64_t>(s, 32));
 }
 
 extern "C" size_t qattn_fwd_workspace_size(int64_t B, int64_t Lq, int64_t Hq, int64_t D, int num_splits) {
@@ -390,6 +452,8 @@ extern "C" int qattn_fwd(qattn_seq q8, const float* q_scale, qattn_seq k8, const
   int ns = num_splits > 0 ? num_splits : qattn_fwd_num_splits(B, Lq, Lk, Hq);
   ns = (int)std::min<int64_t>(ns, p.nKB);
   if (ns < 1) ns = 1;
+  // a workgroup stages the k_scales of at most kMaxTilesPerSplit key tiles
+  ns = (int)std::max<int64_t>(ns, (p.nKB + kMaxTilesPerSplit - 1) / kMaxTilesPerSplit);
   p.nsplit = ns;
   p.tiles_per_split = (int)((p.nKB + ns - 1) / ns);
   hipStream_t st = (hipStream_t)stream;

@@ -15,6 +15,7 @@ from tests.inputs import bf16_bits, cosine, qkv
 pytestmark = pytest.mark.gpu
 COS_KERNEL = 0.99995  # same quantized operands and schedule: only exp2 ulps / fp32 sums differ
 COS_E2E = 0.999
+KERNEL_LAZY_TAU = 1.0  # lazy running-max threshold of qattn_fwd_kernel (kLazyTau in attn.hip)
 
 
 def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None, num_splits=0, q_offset=0,
@@ -46,12 +47,20 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
     tps = (nkb + ns - 1) // ns if ns > 1 else 0  # the GPU's KV-split schedule, restated on the CPU
     ref, ref_lse = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
                                     ks.cpu().numpy(), untile_v(v8), vs.cpu().numpy(), causal=causal, q_offset=q_offset,
-                                    kv_valid=kv_valid, want_lse=True, tiles_per_split=tps)
+                                    kv_valid=kv_valid, want_lse=True, tiles_per_split=tps,
+                                    lazy_tau=KERNEL_LAZY_TAU)
     c = cosine(og, ref)
     err = float(np.abs(og - ref).max())
     lerr = float(np.nanmax(np.abs(lse.cpu().numpy() - ref_lse)))
     log(f"  vs quantized oracle (splits={ns}): cosine={c:.6f} max_abs={err:.4g} lse_max_abs={lerr:.3g}")
     assert c >= COS_KERNEL
+    # the reference's own schedule (no split, eager running max) on the same quantized operands
+    ref0 = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
+                            ks.cpu().numpy(), untile_v(v8), vs.cpu().numpy(), causal=causal, q_offset=q_offset,
+                            kv_valid=kv_valid)
+    c0 = cosine(og, ref0)
+    log(f"  vs reference-schedule quantized math: cosine={c0:.6f} max_abs={float(np.abs(og - ref0).max()):.4g}")
+    assert c0 >= COS_E2E
     assert lerr < 2e-2
     if check_truth:
         truth = oracle.attn_fp64(bf16_bits(q), bf16_bits(k), bf16_bits(v), D ** -0.5, causal=causal,

@@ -382,3 +382,19 @@ def test_split_schedule_restatement(oracle):
     assert 0.999 < cosine(split, base) < 1.0
     truth = oracle.attn_fp64(qb, kb, vb, 128 ** -0.5)
     assert cosine(split, truth) >= 0.999
+
+
+def test_lazy_running_max_schedule(oracle):
+    """The lazy running-max rule (device kernel schedule) only changes which fp8 rounding P gets:
+    tau = 0 with the offset unchanged is the reference rule exactly; tau = 1 stays within the gate."""
+    q, k, v = qkv(1, 256, 2048, 2, 2, seed=37, k_offset_std=0.5)
+    qb, kb, vb = bf16_bits(q), bf16_bits(k), bf16_bits(v)
+    q8, qs = oracle.quant_per_block_int8(qb, sm_scale=128 ** -0.5 * LOG2E, blk=128)
+    k8, ks = oracle.quant_per_block_int8(kb, km_bits=oracle.k_mean_bits(kb), blk=64)
+    v8, vs = oracle.per_channel_fp8(vb)
+    ref = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs)
+    assert np.array_equal(ref, oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, lazy_tau=0.0))
+    lazy = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, lazy_tau=1.0)
+    assert 0.9995 < cosine(lazy, ref) < 1.0
+    truth = oracle.attn_fp64(qb, kb, vb, 128 ** -0.5)
+    assert cosine(lazy, truth) >= 0.999
