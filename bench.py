@@ -67,6 +67,8 @@ def main() -> int:
     ap.add_argument("--config", default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sdpa", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the path shards "
@@ -79,6 +81,15 @@ def main() -> int:
     from telefuser_amd import sageattn2 as sa
     from telefuser_amd.workloads import CONFIGS, make_inputs, peak_ops
 
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda:0")  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read_per_launch": src.numel() * 4,
+                          "bytes_written_per_launch": dst.numel() * 4}))
+        return 0
     _lib.load()
     cfg = CONFIGS[args.config]
     dev = torch.device("cuda:0")
@@ -150,7 +161,7 @@ def main() -> int:
         sdpa_ms = a.elapsed_time(b) / 5
 
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", f"attn_{args.config}_traffic.json")
+    tpath = os.path.join(ROOT, "profiles", f"attn_{args.config}_traffic.txt")
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")

@@ -1,0 +1,74 @@
+"""The C-ABI library loads without a GPU, exports every symbol include/qattn.h declares, and its
+host-side validation reports errors as status codes (no GPU call is reached on these paths)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from tests.conftest import ROOT
+
+
+def _declared():
+    src = open(os.path.join(ROOT, "include", "qattn.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(qattn_[a-z0-9_]+)\s*\(", src)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from telefuser_amd import _lib
+
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libqattn.so not built")
+    return _lib.load()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = _declared()
+    assert "qattn_fwd" in names and "qattn_quant_qk_per_block_int8" in names
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_workspace_queries(lib):
+    assert lib.qattn_fwd_workspace_size(1, 4680, 12, 128, 1) == 0
+    assert lib.qattn_fwd_workspace_size(1, 4680, 12, 128, 4) == 4 * 12 * 4680 * 130 * 4
+    assert lib.qattn_seq_mean_workspace_size(1, 32760, 12, 128) == 12 * 128 * 128 * 4
+    # the C5 shape (444 query blocks) is split, the C2 shape (3072) is not
+    assert lib.qattn_fwd_num_splits(1, 4680, 32760, 12) > 1
+    assert lib.qattn_fwd_num_splits(1, 32760, 32760, 12) == 1
+
+
+def _seq(ptr, sb, sl, sh):
+    from telefuser_amd._lib import QattnSeq
+
+    return QattnSeq(ptr, sb, sl, sh)
+
+
+def test_validation_errors_are_status_codes(lib):
+    s = _seq(16, 128 * 128, 128, 128)
+    buf = ctypes.c_void_p(16)
+    # head ratio
+    rc = lib.qattn_fwd(s, buf, s, buf, buf, 128, buf, s, 0, 1, 128, 128, 3, 2, 128, 1.0, 0, 0, None, None, 1, None,
+                       0, None)
+    assert rc == 6 and b"divisible" in lib.qattn_last_error()
+    # head dim
+    rc = lib.qattn_fwd(s, buf, s, buf, buf, 128, buf, s, 0, 1, 128, 128, 2, 2, 96, 1.0, 0, 0, None, None, 1, None,
+                       0, None)
+    assert rc == 5
+    # bad dtype in the quantizer
+    rc = lib.qattn_quant_per_block_int8(s, 7, 1, 128, 1, 128, None, s, buf, 1.0, 0, 64, 0, None)
+    assert rc == 1
+    # block size
+    rc = lib.qattn_quant_per_block_int8(s, 0, 1, 128, 1, 128, None, s, buf, 1.0, 0, 48, 0, None)
+    assert rc == 9
+    # misaligned rows
+    bad = _seq(16, 128 * 100, 100, 100)
+    rc = lib.qattn_quant_per_block_int8(bad, 0, 1, 128, 1, 128, None, s, buf, 1.0, 0, 64, 0, None)
+    assert rc == 3
+    # missing workspace for a split launch
+    rc = lib.qattn_fwd(s, buf, s, buf, buf, 128, buf, s, 0, 1, 128, 128, 2, 2, 128, 1.0, 0, 0, None, None, 2, None,
+                       0, None)
+    assert rc == 7
