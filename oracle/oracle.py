@@ -42,7 +42,7 @@ def lib():
         L.oq_per_channel_fp8.argtypes = [vp, i32, i64, i64, i64, i64, i64, i64, i64, f32, vp, i64, vp]
         L.oq_qattn_fwd.argtypes = [vp, i64, i64, i64, vp, i64, vp, i64, i64, i64, vp, i64, vp, i64, vp, vp, i32,
                                    i64, i64, i64, i64, i64, i64, i64, i64, i64, f64, i32, i32, i64, vp, i64, i64,
-                                   i64, i64, f64, vp, vp]
+                                   i64, i64, f64, i32, vp, vp]
         L.oq_attn_fp64.argtypes = [vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, f64, i32, i64, vp, vp]
         L.oq_f32_to_e4m3.argtypes = [f32]
         L.oq_f32_to_e4m3.restype = ctypes.c_uint8
@@ -120,10 +120,11 @@ def per_channel_fp8(v_bits, scale_max=448.0, layout="NHD", is_fp16=False, pad=64
 
 def qattn_fwd(q8, q_scale, k8, k_scale, v8=None, v_scale=None, vh_bits=None, *, blkq=128, blkk=64,
               qk_mult=1.0, pv_mode=0, causal=False, q_offset=0, kv_valid=None, is_fp16=False, heads=None,
-              qrows_limit=0, want_lse=False, tiles_per_split=0, lazy_tau=-1.0):
+              qrows_limit=0, want_lse=False, tiles_per_split=0, lazy_tau=-1.0, lsum_rounded=False):
     """Quantized attention in the reference's tile order.  q8/k8 NHD int8; returns fp32 O NHD
     (and log2-domain LSE [B, Hq, Lq] when want_lse).  lazy_tau >= 0 / tiles_per_split > 0 restate the
-    device kernel's lazy running-max rule / KV-split schedule (defaults: the reference's schedule)."""
+    device kernel's lazy running-max rule / KV-split schedule and lsum_rounded its row sum over the
+    rounded P (defaults: the reference's schedule)."""
     q8 = np.ascontiguousarray(q8)
     k8 = np.ascontiguousarray(k8)
     B, Lq, Hq, D = q8.shape
@@ -146,7 +147,7 @@ def qattn_fwd(q8, q_scale, k8, k_scale, v8=None, v_scale=None, vh_bits=None, *, 
                        _p(k_scale), blkk, _p(v8) if pv_mode == 0 else None, Lpad,
                        _p(v_scale) if pv_mode == 0 else None, _p(vh_bits), int(is_fp16), Lk * Hkv * D, Hkv * D, D,
                        B, Lq, Lk, Hq, Hkv, D, float(qk_mult), int(pv_mode), int(causal), int(q_offset), _p(kvv), h0,
-                       h1, int(qrows_limit), int(tiles_per_split), float(lazy_tau), _p(out),
+                       h1, int(qrows_limit), int(tiles_per_split), float(lazy_tau), int(lsum_rounded), _p(out),
                        _p(lse))
     return (out, lse) if want_lse else out
 

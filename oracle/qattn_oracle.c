@@ -301,6 +301,8 @@ void oq_per_channel_fp8(const uint16_t* in, int is_fp16, int64_t B, int64_t L, i
  * lazy_tau >= 0 restates the lazy running-max rule of the device kernel: m moves to rowmax(s) -
  * (offset - tau) only when that exceeds the current m by more than tau (p stays <= 2^offset);
  * lazy_tau < 0 is the reference rule m = max(m, rowmax(s) - offset) of update_mdo.
+ * lsum_rounded != 0 sums the rounded P (what the device kernel's MFMA row sum computes) instead of
+ * the unrounded p the reference's accumulate_d sums.
  * tiles_per_split > 0 restates the KV-split schedule: every run of tiles_per_split key tiles keeps its
  * own (m, d, O) and the partials are merged at the end with weights exp2(m_s - max m).
  *
@@ -313,7 +315,7 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
                   int64_t vsb, int64_t vsl, int64_t vsh, int64_t B, int64_t Lq, int64_t Lk, int64_t Hq,
                   int64_t Hkv, int64_t D, double qk_mult, int pv_mode, int causal, int64_t q_offset,
                   const int32_t* kv_valid, int64_t h_begin, int64_t h_end, int64_t qrows_limit, int64_t tiles_per_split,
-                  double lazy_tau, float* out, float* lse2) {
+                  double lazy_tau, int lsum_rounded, float* out, float* lse2) {
   const int64_t RB = 128; /* query rows per work item */
   int64_t nQB = (Lq + blkq - 1) / blkq;
   int64_t nKB = (Lk + blkk - 1) / blkk;
@@ -386,9 +388,9 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
               has[r] = 1;
               for (int64_t j = k0; j < k1; j++) {
                 double p = exp2(s[j - k0] - m_new);
-                dsum[r] += p;
                 double pr = pv_mode == 0 ? oq_e4m3_to_f32(oq_f32_to_e4m3((float)p))
                                          : oq_bf16_to_f32(oq_f32_to_bf16((float)p));
+                dsum[r] += lsum_rounded ? pr : p;
                 const double* vr = vt + (j - k0) * D;
                 for (int64_t d = 0; d < D; d++) orow[d] += pr * vr[d];
               }

@@ -398,3 +398,21 @@ def test_lazy_running_max_schedule(oracle):
     assert 0.9995 < cosine(lazy, ref) < 1.0
     truth = oracle.attn_fp64(qb, kb, vb, 128 ** -0.5)
     assert cosine(lazy, truth) >= 0.999
+
+
+def test_rounded_row_sum_mode(oracle):
+    """Summing the e4m3-rounded P (as the device's MFMA row sum does) instead of the unrounded p only
+    perturbs the normaliser by the fp8 rounding noise; a uniform V is then reproduced exactly up to
+    the V quantization, since numerator and denominator use the same P."""
+    q, k, v = qkv(1, 128, 512, 1, 1, seed=41)
+    qb, kb = bf16_bits(q), bf16_bits(k)
+    q8, qs = oracle.quant_per_block_int8(qb, sm_scale=128 ** -0.5 * LOG2E, blk=128)
+    k8, ks = oracle.quant_per_block_int8(kb, blk=64)
+    row = torch.linspace(-2, 2, 128).to(torch.bfloat16)
+    vu = bf16_bits(row.expand(1, 512, 1, 128).contiguous())
+    v8, vs = oracle.per_channel_fp8(vu)
+    exact_v = oracle.e4m3_to_f32(v8[0, 0, :, 0]) * vs[0, 0]
+    o = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, lsum_rounded=True)
+    assert np.abs(o[0, :, 0] - exact_v[None]).max() < 1e-5
+    o_ref = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs)
+    assert np.abs(o_ref[0, :, 0] - exact_v[None]).max() > 1e-4  # the reference's normaliser differs
