@@ -128,6 +128,26 @@ int qattn_fwd(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_s
               const int32_t* kv_valid, float* lse, int num_splits, void* workspace, size_t workspace_bytes,
               qattn_stream_t stream);
 
+/*
+ * V (bf16/fp16) copied into the same transposed, tile-permuted layout as qattn_per_channel_fp8 uses,
+ * in its own dtype: v16 [B, H, D, Lpad].  Replaces the V preparation of the reference's fp16-P.V
+ * paths (sageattn_qk_int8_pv_fp16_cuda / _triton, tf-kernel/tf_kernel/sageattn2.py:551-769,930-1194).
+ */
+int qattn_v_tile_half(qattn_seq v, int dtype, int64_t B, int64_t L, int64_t H, int64_t D, uint16_t* v16,
+                      int64_t Lpad, qattn_stream_t stream);
+
+/*
+ * Quantized attention with INT8 Q.K^T and P.V in the half dtype of V (P rounded to that dtype,
+ * fp32 accumulation, no FP8 offset or v_scale): the math of the reference's INT8-QK / FP16-PV kernels
+ * (qk_int8_sv_f16_accum_f32_attn, common_extension.cc:214-218; Triton attn_qk_int8_per_block.py:46-101).
+ * Arguments as qattn_fwd, with v16 from qattn_v_tile_half and v_dtype its dtype.
+ */
+int qattn_fwd_pv16(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const uint16_t* v16,
+                   int v_dtype, int64_t Lpad, qattn_seq o, int out_dtype, int64_t B, int64_t Lq, int64_t Lk,
+                   int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int causal, int64_t q_offset,
+                   const int32_t* kv_valid, float* lse, int num_splits, void* workspace, size_t workspace_bytes,
+                   qattn_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

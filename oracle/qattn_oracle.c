@@ -286,7 +286,8 @@ void oq_per_channel_fp8(const uint16_t* in, int is_fp16, int64_t B, int64_t L, i
  *   for each 64-key tile (blkk):  s = float(Q8.K8^T) * (q_scale * k_scale) * qk_mult
  *     m_new = max(m, rowmax(s) - offset);  p = exp2(s - m_new);  d = d*exp2(m - m_new) + sum(p)
  *     pv_mode 0: O = O*exp2(m-m_new) + e4m3(p) . e4m3(V)   (offset = 8.807, V per-channel fp8)
- *     pv_mode 1: O = O*exp2(m-m_new) + bf16(p) . Vh         (offset = 0, V = bf16/fp16 input values)
+ *     pv_mode 1: O = O*exp2(m-m_new) + half(p) . Vh         (offset = 0, V = bf16/fp16 input values,
+ *                P rounded to the same half type as V)
  *   end: O /= d; pv_mode 0: O *= v_scale[d]
  * Everything not rounded by the reference is carried in double.
  *
@@ -389,7 +390,8 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
               for (int64_t j = k0; j < k1; j++) {
                 double p = exp2(s[j - k0] - m_new);
                 double pr = pv_mode == 0 ? oq_e4m3_to_f32(oq_f32_to_e4m3((float)p))
-                                         : oq_bf16_to_f32(oq_f32_to_bf16((float)p));
+                            : is_fp16   ? oq_f16_to_f32(oq_f32_to_f16((float)p))
+                                        : oq_bf16_to_f32(oq_f32_to_bf16((float)p));
                 dsum[r] += lsum_rounded ? pr : p;
                 const double* vr = vt + (j - k0) * D;
                 for (int64_t d = 0; d < D; d++) orow[d] += pr * vr[d];

@@ -32,6 +32,8 @@ EXPORTED = (
     "qattn_fwd_workspace_size",
     "qattn_fwd_num_splits",
     "qattn_fwd",
+    "qattn_v_tile_half",
+    "qattn_fwd_pv16",
 )
 
 
@@ -78,8 +80,11 @@ def load() -> ctypes.CDLL:
     L.qattn_fwd_num_splits.restype = i32
     L.qattn_fwd.argtypes = [S, vp, S, vp, vp, i64, vp, S, i32, i64, i64, i64, i64, i64, i64, f32, i32, i64, vp, vp,
                             i32, vp, sz, vp]
+    L.qattn_v_tile_half.argtypes = [S, i32, i64, i64, i64, i64, vp, i64, vp]
+    L.qattn_fwd_pv16.argtypes = [S, vp, S, vp, vp, i32, i64, S, i32, i64, i64, i64, i64, i64, i64, f32, i32, i64, vp,
+                                 vp, i32, vp, sz, vp]
     for name in ("qattn_quant_per_block_int8", "qattn_quant_qk_per_block_int8", "qattn_seq_mean",
-                 "qattn_per_channel_fp8", "qattn_fwd"):
+                 "qattn_per_channel_fp8", "qattn_fwd", "qattn_v_tile_half", "qattn_fwd_pv16"):
         getattr(L, name).restype = i32
     _lib = L
     return L

@@ -50,11 +50,11 @@ struct AttnParams {
   int64_t qsb, qsl, qsh;
   const int8_t* k8;
   int64_t ksb, ksl, ksh;
-  const uint8_t* v8;  // [B, Hkv, D, Lpad]
+  const void* v;  // tile-layout V: e4m3 (PV_FP8) or the half dtype, [B, Hkv, D, Lpad]
   int64_t Lpad;
   const float* q_scale;  // [B, Hq, nQB]
   const float* k_scale;  // [B, Hkv, nKB]
-  const float* v_scale;  // [B, Hkv, D]
+  const float* v_scale;  // [B, Hkv, D] (FP8 P.V only)
   void* o;
   int64_t osb, osl, osh;
   float* lse;  // [B, Hq, Lq] or null
@@ -98,10 +98,17 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
       : "memory", "m0");
 }
 
-template <bool IS_FP16_OUT, bool SPLIT>
+// P.V flavours: e4m3 P x e4m3 V (the reference's fp8 kernel, with the 8.807 offset and v_scale), or
+// P rounded to the half dtype of V x V as given (the Triton / SAGE_ATTN_2_8_16 style), fp32 accumulation.
+enum PvKind { PV_FP8 = 0, PV_BF16 = 1, PV_FP16 = 2 };
+
+template <bool IS_FP16_OUT, bool SPLIT, int PV>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(AttnParams p) {
+  constexpr int kVBytes = PV == PV_FP8 ? 1 : 2;    // bytes per V element
+  constexpr int kVDma = 2 * kVBytes;                // V DMA instructions per wave per tile
+  constexpr float kOffset = PV == PV_FP8 ? kFp8Offset : 0.f;
   __shared__ __align__(16) uint8_t lds_k[kNBuf][kBK * kD];
-  __shared__ __align__(16) uint8_t lds_v[kNBuf][kD * kBK];
+  __shared__ __align__(16) uint8_t lds_v[kNBuf][kD * kBK * kVBytes];
   __shared__ float lds_ks[kMaxTilesPerSplit];  // k_scale of this workgroup's key tiles
 
   const int64_t tile_id = xcd_remap(blockIdx.x, gridDim.x);
@@ -150,25 +157,35 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   // side: the lane that owns LDS slot (row, chunk c') fetches global chunk c = c' ^ swizzle(row).
   // Each wave moves 2 x 1 KiB of K and 2 x 1 KiB of V per tile; no VGPRs are spent on staging.
   const int8_t* kbase = p.k8 + b * p.ksb + hk * p.ksh;
-  const uint8_t* vbase = p.v8 + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad;
+  const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad * kVBytes;
   // per-lane DMA source offsets relative to the tile start (first K row / first V column)
   int64_t koff[2];
-  int voff[2];
+  int voff[kVDma];
   int kr[2];
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     const int slot = (i * 4 + w) * 64 + lane;
     kr[i] = slot >> 3;
     const int kc = (slot & 7) ^ ((kr[i] >> 1) & 7);
-    const int vd = slot >> 2;
-    const int vc = (slot & 3) ^ ((vd >> 2) & 3);
     koff[i] = kr[i] * p.ksl + kc * 16;
-    voff[i] = (int)(vd * p.Lpad + vc * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < kVDma; i++) {
+    const int slot = (i * 4 + w) * 64 + lane;
+    if constexpr (PV == PV_FP8) {  // 128 rows x 4 chunks, v_lds_off swizzle
+      const int vd = slot >> 2;
+      const int vc = (slot & 3) ^ ((vd >> 2) & 3);
+      voff[i] = (int)(vd * p.Lpad + vc * 16);
+    } else {  // 128 rows x 8 chunks of 16 bytes (8 halves), k_lds_off swizzle
+      const int vd = slot >> 3;
+      const int vc = (slot & 7) ^ ((vd >> 1) & 7);
+      voff[i] = (int)(vd * p.Lpad * 2 + vc * 16);
+    }
   }
   const int64_t k_step = (int64_t)kBK * p.ksl;
   auto dma_tile = [&](int64_t t, int buf) {
     const int8_t* kt = kbase + t * k_step;
-    const uint8_t* vt = vbase + t * kBK;
+    const uint8_t* vt = vbase + t * kBK * kVBytes;
     const bool clamp = t * kBK + kBK > p.Lk;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
@@ -176,8 +193,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
       const int8_t* src = kt + koff[i];
       if (clamp) src = kbase + min(t * kBK + kr[i], p.Lk - 1) * p.ksl + (koff[i] - kr[i] * p.ksl);
       lds_dma16(src, &lds_k[buf][(i * 4 + w) * 1024]);
-      lds_dma16(vt + voff[i], &lds_v[buf][(i * 4 + w) * 1024]);
     }
+#pragma unroll
+    for (int i = 0; i < kVDma; i++) lds_dma16(vt + voff[i], &lds_v[buf][(i * 4 + w) * 1024]);
   };
 
   v16f o[4];
@@ -248,7 +266,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
     // <= 2^8.807 = 448 (the e4m3 maximum), so the FP8 range is honoured while the O rescale (64
     // multiplies per lane) is skipped on almost every tile.  A row whose keys in this tile are all
     // masked never moves m.
-    const float m_tile = mx == INT32_MIN ? kMInit : fmaf((float)mx, cs, -(kFp8Offset - kLazyTau));
+    const float m_tile = mx == INT32_MIN ? kMInit : fmaf((float)mx, cs, -(kOffset - kLazyTau));
     const bool grow = m_tile > m_run + kLazyTau;
     if (__any(grow)) {
       const float m_new = grow ? m_tile : m_run;
@@ -261,48 +279,86 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
       m_run = m_new;
     }
     const float neg_m = -m_run;
-    v8i pf;
-    // p = exp2(s * cs - m), packed to e4m3; masked logits (INT32_MIN) become p = 0 exactly (the
-    // sentinel times a tiny block scale is not necessarily very negative)
-    auto body = [&](auto mk) {
-      float lsum = 0.f;
+    // p = exp2(s * cs - m); masked logits (INT32_MIN) become p = 0 exactly (the sentinel times a tiny
+    // block scale is not necessarily very negative)
+    auto p4 = [&](int j, float (&pv)[4], auto mk) {
+      const int kb = j >> 2, r0 = (j & 3) * 4;
 #pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const int kb = j >> 2, r0 = (j & 3) * 4;
-        float pv[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int sv = s[kb][r0 + e];
-          pv[e] = __builtin_amdgcn_exp2f(fmaf((float)sv, cs, neg_m));
-          if constexpr (decltype(mk)::value) pv[e] = sv == INT32_MIN ? 0.f : pv[e];
-        }
-        lsum += (pv[0] + pv[1]) + (pv[2] + pv[3]);
-        const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], 0, false);
-        pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
+      for (int e = 0; e < 4; e++) {
+        const int sv = s[kb][r0 + e];
+        pv[e] = __builtin_amdgcn_exp2f(fmaf((float)sv, cs, neg_m));
+        if constexpr (decltype(mk)::value) pv[e] = sv == INT32_MIN ? 0.f : pv[e];
       }
-      l_run += lsum;
     };
-    if (masked) body(std::true_type{});
-    else body(std::false_type{});
+    if constexpr (PV == PV_FP8) {
+      v8i pf;  // P^T as the e4m3 B operand: byte s of the lane = slot s = 16 kb + r
+      auto body = [&](auto mk) {
+        float lsum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          float pv[4];
+          p4(j, pv, mk);
+          lsum += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+          const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], 0, false);
+          pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
+        }
+        l_run += lsum;
+      };
+      if (masked) body(std::true_type{});
+      else body(std::false_type{});
 
-    // ---- O^T += V^T . P^T; V^T fragments streamed from LDS ----
-    {
-      auto load_v1 = [&](int dblk) -> v8i {
+      // ---- O^T += V^T . P^T (FP8 MFMA, K = 64 keys) ----
+      v8i vf[4];
+#pragma unroll
+      for (int dblk = 0; dblk < 4; dblk++) {
         const int d = dblk * 32 + lq;
         const v4i a0 = *reinterpret_cast<const v4i*>(&lds_v[buf][v_lds_off(d, 2 * hf)]);
         const v4i a1 = *reinterpret_cast<const v4i*>(&lds_v[buf][v_lds_off(d, 2 * hf + 1)]);
-        return v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-      };
-      v8i vf[4];
-#pragma unroll
-      for (int dblk = 0; dblk < 4; dblk++) vf[dblk] = load_v1(dblk);
+        vf[dblk] = v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+      }
 #pragma unroll
       for (int dblk = 0; dblk < 4; dblk++)
         o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, o[dblk], 0, 0, 0, 0, 0, 0);
+    } else {
+      // P^T in the half dtype: chunk c (16 keys of the MFMA's K dimension) = slots 8c .. 8c+7
+      typedef __attribute__((ext_vector_type(8))) __bf16 v8bf;
+      typedef __attribute__((ext_vector_type(8))) _Float16 v8h;
+      using HV = std::conditional_t<PV == PV_BF16, v8bf, v8h>;
+      using HS = std::conditional_t<PV == PV_BF16, __bf16, _Float16>;
+      HV ph[4];
+      auto body = [&](auto mk) {
+        float lsum = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          float pv[4];
+          p4(j, pv, mk);
+          lsum += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+#pragma unroll
+          for (int e = 0; e < 4; e++) ph[j >> 1][(j & 1) * 4 + e] = (HS)pv[e];  // RNE
+        }
+        l_run += lsum;
+      };
+      if (masked) body(std::true_type{});
+      else body(std::false_type{});
+
+      // ---- O^T += V^T . P^T (half MFMA 32x32x16, 4 K-chunks per 32-channel block) ----
+#pragma unroll
+      for (int dblk = 0; dblk < 4; dblk++) {
+        const int d = dblk * 32 + lq;
+        HV vf[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+          vf[c] = *reinterpret_cast<const HV*>(&lds_v[buf][k_lds_off(d, hf * 4 + c)]);
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          if constexpr (PV == PV_BF16) o[dblk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[c], ph[c], o[dblk], 0, 0, 0);
+          else o[dblk] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[c], ph[c], o[dblk], 0, 0, 0);
+        }
+      }
     }
 
     // tile t+1 must have landed; the DMAs of the tiles after it may stay in flight
-    if (issue) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(4 * (kPrefetch - 1)) : "memory");
+    if (issue) asm volatile("s_waitcnt vmcnt(%0)" ::"n"((2 + kVDma) * (kPrefetch - 1)) : "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     buf = buf + 1 == kNBuf ? 0 : buf + 1;
@@ -333,14 +389,14 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
     return;
   }
   const float inv_l = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  const float* vs = p.v_scale + (b * p.Hkv + hk) * kD;
+  const float* vs = PV == PV_FP8 ? p.v_scale + (b * p.Hkv + hk) * kD : nullptr;
   uint16_t* orow = static_cast<uint16_t*>(p.o) + b * p.osb + qrow * p.osl + h * p.osh;
 #pragma unroll
   for (int dblk = 0; dblk < 4; dblk++)
 #pragma unroll
     for (int g = 0; g < 4; g++) {
       const int d = dblk * 32 + g * 8 + hf * 4;
-      const v4f sc = *reinterpret_cast<const v4f*>(vs + d);
+      const v4f sc = PV == PV_FP8 ? *reinterpret_cast<const v4f*>(vs + d) : v4f{1.f, 1.f, 1.f, 1.f};
       uint16_t hv[4];
 #pragma unroll
       for (int e = 0; e < 4; e++) hv[e] = f32_to_half<IS_FP16_OUT>(o[dblk][g * 4 + e] * inv_l * sc[e]);
@@ -376,10 +432,10 @@ __global__ __launch_bounds__(256) void qattn_combine_kernel(AttnParams p) {
     a1 += wo[1] * f;
   }
   const float inv = L > 0.f ? 1.0f / L : 0.f;
-  const float* vs = p.v_scale + (b * p.Hkv + hk) * kD + lane * 2;
+  const float* vs = p.v_scale ? p.v_scale + (b * p.Hkv + hk) * kD + lane * 2 : nullptr;
   uint16_t* orow = static_cast<uint16_t*>(p.o) + b * p.osb + qrow * p.osl + h * p.osh + lane * 2;
-  orow[0] = f32_to_half<IS_FP16_OUT>(a0 * inv * vs[0]);
-  orow[1] = f32_to_half<IS_FP16_OUT>(a1 * inv * vs[1]);
+  orow[0] = f32_to_half<IS_FP16_OUT>(a0 * inv * (vs ? vs[0] : 1.f));
+  orow[1] = f32_to_half<IS_FP16_OUT>(a1 * inv * (vs ? vs[1] : 1.f));
   if (p.lse && lane == 0) p.lse[(b * p.Hq + h) * p.Lq + qrow] = L > 0.f ? __builtin_log2f(L) + M : -INFINITY;
 }
 
@@ -406,39 +462,63 @@ extern "C" size_t qattn_fwd_workspace_size(int64_t B, int64_t Lq, int64_t Hq, in
   return (size_t)num_splits * B * Hq * Lq * (D + 2) * sizeof(float);
 }
 
-extern "C" int qattn_fwd(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const uint8_t* v8,
-                         int64_t Lpad, const float* v_scale, qattn_seq o, int out_dtype, int64_t B, int64_t Lq,
-                         int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int causal,
-                         int64_t q_offset, const int32_t* kv_valid, float* lse, int num_splits, void* workspace,
-                         size_t workspace_bytes, qattn_stream_t stream) {
+template <int PV>
+static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, size_t workspace_bytes, hipStream_t st,
+                      int64_t D) {
+  const int64_t grid = p.B * p.Hq * p.nQB * ns;
+  QATTN_REQUIRE(grid < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
+  p.nsplit = ns;
+  p.tiles_per_split = (int)((p.nKB + ns - 1) / ns);
+  if (ns > 1) {
+    QATTN_REQUIRE(workspace && workspace_bytes >= qattn_fwd_workspace_size(p.B, p.Lq, p.Hq, D, ns), QATTN_ERR_WORKSPACE,
+                  "qattn_fwd with %d KV splits needs %zu workspace bytes", ns,
+                  qattn_fwd_workspace_size(p.B, p.Lq, p.Hq, D, ns));
+    p.ws_o = static_cast<float*>(workspace);
+    p.ws_ml = p.ws_o + (int64_t)ns * p.B * p.Hq * p.Lq * D;
+    if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, true, PV><<<grid, kThreads, 0, st>>>(p);
+    else qattn_fwd_kernel<true, true, PV><<<grid, kThreads, 0, st>>>(p);
+    const int64_t rows = p.B * p.Hq * p.Lq;
+    if (out_dtype == QATTN_BF16) qattn_combine_kernel<false><<<(rows + 3) / 4, 256, 0, st>>>(p);
+    else qattn_combine_kernel<true><<<(rows + 3) / 4, 256, 0, st>>>(p);
+  } else {
+    if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, false, PV><<<grid, kThreads, 0, st>>>(p);
+    else qattn_fwd_kernel<true, false, PV><<<grid, kThreads, 0, st>>>(p);
+  }
+  return check_launch("qattn_fwd");
+}
+
+static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale,
+                     const void* v, int64_t Lpad, qattn_seq o, int out_dtype, int64_t B, int64_t Lq, int64_t Lk,
+                     int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int causal, int64_t q_offset,
+                     const int32_t* kv_valid, float* lse, int num_splits) {
   QATTN_REQUIRE(out_dtype == QATTN_BF16 || out_dtype == QATTN_FP16, QATTN_ERR_DTYPE, "out dtype must be bf16 or fp16");
   QATTN_REQUIRE(D == kD, QATTN_ERR_HEAD_DIM, "qattn_fwd needs head_dim 128 (pad smaller heads), got %lld",
                 (long long)D);
   QATTN_REQUIRE(B >= 0 && Lq >= 0 && Lk >= 0 && Hq > 0 && Hkv > 0, QATTN_ERR_SHAPE, "bad sizes");
   QATTN_REQUIRE(Hq % Hkv == 0, QATTN_ERR_HEAD_RATIO, "num_qo_heads (%lld) must be divisible by num_kv_heads (%lld)",
                 (long long)Hq, (long long)Hkv);
-  if (B * Lq == 0) return QATTN_OK;
+  if (B * Lq == 0) return -1;  // nothing to do
   QATTN_REQUIRE(Lk > 0, QATTN_ERR_SHAPE, "kv_len must be positive");
   QATTN_REQUIRE(Lpad % kBK == 0 && Lpad >= (Lk + kBK - 1) / kBK * kBK, QATTN_ERR_SHAPE,
                 "Lpad must be a multiple of 64 covering kv_len");
-  for (const qattn_seq* s : {&q8, &k8}) {
-    QATTN_REQUIRE(s->data && aligned16(s->data), QATTN_ERR_ALIGN, "q8/k8 must be 16-byte aligned");
-    QATTN_REQUIRE(s->sb % 16 == 0 && s->sl % 16 == 0 && s->sh % 16 == 0, QATTN_ERR_STRIDE,
+  for (const qattn_seq* sq : {&q8, &k8}) {
+    QATTN_REQUIRE(sq->data && aligned16(sq->data), QATTN_ERR_ALIGN, "q8/k8 must be 16-byte aligned");
+    QATTN_REQUIRE(sq->sb % 16 == 0 && sq->sl % 16 == 0 && sq->sh % 16 == 0, QATTN_ERR_STRIDE,
                   "q8/k8 strides must be multiples of 16 bytes");
   }
   QATTN_REQUIRE(o.data && aligned16(o.data), QATTN_ERR_ALIGN, "output must be 16-byte aligned");
   QATTN_REQUIRE(o.sb % 8 == 0 && o.sl % 8 == 0 && o.sh % 8 == 0, QATTN_ERR_STRIDE,
                 "output strides must be multiples of 16 bytes");
-  QATTN_REQUIRE(v8 && aligned16(v8) && q_scale && k_scale && v_scale, QATTN_ERR_ARG, "null scale or v8 pointer");
+  QATTN_REQUIRE(v && aligned16(v) && q_scale && k_scale, QATTN_ERR_ARG, "null scale or V pointer");
   QATTN_REQUIRE(!causal || q_offset >= 0, QATTN_ERR_ARG, "q_offset must be >= 0");
 
-  AttnParams p{};
+  p = AttnParams{};
   p.q8 = static_cast<const int8_t*>(q8.data);
   p.qsb = q8.sb; p.qsl = q8.sl; p.qsh = q8.sh;
   p.k8 = static_cast<const int8_t*>(k8.data);
   p.ksb = k8.sb; p.ksl = k8.sl; p.ksh = k8.sh;
-  p.v8 = v8; p.Lpad = Lpad;
-  p.q_scale = q_scale; p.k_scale = k_scale; p.v_scale = v_scale;
+  p.v = v; p.Lpad = Lpad;
+  p.q_scale = q_scale; p.k_scale = k_scale;
   p.o = o.data; p.osb = o.sb; p.osl = o.sl; p.osh = o.sh;
   p.lse = lse; p.kv_valid = kv_valid;
   p.B = B; p.Lq = Lq; p.Lk = Lk; p.Hq = Hq; p.Hkv = Hkv;
@@ -449,32 +529,43 @@ extern "C" int qattn_fwd(qattn_seq q8, const float* q_scale, qattn_seq k8, const
   p.causal = causal ? 1 : 0;
   p.qk_mult = qk_mult;
 
-  int ns = num_splits > 0 ? num_splits : qattn_fwd_num_splits(B, Lq, Lk, Hq);
+  ns = num_splits > 0 ? num_splits : qattn_fwd_num_splits(B, Lq, Lk, Hq);
   ns = (int)std::min<int64_t>(ns, p.nKB);
   if (ns < 1) ns = 1;
   // a workgroup stages the k_scales of at most kMaxTilesPerSplit key tiles
   ns = (int)std::max<int64_t>(ns, (p.nKB + kMaxTilesPerSplit - 1) / kMaxTilesPerSplit);
-  p.nsplit = ns;
-  p.tiles_per_split = (int)((p.nKB + ns - 1) / ns);
-  hipStream_t st = (hipStream_t)stream;
-  const int64_t grid = B * Hq * p.nQB * ns;
-  QATTN_REQUIRE(grid < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
-  if (ns > 1) {
-    QATTN_REQUIRE(workspace && workspace_bytes >= qattn_fwd_workspace_size(B, Lq, Hq, D, ns), QATTN_ERR_WORKSPACE,
-                  "qattn_fwd with %d KV splits needs %zu workspace bytes", ns,
-                  qattn_fwd_workspace_size(B, Lq, Hq, D, ns));
-    p.ws_o = static_cast<float*>(workspace);
-    p.ws_ml = p.ws_o + (int64_t)ns * B * Hq * Lq * D;
-    if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, true><<<grid, kThreads, 0, st>>>(p);
-    else qattn_fwd_kernel<true, true><<<grid, kThreads, 0, st>>>(p);
-    const int64_t rows = B * Hq * Lq;
-    if (out_dtype == QATTN_BF16) qattn_combine_kernel<false><<<(rows + 3) / 4, 256, 0, st>>>(p);
-    else qattn_combine_kernel<true><<<(rows + 3) / 4, 256, 0, st>>>(p);
-  } else {
-    p.nsplit = 1;
-    p.tiles_per_split = (int)p.nKB;
-    if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, false><<<grid, kThreads, 0, st>>>(p);
-    else qattn_fwd_kernel<true, false><<<grid, kThreads, 0, st>>>(p);
-  }
-  return check_launch("qattn_fwd");
+  return QATTN_OK;
+}
+
+extern "C" int qattn_fwd(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const uint8_t* v8,
+                         int64_t Lpad, const float* v_scale, qattn_seq o, int out_dtype, int64_t B, int64_t Lq,
+                         int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int causal,
+                         int64_t q_offset, const int32_t* kv_valid, float* lse, int num_splits, void* workspace,
+                         size_t workspace_bytes, qattn_stream_t stream) {
+  AttnParams p;
+  int ns = 1;
+  const int rc = setup_fwd(p, ns, q8, q_scale, k8, k_scale, v8, Lpad, o, out_dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult,
+                           causal, q_offset, kv_valid, lse, num_splits);
+  if (rc < 0) return QATTN_OK;
+  if (rc) return rc;
+  QATTN_REQUIRE(v_scale, QATTN_ERR_ARG, "v_scale is null");
+  p.v_scale = v_scale;
+  return launch_fwd<PV_FP8>(p, out_dtype, ns, workspace, workspace_bytes, (hipStream_t)stream, D);
+}
+
+extern "C" int qattn_fwd_pv16(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale,
+                              const uint16_t* v16, int v_dtype, int64_t Lpad, qattn_seq o, int out_dtype, int64_t B,
+                              int64_t Lq, int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int causal,
+                              int64_t q_offset, const int32_t* kv_valid, float* lse, int num_splits, void* workspace,
+                              size_t workspace_bytes, qattn_stream_t stream) {
+  QATTN_REQUIRE(v_dtype == QATTN_BF16 || v_dtype == QATTN_FP16, QATTN_ERR_DTYPE, "V dtype must be bf16 or fp16");
+  AttnParams p;
+  int ns = 1;
+  const int rc = setup_fwd(p, ns, q8, q_scale, k8, k_scale, v16, Lpad, o, out_dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult,
+                           causal, q_offset, kv_valid, lse, num_splits);
+  if (rc < 0) return QATTN_OK;
+  if (rc) return rc;
+  p.v_scale = nullptr;
+  if (v_dtype == QATTN_BF16) return launch_fwd<PV_BF16>(p, out_dtype, ns, workspace, workspace_bytes, (hipStream_t)stream, D);
+  return launch_fwd<PV_FP16>(p, out_dtype, ns, workspace, workspace_bytes, (hipStream_t)stream, D);
 }

@@ -247,6 +247,39 @@ __global__ __launch_bounds__(256) void v_fp8_kernel(const uint16_t* in, int64_t 
   }
 }
 
+
+// V (half) -> the same transposed, tile-permuted layout in its own dtype, for the bf16/fp16 P.V path
+template <int D>
+__global__ __launch_bounds__(256) void v_tile_half_kernel(const uint16_t* in, int64_t sb, int64_t sl, int64_t sh,
+                                                          int64_t L, int64_t H, uint16_t* v16, int64_t Lpad) {
+  constexpr int TPR = D / 8;
+  __shared__ __align__(16) uint16_t tile[D][64];
+  const int64_t t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 64 * TPR / 256; i++) {
+    const int c = tid + i * 256;
+    const int row = c / TPR, dc = c % TPR;
+    const int64_t l = t * 64 + row;
+    uint16_t hv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (l < L) {
+      v4u raw = *reinterpret_cast<const v4u*>(in + b * sb + l * sl + h * sh + dc * 8);
+      __builtin_memcpy(hv, &raw, 16);
+    }
+    const int pos = vtile_pos(row);
+#pragma unroll
+    for (int e = 0; e < 8; e++) tile[dc * 8 + e][pos] = hv[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < D * 8 / 256; i++) {
+    const int c = tid + i * 256;
+    const int d = c / 8, cc = c % 8;
+    *reinterpret_cast<v4u*>(v16 + ((b * H + h) * D + d) * Lpad + t * 64 + cc * 8) =
+        *reinterpret_cast<const v4u*>(&tile[d][cc * 8]);
+  }
+}
+
 // ------------------------------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------------------------------
@@ -425,4 +458,21 @@ extern "C" int qattn_per_channel_fp8(qattn_seq v, int dtype, int64_t B, int64_t 
     else v_fp8_kernel<true, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad);
   }
   return check_launch("per_channel_fp8");
+}
+
+extern "C" int qattn_v_tile_half(qattn_seq v, int dtype, int64_t B, int64_t L, int64_t H, int64_t D, uint16_t* v16,
+                                 int64_t Lpad, qattn_stream_t stream) {
+  int rc;
+  if ((rc = check_common(dtype, D, QATTN_QUANT_CUDA, 64))) return rc;
+  QATTN_REQUIRE(B > 0 && L > 0 && H > 0, QATTN_ERR_SHAPE, "v_tile_half needs non-empty input");
+  if ((rc = check_seq("v", v, 2))) return rc;
+  QATTN_REQUIRE(Lpad >= (L + 63) / 64 * 64 && Lpad % 64 == 0, QATTN_ERR_SHAPE,
+                "Lpad must be a multiple of 64 and >= L rounded up to 64");
+  QATTN_REQUIRE(v16 && aligned16(v16), QATTN_ERR_ALIGN, "v16 must be non-null and 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  dim3 grid((unsigned)(Lpad / 64), (unsigned)H, (unsigned)B);
+  const uint16_t* p = static_cast<const uint16_t*>(v.data);
+  if (D == 128) v_tile_half_kernel<128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, v16, Lpad);
+  else v_tile_half_kernel<64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, v16, Lpad);
+  return check_launch("v_tile_half");
 }

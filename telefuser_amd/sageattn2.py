@@ -20,7 +20,6 @@ Differences from the reference, all deliberate:
 
 from __future__ import annotations
 
-import math
 import warnings
 from typing import Any, Optional
 
@@ -127,6 +126,17 @@ def per_channel_fp8(v: torch.Tensor, tensor_layout: str = "HND", scale_max: floa
     return v_fp8, v_scale, None
 
 
+def v_tile_half(v: torch.Tensor, tensor_layout: str = "HND") -> torch.Tensor:
+    """V in the kernels' transposed tile layout, in its own dtype: [B, H, D, Lpad] (bf16/fp16 P.V path)."""
+    L = _lib.load()
+    b, l, h, d = _dims(v, tensor_layout)
+    lpad = (l + 63) // 64 * 64
+    v16 = torch.empty((b, h, d, lpad), dtype=v.dtype, device=v.device)
+    _lib.check(L.qattn_v_tile_half(_lib.seq(v, tensor_layout), _lib.dtype_code(v.dtype), b, l, h, d, _lib.ptr(v16),
+                                   lpad, _lib.stream_of(v)))
+    return v16
+
+
 def _kv_valid_tensor(kv_valid_len, b: int, device) -> Optional[torch.Tensor]:
     if kv_valid_len is None:
         return None
@@ -142,23 +152,32 @@ def qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout
               qk_mult=1.0, is_causal=False, q_offset=0, kv_valid_len=None, return_lse=False, num_splits=0,
               out: Optional[torch.Tensor] = None):
     """Attention on already-quantized operands (the torch.ops.tf_kernel.qk_int8_sv_f8_accum_f32_fuse_v_scale
-    _attn op, common_extension.cc:239-258).  Returns o (and the log2-domain LSE [B, Hq, Lq] if asked)."""
+    _attn op, common_extension.cc:239-258).  With v_scale=None, v_fp8 is the half-dtype V tile from
+    ``v_tile_half`` and P.V runs in that dtype (qk_int8_sv_f16_accum_f32_attn, common_extension.cc:214-218).
+    Returns o (and the log2-domain LSE [B, Hq, Lq] if asked)."""
     L = _lib.load()
     b, lq, hq, d = _dims(q_int8, tensor_layout)
     _, lk, hkv, _ = _dims(k_int8, tensor_layout)
     if hq % hkv != 0:
         raise ValueError(f"num_qo_heads ({hq}) must be divisible by num_kv_heads ({hkv})")
     o = out if out is not None else torch.empty(q_int8.shape, dtype=out_dtype, device=q_int8.device)
+    half_v = v_scale is None  # v_fp8 is then the half-dtype tile layout from v_tile_half
     lse = torch.empty((b, hq, lq), dtype=torch.float32, device=q_int8.device) if return_lse else None
     kvv = _kv_valid_tensor(kv_valid_len, b, q_int8.device)
     ns = num_splits if num_splits > 0 else L.qattn_fwd_num_splits(b, lq, lk, hq)
     wsb = L.qattn_fwd_workspace_size(b, lq, hq, d, ns)
     ws = torch.empty(wsb, dtype=torch.uint8, device=q_int8.device) if wsb else None
-    _lib.check(L.qattn_fwd(
-        _lib.seq(q_int8, tensor_layout), _lib.ptr(q_scale), _lib.seq(k_int8, tensor_layout), _lib.ptr(k_scale),
-        _lib.ptr(v_fp8), v_fp8.shape[-1], _lib.ptr(v_scale), _lib.seq(o, tensor_layout), _lib.dtype_code(o.dtype), b,
-        lq, lk, hq, hkv, d, float(qk_mult), int(bool(is_causal)), int(q_offset), _lib.ptr(kvv), _lib.ptr(lse), ns,
-        _lib.ptr(ws), wsb, _lib.stream_of(q_int8)))
+    common = (_lib.seq(o, tensor_layout), _lib.dtype_code(o.dtype), b, lq, lk, hq, hkv, d, float(qk_mult),
+              int(bool(is_causal)), int(q_offset), _lib.ptr(kvv), _lib.ptr(lse), ns, _lib.ptr(ws), wsb,
+              _lib.stream_of(q_int8))
+    if half_v:
+        _lib.check(L.qattn_fwd_pv16(
+            _lib.seq(q_int8, tensor_layout), _lib.ptr(q_scale), _lib.seq(k_int8, tensor_layout), _lib.ptr(k_scale),
+            _lib.ptr(v_fp8), _lib.dtype_code(v_fp8.dtype), v_fp8.shape[-1], *common))
+    else:
+        _lib.check(L.qattn_fwd(
+            _lib.seq(q_int8, tensor_layout), _lib.ptr(q_scale), _lib.seq(k_int8, tensor_layout), _lib.ptr(k_scale),
+            _lib.ptr(v_fp8), v_fp8.shape[-1], _lib.ptr(v_scale), *common))
     return (o, lse) if return_lse else o
 
 
@@ -171,16 +190,8 @@ def _pad_head_dim(x: torch.Tensor) -> torch.Tensor:
     return torch.nn.functional.pad(x, (0, 128 - d))
 
 
-def sageattn_qk_int8_pv_fp8_cuda(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str = "HND",
-                                 is_causal: bool = False, qk_quant_gran: str = "per_thread",
-                                 sm_scale: Optional[float] = None, pv_accum_dtype: str = "fp32+fp16",
-                                 smooth_k: bool = True, smooth_v: bool = False, return_lse: bool = False,
-                                 kv_valid_len=None, q_offset: int = 0, **kwargs: Any):
-    """INT8 Q.K^T + FP8 P.V attention (signature of sageattn2.py:1197-1210).
-
-    Extra keyword arguments beyond the reference: ``kv_valid_len`` (int or per-batch sequence: keys at
-    or beyond it are masked) and ``q_offset`` (causal diagonal offset, kv > q + q_offset is masked).
-    """
+def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv_accum_dtype, smooth_k, smooth_v,
+                  return_lse, kv_valid_len, q_offset, pv, quant_variant="cuda"):
     dtype = q.dtype
     if not q.is_cuda:
         raise AssertionError("Input tensors must be on cuda.")
@@ -205,10 +216,13 @@ def sageattn_qk_int8_pv_fp8_cuda(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
 
     km = k_mean(k, tensor_layout) if smooth_k else None
     q_int8, q_scale, k_int8, k_scale = per_block_int8(q, k, km, BLKQ, BLKK, sm_scale=sm_scale,
-                                                      tensor_layout=tensor_layout)
+                                                      tensor_layout=tensor_layout, variant=quant_variant)
     if smooth_v:
         warnings.warn(f"pv_accum_dtype is '{pv_accum_dtype}', smooth_v will be ignored.")
-    v_fp8, v_scale, _ = per_channel_fp8(v, tensor_layout=tensor_layout, scale_max=448.0)
+    if pv == "fp8":
+        v_fp8, v_scale, _ = per_channel_fp8(v, tensor_layout=tensor_layout, scale_max=448.0)
+    else:
+        v_fp8, v_scale = v_tile_half(v, tensor_layout), None
     res = qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, tensor_layout=tensor_layout, out_dtype=dtype,
                     is_causal=is_causal, q_offset=q_offset, kv_valid_len=kv_valid_len, return_lse=return_lse)
     o, lse = res if return_lse else (res, None)
@@ -225,6 +239,20 @@ def sageattn_qk_int8_pv_fp8_cuda(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
     return o, lse
 
 
+def sageattn_qk_int8_pv_fp8_cuda(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str = "HND",
+                                 is_causal: bool = False, qk_quant_gran: str = "per_thread",
+                                 sm_scale: Optional[float] = None, pv_accum_dtype: str = "fp32+fp16",
+                                 smooth_k: bool = True, smooth_v: bool = False, return_lse: bool = False,
+                                 kv_valid_len=None, q_offset: int = 0, **kwargs: Any):
+    """INT8 Q.K^T + FP8 P.V attention (signature of sageattn2.py:1197-1210).
+
+    Extra keyword arguments beyond the reference: ``kv_valid_len`` (int or per-batch sequence: keys at
+    or beyond it are masked) and ``q_offset`` (causal diagonal offset, kv > q + q_offset is masked).
+    """
+    return _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv_accum_dtype, smooth_k,
+                         smooth_v, return_lse, kv_valid_len, q_offset, pv="fp8")
+
+
 def sageattn_qk_int8_pv_fp8_cuda_sm90(*args, **kwargs):
     """Same entry as sageattn_qk_int8_pv_fp8_cuda (the reference's Hopper variant, sageattn2.py:1460)."""
     return sageattn_qk_int8_pv_fp8_cuda(*args, **kwargs)
@@ -233,12 +261,22 @@ def sageattn_qk_int8_pv_fp8_cuda_sm90(*args, **kwargs):
 def sageattn_qk_int8_pv_fp16_cuda(q, k, v, tensor_layout: str = "HND", is_causal: bool = False,
                                   qk_quant_gran: str = "per_thread", sm_scale: Optional[float] = None,
                                   pv_accum_dtype: str = "fp32", smooth_k: bool = True, smooth_v: bool = False,
-                                  return_lse: bool = False, **kwargs: Any):
-    """Reference SAGE_ATTN_2_8_16 entry (sageattn2.py:930).  Served by the FP8 P.V kernel."""
-    return sageattn_qk_int8_pv_fp8_cuda(q, k, v, tensor_layout=tensor_layout, is_causal=is_causal,
-                                        qk_quant_gran=qk_quant_gran, sm_scale=sm_scale,
-                                        pv_accum_dtype=pv_accum_dtype, smooth_k=smooth_k, smooth_v=smooth_v,
-                                        return_lse=return_lse, **kwargs)
+                                  return_lse: bool = False, kv_valid_len=None, q_offset: int = 0, **kwargs: Any):
+    """INT8 Q.K^T + half-precision P.V (reference SAGE_ATTN_2_8_16 entry, sageattn2.py:930-1194): P is
+    rounded to V's dtype and multiplied with V unquantized, accumulating in fp32."""
+    return _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv_accum_dtype, smooth_k,
+                         smooth_v, return_lse, kv_valid_len, q_offset, pv="half")
+
+
+def sageattn_qk_int8_pv_fp16_triton(q, k, v, tensor_layout: str = "HND", quantization_backend: str = "triton",
+                                    is_causal: bool = False, attn_mask=None, sm_scale: Optional[float] = None,
+                                    smooth_k: bool = True, return_lse: bool = False, kv_valid_len=None,
+                                    q_offset: int = 0, **kwargs: Any):
+    """Reference Triton entry (sageattn2.py:551-769): per-block quantizer with the Triton rounding
+    (``quantization_backend="triton"``) or the CUDA one (``"cuda"``), half-precision P.V."""
+    variant = "triton" if quantization_backend == "triton" else "cuda"
+    return _sage_forward(q, k, v, tensor_layout, is_causal, "per_block", sm_scale, "fp32", smooth_k, False,
+                         return_lse, kv_valid_len, q_offset, pv="half", quant_variant=variant)
 
 
 def sageattn(q, k, v, tensor_layout: str = "HND", is_causal: bool = False, sm_scale: Optional[float] = None,
@@ -260,4 +298,6 @@ __all__ = [
     "sageattn_qk_int8_pv_fp8_cuda",
     "sageattn_qk_int8_pv_fp8_cuda_sm90",
     "sageattn_qk_int8_pv_fp16_cuda",
+    "sageattn_qk_int8_pv_fp16_triton",
+    "v_tile_half",
 ]

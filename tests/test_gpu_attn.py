@@ -19,7 +19,7 @@ KERNEL_LAZY_TAU = 1.0  # lazy running-max threshold of qattn_fwd_kernel (kLazyTa
 
 
 def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None, num_splits=0, q_offset=0,
-                   check_truth=True):
+                   check_truth=True, pv="fp8"):
     dev = require_gpu()
     from telefuser_amd import _lib
     from telefuser_amd import sageattn2 as sa
@@ -33,7 +33,10 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
         qd, kd, vd = (t.transpose(1, 2).contiguous() for t in (qd, kd, vd))
     km = sa.k_mean(kd, layout)
     q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=D ** -0.5, tensor_layout=layout)
-    v8, vs, _ = sa.per_channel_fp8(vd, tensor_layout=layout)
+    if pv == "fp8":
+        v8, vs, _ = sa.per_channel_fp8(vd, tensor_layout=layout)
+    else:
+        v8, vs = sa.v_tile_half(vd, tensor_layout=layout), None
     o, lse = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout=layout, out_dtype=q.dtype, is_causal=causal,
                           q_offset=q_offset, kv_valid_len=kv_valid, num_splits=num_splits, return_lse=True)
     torch.cuda.synchronize()
@@ -45,8 +48,12 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
     ns = num_splits if num_splits > 0 else L.qattn_fwd_num_splits(B, Lq, Lk, Hq)
     ns = min(ns, nkb)
     tps = (nkb + ns - 1) // ns if ns > 1 else 0  # the GPU's KV-split schedule, restated on the CPU
+    f16 = q.dtype == torch.float16
+    vargs = (dict(v8=untile_v(v8), v_scale=vs.cpu().numpy()) if pv == "fp8"
+             else dict(vh_bits=bf16_bits(v) if not f16 else v.contiguous().view(torch.int16).numpy().view(np.uint16),
+                       pv_mode=1, is_fp16=f16))
     ref, ref_lse = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
-                                    ks.cpu().numpy(), untile_v(v8), vs.cpu().numpy(), causal=causal, q_offset=q_offset,
+                                    ks.cpu().numpy(), **vargs, causal=causal, q_offset=q_offset,
                                     kv_valid=kv_valid, want_lse=True, tiles_per_split=tps,
                                     lazy_tau=KERNEL_LAZY_TAU)
     c = cosine(og, ref)
@@ -56,15 +63,15 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
     assert c >= COS_KERNEL
     # the reference's own schedule (no split, eager running max) on the same quantized operands
     ref0 = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
-                            ks.cpu().numpy(), untile_v(v8), vs.cpu().numpy(), causal=causal, q_offset=q_offset,
-                            kv_valid=kv_valid)
+                            ks.cpu().numpy(), **vargs, causal=causal, q_offset=q_offset, kv_valid=kv_valid)
     c0 = cosine(og, ref0)
     log(f"  vs reference-schedule quantized math: cosine={c0:.6f} max_abs={float(np.abs(og - ref0).max()):.4g}")
     assert c0 >= COS_E2E
     assert lerr < 2e-2
     if check_truth:
-        truth = oracle.attn_fp64(bf16_bits(q), bf16_bits(k), bf16_bits(v), D ** -0.5, causal=causal,
-                                 q_offset=q_offset, kv_valid=kv_valid)
+        bits = (lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)) if f16 else bf16_bits
+        truth = oracle.attn_fp64(bits(q), bits(k), bits(v), D ** -0.5, causal=causal,
+                                 q_offset=q_offset, kv_valid=kv_valid, is_fp16=f16)
         ct = cosine(og, truth)
         log(f"  vs fp64 truth: cosine={ct:.6f} max_abs={float(np.abs(og - truth).max()):.4g}")
         assert ct >= COS_E2E
@@ -164,3 +171,31 @@ def test_full_size_wan_480p_against_sdpa():
     log(f"  cosine vs SDPA {c:.6f}, max abs {float((a - b).abs().max()):.4g}")
     assert c >= 0.999
     assert torch.isfinite(o).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_half_pv_variant(oracle, dtype):
+    """INT8 Q.K^T with P.V in the half dtype of V (the reference's SAGE_ATTN_2_8_16 / Triton math)."""
+    q, k, v = qkv(1, 777, 1000, 2, 2, seed=12, k_offset_std=0.5, dtype=dtype)
+    _run_and_check(oracle, q, k, v, pv="half")
+
+
+def test_half_pv_causal_split_padding(oracle):
+    q, k, v = qkv(2, 300, 1300, 2, 1, seed=13)
+    _run_and_check(oracle, q, k, v, pv="half", num_splits=3, kv_valid=[1300, 900])
+    _run_and_check(oracle, q, k[:, :300], v[:, :300], pv="half", causal=True)
+
+
+def test_pv16_api_entry_points(oracle):
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    q, k, v = qkv(1, 256, 512, 2, 2, seed=14, dtype=torch.float16)
+    truth = oracle.attn_fp64(*(t.contiguous().view(torch.int16).numpy().view(np.uint16) for t in (q, k, v)),
+                             128 ** -0.5, is_fp16=True)
+    for fn in (sa.sageattn_qk_int8_pv_fp16_cuda, sa.sageattn_qk_int8_pv_fp16_triton):
+        o = fn(q.to(dev), k.to(dev), v.to(dev), tensor_layout="NHD")
+        assert o.dtype == torch.float16 and o.shape == q.shape
+        c = cosine(o.float().cpu().numpy(), truth)
+        log(f"{fn.__name__}: cosine {c:.6f}")
+        assert c >= 0.9995  # better than the FP8 P.V path: P and V are not rounded to e4m3
