@@ -199,3 +199,18 @@ def test_pv16_api_entry_points(oracle):
         c = cosine(o.float().cpu().numpy(), truth)
         log(f"{fn.__name__}: cosine {c:.6f}")
         assert c >= 0.9995  # better than the FP8 P.V path: P and V are not rounded to e4m3
+
+
+def test_attention_front_door_on_gpu(oracle):
+    """telefuser-style attention() with the SAGE implementations, BSND and BNSD, against fp64 truth."""
+    dev = require_gpu()
+    from telefuser_amd import attention as A
+
+    q, k, v = qkv(1, 300, 400, 2, 2, seed=15, k_offset_std=0.5)
+    truth = oracle.attn_fp64(bf16_bits(q), bf16_bits(k), bf16_bits(v), 128 ** -0.5)
+    for impl in (A.AttnImplType.SAGE_ATTN_2_8_8, A.AttnImplType.SAGE_ATTN_2_8_16, A.AttnImplType.SAGE_ATTN_2_8_8_SM90):
+        o = A.attention(q.to(dev), k.to(dev), v.to(dev), attn_impl=impl)
+        assert cosine(o.float().cpu().numpy(), truth) >= COS_E2E
+        ob = A.attention(*(t.to(dev).transpose(1, 2) for t in (q, k, v)), attn_impl=impl, input_layout="BNSD",
+                         output_layout="BNSD")
+        assert torch.equal(ob.transpose(1, 2).cpu(), o.cpu())
