@@ -148,6 +148,24 @@ int qattn_fwd_pv16(qattn_seq q8, const float* q_scale, qattn_seq k8, const float
                    const int32_t* kv_valid, float* lse, int num_splits, void* workspace, size_t workspace_bytes,
                    qattn_stream_t stream);
 
+/*
+ * Streaming KV cache, V side: FP8 V with a running ("sticky") per-channel amax.
+ * The cache keeps V in its own dtype (v: sequence tensor over cache slots [0, fill)) next to an FP8
+ * copy v8 [B, H, D, Lpad] in the tile layout of qattn_per_channel_fp8.  After the caller has written
+ * new rows into the slot ranges [begin0, end0) and [begin1, end1) (either may be empty), this call
+ *   amax[b, h, d] = max(amax, max |v| over the new rows);   v_scale = amax / scale_max
+ * and re-encodes, with scale_max / amax, the FP8 tiles that overlap the new rows - or every tile of a
+ * (b, h) whose amax grew.  amax (fp32 [B, H, D], zero-initialised by the caller) persists across
+ * calls.  No host synchronisation.  Replaces the per-step per_channel_fp8 of the whole attention
+ * window that the reference's streaming self-attention performs through attention()
+ * (telefuser/models/lingbot_world_fast_dit.py:150-183; sageattn2.py:320-407).
+ */
+size_t qattn_v_fp8_cache_workspace_size(int64_t B, int64_t n0, int64_t n1, int64_t H, int64_t D);
+int qattn_v_fp8_cache_update(qattn_seq v, int dtype, int64_t B, int64_t fill, int64_t H, int64_t D, int64_t begin0,
+                             int64_t end0, int64_t begin1, int64_t end1, float scale_max, float* amax, uint8_t* v8,
+                             int64_t Lpad, float* v_scale, void* workspace, size_t workspace_bytes,
+                             qattn_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

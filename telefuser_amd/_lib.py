@@ -83,7 +83,11 @@ def load() -> ctypes.CDLL:
     L.qattn_v_tile_half.argtypes = [S, i32, i64, i64, i64, i64, vp, i64, vp]
     L.qattn_fwd_pv16.argtypes = [S, vp, S, vp, vp, i32, i64, S, i32, i64, i64, i64, i64, i64, i64, f32, i32, i64, vp,
                                  vp, i32, vp, sz, vp]
-    for name in ("qattn_quant_per_block_int8", "qattn_quant_qk_per_block_int8", "qattn_seq_mean",
+    L.qattn_v_fp8_cache_workspace_size.argtypes = [i64, i64, i64, i64, i64]
+    L.qattn_v_fp8_cache_workspace_size.restype = sz
+    L.qattn_v_fp8_cache_update.argtypes = [S, i32, i64, i64, i64, i64, i64, i64, i64, i64, f32, vp, vp, i64, vp, vp,
+                                           sz, vp]
+    for name in ("qattn_v_fp8_cache_update", "qattn_quant_per_block_int8", "qattn_quant_qk_per_block_int8", "qattn_seq_mean",
                  "qattn_per_channel_fp8", "qattn_fwd", "qattn_v_tile_half", "qattn_fwd_pv16"):
         getattr(L, name).restype = i32
     _lib = L

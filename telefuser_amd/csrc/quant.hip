@@ -174,13 +174,30 @@ __global__ __launch_bounds__(256) void col_partial_kernel(const uint16_t* in, in
   }
 }
 
+// Chunk partials -> one value per (b, h, d).  One workgroup per (b, h), one thread per channel; the
+// loop over chunks keeps 4 independent loads in flight (it is latency-bound, not bandwidth-bound).
+template <int MODE, int D>
+__device__ __forceinline__ float reduce_chunks(const float* part, int64_t bh, int64_t nchunk, int d) {
+  float a[4] = {0.f, 0.f, 0.f, 0.f};
+  int64_t c = 0;
+  for (; c + 4 <= nchunk; c += 4)
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const float x = part[(bh * nchunk + c + u) * D + d];
+      a[u] = MODE == 0 ? a[u] + x : fmaxf(a[u], x);
+    }
+  for (; c < nchunk; c++) {
+    const float x = part[(bh * nchunk + c) * D + d];
+    a[0] = MODE == 0 ? a[0] + x : fmaxf(a[0], x);
+  }
+  return MODE == 0 ? (a[0] + a[1]) + (a[2] + a[3]) : fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
+}
+
 template <bool IS_FP16, int D>
 __global__ void mean_finalize_kernel(const float* part, int64_t nchunk, int64_t L, uint16_t* mean) {
   const int64_t bh = blockIdx.x;
   const int d = threadIdx.x;
-  float s = 0.f;
-  for (int64_t c = 0; c < nchunk; c++) s += part[(bh * nchunk + c) * D + d];
-  mean[bh * D + d] = f32_to_half<IS_FP16>(s / (float)L);
+  mean[bh * D + d] = f32_to_half<IS_FP16>(reduce_chunks<0, D>(part, bh, nchunk, d) / (float)L);
 }
 
 template <int D>
@@ -188,10 +205,29 @@ __global__ void vscale_finalize_kernel(const float* part, int64_t nchunk, float 
                                        float* recp) {
   const int64_t bh = blockIdx.x;
   const int d = threadIdx.x;
-  float a = 0.f;
-  for (int64_t c = 0; c < nchunk; c++) a = fmaxf(a, part[(bh * nchunk + c) * D + d]);
+  const float a = reduce_chunks<1, D>(part, bh, nchunk, d);
   v_scale[bh * D + d] = a / scale_max;
   recp[bh * D + d] = scale_max / a;
+}
+
+// Streaming cache: fold the amax of the freshly written rows (two partial sets, one per slot range)
+// into the running per-channel amax, publish v_scale / recp from it, and flag the (b, h) whose amax
+// grew - their whole FP8 V must be rewritten with the new scale.
+template <int D>
+__global__ void vcache_scale_kernel(const float* part0, int64_t nchunk0, const float* part1, int64_t nchunk1,
+                                    float scale_max, float* amax, float* v_scale, float* recp, int* grown) {
+  const int64_t bh = blockIdx.x;
+  const int d = threadIdx.x;
+  float a = 0.f;
+  if (nchunk0) a = reduce_chunks<1, D>(part0, bh, nchunk0, d);
+  if (nchunk1) a = fmaxf(a, reduce_chunks<1, D>(part1, bh, nchunk1, d));
+  const float old = amax[bh * D + d];
+  const float now = fmaxf(old, a);
+  amax[bh * D + d] = now;
+  v_scale[bh * D + d] = now / scale_max;
+  recp[bh * D + d] = scale_max / now;
+  const int g = __syncthreads_or(now > old);
+  if (d == 0) grown[bh] = g;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -210,14 +246,26 @@ __device__ __forceinline__ uint8_t f32_to_e4m3_sat(float y) {
   return (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(y, 0.f, 0, false) & 0xff);
 }
 
+// Tiles a streaming-cache update must rewrite: every tile of a (b, h) whose scale grew, otherwise
+// only the tiles that overlap the freshly written slot ranges [r[0], r[1]) and [r[2], r[3]).
+struct VTileFilter {
+  const int* grown;  // [B, H] or null (= rewrite every tile)
+  int64_t r[4];
+};
+
 template <bool IS_FP16, int D>
 __global__ __launch_bounds__(256) void v_fp8_kernel(const uint16_t* in, int64_t sb, int64_t sl, int64_t sh,
                                                     int64_t L, int64_t H, const float* recp, uint8_t* v8,
-                                                    int64_t Lpad) {
+                                                    int64_t Lpad, VTileFilter filt) {
   constexpr int TPR = D / 8;
   __shared__ __align__(16) uint8_t tile[D][64];
   const int64_t t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
+  if (filt.grown && !filt.grown[b * H + h]) {
+    const int64_t lo = t * 64, hi = lo + 64;
+    const bool hit = (filt.r[0] < hi && lo < filt.r[1]) || (filt.r[2] < hi && lo < filt.r[3]);
+    if (!hit) return;  // uniform over the workgroup
+  }
   const float* rc = recp + (b * H + h) * D;
 #pragma unroll
   for (int i = 0; i < 64 * TPR / 256; i++) {
@@ -450,12 +498,13 @@ extern "C" int qattn_per_channel_fp8(qattn_seq v, int dtype, int64_t B, int64_t 
   else vscale_finalize_kernel<64><<<B * H, 64, 0, st>>>(part, nchunk, scale_max, v_scale, recp);
   dim3 grid((unsigned)(Lpad / 64), (unsigned)H, (unsigned)B);
   const uint16_t* p = static_cast<const uint16_t*>(v.data);
+  const VTileFilter nof{nullptr, {0, 0, 0, 0}};
   if (dtype == QATTN_BF16) {
-    if (D == 128) v_fp8_kernel<false, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad);
-    else v_fp8_kernel<false, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad);
+    if (D == 128) v_fp8_kernel<false, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof);
+    else v_fp8_kernel<false, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof);
   } else {
-    if (D == 128) v_fp8_kernel<true, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad);
-    else v_fp8_kernel<true, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad);
+    if (D == 128) v_fp8_kernel<true, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof);
+    else v_fp8_kernel<true, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof);
   }
   return check_launch("per_channel_fp8");
 }
@@ -475,4 +524,56 @@ extern "C" int qattn_v_tile_half(qattn_seq v, int dtype, int64_t B, int64_t L, i
   if (D == 128) v_tile_half_kernel<128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, v16, Lpad);
   else v_tile_half_kernel<64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, v16, Lpad);
   return check_launch("v_tile_half");
+}
+
+
+extern "C" size_t qattn_v_fp8_cache_workspace_size(int64_t B, int64_t n0, int64_t n1, int64_t H, int64_t D) {
+  return (size_t)(B * H * (col_chunks(n0) + col_chunks(n1)) * D + B * H * D + B * H) * sizeof(float);
+}
+
+extern "C" int qattn_v_fp8_cache_update(qattn_seq v, int dtype, int64_t B, int64_t fill, int64_t H, int64_t D,
+                                        int64_t begin0, int64_t end0, int64_t begin1, int64_t end1,
+                                        float scale_max, float* amax, uint8_t* v8, int64_t Lpad, float* v_scale,
+                                        void* workspace, size_t workspace_bytes, qattn_stream_t stream) {
+  int rc;
+  if ((rc = check_common(dtype, D, QATTN_QUANT_CUDA, 64))) return rc;
+  QATTN_REQUIRE(B > 0 && H > 0 && fill > 0, QATTN_ERR_SHAPE, "v_fp8_cache_update needs a non-empty cache");
+  QATTN_REQUIRE(0 <= begin0 && begin0 <= end0 && end0 <= fill && 0 <= begin1 && begin1 <= end1 && end1 <= fill,
+                QATTN_ERR_ARG, "slot ranges must lie inside [0, fill)");
+  if ((rc = check_seq("v", v, 2))) return rc;
+  QATTN_REQUIRE(Lpad >= (fill + 63) / 64 * 64 && Lpad % 64 == 0, QATTN_ERR_SHAPE,
+                "Lpad must be a multiple of 64 and >= fill rounded up to 64");
+  QATTN_REQUIRE(v8 && aligned16(v8) && v_scale && amax, QATTN_ERR_ALIGN, "v8 must be non-null and 16-byte aligned");
+  const int64_t n0 = end0 - begin0, n1 = end1 - begin1;
+  QATTN_REQUIRE(workspace && workspace_bytes >= qattn_v_fp8_cache_workspace_size(B, n0, n1, H, D),
+                QATTN_ERR_WORKSPACE, "v_fp8_cache_update workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t c0 = col_chunks(n0), c1 = col_chunks(n1);
+  float* part0 = static_cast<float*>(workspace);
+  float* part1 = part0 + B * H * c0 * D;
+  float* recp = part1 + B * H * c1 * D;
+  int* grown = reinterpret_cast<int*>(recp + B * H * D);
+  const int esz = 2;
+  auto range_view = [&](int64_t begin) {
+    qattn_seq s = v;
+    s.data = static_cast<char*>(v.data) + begin * v.sl * esz;
+    return s;
+  };
+  if (n0) launch_col<1>(range_view(begin0), dtype, B, n0, H, D, c0, part0, st);
+  if (n1) launch_col<1>(range_view(begin1), dtype, B, n1, H, D, c1, part1, st);
+  if (D == 128)
+    vcache_scale_kernel<128><<<B * H, 128, 0, st>>>(part0, c0, part1, c1, scale_max, amax, v_scale, recp, grown);
+  else
+    vcache_scale_kernel<64><<<B * H, 64, 0, st>>>(part0, c0, part1, c1, scale_max, amax, v_scale, recp, grown);
+  const VTileFilter filt{grown, {begin0, end0, begin1, end1}};
+  dim3 grid((unsigned)((fill + 63) / 64), (unsigned)H, (unsigned)B);
+  const uint16_t* p = static_cast<const uint16_t*>(v.data);
+  if (dtype == QATTN_BF16) {
+    if (D == 128) v_fp8_kernel<false, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, fill, H, recp, v8, Lpad, filt);
+    else v_fp8_kernel<false, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, fill, H, recp, v8, Lpad, filt);
+  } else {
+    if (D == 128) v_fp8_kernel<true, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, fill, H, recp, v8, Lpad, filt);
+    else v_fp8_kernel<true, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, fill, H, recp, v8, Lpad, filt);
+  }
+  return check_launch("v_fp8_cache_update");
 }
