@@ -36,27 +36,86 @@ def _cpu_baseline(cfg, budget_s: float = 12.0) -> dict:
     kb = k[:, :, h:h + 1].contiguous().view(torch.int16).numpy().view(np.uint16)
     vb = v[:, :, h:h + 1].contiguous().view(torch.int16).numpy().view(np.uint16)
     sm = cfg.D ** -0.5
-    rows = 256
+    # grow the sample (queries first, then heads) until one pass takes about budget_s / 2 .. budget_s
+    rows, heads = 256, 1
     while True:
+        qh, kh, vh = (np.ascontiguousarray(x[:, :, :heads]) for x in (qb, kb, vb))
         t0 = time.perf_counter()
-        km = oracle.k_mean_bits(kb)
-        q8, qs = oracle.quant_per_block_int8(np.ascontiguousarray(qb[:, :rows]), sm_scale=sm * oracle.LOG2E, blk=128)
-        k8, ks = oracle.quant_per_block_int8(kb, km_bits=km, blk=64)
-        v8, vs = oracle.per_channel_fp8(vb)
+        km = oracle.k_mean_bits(kh)
+        q8, qs = oracle.quant_per_block_int8(np.ascontiguousarray(qh[:, :rows]), sm_scale=sm * oracle.LOG2E, blk=128)
+        k8, ks = oracle.quant_per_block_int8(kh, km_bits=km, blk=64)
+        v8, vs = oracle.per_channel_fp8(vh)
         oracle.qattn_fwd(q8, qs, k8, ks, v8, vs)
         dt = time.perf_counter() - t0
-        if dt * 4 > budget_s or rows * 4 > cfg.Lq:
+        if dt * 2 > budget_s:
             break
-        rows *= 4
-    ops = 4.0 * rows * cfg.Lk * cfg.D
+        if rows < cfg.Lq:
+            rows = min(cfg.Lq, rows * 4)
+        elif heads < cfg.Hkv:
+            heads = min(cfg.Hkv, heads * 2)
+        else:
+            break
+    calls = 1
+    if dt * 2 < budget_s:  # the whole call is short: time repeated calls (as the layers of a step would)
+        calls = max(1, int(budget_s / max(dt, 1e-3)))
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            km = oracle.k_mean_bits(kh)
+            q8, qs = oracle.quant_per_block_int8(np.ascontiguousarray(qh[:, :rows]), sm_scale=sm * oracle.LOG2E,
+                                                 blk=128)
+            k8, ks = oracle.quant_per_block_int8(kh, km_bits=km, blk=64)
+            v8, vs = oracle.per_channel_fp8(vh)
+            oracle.qattn_fwd(q8, qs, k8, ks, v8, vs)
+        dt = time.perf_counter() - t0
+    ops = 4.0 * rows * heads * cfg.Lk * cfg.D * calls
     return {
         "value": round(ops / dt / 1e12, 6),
         "unit": "TOPS",
         "cores": oracle.num_threads(),
         "kind": "port",
-        "sample": f"1 of {cfg.Hq} heads, first {rows} of {cfg.Lq} queries x all {cfg.Lk} keys "
-                  f"(K mean + Q/K/V quantizers + attention), {dt:.2f} s",
+        "sample": f"{calls} call(s) of {heads} of {cfg.Hq} heads, first {rows} of {cfg.Lq} queries x all "
+                  f"{cfg.Lk} keys (K mean + Q/K/V quantizers + attention), {dt:.2f} s",
     }
+
+
+def _stream_bench(steps: int = 20, warmup: int = 3) -> dict:
+    """Steady-state streaming step at the C5 shape (4680-token chunk vs a full 32760-slot rolling cache):
+    the reference call site (bf16 dict cache, roll + attention() re-quantizing the window) against
+    QuantizedKVCache (ring, incremental quantization)."""
+    import torch
+
+    from telefuser_amd.attention import AttentionConfig, AttnImplType
+    from telefuser_amd.kv_cache import QuantizedKVCache, streaming_self_attention
+    from telefuser_amd.workloads import CONFIGS
+
+    cfg = CONFIGS["c5"]
+    dev = torch.device("cuda:0")
+    n, size, H, D = cfg.Lq, cfg.Lk, cfg.Hq, cfg.D
+    g = torch.Generator(device=dev).manual_seed(5)
+    chunks = [tuple(torch.randn((1, n, H, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+              for _ in range(4)]
+    frames = size // n  # local_attn_size in chunks; every step after the first `frames` evicts one chunk
+    cfg_sage = AttentionConfig(attn_impl=AttnImplType.SAGE_ATTN_2_8_8)
+    ref = {"k": torch.zeros((1, size, H, D), dtype=torch.bfloat16, device=dev),
+           "v": torch.zeros((1, size, H, D), dtype=torch.bfloat16, device=dev),
+           "global_end_index": 0, "local_end_index": 0}
+    cache = QuantizedKVCache(1, size, H, D, device=dev)
+    out = {}
+    for name, target in (("reference_dict", ref), ("quantized_ring", cache)):
+        for i in range(frames + warmup):
+            q, k, v = chunks[i % 4]
+            streaming_self_attention(q, k, v, target, i * n, local_attn_size=frames, attention_config=cfg_sage)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(frames + warmup, frames + warmup + steps):
+            q, k, v = chunks[i % 4]
+            streaming_self_attention(q, k, v, target, i * n, local_attn_size=frames, attention_config=cfg_sage)
+        torch.cuda.synchronize()
+        out[name] = (time.perf_counter() - t0) * 1e3 / steps
+    return {"workload": cfg.name + " (steady state, cache full, one chunk evicted per step)",
+            "ms_per_step_reference_path": round(out["reference_dict"], 4),
+            "ms_per_step_quantized_cache": round(out["quantized_ring"], 4),
+            "speedup": round(out["reference_dict"] / out["quantized_ring"], 3)}
 
 
 def main() -> int:
@@ -67,12 +126,13 @@ def main() -> int:
     ap.add_argument("--config", default="c2")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sdpa", action="store_true")
+    ap.add_argument("--no-stream", action="store_true", help="skip the streaming KV-cache comparison")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the path shards "
-              "per head across GPUs with no collectives inside the op - see DESIGN.md", file=sys.stderr)
+              "per head across GPUs with no collectives inside the op", file=sys.stderr)
         return 2
 
     import torch
@@ -191,6 +251,9 @@ def main() -> int:
         "sdpa_bf16_ms": None if sdpa_ms is None else round(sdpa_ms, 4),
         "speedup_vs_sdpa": None if sdpa_ms is None else round(sdpa_ms / ms_per_step, 3),
     }
+    if not args.no_stream:
+        print("[bench] streaming KV-cache comparison", file=sys.stderr, flush=True)
+        line["streaming_kv_cache"] = _stream_bench()
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = _cpu_baseline(cfg)
