@@ -45,6 +45,12 @@ enum qattn_status {
 
 enum qattn_dtype { QATTN_BF16 = 0, QATTN_FP16 = 1 };
 
+/* Q/K scale granularity: the reference's QuantGranularity codes (attn_utils.cuh:41-64) */
+enum qattn_gran { QATTN_GRAN_BLOCK = 1, QATTN_GRAN_WARP = 2, QATTN_GRAN_THREAD = 3 };
+
+/* V operand of qattn_fwd_ex */
+enum qattn_v_kind { QATTN_V_FP8 = 0, QATTN_V_BF16 = 1, QATTN_V_FP16 = 2 };
+
 /* rounding / smoothing semantics of the per-block INT8 quantizer */
 enum qattn_quant_variant {
   QATTN_QUANT_CUDA = 0,  /* QuantInt8Kernel: fp32 (x - km) * sm_scale, amax floor 1e-7, RNE + saturate */
@@ -80,6 +86,32 @@ int qattn_quant_qk_per_block_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B
                                   int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean, qattn_seq q_out,
                                   qattn_seq k_out, float* q_scale, float* k_scale, float sm_scale, int blkq,
                                   int blkk, int variant, qattn_stream_t stream);
+
+/*
+ * Per-warp INT8 quantization of Q and K in one launch: sageattn2.per_warp_int8 (sageattn2.py:190-280 ->
+ * quant_per_warp_int8_cuda fused.cu:698-780 for Q, QuantInt8Kernel per 64-row block for K).  The
+ * QuantInt8Kernel rounding (amax floor 1e-7, RNE + saturate), no sm_scale folded in:
+ *   q_scale [B, Hq, ceil(Lq/128)*4]: one scale per 32 rows (empty trailing warp blocks: 1e-7/127);
+ *   k_scale [B, Hkv, ceil(Lk/64)], K = k - k_mean in fp32 when k_mean is given.
+ */
+int qattn_quant_qk_per_warp_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq, int64_t Lk,
+                                 int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean, qattn_seq q_out,
+                                 qattn_seq k_out, float* q_scale, float* k_scale, qattn_stream_t stream);
+
+/*
+ * Per-thread INT8 quantization of Q and K in one launch: the Triton per_thread_int8 of the reference's
+ * default SAGE_ATTN_2_8_8 path (tf-kernel/tf_kernel/triton/quant_per_thread.py:22-158,267-369;
+ * chosen at sageattn2.py:1360-1365).  Scales follow the NVIDIA mma fragment a thread holds:
+ *   q_scale [B, Hq, ceil(Lq/128)*32]: 32-row warp blocks, rows with equal row % 8 share a scale
+ *     (index (row / 32) * 8 + row % 8; trailing warp blocks of the last 128-row block get 1e-7);
+ *   k_scale [B, Hkv, ceil(Lk/64)*4]: 64-row blocks, rows with equal (row % 8) / 2 share a scale
+ *     (index (row / 64) * 4 + (row % 8) / 2).
+ * scale = amax / 127 + 1e-7, q = round-half-away(x / scale); K = half-rounded (k - k_mean) when k_mean
+ * is given; sm_scale is not folded in (qattn_fwd_ex applies it, qk_quant_gran = QATTN_GRAN_THREAD).
+ */
+int qattn_quant_qk_per_thread_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq, int64_t Lk,
+                                   int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean, qattn_seq q_out,
+                                   qattn_seq k_out, float* q_scale, float* k_scale, qattn_stream_t stream);
 
 /*
  * Mean over the sequence, rounded to the input dtype: mean[b, h, d] (contiguous [B, H, D]).
@@ -165,6 +197,26 @@ int qattn_v_fp8_cache_update(qattn_seq v, int dtype, int64_t B, int64_t fill, in
                              int64_t end0, int64_t begin1, int64_t end1, float scale_max, float* amax, uint8_t* v8,
                              int64_t Lpad, float* v_scale, void* workspace, size_t workspace_bytes,
                              qattn_stream_t stream);
+
+/*
+ * General form of qattn_fwd / qattn_fwd_pv16 with the Q/K scale granularity of the reference's kernels
+ * (the qk_quant_gran argument of qk_int8_sv_f8_accum_f32_fuse_v_scale_attn(_inst_buf) and
+ * qk_int8_sv_f16_accum_f32_attn, common_extension.cc:214-258; sm89 kernel :136,318-323):
+ *   QATTN_GRAN_BLOCK:  q_scale [B, Hq, ceil(Lq/128)],     k_scale [B, Hkv, ceil(Lk/64)]
+ *   QATTN_GRAN_WARP:   q_scale [B, Hq, ceil(Lq/128)*4],   k_scale [B, Hkv, ceil(Lk/64)]
+ *   QATTN_GRAN_THREAD: q_scale [B, Hq, ceil(Lq/128)*32],  k_scale [B, Hkv, ceil(Lk/64)*4]
+ * (layouts of qattn_quant_qk_per_warp_int8 / qattn_quant_qk_per_thread_int8).  For per-warp and
+ * per-thread scales sm_scale is not in Q: pass qk_mult = sm_scale * 1.44269504.
+ *   v_kind QATTN_V_FP8: v = e4m3 tile layout + v_scale;  QATTN_V_BF16 / _FP16: v from qattn_v_tile_half.
+ * The number of KV splits depends on v_kind and the granularity: size the workspace with
+ * qattn_fwd_ex_num_splits (or pass an explicit num_splits >= it).
+ */
+int qattn_fwd_ex_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int v_kind, int qk_quant_gran);
+int qattn_fwd_ex(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const void* v, int v_kind,
+                 int64_t Lpad, const float* v_scale, qattn_seq o, int out_dtype, int64_t B, int64_t Lq, int64_t Lk,
+                 int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int qk_quant_gran, int causal, int64_t q_offset,
+                 const int32_t* kv_valid, float* lse, int num_splits, void* workspace, size_t workspace_bytes,
+                 qattn_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -42,7 +42,9 @@ def lib():
         L.oq_per_channel_fp8.argtypes = [vp, i32, i64, i64, i64, i64, i64, i64, i64, f32, vp, i64, vp]
         L.oq_qattn_fwd.argtypes = [vp, i64, i64, i64, vp, i64, vp, i64, i64, i64, vp, i64, vp, i64, vp, vp, i32,
                                    i64, i64, i64, i64, i64, i64, i64, i64, i64, f64, i32, i32, i64, vp, i64, i64,
-                                   i64, i64, f64, i32, vp, vp]
+                                   i64, i64, f64, i32, i32, i32, vp, vp]
+        L.oq_quant_per_thread_int8.argtypes = [vp, i32, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, i32, vp,
+                                               i64, i64, i64, vp]
         L.oq_attn_fp64.argtypes = [vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, f64, i32, i64, vp, vp]
         L.oq_f32_to_e4m3.argtypes = [f32]
         L.oq_f32_to_e4m3.restype = ctypes.c_uint8
@@ -106,6 +108,20 @@ def quant_per_block_int8(x_bits, km_bits=None, sm_scale=None, blk=128, layout="N
     return out, scale
 
 
+def quant_per_thread_int8(x_bits, km_bits=None, is_key=False, layout="NHD", is_fp16=False):
+    """Triton per-thread quantizer (triton/quant_per_thread.py:22-158,267-369).  Returns (int8 tensor same
+    layout, fp32 scale [B, H, n]) with n = ceil(L/128)*32 for queries, ceil(L/64)*4 for keys."""
+    x_bits = _bits(x_bits)
+    B, L, H, D, sb, sl, sh = _dims_nhd(x_bits, layout)
+    out = np.zeros(x_bits.shape, np.int8)
+    n = (L + 63) // 64 * 4 if is_key else (L + 127) // 128 * 32
+    scale = np.zeros((B, H, n), np.float32)
+    km_arr = None if km_bits is None else np.ascontiguousarray(km_bits.reshape(B, H, D))
+    lib().oq_quant_per_thread_int8(_p(x_bits), int(is_fp16), B, L, H, D, sb, sl, sh, _p(km_arr), H * D, D,
+                                   int(bool(is_key)), _p(out), sb, sl, sh, _p(scale))
+    return out, scale
+
+
 def per_channel_fp8(v_bits, scale_max=448.0, layout="NHD", is_fp16=False, pad=64):
     """V -> (e4m3 bytes [B, H, D, Lpad] in plain key order, v_scale [B, H, D]).  fused.cu:332-445."""
     v_bits = _bits(v_bits)
@@ -120,11 +136,13 @@ def per_channel_fp8(v_bits, scale_max=448.0, layout="NHD", is_fp16=False, pad=64
 
 def qattn_fwd(q8, q_scale, k8, k_scale, v8=None, v_scale=None, vh_bits=None, *, blkq=128, blkk=64,
               qk_mult=1.0, pv_mode=0, causal=False, q_offset=0, kv_valid=None, is_fp16=False, heads=None,
-              qrows_limit=0, want_lse=False, tiles_per_split=0, lazy_tau=-1.0, lsum_rounded=False):
+              qrows_limit=0, want_lse=False, tiles_per_split=0, lazy_tau=-1.0, lsum_rounded=False, q_gran=1,
+              k_gran=1):
     """Quantized attention in the reference's tile order.  q8/k8 NHD int8; returns fp32 O NHD
     (and log2-domain LSE [B, Hq, Lq] when want_lse).  lazy_tau >= 0 / tiles_per_split > 0 restate the
     device kernel's lazy running-max rule / KV-split schedule and lsum_rounded its row sum over the
-    rounded P (defaults: the reference's schedule)."""
+    rounded P (defaults: the reference's schedule).  q_gran / k_gran: scale granularity codes of the reference
+    (1 per block, 2 per warp, 3 per thread) - see oq_qattn_fwd."""
     q8 = np.ascontiguousarray(q8)
     k8 = np.ascontiguousarray(k8)
     B, Lq, Hq, D = q8.shape
@@ -147,7 +165,8 @@ def qattn_fwd(q8, q_scale, k8, k_scale, v8=None, v_scale=None, vh_bits=None, *, 
                        _p(k_scale), blkk, _p(v8) if pv_mode == 0 else None, Lpad,
                        _p(v_scale) if pv_mode == 0 else None, _p(vh_bits), int(is_fp16), Lk * Hkv * D, Hkv * D, D,
                        B, Lq, Lk, Hq, Hkv, D, float(qk_mult), int(pv_mode), int(causal), int(q_offset), _p(kvv), h0,
-                       h1, int(qrows_limit), int(tiles_per_split), float(lazy_tau), int(lsum_rounded), _p(out),
+                       h1, int(qrows_limit), int(tiles_per_split), float(lazy_tau), int(lsum_rounded), int(q_gran),
+                       int(k_gran), _p(out),
                        _p(lse))
     return (out, lse) if want_lse else out
 

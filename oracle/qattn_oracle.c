@@ -235,6 +235,62 @@ void oq_quant_per_block_int8_triton(const uint16_t* in, int is_fp16, int64_t B, 
       }
 }
 
+/*
+ * Triton per-thread quantizer (tf-kernel/tf_kernel/triton/quant_per_thread.py:22-158, wrapper :267-369).
+ * The scale groups follow the NVIDIA mma fragment a thread holds:
+ *   query (is_key = 0): 32-row warp blocks; rows r with the same r % 8 share a scale (4 rows x D);
+ *     scale index = block * 8 + r % 8; the scale array has ceil(L / 128) * 4 * 8 entries per (b, h)
+ *     (trailing blocks with no rows get scale 1e-7), no sm_scale folded in;
+ *   key (is_key = 1): 64-row blocks; rows with the same (r % 8) / 2 share a scale (16 rows x D);
+ *     scale index = block * 4 + (r % 8) / 2; ceil(L / 64) * 4 entries per (b, h).
+ *   k - km is a torch op on half tensors (rounded to the input dtype, :285-286);
+ *   scale = max|x| / 127 + 1e-7; q = trunc(x / scale + 0.5 * sign)  (:63-70, :145-158)
+ * Masked tail rows load as 0 and do not change the max.
+ */
+void oq_quant_per_thread_int8(const uint16_t* in, int is_fp16, int64_t B, int64_t L, int64_t H, int64_t D,
+                              int64_t sb, int64_t sl, int64_t sh, const uint16_t* km, int64_t kmb, int64_t kmh,
+                              int is_key, int8_t* out, int64_t ob, int64_t ol, int64_t oh, float* scale) {
+  const int64_t blk = is_key ? 64 : 32, ncls = is_key ? 4 : 8;
+  const int64_t nblk = is_key ? (L + 63) / 64 : (L + 127) / 128 * 4;
+#pragma omp parallel for collapse(3) schedule(static)
+  for (int64_t b = 0; b < B; b++)
+    for (int64_t h = 0; h < H; h++)
+      for (int64_t n = 0; n < nblk; n++)
+        for (int64_t c = 0; c < ncls; c++) {
+          float amax = 0.f;
+          for (int64_t r = 0; r < blk; r++) {
+            const int64_t cls = is_key ? (r % 8) / 2 : r % 8;
+            const int64_t l = n * blk + r;
+            if (cls != c || l >= L) continue;
+            for (int64_t d = 0; d < D; d++) {
+              float x = load_h(in + b * sb + l * sl + h * sh + d, is_fp16);
+              if (km) {
+                float diff = x - load_h(km + b * kmb + h * kmh + d, is_fp16);
+                x = is_fp16 ? oq_f16_to_f32(oq_f32_to_f16(diff)) : oq_bf16_to_f32(oq_f32_to_bf16(diff));
+              }
+              amax = fmaxf(amax, fabsf(x));
+            }
+          }
+          volatile float q127 = amax / 127.0f;
+          volatile float sc = q127 + 0.0000001f;
+          scale[(b * H + h) * nblk * ncls + n * ncls + c] = sc;
+          for (int64_t r = 0; r < blk; r++) {
+            const int64_t cls = is_key ? (r % 8) / 2 : r % 8;
+            const int64_t l = n * blk + r;
+            if (cls != c || l >= L) continue;
+            for (int64_t d = 0; d < D; d++) {
+              float x = load_h(in + b * sb + l * sl + h * sh + d, is_fp16);
+              if (km) {
+                float diff = x - load_h(km + b * kmb + h * kmh + d, is_fp16);
+                x = is_fp16 ? oq_f16_to_f32(oq_f32_to_f16(diff)) : oq_bf16_to_f32(oq_f32_to_bf16(diff));
+              }
+              volatile float t = x / sc;
+              out[b * ob + l * ol + h * oh + d] = oq_f32_to_s8_half_away(t);
+            }
+          }
+        }
+}
+
 /* ------------------------------------------------------------------------------------------ */
 /* per-channel FP8 V quantizer                                                                 */
 /* ------------------------------------------------------------------------------------------ */
@@ -291,8 +347,12 @@ void oq_per_channel_fp8(const uint16_t* in, int is_fp16, int64_t B, int64_t L, i
  *   end: O /= d; pv_mode 0: O *= v_scale[d]
  * Everything not rounded by the reference is carried in double.
  *
- * q8: element (b,l,h,d) at q8[b*qsb + l*qsl + h*qsh + d]; k8 likewise with ks*; q_scale [B,Hq,nQB]
- * with block blkq; k_scale [B,Hkv,nKB] with block blkk (one scale per key tile, blkk = tile).
+ * q8: element (b,l,h,d) at q8[b*qsb + l*qsl + h*qsh + d]; k8 likewise with ks*.
+ * Scale granularity (the reference's QuantGranularity codes, attn_utils.cuh:41-64):
+ *   q_gran 1: q_scale [B,Hq,nQB] with block blkq;  2 (per warp): one scale per 32 rows, ceil(Lq/128)*4
+ *   entries;  3 (per thread): (row / 32) * 8 + row % 8, ceil(Lq/128)*32 entries.
+ *   k_gran 1 / 2: k_scale [B,Hkv,nKB] one per key tile (blkk);  3: tile * 4 + (key % 8) / 2, nKB*4 entries.
+ *   (per-warp K is per-block K; quant_per_thread.py:267-369, fused.cu:698-780.)
  * pv_mode 0: v8 is the plain transposed [B,Hkv,D,Lpad] e4m3 tensor, v_scale [B,Hkv,D].
  * pv_mode 1: vh is (b,l,h,d) at vh[b*vsb + l*vsl + h*vsh + d] (bf16 or fp16 bits).
  * kv_valid: per-batch number of valid keys (NULL = Lk); causal: top-left aligned kv > q + q_offset masked.
@@ -316,10 +376,13 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
                   int64_t vsb, int64_t vsl, int64_t vsh, int64_t B, int64_t Lq, int64_t Lk, int64_t Hq,
                   int64_t Hkv, int64_t D, double qk_mult, int pv_mode, int causal, int64_t q_offset,
                   const int32_t* kv_valid, int64_t h_begin, int64_t h_end, int64_t qrows_limit, int64_t tiles_per_split,
-                  double lazy_tau, int lsum_rounded, float* out, float* lse2) {
+                  double lazy_tau, int lsum_rounded, int q_gran, int k_gran, float* out, float* lse2) {
   const int64_t RB = 128; /* query rows per work item */
   int64_t nQB = (Lq + blkq - 1) / blkq;
   int64_t nKB = (Lk + blkk - 1) / blkk;
+  /* scale entries per (b, h): per-block / per-warp (32 rows) / per-thread (32-row block x 8 classes) */
+  const int64_t nQS = q_gran == 3 ? (Lq + 127) / 128 * 32 : q_gran == 2 ? (Lq + 127) / 128 * 4 : nQB;
+  const int64_t nKS = k_gran == 3 ? nKB * 4 : nKB;
   int64_t group = Hq / Hkv;
   int64_t rows = qrows_limit > 0 && qrows_limit < Lq ? qrows_limit : Lq;
   int64_t nRB = (rows + RB - 1) / RB;
@@ -351,7 +414,7 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
           memset(o, 0, sizeof(double) * nr * D);
           for (int64_t t = t0; t < t1 && t * blkk < valid; t++) {
             int64_t k0 = t * blkk, kend = k0 + blkk < valid ? k0 + blkk : valid;
-            double ks = k_scale[(b * Hkv + hk) * nKB + t];
+            const float* ksrow = k_scale + (b * Hkv + hk) * nKS;
             for (int64_t j = k0; j < kend; j++)
               for (int64_t d = 0; d < D; d++) {
                 double vv;
@@ -365,13 +428,15 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
               if (causal && i + q_offset + 1 < k1) k1 = i + q_offset + 1;
               if (k1 <= k0) continue;
               const int8_t* qrow = q8 + b * qsb + i * qsl + h * qsh;
-              double c = (double)q_scale[(b * Hq + h) * nQB + i / blkq] * ks * qk_mult;
+              const int64_t qi = q_gran == 3 ? (i / 32) * 8 + i % 8 : q_gran == 2 ? i / 32 : i / blkq;
+              const double qsv = (double)q_scale[(b * Hq + h) * nQS + qi];
               double mx = -1e300;
               for (int64_t j = k0; j < k1; j++) {
                 const int8_t* krow = k8 + b * ksb + j * ksl + hk * ksh;
                 int32_t acc = 0;
                 for (int64_t d = 0; d < D; d++) acc += (int32_t)qrow[d] * (int32_t)krow[d];
-                s[j - k0] = (double)acc * c;
+                const double ks = ksrow[k_gran == 3 ? t * 4 + (j % 8) / 2 : t];
+                s[j - k0] = (double)acc * (qsv * ks * qk_mult);
                 if (s[j - k0] > mx) mx = s[j - k0];
               }
               double m_new;

@@ -19,6 +19,8 @@ QATTN_BF16 = 0
 QATTN_FP16 = 1
 QATTN_QUANT_CUDA = 0
 QATTN_QUANT_TRITON = 1
+QATTN_GRAN_BLOCK, QATTN_GRAN_WARP, QATTN_GRAN_THREAD = 1, 2, 3
+QATTN_V_FP8, QATTN_V_BF16, QATTN_V_FP16 = 0, 1, 2
 
 EXPORTED = (
     "qattn_last_error",
@@ -87,7 +89,14 @@ def load() -> ctypes.CDLL:
     L.qattn_v_fp8_cache_workspace_size.restype = sz
     L.qattn_v_fp8_cache_update.argtypes = [S, i32, i64, i64, i64, i64, i64, i64, i64, i64, f32, vp, vp, i64, vp, vp,
                                            sz, vp]
-    for name in ("qattn_v_fp8_cache_update", "qattn_quant_per_block_int8", "qattn_quant_qk_per_block_int8", "qattn_seq_mean",
+    L.qattn_quant_qk_per_warp_int8.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, vp]
+    L.qattn_quant_qk_per_thread_int8.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, vp]
+    L.qattn_fwd_ex_num_splits.argtypes = [i64, i64, i64, i64, i32, i32]
+    L.qattn_fwd_ex_num_splits.restype = i32
+    L.qattn_fwd_ex.argtypes = [S, vp, S, vp, vp, i32, i64, vp, S, i32, i64, i64, i64, i64, i64, i64, f32, i32, i32,
+                               i64, vp, vp, i32, vp, sz, vp]
+    for name in ("qattn_quant_qk_per_warp_int8", "qattn_quant_qk_per_thread_int8", "qattn_fwd_ex",
+                 "qattn_v_fp8_cache_update", "qattn_quant_per_block_int8", "qattn_quant_qk_per_block_int8", "qattn_seq_mean",
                  "qattn_per_channel_fp8", "qattn_fwd", "qattn_v_tile_half", "qattn_fwd_pv16"):
         getattr(L, name).restype = i32
     _lib = L

@@ -38,7 +38,11 @@ constexpr int kBQ = 128;  // query quantization block
 constexpr int kWavesPerSimd = 2;  // occupancy target: 2 workgroups of 4 waves per CU
 constexpr int kPrefetch = 2;      // K/V tiles in flight ahead of the one being computed
 constexpr int kNBuf = kPrefetch + 1;
-constexpr int kMaxTilesPerSplit = 2048;  // key tiles per workgroup (k_scales staged in LDS)
+// k_scales staged in LDS per workgroup (floats).  Sized so that two workgroups per CU still fit in the
+// 160 KiB of LDS next to the K/V buffers: 24 + 24 + 30 KiB (FP8 V) or 24 + 48 + 6 KiB (half V).
+template <int PV> constexpr int ks_lds_floats() { return PV == 0 ? 7680 : 1536; }
+// per-thread K scales: 4 per 64-key tile (one per mma lane-pair class), otherwise 1
+constexpr int ks_per_tile(bool kt) { return kt ? 4 : 1; }
 constexpr int kBK = 64;
 constexpr int kThreads = 256;
 constexpr float kFp8Offset = 8.807f;  // attn_utils.cuh:35 S_FP8_OFFSET
@@ -52,8 +56,8 @@ struct AttnParams {
   int64_t ksb, ksl, ksh;
   const void* v;  // tile-layout V: e4m3 (PV_FP8) or the half dtype, [B, Hkv, D, Lpad]
   int64_t Lpad;
-  const float* q_scale;  // [B, Hq, nQB]
-  const float* k_scale;  // [B, Hkv, nKB]
+  const float* q_scale;  // [B, Hq, nQS]: per 128-row block, per 32-row warp block, or per thread class
+  const float* k_scale;  // [B, Hkv, nKS]: per 64-key tile, or 4 lane-pair classes per tile
   const float* v_scale;  // [B, Hkv, D] (FP8 P.V only)
   void* o;
   int64_t osb, osl, osh;
@@ -62,6 +66,8 @@ struct AttnParams {
   float* ws_o;   // split partials [split][B][Hq][Lq][D]
   float* ws_ml;  // [split][B][Hq][Lq][2]
   int64_t B, Lq, Lk, Hq, Hkv, nQB, nKB;
+  int64_t nQS, nKS;  // scale entries per (b, h)
+  int qgran;         // QATTN_GRAN_BLOCK / _WARP / _THREAD (q_scale indexing)
   int64_t q_offset;
   int group;
   int nsplit;
@@ -102,14 +108,15 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
 // P rounded to the half dtype of V x V as given (the Triton / SAGE_ATTN_2_8_16 style), fp32 accumulation.
 enum PvKind { PV_FP8 = 0, PV_BF16 = 1, PV_FP16 = 2 };
 
-template <bool IS_FP16_OUT, bool SPLIT, int PV>
+template <bool IS_FP16_OUT, bool SPLIT, int PV, bool KT>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(AttnParams p) {
+  constexpr int KS = ks_per_tile(KT);
   constexpr int kVBytes = PV == PV_FP8 ? 1 : 2;    // bytes per V element
   constexpr int kVDma = 2 * kVBytes;                // V DMA instructions per wave per tile
   constexpr float kOffset = PV == PV_FP8 ? kFp8Offset : 0.f;
   __shared__ __align__(16) uint8_t lds_k[kNBuf][kBK * kD];
   __shared__ __align__(16) uint8_t lds_v[kNBuf][kD * kBK * kVBytes];
-  __shared__ float lds_ks[kMaxTilesPerSplit];  // k_scale of this workgroup's key tiles
+  __shared__ float lds_ks[ks_lds_floats<PV>()];  // k_scales of this workgroup's key tiles
 
   const int64_t tile_id = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t qb = tile_id % p.nQB;
@@ -149,8 +156,13 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
 #pragma unroll
     for (int m = 0; m < 4; m++) asm volatile("" ::"v"(qf[m]));
   }
-  const float qs = p.q_scale[(b * p.Hq + h) * p.nQB + qb] * p.qk_mult;
-  const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKB;
+  // q_scale of this lane's query row: one per 128-row block, per wave (32 rows), or per row class
+  // (rows with equal row % 8 inside the wave's 32 rows: the reference's per-thread grouping)
+  const int64_t qsi = p.qgran == QATTN_GRAN_THREAD ? (qb * 4 + w) * 8 + (lq & 7)
+                      : p.qgran == QATTN_GRAN_WARP ? qb * 4 + w
+                                                   : qb;
+  const float qs = p.q_scale[(b * p.Hq + h) * p.nQS + qsi] * p.qk_mult;
+  const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
 
   // global -> LDS copies go through the LDS-DMA path (global_load_lds_dwordx4): lane j of a wave
   // writes the 16 bytes at LDS slot (wave base + 16 j), so the XOR swizzle is applied on the global
@@ -209,7 +221,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   // iteration t issues tile t + kPrefetch into buffer (t + kPrefetch) % kNBuf, which was last read in
   // iteration t - 1.  The k_scales of all tiles are staged in LDS once, so the only VMEM traffic in the
   // loop is the 4 DMA instructions per tile and the vmcnt accounting below is exact.
-  for (int64_t t = t_begin + tid; t < t_end; t += kThreads) lds_ks[t - t_begin] = ks_ptr[t];
+  for (int64_t i = tid; i < (t_end - t_begin) * KS; i += kThreads) lds_ks[i] = ks_ptr[t_begin * KS + i];
 #pragma unroll
   for (int d = 0; d < kPrefetch; d++)
     if (t_begin + d < t_end) dma_tile(t_begin + d, d);
@@ -220,7 +232,15 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   for (int64_t t = t_begin; t < t_end; t++) {
     const bool issue = t + kPrefetch < t_end;
     if (issue) dma_tile(t + kPrefetch, buf == 0 ? kNBuf - 1 : buf - 1);
-    const float ks_cur = lds_ks[t - t_begin];
+    // logit scale(s) of this lane: with per-thread K scales, key kappa of the tile belongs to class
+    // (kappa % 8) / 2 = 2 hf + (r & 3) / 2 for accumulator element r, so a lane needs two of them
+    float cs_a, cs_b;
+    if constexpr (KT) {
+      cs_a = qs * lds_ks[(t - t_begin) * 4 + 2 * hf];
+      cs_b = qs * lds_ks[(t - t_begin) * 4 + 2 * hf + 1];
+    } else {
+      cs_a = cs_b = qs * lds_ks[t - t_begin];
+    }
 
     // ---- S^T = K . Q^T: two 32-key blocks x 4 MFMAs over D = 128; K fragments streamed from LDS ----
     v16i s[2];
@@ -251,22 +271,38 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
     }
 
     // ---- online softmax ----
-    int mx = max(s[0][0], s[0][1]);
+    float m_tile;
+    if constexpr (!KT) {
+      int mx = max(s[0][0], s[0][1]);
 #pragma unroll
-    for (int r = 2; r < 16; r++) mx = max(mx, s[0][r]);
+      for (int r = 2; r < 16; r++) mx = max(mx, s[0][r]);
 #pragma unroll
-    for (int r = 0; r < 16; r++) mx = max(mx, s[1][r]);
-    {  // lanes l and l^32 hold the two key halves of the same query row
-      const auto sw = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);
-      mx = max((int)sw[0], (int)sw[1]);
+      for (int r = 0; r < 16; r++) mx = max(mx, s[1][r]);
+      {  // lanes l and l^32 hold the two key halves of the same query row
+        const auto sw = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);
+        mx = max((int)sw[0], (int)sw[1]);
+      }
+      // Lazy rescale: the running max m is only moved when the tile max exceeds it by more than
+      // kLazyTau (log2 units), per row.  With the offset lowered by the same tau, p = exp2(s - m) stays
+      // <= 2^8.807 = 448 (the e4m3 maximum), so the FP8 range is honoured while the O rescale (64
+      // multiplies per lane) is skipped on almost every tile.  A row whose keys in this tile are all
+      // masked never moves m.
+      m_tile = mx == INT32_MIN ? kMInit : fmaf((float)mx, cs_a, -(kOffset - kLazyTau));
+    } else {  // two scale classes per lane: max per class, scaled, then across the lane pair
+      int ma = INT32_MIN, mb = INT32_MIN;
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          if ((r & 3) < 2) ma = max(ma, s[kb][r]);
+          else mb = max(mb, s[kb][r]);
+        }
+      const float fa = ma == INT32_MIN ? kMInit : fmaf((float)ma, cs_a, -(kOffset - kLazyTau));
+      const float fb = mb == INT32_MIN ? kMInit : fmaf((float)mb, cs_b, -(kOffset - kLazyTau));
+      float mt = fmaxf(fa, fb);
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+      m_tile = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
     }
-    const float cs = qs * ks_cur;
-    // Lazy rescale: the running max m is only moved when the tile max exceeds it by more than
-    // kLazyTau (log2 units), per row.  With the offset lowered by the same tau, p = exp2(s - m) stays
-    // <= 2^8.807 = 448 (the e4m3 maximum), so the FP8 range is honoured while the O rescale (64
-    // multiplies per lane) is skipped on almost every tile.  A row whose keys in this tile are all
-    // masked never moves m.
-    const float m_tile = mx == INT32_MIN ? kMInit : fmaf((float)mx, cs, -(kOffset - kLazyTau));
     const bool grow = m_tile > m_run + kLazyTau;
     if (__any(grow)) {
       const float m_new = grow ? m_tile : m_run;
@@ -286,7 +322,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int sv = s[kb][r0 + e];
-        pv[e] = __builtin_amdgcn_exp2f(fmaf((float)sv, cs, neg_m));
+        pv[e] = __builtin_amdgcn_exp2f(fmaf((float)sv, e < 2 ? cs_a : cs_b, neg_m));
         if constexpr (decltype(mk)::value) pv[e] = sv == INT32_MIN ? 0.f : pv[e];
       }
     };
@@ -443,18 +479,32 @@ __global__ __launch_bounds__(256) void qattn_combine_kernel(AttnParams p) {
 
 using namespace qattn;
 
-extern "C" int qattn_fwd_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq) {
+// key tiles one workgroup can cover (its k_scales are staged in LDS)
+static int64_t max_tiles_per_split(int pv, bool kt) {
+  const int floats = pv == PV_FP8 ? ks_lds_floats<PV_FP8>() : ks_lds_floats<PV_BF16>();
+  return floats / ks_per_tile(kt);
+}
+
+static int num_splits_for(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t max_tiles) {
   const int64_t wgs = B * Hq * ((Lq + kBQ - 1) / kBQ);
   const int64_t nkb = (Lk + kBK - 1) / kBK;
   if (wgs <= 0 || nkb <= 0) return 1;
   // 256 CUs x 2 resident workgroups; split only when the grid leaves the chip mostly idle and every
   // split still gets at least 8 key tiles
   const int64_t target = 1024;
-  const int64_t min_s = (nkb + kMaxTilesPerSplit - 1) / kMaxTilesPerSplit;
+  const int64_t min_s = (nkb + max_tiles - 1) / max_tiles;
   if (wgs >= target / 2) return (int)min_s;
   int64_t s = (target + wgs - 1) / wgs;
   s = std::min<int64_t>(s, nkb / 8);
   return (int)std::max<int64_t>(min_s, std::min<int64_t>(s, 32));
+}
+
+extern "C" int qattn_fwd_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq) {
+  return num_splits_for(B, Lq, Lk, Hq, max_tiles_per_split(PV_FP8, false));
+}
+
+extern "C" int qattn_fwd_ex_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int v_kind, int qk_quant_gran) {
+  return num_splits_for(B, Lq, Lk, Hq, max_tiles_per_split(v_kind, qk_quant_gran == QATTN_GRAN_THREAD));
 }
 
 extern "C" size_t qattn_fwd_workspace_size(int64_t B, int64_t Lq, int64_t Hq, int64_t D, int num_splits) {
@@ -462,7 +512,7 @@ extern "C" size_t qattn_fwd_workspace_size(int64_t B, int64_t Lq, int64_t Hq, in
   return (size_t)num_splits * B * Hq * Lq * (D + 2) * sizeof(float);
 }
 
-template <int PV>
+template <int PV, bool KT>
 static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, size_t workspace_bytes, hipStream_t st,
                       int64_t D) {
   const int64_t grid = p.B * p.Hq * p.nQB * ns;
@@ -475,14 +525,14 @@ static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, siz
                   qattn_fwd_workspace_size(p.B, p.Lq, p.Hq, D, ns));
     p.ws_o = static_cast<float*>(workspace);
     p.ws_ml = p.ws_o + (int64_t)ns * p.B * p.Hq * p.Lq * D;
-    if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, true, PV><<<grid, kThreads, 0, st>>>(p);
-    else qattn_fwd_kernel<true, true, PV><<<grid, kThreads, 0, st>>>(p);
+    if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, true, PV, KT><<<grid, kThreads, 0, st>>>(p);
+    else qattn_fwd_kernel<true, true, PV, KT><<<grid, kThreads, 0, st>>>(p);
     const int64_t rows = p.B * p.Hq * p.Lq;
     if (out_dtype == QATTN_BF16) qattn_combine_kernel<false><<<(rows + 3) / 4, 256, 0, st>>>(p);
     else qattn_combine_kernel<true><<<(rows + 3) / 4, 256, 0, st>>>(p);
   } else {
-    if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, false, PV><<<grid, kThreads, 0, st>>>(p);
-    else qattn_fwd_kernel<true, false, PV><<<grid, kThreads, 0, st>>>(p);
+    if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, false, PV, KT><<<grid, kThreads, 0, st>>>(p);
+    else qattn_fwd_kernel<true, false, PV, KT><<<grid, kThreads, 0, st>>>(p);
   }
   return check_launch("qattn_fwd");
 }
@@ -490,10 +540,12 @@ static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, siz
 static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale,
                      const void* v, int64_t Lpad, qattn_seq o, int out_dtype, int64_t B, int64_t Lq, int64_t Lk,
                      int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int causal, int64_t q_offset,
-                     const int32_t* kv_valid, float* lse, int num_splits) {
+                     const int32_t* kv_valid, float* lse, int num_splits, int pv, int gran) {
   QATTN_REQUIRE(out_dtype == QATTN_BF16 || out_dtype == QATTN_FP16, QATTN_ERR_DTYPE, "out dtype must be bf16 or fp16");
   QATTN_REQUIRE(D == kD, QATTN_ERR_HEAD_DIM, "qattn_fwd needs head_dim 128 (pad smaller heads), got %lld",
                 (long long)D);
+  QATTN_REQUIRE(gran == QATTN_GRAN_BLOCK || gran == QATTN_GRAN_WARP || gran == QATTN_GRAN_THREAD, QATTN_ERR_ARG,
+                "qk_quant_gran must be 1 (per block), 2 (per warp) or 3 (per thread), got %d", gran);
   QATTN_REQUIRE(B >= 0 && Lq >= 0 && Lk >= 0 && Hq > 0 && Hkv > 0, QATTN_ERR_SHAPE, "bad sizes");
   QATTN_REQUIRE(Hq % Hkv == 0, QATTN_ERR_HEAD_RATIO, "num_qo_heads (%lld) must be divisible by num_kv_heads (%lld)",
                 (long long)Hq, (long long)Hkv);
@@ -524,17 +576,53 @@ static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale,
   p.B = B; p.Lq = Lq; p.Lk = Lk; p.Hq = Hq; p.Hkv = Hkv;
   p.nQB = (Lq + kBQ - 1) / kBQ;
   p.nKB = (Lk + kBK - 1) / kBK;
+  p.qgran = gran;
+  p.nQS = gran == QATTN_GRAN_THREAD ? p.nQB * 32 : gran == QATTN_GRAN_WARP ? p.nQB * 4 : p.nQB;
+  p.nKS = gran == QATTN_GRAN_THREAD ? p.nKB * 4 : p.nKB;
   p.q_offset = q_offset;
   p.group = (int)(Hq / Hkv);
   p.causal = causal ? 1 : 0;
   p.qk_mult = qk_mult;
 
-  ns = num_splits > 0 ? num_splits : qattn_fwd_num_splits(B, Lq, Lk, Hq);
+  const int64_t max_tiles = max_tiles_per_split(pv, gran == QATTN_GRAN_THREAD);
+  ns = num_splits > 0 ? num_splits : num_splits_for(B, Lq, Lk, Hq, max_tiles);
   ns = (int)std::min<int64_t>(ns, p.nKB);
   if (ns < 1) ns = 1;
-  // a workgroup stages the k_scales of at most kMaxTilesPerSplit key tiles
-  ns = (int)std::max<int64_t>(ns, (p.nKB + kMaxTilesPerSplit - 1) / kMaxTilesPerSplit);
+  // a workgroup stages the k_scales of at most max_tiles key tiles
+  ns = (int)std::max<int64_t>(ns, (p.nKB + max_tiles - 1) / max_tiles);
   return QATTN_OK;
+}
+
+template <int PV>
+static int launch_gran(AttnParams& p, int gran, int out_dtype, int ns, void* ws, size_t wsb, hipStream_t st,
+                       int64_t D) {
+  if (gran == QATTN_GRAN_THREAD) return launch_fwd<PV, true>(p, out_dtype, ns, ws, wsb, st, D);
+  return launch_fwd<PV, false>(p, out_dtype, ns, ws, wsb, st, D);
+}
+
+extern "C" int qattn_fwd_ex(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const void* v,
+                            int v_kind, int64_t Lpad, const float* v_scale, qattn_seq o, int out_dtype, int64_t B,
+                            int64_t Lq, int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult,
+                            int qk_quant_gran, int causal, int64_t q_offset, const int32_t* kv_valid, float* lse,
+                            int num_splits, void* workspace, size_t workspace_bytes, qattn_stream_t stream) {
+  QATTN_REQUIRE(v_kind == QATTN_V_FP8 || v_kind == QATTN_V_BF16 || v_kind == QATTN_V_FP16, QATTN_ERR_DTYPE,
+                "v_kind must be 0 (fp8), 1 (bf16) or 2 (fp16), got %d", v_kind);
+  AttnParams p;
+  int ns = 1;
+  const int pv = v_kind == QATTN_V_FP8 ? PV_FP8 : v_kind == QATTN_V_BF16 ? PV_BF16 : PV_FP16;
+  const int rc = setup_fwd(p, ns, q8, q_scale, k8, k_scale, v, Lpad, o, out_dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult,
+                           causal, q_offset, kv_valid, lse, num_splits, pv, qk_quant_gran);
+  if (rc < 0) return QATTN_OK;
+  if (rc) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if (pv == PV_FP8) {
+    QATTN_REQUIRE(v_scale, QATTN_ERR_ARG, "v_scale is null");
+    p.v_scale = v_scale;
+    return launch_gran<PV_FP8>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D);
+  }
+  p.v_scale = nullptr;
+  if (pv == PV_BF16) return launch_gran<PV_BF16>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D);
+  return launch_gran<PV_FP16>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D);
 }
 
 extern "C" int qattn_fwd(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const uint8_t* v8,
@@ -542,15 +630,9 @@ extern "C" int qattn_fwd(qattn_seq q8, const float* q_scale, qattn_seq k8, const
                          int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int causal,
                          int64_t q_offset, const int32_t* kv_valid, float* lse, int num_splits, void* workspace,
                          size_t workspace_bytes, qattn_stream_t stream) {
-  AttnParams p;
-  int ns = 1;
-  const int rc = setup_fwd(p, ns, q8, q_scale, k8, k_scale, v8, Lpad, o, out_dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult,
-                           causal, q_offset, kv_valid, lse, num_splits);
-  if (rc < 0) return QATTN_OK;
-  if (rc) return rc;
-  QATTN_REQUIRE(v_scale, QATTN_ERR_ARG, "v_scale is null");
-  p.v_scale = v_scale;
-  return launch_fwd<PV_FP8>(p, out_dtype, ns, workspace, workspace_bytes, (hipStream_t)stream, D);
+  return qattn_fwd_ex(q8, q_scale, k8, k_scale, v8, QATTN_V_FP8, Lpad, v_scale, o, out_dtype, B, Lq, Lk, Hq, Hkv, D,
+                      qk_mult, QATTN_GRAN_BLOCK, causal, q_offset, kv_valid, lse, num_splits, workspace,
+                      workspace_bytes, stream);
 }
 
 extern "C" int qattn_fwd_pv16(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale,
@@ -559,13 +641,7 @@ extern "C" int qattn_fwd_pv16(qattn_seq q8, const float* q_scale, qattn_seq k8, 
                               int64_t q_offset, const int32_t* kv_valid, float* lse, int num_splits, void* workspace,
                               size_t workspace_bytes, qattn_stream_t stream) {
   QATTN_REQUIRE(v_dtype == QATTN_BF16 || v_dtype == QATTN_FP16, QATTN_ERR_DTYPE, "V dtype must be bf16 or fp16");
-  AttnParams p;
-  int ns = 1;
-  const int rc = setup_fwd(p, ns, q8, q_scale, k8, k_scale, v16, Lpad, o, out_dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult,
-                           causal, q_offset, kv_valid, lse, num_splits);
-  if (rc < 0) return QATTN_OK;
-  if (rc) return rc;
-  p.v_scale = nullptr;
-  if (v_dtype == QATTN_BF16) return launch_fwd<PV_BF16>(p, out_dtype, ns, workspace, workspace_bytes, (hipStream_t)stream, D);
-  return launch_fwd<PV_FP16>(p, out_dtype, ns, workspace, workspace_bytes, (hipStream_t)stream, D);
+  return qattn_fwd_ex(q8, q_scale, k8, k_scale, v16, v_dtype == QATTN_BF16 ? QATTN_V_BF16 : QATTN_V_FP16, Lpad,
+                      nullptr, o, out_dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult, QATTN_GRAN_BLOCK, causal, q_offset,
+                      kv_valid, lse, num_splits, workspace, workspace_bytes, stream);
 }

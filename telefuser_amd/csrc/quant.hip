@@ -27,6 +27,8 @@ struct QuantJob {
   int has_sm_scale;
   float sm_scale;
   int64_t nwg;  // B * H * nblk
+  int ncls;     // scale classes per block: 1 (per block), 8 (per-thread Q), 4 (per-thread K)
+  int cls_shift;  // class of row r = (r % 8) >> cls_shift  (3, 0, 1 for the cases above)
 };
 
 struct QuantArgs {
@@ -35,6 +37,9 @@ struct QuantArgs {
 };
 
 constexpr int kQuantThreads = 256;
+// Rounding of the Triton per-thread quantizer (quant_per_thread.py:63-70): scale = amax/127 + 1e-7,
+// half-rounded K - km, round half away.  Used with per-thread scale classes only.
+constexpr int QATTN_QUANT_TRITON_THREAD = 2;
 
 // Round-half-away-from-zero of the Triton kernel: t + 0.5*sign, truncate; NaN -> 0.
 __device__ __forceinline__ int8_t s8_half_away(float t) {
@@ -55,7 +60,6 @@ template <bool IS_FP16, int VARIANT, int D>
 __global__ __launch_bounds__(kQuantThreads) void quant_per_block_kernel(QuantArgs args) {
   constexpr int TPR = D / 8;                       // threads (16-byte chunks) per row
   constexpr int MAXC = 128 * TPR / kQuantThreads;  // chunks per thread at blk = 128
-  __shared__ float red[kQuantThreads / 64];
 
   int64_t wg = blockIdx.x;
   int j = 0;
@@ -69,6 +73,11 @@ __global__ __launch_bounds__(kQuantThreads) void quant_per_block_kernel(QuantArg
   const int64_t b = wg / (J.nblk * J.H);
   const int tid = threadIdx.x;
   const int nchunks = J.blk * TPR;
+
+  // the scale class of a row: rows r with equal (r % 8) / (8 / ncls) share a scale.  Every thread
+  // touches rows of a single class (rows per pass, 256 / TPR, is a multiple of 8).
+  constexpr int RPP = kQuantThreads / TPR;
+  const int cls = ((tid / TPR) & 7) >> J.cls_shift;
 
   float x[MAXC][8];
   float amax = VARIANT == QATTN_QUANT_CUDA ? 0.0000001f : 0.f;
@@ -96,8 +105,8 @@ __global__ __launch_bounds__(kQuantThreads) void quant_per_block_kernel(QuantArg
         float v = half_to_f32<IS_FP16>(hv[e]);
         if (J.mean) {
           v = v - mv[e];
-          // Triton path: k - km is a torch op on half tensors, rounded back to the half type
-          if constexpr (VARIANT == QATTN_QUANT_TRITON) v = half_to_f32<IS_FP16>(f32_to_half<IS_FP16>(v));
+          // Triton paths: k - km is a torch op on half tensors, rounded back to the half type
+          if constexpr (VARIANT != QATTN_QUANT_CUDA) v = half_to_f32<IS_FP16>(f32_to_half<IS_FP16>(v));
         }
         if (J.has_sm_scale) v = v * J.sm_scale;
         x[i][e] = v;
@@ -105,13 +114,28 @@ __global__ __launch_bounds__(kQuantThreads) void quant_per_block_kernel(QuantArg
       }
     }
   }
-  amax = wave_max(amax);
-  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  // max over the TPR lanes of a row, then over the row slots of each class through LDS
+#pragma unroll
+  for (int o = 1; o < TPR; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  __shared__ float row_max[RPP];
+  if (tid % TPR == 0) row_max[tid / TPR] = amax;
   __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  auto class_max = [&](int k) {
+    float a = VARIANT == QATTN_QUANT_CUDA ? 0.0000001f : 0.f;
+#pragma unroll
+    for (int r = 0; r < RPP; r++)
+      if (((r & 7) >> J.cls_shift) == k) a = fmaxf(a, row_max[r]);
+    return a;
+  };
+  amax = class_max(cls);
 
-  const float scale = amax / 127.0f;  // IEEE division (hipcc default: correctly rounded)
-  if (tid == 0) J.scale[(b * J.H + h) * J.nblk + n] = scale;
+  // IEEE division (hipcc default: correctly rounded)
+  auto scale_of = [](float a) {
+    if constexpr (VARIANT == QATTN_QUANT_TRITON_THREAD) return a / 127.0f + 0.0000001f;
+    else return a / 127.0f;
+  };
+  const float scale = scale_of(amax);
+  if (tid < J.ncls) J.scale[((b * J.H + h) * J.nblk + n) * J.ncls + tid] = scale_of(class_max(tid));
   const float inv = 127.0f / amax;
 
 #pragma unroll
@@ -353,19 +377,25 @@ static bool fill_job(QuantJob& J, const qattn_seq& in, const qattn_seq& out, int
   J.has_sm_scale = has_sm;
   J.sm_scale = sm_scale;
   J.nwg = B * H * J.nblk;
+  J.ncls = 1;
+  J.cls_shift = 3;
   return true;
 }
 
 template <int D>
 static void launch_quant(const QuantArgs& a, int dtype, int variant, int64_t nwg, hipStream_t st) {
   dim3 grid((unsigned)nwg), block(kQuantThreads);
+#define QATTN_QK(F16, V) quant_per_block_kernel<F16, V, D><<<grid, block, 0, st>>>(a)
   if (dtype == QATTN_BF16) {
-    if (variant == QATTN_QUANT_CUDA) quant_per_block_kernel<false, QATTN_QUANT_CUDA, D><<<grid, block, 0, st>>>(a);
-    else quant_per_block_kernel<false, QATTN_QUANT_TRITON, D><<<grid, block, 0, st>>>(a);
+    if (variant == QATTN_QUANT_CUDA) QATTN_QK(false, QATTN_QUANT_CUDA);
+    else if (variant == QATTN_QUANT_TRITON) QATTN_QK(false, QATTN_QUANT_TRITON);
+    else QATTN_QK(false, QATTN_QUANT_TRITON_THREAD);
   } else {
-    if (variant == QATTN_QUANT_CUDA) quant_per_block_kernel<true, QATTN_QUANT_CUDA, D><<<grid, block, 0, st>>>(a);
-    else quant_per_block_kernel<true, QATTN_QUANT_TRITON, D><<<grid, block, 0, st>>>(a);
+    if (variant == QATTN_QUANT_CUDA) QATTN_QK(true, QATTN_QUANT_CUDA);
+    else if (variant == QATTN_QUANT_TRITON) QATTN_QK(true, QATTN_QUANT_TRITON);
+    else QATTN_QK(true, QATTN_QUANT_TRITON_THREAD);
   }
+#undef QATTN_QK
 }
 
 static int run_quant(QuantArgs& a, int dtype, int64_t D, int variant, hipStream_t st) {
@@ -430,6 +460,62 @@ extern "C" int qattn_quant_qk_per_block_int8(qattn_seq q, qattn_seq k, int dtype
   }
   if (a.njobs == 0) return QATTN_OK;
   return run_quant(a, dtype, D, variant, (hipStream_t)stream);
+}
+
+extern "C" int qattn_quant_qk_per_warp_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq, int64_t Lk,
+                                             int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean, qattn_seq q_out,
+                                             qattn_seq k_out, float* q_scale, float* k_scale, qattn_stream_t stream) {
+  int rc;
+  if ((rc = check_common(dtype, D, QATTN_QUANT_CUDA, 64))) return rc;
+  QATTN_REQUIRE(B >= 0 && Lq >= 0 && Lk >= 0 && Hq >= 0 && Hkv >= 0, QATTN_ERR_SHAPE, "negative size");
+  QATTN_REQUIRE(q_scale && k_scale, QATTN_ERR_ARG, "scale is null");
+  QuantArgs a{};
+  a.njobs = 0;
+  if (B * Lq * Hq > 0) {
+    if ((rc = check_seq("q", q, 2)) || (rc = check_seq("q_out", q_out, 1))) return rc;
+    QuantJob& J = a.job[a.njobs++];
+    fill_job(J, q, q_out, B, Lq, Hq, nullptr, q_scale, 1.0f, 0, 32);
+    J.nblk = (Lq + 127) / 128 * 4;  // the reference's grid: warp blocks of every 128-row CTA block
+    J.nwg = B * Hq * J.nblk;
+  }
+  if (B * Lk * Hkv > 0) {
+    if ((rc = check_seq("k", k, 2)) || (rc = check_seq("k_out", k_out, 1))) return rc;
+    QATTN_REQUIRE(k_mean == nullptr || aligned16(k_mean), QATTN_ERR_ALIGN, "k_mean must be 16-byte aligned");
+    fill_job(a.job[a.njobs++], k, k_out, B, Lk, Hkv, k_mean, k_scale, 1.0f, 0, 64);
+  }
+  if (a.njobs == 0) return QATTN_OK;
+  return run_quant(a, dtype, D, QATTN_QUANT_CUDA, (hipStream_t)stream);
+}
+
+extern "C" int qattn_quant_qk_per_thread_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq,
+                                               int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean,
+                                               qattn_seq q_out, qattn_seq k_out, float* q_scale, float* k_scale,
+                                               qattn_stream_t stream) {
+  int rc;
+  if ((rc = check_common(dtype, D, QATTN_QUANT_TRITON, 64))) return rc;
+  QATTN_REQUIRE(B >= 0 && Lq >= 0 && Lk >= 0 && Hq >= 0 && Hkv >= 0, QATTN_ERR_SHAPE, "negative size");
+  QATTN_REQUIRE(q_scale && k_scale, QATTN_ERR_ARG, "scale is null");
+  QuantArgs a{};
+  a.njobs = 0;
+  if (B * Lq * Hq > 0) {
+    if ((rc = check_seq("q", q, 2)) || (rc = check_seq("q_out", q_out, 1))) return rc;
+    QuantJob& J = a.job[a.njobs++];
+    fill_job(J, q, q_out, B, Lq, Hq, nullptr, q_scale, 1.0f, 0, 32);
+    J.nblk = (Lq + 127) / 128 * 4;  // warp blocks of the 128-row CTA grid, trailing ones empty
+    J.nwg = B * Hq * J.nblk;
+    J.ncls = 8;
+    J.cls_shift = 0;
+  }
+  if (B * Lk * Hkv > 0) {
+    if ((rc = check_seq("k", k, 2)) || (rc = check_seq("k_out", k_out, 1))) return rc;
+    QATTN_REQUIRE(k_mean == nullptr || aligned16(k_mean), QATTN_ERR_ALIGN, "k_mean must be 16-byte aligned");
+    QuantJob& J = a.job[a.njobs++];
+    fill_job(J, k, k_out, B, Lk, Hkv, k_mean, k_scale, 1.0f, 0, 64);
+    J.ncls = 4;
+    J.cls_shift = 1;
+  }
+  if (a.njobs == 0) return QATTN_OK;
+  return run_quant(a, dtype, D, QATTN_QUANT_TRITON_THREAD, (hipStream_t)stream);
 }
 
 static int64_t col_chunks(int64_t L) { return (L + kColChunk - 1) / kColChunk; }

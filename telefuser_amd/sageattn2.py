@@ -7,9 +7,10 @@ functions of tf-kernel/tf_kernel/sageattn2.py: ``per_block_int8`` (:96-187), ``p
 (:1460-1693), ``sageattn_qk_int8_pv_fp16_cuda`` (:930-1194) and ``sageattn`` (:415-548).
 
 Differences from the reference, all deliberate:
-  * Q/K are always quantized per block (Q blocks of 128 rows with sm_scale*log2e folded in, K blocks of
-    64 rows after K-mean smoothing) - the ``per_block_int8`` semantics.  ``qk_quant_gran`` is accepted
-    for signature compatibility; the per-warp / per-thread granularities are not used.
+  * ``qk_quant_gran`` selects the reference's quantizer: "per_thread" (the default, Triton
+    quant_per_thread.py), "per_warp" (CUDA quant_per_warp_int8) or the extra "per_block" (CUDA
+    QuantInt8Kernel with sm_scale*log2e folded into Q).  Per-warp Q blocks are always 32 rows (the
+    reference uses 16 for head_dim 128 with "fp16+fp32" accumulation).
   * ``pv_accum_dtype`` variants all accumulate P.V in full fp32 (MFMA accumulators are fp32), so
     "fp32", "fp32+fp32" and "fp32+fp16" give the same result; V uses scale_max 448.
   * ``kv_valid_len`` (per-batch number of valid keys) is honoured; ``attn_mask`` is ignored exactly as
@@ -92,6 +93,43 @@ def per_block_int8(q: torch.Tensor, k: torch.Tensor, km: Optional[torch.Tensor] 
     return q_int8, q_scale, k_int8, k_scale
 
 
+def per_warp_int8(q: torch.Tensor, k: torch.Tensor, km: Optional[torch.Tensor] = None, BLKQ: int = 128,
+                  WARPQ: int = 32, BLKK: int = 64, tensor_layout: str = "HND"):
+    """sageattn2.per_warp_int8 (sageattn2.py:190-280): Q per 32-row warp block (no sm_scale folded in),
+    K per 64-row block after km.  Returns (q_int8, q_scale [B, Hq, ceil(Lq/128)*4], k_int8, k_scale)."""
+    if (BLKQ, WARPQ, BLKK) != (128, 32, 64):
+        raise ValueError("per_warp_int8 supports BLKQ=128, WARPQ=32, BLKK=64")
+    return _quant_gran(q, k, km, tensor_layout, "qattn_quant_qk_per_warp_int8", 4, 1)
+
+
+def per_thread_int8(q: torch.Tensor, k: torch.Tensor, km: Optional[torch.Tensor] = None, BLKQ: int = 128,
+                    WARPQ: int = 32, BLKK: int = 64, WARPK: int = 64, sm_scale=None, tensor_layout: str = "HND"):
+    """triton.quant_per_thread.per_thread_int8 (quant_per_thread.py:267-369): per-thread scale classes,
+    scale = amax/127 + 1e-7, round half away, K = half-rounded (k - km); sm_scale is not folded in.
+    Returns (q_int8, q_scale [B, Hq, ceil(Lq/128)*32], k_int8, k_scale [B, Hkv, ceil(Lk/64)*4])."""
+    if (BLKQ, WARPQ, BLKK, WARPK) != (128, 32, 64, 64):
+        raise ValueError("per_thread_int8 supports BLKQ=128, WARPQ=32, BLKK=64, WARPK=64")
+    return _quant_gran(q, k, km, tensor_layout, "qattn_quant_qk_per_thread_int8", 32, 4)
+
+
+def _quant_gran(q, k, km, tensor_layout, entry, q_per_blk, k_per_blk):
+    L = _lib.load()
+    if q.dtype != k.dtype:
+        raise ValueError("q and k must have the same dtype")
+    b, lq, hq, d = _dims(q, tensor_layout)
+    _, lk, hkv, _ = _dims(k, tensor_layout)
+    q_int8 = torch.empty(q.shape, dtype=torch.int8, device=q.device)
+    k_int8 = torch.empty(k.shape, dtype=torch.int8, device=k.device)
+    q_scale = torch.empty((b, hq, (lq + 127) // 128 * q_per_blk), dtype=torch.float32, device=q.device)
+    k_scale = torch.empty((b, hkv, (lk + 63) // 64 * k_per_blk), dtype=torch.float32, device=q.device)
+    kmc = None if km is None else _mean_3d(km.to(k.dtype), b, hkv, d, tensor_layout)
+    _lib.check(getattr(L, entry)(
+        _lib.seq(q, tensor_layout), _lib.seq(k, tensor_layout), _lib.dtype_code(q.dtype), b, lq, lk, hq, hkv, d,
+        _lib.ptr(kmc), _lib.seq(q_int8, tensor_layout), _lib.seq(k_int8, tensor_layout), _lib.ptr(q_scale),
+        _lib.ptr(k_scale), _lib.stream_of(q)))
+    return q_int8, q_scale, k_int8, k_scale
+
+
 def quant_per_block_int8(x: torch.Tensor, block_size: int, sm_scale: Optional[float] = None,
                          mean: Optional[torch.Tensor] = None, tensor_layout: str = "HND", variant: str = "cuda"):
     """One-tensor form: torch.ops.tf_kernel.quant_per_block_int8_cuda(_with_sm_scale / _fuse_sub_mean)
@@ -148,36 +186,38 @@ def _kv_valid_tensor(kv_valid_len, b: int, device) -> Optional[torch.Tensor]:
     return t.to(device=device, dtype=torch.int32).contiguous()
 
 
+_GRAN = {"per_block": _lib.QATTN_GRAN_BLOCK, "per_warp": _lib.QATTN_GRAN_WARP, "per_thread": _lib.QATTN_GRAN_THREAD}
+
+
 def qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout="HND", out_dtype=torch.bfloat16,
               qk_mult=1.0, is_causal=False, q_offset=0, kv_valid_len=None, return_lse=False, num_splits=0,
-              out: Optional[torch.Tensor] = None):
+              qk_quant_gran="per_block", out: Optional[torch.Tensor] = None):
     """Attention on already-quantized operands (the torch.ops.tf_kernel.qk_int8_sv_f8_accum_f32_fuse_v_scale
     _attn op, common_extension.cc:239-258).  With v_scale=None, v_fp8 is the half-dtype V tile from
     ``v_tile_half`` and P.V runs in that dtype (qk_int8_sv_f16_accum_f32_attn, common_extension.cc:214-218).
-    Returns o (and the log2-domain LSE [B, Hq, Lq] if asked)."""
+    ``qk_quant_gran`` names the layout of q_scale / k_scale ("per_block", "per_warp", "per_thread"); for
+    the last two pass qk_mult = sm_scale * 1.44269504.  Returns o (and the log2-domain LSE [B, Hq, Lq])."""
     L = _lib.load()
     b, lq, hq, d = _dims(q_int8, tensor_layout)
     _, lk, hkv, _ = _dims(k_int8, tensor_layout)
     if hq % hkv != 0:
         raise ValueError(f"num_qo_heads ({hq}) must be divisible by num_kv_heads ({hkv})")
+    gran = _GRAN[qk_quant_gran]
     o = out if out is not None else torch.empty(q_int8.shape, dtype=out_dtype, device=q_int8.device)
-    half_v = v_scale is None  # v_fp8 is then the half-dtype tile layout from v_tile_half
+    if v_scale is None:  # v_fp8 is then the half-dtype tile layout from v_tile_half
+        v_kind = _lib.QATTN_V_BF16 if v_fp8.dtype == torch.bfloat16 else _lib.QATTN_V_FP16
+    else:
+        v_kind = _lib.QATTN_V_FP8
     lse = torch.empty((b, hq, lq), dtype=torch.float32, device=q_int8.device) if return_lse else None
     kvv = _kv_valid_tensor(kv_valid_len, b, q_int8.device)
-    ns = num_splits if num_splits > 0 else L.qattn_fwd_num_splits(b, lq, lk, hq)
+    ns = num_splits if num_splits > 0 else L.qattn_fwd_ex_num_splits(b, lq, lk, hq, v_kind, gran)
     wsb = L.qattn_fwd_workspace_size(b, lq, hq, d, ns)
     ws = torch.empty(wsb, dtype=torch.uint8, device=q_int8.device) if wsb else None
-    common = (_lib.seq(o, tensor_layout), _lib.dtype_code(o.dtype), b, lq, lk, hq, hkv, d, float(qk_mult),
-              int(bool(is_causal)), int(q_offset), _lib.ptr(kvv), _lib.ptr(lse), ns, _lib.ptr(ws), wsb,
-              _lib.stream_of(q_int8))
-    if half_v:
-        _lib.check(L.qattn_fwd_pv16(
-            _lib.seq(q_int8, tensor_layout), _lib.ptr(q_scale), _lib.seq(k_int8, tensor_layout), _lib.ptr(k_scale),
-            _lib.ptr(v_fp8), _lib.dtype_code(v_fp8.dtype), v_fp8.shape[-1], *common))
-    else:
-        _lib.check(L.qattn_fwd(
-            _lib.seq(q_int8, tensor_layout), _lib.ptr(q_scale), _lib.seq(k_int8, tensor_layout), _lib.ptr(k_scale),
-            _lib.ptr(v_fp8), v_fp8.shape[-1], _lib.ptr(v_scale), *common))
+    _lib.check(L.qattn_fwd_ex(
+        _lib.seq(q_int8, tensor_layout), _lib.ptr(q_scale), _lib.seq(k_int8, tensor_layout), _lib.ptr(k_scale),
+        _lib.ptr(v_fp8), v_kind, v_fp8.shape[-1], _lib.ptr(v_scale), _lib.seq(o, tensor_layout),
+        _lib.dtype_code(o.dtype), b, lq, lk, hq, hkv, d, float(qk_mult), gran, int(bool(is_causal)), int(q_offset),
+        _lib.ptr(kvv), _lib.ptr(lse), ns, _lib.ptr(ws), wsb, _lib.stream_of(q_int8)))
     return (o, lse) if return_lse else o
 
 
@@ -215,8 +255,14 @@ def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv
         raise ValueError(f"num_qo_heads ({hq}) must be divisible by num_kv_heads ({hkv})")
 
     km = k_mean(k, tensor_layout) if smooth_k else None
-    q_int8, q_scale, k_int8, k_scale = per_block_int8(q, k, km, BLKQ, BLKK, sm_scale=sm_scale,
-                                                      tensor_layout=tensor_layout, variant=quant_variant)
+    qk_mult = 1.0
+    if qk_quant_gran == "per_block":
+        q_int8, q_scale, k_int8, k_scale = per_block_int8(q, k, km, BLKQ, BLKK, sm_scale=sm_scale,
+                                                          tensor_layout=tensor_layout, variant=quant_variant)
+    else:  # sm_scale stays out of Q and is applied by the attention kernel (sm89 kernel :136,318-323)
+        quant = per_thread_int8 if qk_quant_gran == "per_thread" else per_warp_int8
+        q_int8, q_scale, k_int8, k_scale = quant(q, k, km, tensor_layout=tensor_layout)
+        qk_mult = sm_scale * LOG2E
     if smooth_v:
         warnings.warn(f"pv_accum_dtype is '{pv_accum_dtype}', smooth_v will be ignored.")
     if pv == "fp8":
@@ -224,7 +270,8 @@ def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv
     else:
         v_fp8, v_scale = v_tile_half(v, tensor_layout), None
     res = qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, tensor_layout=tensor_layout, out_dtype=dtype,
-                    is_causal=is_causal, q_offset=q_offset, kv_valid_len=kv_valid_len, return_lse=return_lse)
+                    qk_mult=qk_mult, is_causal=is_causal, q_offset=q_offset, kv_valid_len=kv_valid_len,
+                    return_lse=return_lse, qk_quant_gran=qk_quant_gran)
     o, lse = res if return_lse else (res, None)
     o = o[..., :head_dim_og]
     if not return_lse:
@@ -282,7 +329,8 @@ def sageattn_qk_int8_pv_fp16_triton(q, k, v, tensor_layout: str = "HND", quantiz
 def sageattn(q, k, v, tensor_layout: str = "HND", is_causal: bool = False, sm_scale: Optional[float] = None,
              return_lse: bool = False, **kwargs: Any):
     """Architecture dispatch of the reference (sageattn2.py:415-548): gfx950 always takes the
-    INT8-QK / FP8-PV kernel."""
+    INT8-QK / FP8-PV kernel with per-warp scales, as the reference's sm89 branch does (:530-542)."""
+    kwargs.setdefault("qk_quant_gran", "per_warp")
     return sageattn_qk_int8_pv_fp8_cuda(q, k, v, tensor_layout=tensor_layout, is_causal=is_causal,
                                         sm_scale=sm_scale, pv_accum_dtype="fp32+fp32", return_lse=return_lse,
                                         **kwargs)
@@ -290,6 +338,8 @@ def sageattn(q, k, v, tensor_layout: str = "HND", is_causal: bool = False, sm_sc
 
 __all__ = [
     "per_block_int8",
+    "per_warp_int8",
+    "per_thread_int8",
     "quant_per_block_int8",
     "per_channel_fp8",
     "k_mean",

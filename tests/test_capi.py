@@ -72,3 +72,22 @@ def test_validation_errors_are_status_codes(lib):
     rc = lib.qattn_fwd(s, buf, s, buf, buf, 128, buf, s, 0, 1, 128, 128, 2, 2, 128, 1.0, 0, 0, None, None, 2, None,
                        0, None)
     assert rc == 7
+
+
+def test_fwd_ex_granularity_validation_and_splits(lib):
+    s = _seq(16, 128 * 128, 128, 128)
+    buf = ctypes.c_void_p(16)
+
+    def call(v_kind, gran, ns=1):
+        return lib.qattn_fwd_ex(s, buf, s, buf, buf, v_kind, 128, buf, s, 0, 1, 128, 128, 2, 2, 128, 1.0, gran, 0, 0,
+                                None, None, ns, None, 0, None)
+
+    assert call(0, 4) == 9 and b"qk_quant_gran" in lib.qattn_last_error()
+    assert call(3, 1) == 1
+    assert call(1, 3, ns=2) == 7  # a split launch still needs its workspace
+    # per-thread K scales take 4x the LDS staging per tile: long keys need more splits
+    lk = 2000 * 64
+    assert lib.qattn_fwd_ex_num_splits(1, 32760, lk, 12, 0, 3) >= lib.qattn_fwd_ex_num_splits(1, 32760, lk, 12, 0, 1)
+    assert lib.qattn_fwd_ex_num_splits(1, 75600, 75600, 40, 0, 3) == 1  # C3 fits one split with FP8 V
+    assert lib.qattn_fwd_ex_num_splits(1, 75600, 75600, 40, 1, 3) > 1   # half V leaves less LDS for scales
+    assert lib.qattn_fwd_ex_num_splits(1, 4680, 32760, 12, 0, 1) == lib.qattn_fwd_num_splits(1, 4680, 32760, 12)

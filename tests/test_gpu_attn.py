@@ -18,8 +18,11 @@ COS_E2E = 0.999
 KERNEL_LAZY_TAU = 1.0  # lazy running-max threshold of qattn_fwd_kernel (kLazyTau in attn.hip)
 
 
+GRAN_CODE = {"per_block": 1, "per_warp": 2, "per_thread": 3}
+
+
 def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None, num_splits=0, q_offset=0,
-                   check_truth=True, pv="fp8"):
+                   check_truth=True, pv="fp8", gran="per_block"):
     dev = require_gpu()
     from telefuser_amd import _lib
     from telefuser_amd import sageattn2 as sa
@@ -27,25 +30,33 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
     B, Lq, Hq, D = q.shape
     Lk, Hkv = k.shape[1], k.shape[2]
     log(f"attn B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} layout={layout} causal={causal} kv_valid={kv_valid} "
-        f"splits={num_splits}")
+        f"splits={num_splits} gran={gran} pv={pv}")
     qd, kd, vd = (t.to(dev) for t in (q, k, v))
     if layout == "HND":
         qd, kd, vd = (t.transpose(1, 2).contiguous() for t in (qd, kd, vd))
     km = sa.k_mean(kd, layout)
-    q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=D ** -0.5, tensor_layout=layout)
+    qk_mult = 1.0
+    if gran == "per_block":
+        q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=D ** -0.5, tensor_layout=layout)
+    else:
+        quant = sa.per_thread_int8 if gran == "per_thread" else sa.per_warp_int8
+        q8, qs, k8, ks = quant(qd, kd, km, tensor_layout=layout)
+        qk_mult = D ** -0.5 * sa.LOG2E
     if pv == "fp8":
         v8, vs, _ = sa.per_channel_fp8(vd, tensor_layout=layout)
     else:
         v8, vs = sa.v_tile_half(vd, tensor_layout=layout), None
     o, lse = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout=layout, out_dtype=q.dtype, is_causal=causal,
-                          q_offset=q_offset, kv_valid_len=kv_valid, num_splits=num_splits, return_lse=True)
+                          q_offset=q_offset, kv_valid_len=kv_valid, num_splits=num_splits, return_lse=True,
+                          qk_mult=qk_mult, qk_quant_gran=gran)
     torch.cuda.synchronize()
     if layout == "HND":
         o, q8, k8 = o.transpose(1, 2), q8.transpose(1, 2), k8.transpose(1, 2)
     og = o.float().cpu().numpy()
     L = _lib.load()
     nkb = (Lk + 63) // 64
-    ns = num_splits if num_splits > 0 else L.qattn_fwd_num_splits(B, Lq, Lk, Hq)
+    v_kind = 0 if pv == "fp8" else (2 if q.dtype == torch.float16 else 1)
+    ns = num_splits if num_splits > 0 else L.qattn_fwd_ex_num_splits(B, Lq, Lk, Hq, v_kind, GRAN_CODE[gran])
     ns = min(ns, nkb)
     tps = (nkb + ns - 1) // ns if ns > 1 else 0  # the GPU's KV-split schedule, restated on the CPU
     f16 = q.dtype == torch.float16
@@ -55,7 +66,8 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
     ref, ref_lse = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
                                     ks.cpu().numpy(), **vargs, causal=causal, q_offset=q_offset,
                                     kv_valid=kv_valid, want_lse=True, tiles_per_split=tps,
-                                    lazy_tau=KERNEL_LAZY_TAU)
+                                    lazy_tau=KERNEL_LAZY_TAU, qk_mult=qk_mult, q_gran=GRAN_CODE[gran],
+                                    k_gran=GRAN_CODE[gran])
     c = cosine(og, ref)
     err = float(np.abs(og - ref).max())
     lerr = float(np.nanmax(np.abs(lse.cpu().numpy() - ref_lse)))
@@ -63,7 +75,8 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
     assert c >= COS_KERNEL
     # the reference's own schedule (no split, eager running max) on the same quantized operands
     ref0 = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
-                            ks.cpu().numpy(), **vargs, causal=causal, q_offset=q_offset, kv_valid=kv_valid)
+                            ks.cpu().numpy(), **vargs, causal=causal, q_offset=q_offset, kv_valid=kv_valid,
+                            qk_mult=qk_mult, q_gran=GRAN_CODE[gran], k_gran=GRAN_CODE[gran])
     c0 = cosine(og, ref0)
     log(f"  vs reference-schedule quantized math: cosine={c0:.6f} max_abs={float(np.abs(og - ref0).max()):.4g}")
     assert c0 >= COS_E2E
@@ -214,3 +227,28 @@ def test_attention_front_door_on_gpu(oracle):
         ob = A.attention(*(t.to(dev).transpose(1, 2) for t in (q, k, v)), attn_impl=impl, input_layout="BNSD",
                          output_layout="BNSD")
         assert torch.equal(ob.transpose(1, 2).cpu(), o.cpu())
+
+
+@pytest.mark.parametrize("gran", ["per_thread", "per_warp"])
+@pytest.mark.parametrize("case", ["ragged", "gqa_hnd", "causal_offset", "padding", "split", "pv_bf16"])
+def test_quant_granularities(oracle, gran, case):
+    """The reference's default path: per-thread (Triton) or per-warp (CUDA) Q/K scales, sm_scale applied by
+    the kernel (sageattn2.py:1356-1365), against the oracle on the same quantized operands and fp64 truth."""
+    if case == "ragged":
+        q, k, v = qkv(1, 333, 517, 2, 2, seed=31, k_offset_std=0.5)
+        _run_and_check(oracle, q, k, v, gran=gran)
+    elif case == "gqa_hnd":
+        q, k, v = qkv(2, 260, 300, 4, 2, seed=32, k_offset_std=1.0)
+        _run_and_check(oracle, q, k, v, gran=gran, layout="HND")
+    elif case == "causal_offset":
+        q, k, v = qkv(1, 200, 900, 2, 2, seed=33)
+        _run_and_check(oracle, q, k, v, gran=gran, causal=True, q_offset=700)
+    elif case == "padding":
+        q, k, v = qkv(2, 300, 512, 2, 2, seed=34)
+        _run_and_check(oracle, q, k, v, gran=gran, kv_valid=[400, 77])
+    elif case == "split":
+        q, k, v = qkv(1, 256, 3000, 2, 2, seed=35, k_offset_std=0.5)
+        _run_and_check(oracle, q, k, v, gran=gran, num_splits=3)
+    else:
+        q, k, v = qkv(1, 300, 400, 2, 2, seed=36, k_offset_std=0.5)
+        _run_and_check(oracle, q, k, v, gran=gran, pv="half")

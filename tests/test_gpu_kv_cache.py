@@ -6,8 +6,8 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import log, require_gpu, untile_v
-from inputs import bf16_bits, cosine
+from tests.gpu_util import log, require_gpu, untile_v
+from tests.inputs import bf16_bits, cosine
 
 pytestmark = pytest.mark.gpu
 

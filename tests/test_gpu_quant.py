@@ -49,6 +49,49 @@ def test_qk_quant_bit_exact(oracle, B, Lq, Lk, Hq, Hkv, layout, dtype, variant):
     assert np.array_equal(k8.cpu().numpy(), ok8)
 
 
+@pytest.mark.parametrize("B,Lq,Lk,Hq,Hkv,layout,dtype", [
+    (1, 1024, 1024, 2, 2, "NHD", torch.bfloat16),
+    (2, 1000, 777, 4, 2, "NHD", torch.bfloat16),   # ragged: empty trailing warp blocks, partial key blocks
+    (1, 300, 130, 3, 3, "HND", torch.bfloat16),
+    (1, 517, 333, 2, 1, "NHD", torch.float16),
+])
+def test_per_thread_and_per_warp_quant_bit_exact(oracle, B, Lq, Lk, Hq, Hkv, layout, dtype):
+    """The reference's default quantizers: Triton per_thread_int8 and CUDA per_warp_int8."""
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    log(f"per_thread/per_warp quant B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} {layout} {dtype}")
+    q, k, _ = qkv(B, Lq, Lk, Hq, Hkv, seed=102, k_offset_std=0.5, dtype=dtype)
+    if layout == "HND":
+        q, k = q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
+    qd, kd = q.to(dev), k.to(dev)
+    km = sa.k_mean(kd, layout)
+    f16 = dtype == torch.float16
+    kmb = _as_bits(km)
+    # per thread
+    q8, qs, k8, ks = sa.per_thread_int8(qd, kd, km, tensor_layout=layout)
+    torch.cuda.synchronize()
+    oq8, oqs = oracle.quant_per_thread_int8(_as_bits(q), layout=layout, is_fp16=f16)
+    ok8, oks = oracle.quant_per_thread_int8(_as_bits(k), km_bits=kmb, is_key=True, layout=layout, is_fp16=f16)
+    assert np.array_equal(qs.cpu().numpy(), oqs)
+    assert np.array_equal(ks.cpu().numpy(), oks)
+    assert np.array_equal(q8.cpu().numpy(), oq8)
+    assert np.array_equal(k8.cpu().numpy(), ok8)
+    # per warp: QuantInt8Kernel over 32-row blocks (no sm_scale), padded to 4 per 128-row block
+    q8, qs, k8, ks = sa.per_warp_int8(qd, kd, km, tensor_layout=layout)
+    torch.cuda.synchronize()
+    oq8, oqs = oracle.quant_per_block_int8(_as_bits(q), blk=32, layout=layout, is_fp16=f16)
+    ok8, oks = oracle.quant_per_block_int8(_as_bits(k), km_bits=kmb, blk=64, layout=layout, is_fp16=f16)
+    n32 = oqs.shape[-1]
+    qs = qs.cpu().numpy()
+    assert qs.shape[-1] == (Lq + 127) // 128 * 4
+    assert np.array_equal(qs[..., :n32], oqs)
+    assert (qs[..., n32:] == np.float32(np.float32(1e-7) / np.float32(127.0))).all()
+    assert np.array_equal(ks.cpu().numpy(), oks)
+    assert np.array_equal(q8.cpu().numpy(), oq8)
+    assert np.array_equal(k8.cpu().numpy(), ok8)
+
+
 def test_quant_known_answers_on_gpu(oracle):
     """Closed-form cases (ties, all-zero block, tail rows) through the single-tensor entry."""
     dev = require_gpu()

@@ -416,3 +416,118 @@ def test_rounded_row_sum_mode(oracle):
     assert np.abs(o[0, :, 0] - exact_v[None]).max() < 1e-5
     o_ref = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs)
     assert np.abs(o_ref[0, :, 0] - exact_v[None]).max() > 1e-4  # the reference's normaliser differs
+
+
+# ------------------------------------------------------------------------------------------------
+# per-thread quantizer (triton/quant_per_thread.py) and scale granularities of the attention oracle
+# ------------------------------------------------------------------------------------------------
+
+def test_per_thread_query_classes_closed_form(oracle):
+    """Row r holds the constant r + 1: the scale of (warp block n, class c) is the largest row of the
+    class, (32 n + 24 + c + 1) / 127 + 1e-7; trailing warp blocks of the 128-row padding get 1e-7."""
+    L = 70
+    x = np.repeat(np.arange(1, L + 1, dtype=np.float32)[:, None], 128, axis=1)
+    bits = _bits(x.ravel().tolist(), (1, L, 1, 128))
+    q8, qs = oracle.quant_per_thread_int8(bits)
+    assert qs.shape == (1, 1, 32)
+    for n in range(4):
+        for c in range(8):
+            rows = [32 * n + 8 * j + c for j in range(4) if 32 * n + 8 * j + c < L]
+            amax = np.float32(max(rows) + 1) if rows else np.float32(0)
+            want = np.float32(np.float32(amax / np.float32(127.0)) + np.float32(1e-7))
+            assert qs[0, 0, n * 8 + c] == want, (n, c)
+    # the largest row of every class quantizes to 127 (x / scale just below 127, rounds half away)
+    for c in range(8):
+        top = max(r for r in range(L) if r % 8 == c)  # the largest row of its class and warp block
+        assert q8[0, top, 0, 0] == 127
+
+
+def test_per_thread_key_classes_closed_form(oracle):
+    """Key class c of a 64-row block holds rows 8j + 2c and 8j + 2c + 1 (mma lane pairs)."""
+    L = 64
+    x = np.repeat(np.arange(1, L + 1, dtype=np.float32)[:, None], 128, axis=1)
+    k8, ks = oracle.quant_per_thread_int8(_bits(x.ravel().tolist(), (1, L, 1, 128)), is_key=True)
+    assert ks.shape == (1, 1, 4)
+    for c in range(4):
+        want = np.float32(np.float32(np.float32(56 + 2 * c + 2) / np.float32(127.0)) + np.float32(1e-7))
+        assert ks[0, 0, c] == want
+    assert (k8[0, 56 + 2 * np.arange(4) + 1, 0, :] == 127).all()
+
+
+def test_per_thread_zero_rows_and_half_away(oracle):
+    x = np.zeros((1, 32, 1, 128), np.float32)
+    x[0, 1, 0, :3] = [2.0, -2.0, 1.0]  # class 1: amax 2 -> scale 2/127 + 1e-7
+    q8, qs = oracle.quant_per_thread_int8(bf16_bits(torch.from_numpy(x)))
+    assert qs[0, 0, 0] == np.float32(1e-7) and (q8[0, 0] == 0).all()
+    sc = np.float32(np.float32(2.0 / np.float32(127.0)) + np.float32(1e-7))
+    t = np.float32(1.0) / sc  # 63.4999968...: half-away keeps 63
+    assert q8[0, 1, 0, 0] == 127 and q8[0, 1, 0, 1] == -127 and q8[0, 1, 0, 2] == int(np.trunc(t + 0.5))
+
+
+@pytest.mark.parametrize("L,is_key", [(300, False), (300, True), (1000, True), (129, False)])
+def test_per_thread_random_matches_numpy_restatement(oracle, L, is_key):
+    """Vectorised float32 numpy version with the class mapping built by reshapes (not index formulas)."""
+    g = torch.Generator().manual_seed(L)
+    x = (torch.randn((2, L, 3, 128), generator=g) * 2).to(torch.bfloat16)
+    km = (torch.randn((2, 1, 3, 128), generator=g)).to(torch.bfloat16) if is_key else None
+    xd = (x - km) if is_key else x  # torch bf16 op, as the reference wrapper does
+    q8, sc = oracle.quant_per_thread_int8(bf16_bits(x), None if km is None else bf16_bits(km[:, 0]), is_key=is_key)
+    xf = xd.float().numpy()
+    blk = 64 if is_key else 32
+    nb = -(-L // 64) if is_key else -(-L // 128) * 4
+    pad = np.zeros((2, nb * blk, 3, 128), np.float32)
+    pad[:, :L] = xf
+    if is_key:  # [b, n, j(8), cls(4), pair(2), h, d]
+        v = pad.reshape(2, nb, 8, 4, 2, 3, 128)
+        amax = np.abs(v).max(axis=(2, 4, 6))                 # [b, n, cls, h]
+    else:       # [b, n, j(4), cls(8), h, d]
+        v = pad.reshape(2, nb, 4, 8, 3, 128)
+        amax = np.abs(v).max(axis=(2, 5))
+    scale = (amax / np.float32(127.0) + np.float32(1e-7)).astype(np.float32)
+    want_sc = scale.transpose(0, 3, 1, 2).reshape(2, 3, -1)
+    assert np.array_equal(sc, want_sc)
+    if is_key:
+        sfull = np.broadcast_to(scale[:, :, None, :, None, :, None], v.shape).reshape(2, nb * blk, 3, 128)
+    else:
+        sfull = np.broadcast_to(scale[:, :, None, :, :, None], v.shape).reshape(2, nb * blk, 3, 128)
+    t = (pad / sfull).astype(np.float32)
+    want = np.trunc(t + np.where(t >= 0, 0.5, -0.5).astype(np.float32)).astype(np.int8)[:, :L]
+    assert np.array_equal(q8, want)
+
+
+def test_attention_oracle_granularity_indexing(oracle):
+    """Per-warp / per-thread scales fed as expanded per-block-equivalent data give the same O: a tensor
+    whose scales are constant inside every 128-query / 64-key block must not depend on the granularity."""
+    q, k, v = qkv(1, 200, 300, 2, 1, seed=11)
+    qb, kb, vb = bf16_bits(q), bf16_bits(k), bf16_bits(v)
+    q8, qs = oracle.quant_per_block_int8(qb, sm_scale=128 ** -0.5 * LOG2E, blk=128)
+    k8, ks = oracle.quant_per_block_int8(kb, blk=64)
+    v8, vs = oracle.per_channel_fp8(vb)
+    base = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs)
+    qs_w = np.repeat(qs, 4, axis=-1)           # 4 warps per 128-row block
+    qs_t = np.repeat(qs_w, 8, axis=-1)         # 8 lane classes per warp
+    ks_t = np.repeat(ks, 4, axis=-1)           # 4 lane-pair classes per key block
+    for qg, qsg in ((2, qs_w), (3, qs_t)):
+        for kg, ksg in ((1, ks), (3, ks_t)):
+            o = oracle.qattn_fwd(q8, qsg, k8, ksg, v8, vs, q_gran=qg, k_gran=kg)
+            assert np.array_equal(o, base), (qg, kg)
+    # and a scale change in one class touches exactly the rows / keys of that class
+    qs_t2 = qs_t.copy()
+    qs_t2[0, 0, 3] *= 2.0  # warp block 0, class 3: rows 3, 11, 19, 27 of head 0
+    o2 = oracle.qattn_fwd(q8, qs_t2, k8, ks, v8, vs, q_gran=3, k_gran=1)
+    changed = np.nonzero(np.abs(o2 - base).max(axis=-1) > 0)
+    assert sorted(set(zip(changed[1].tolist(), changed[2].tolist()))) == [(3, 0), (11, 0), (19, 0), (27, 0)]
+    ks_t2 = ks_t.copy()
+    ks_t2[0, 0, 4 + 2] *= 0.25  # key block 1, class 2: keys 64 + 8j + 4, 64 + 8j + 5 only
+    o3 = oracle.qattn_fwd(q8, qs, k8, ks_t2, v8, vs, q_gran=1, k_gran=3)
+    sel = [64 + 8 * j + 4 + e for j in range(8) for e in range(2)]
+    # against a direct float64 softmax over the dequantized logits with that class rescaled
+    qf = q8[0, :, 0].astype(np.float64) * np.repeat(qs[0, 0], 128)[:200, None]
+    kscale = np.repeat(ks[0, 0], 64)[:300].astype(np.float64)
+    kscale[sel] *= 0.25
+    kf = k8[0, :, 0].astype(np.float64) * kscale[:, None]
+    s = qf @ kf.T
+    p = np.exp2(s - s.max(axis=1, keepdims=True))
+    vf = oracle.e4m3_to_f32(v8[0, 0, :, :300]).T.astype(np.float64) * vs[0, 0][None, :]
+    ref = (p @ vf) / p.sum(axis=1, keepdims=True)
+    assert cosine(o3[0, :, 0], ref) > 0.9995
