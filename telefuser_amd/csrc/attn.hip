@@ -88,20 +88,36 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t n) {
 __device__ __forceinline__ int k_lds_off(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
 __device__ __forceinline__ int v_lds_off(int d, int c) { return d * 64 + ((c ^ ((d >> 2) & 3)) << 4); }
 
-// One 16-byte-per-lane global -> LDS DMA (global_load_lds_dwordx4): lane j's 16 bytes land at
-// lds_base + 16 j.  Issued through inline asm so the compiler does not treat every later LDS read
-// as a possible alias of the in-flight DMA (it would otherwise put an s_waitcnt vmcnt(0) in front of
-// them and serialise the prefetch); completion is tracked with explicit vmcnt waits instead.
-__device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
-  const uint32_t lds =
-      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)lds_base);
+// Buffer resource (V#) for raw, unswizzled byte addressing of [base, base + bytes): loads whose offset
+// is at or past `bytes` return zeros instead of touching memory.
+__device__ __forceinline__ v4u make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  v4u r;
+  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);
+  r[2] = __builtin_amdgcn_readfirstlane(bytes);
+  r[3] = 0x00020000u;  // raw buffer, 32-bit data format
+  return r;
+}
+
+// One 16-byte-per-lane buffer -> LDS DMA (buffer_load_dwordx4 ... lds): lane j's 16 bytes, read at
+// base + soff + voff_j, land at LDS address lds + 16 j.  The per-lane offsets are loop-invariant
+// VGPRs and the tile advance is a scalar offset, so issuing a tile costs no VALU work.  Issued through
+// inline asm so the compiler does not treat every later LDS read as a possible alias of the in-flight
+// DMA (it would otherwise put an s_waitcnt vmcnt(0) in front of them and serialise the prefetch);
+// completion is tracked with explicit vmcnt waits instead.
+__device__ __forceinline__ void lds_dma16(uint32_t voff, v4u rsrc, uint32_t soff, uint32_t lds) {
   asm volatile(
-      "s_mov_b32 m0, %1\n\t"
+      "s_mov_b32 m0, %3\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, off"
+      "buffer_load_dwordx4 %0, %1, %2 offen lds"
       :
-      : "v"(src), "s"(lds)
+      : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds)
       : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
 }
 
 // P.V flavours: e4m3 P x e4m3 V (the reference's fp8 kernel, with the 8.807 offset and v_scale), or
@@ -164,22 +180,23 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   const float qs = p.q_scale[(b * p.Hq + h) * p.nQS + qsi] * p.qk_mult;
   const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
 
-  // global -> LDS copies go through the LDS-DMA path (global_load_lds_dwordx4): lane j of a wave
+  // global -> LDS copies go through the LDS-DMA path (buffer_load_dwordx4 ... lds): lane j of a wave
   // writes the 16 bytes at LDS slot (wave base + 16 j), so the XOR swizzle is applied on the global
   // side: the lane that owns LDS slot (row, chunk c') fetches global chunk c = c' ^ swizzle(row).
-  // Each wave moves 2 x 1 KiB of K and 2 x 1 KiB of V per tile; no VGPRs are spent on staging.
+  // Each wave moves 2 x 1 KiB of K and kVDma x 1 KiB of V per tile; no VGPRs are spent on staging.
+  // K rows at or past Lk fall outside the K buffer range and arrive as zeros (masked anyway).
   const int8_t* kbase = p.k8 + b * p.ksb + hk * p.ksh;
   const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad * kVBytes;
-  // per-lane DMA source offsets relative to the tile start (first K row / first V column)
-  int64_t koff[2];
-  int voff[kVDma];
-  int kr[2];
+  const v4u krsrc = make_rsrc(kbase, (uint32_t)((p.Lk - 1) * p.ksl + kD));
+  const v4u vrsrc = make_rsrc(vbase, (uint32_t)((int64_t)kD * p.Lpad * kVBytes));
+  // per-lane byte offsets relative to the tile start (first K row / first V column)
+  uint32_t koff[2], voff[kVDma];
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     const int slot = (i * 4 + w) * 64 + lane;
-    kr[i] = slot >> 3;
-    const int kc = (slot & 7) ^ ((kr[i] >> 1) & 7);
-    koff[i] = kr[i] * p.ksl + kc * 16;
+    const int kr = slot >> 3;
+    const int kc = (slot & 7) ^ ((kr >> 1) & 7);
+    koff[i] = (uint32_t)(kr * p.ksl + kc * 16);
   }
 #pragma unroll
   for (int i = 0; i < kVDma; i++) {
@@ -187,27 +204,23 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
     if constexpr (PV == PV_FP8) {  // 128 rows x 4 chunks, v_lds_off swizzle
       const int vd = slot >> 2;
       const int vc = (slot & 3) ^ ((vd >> 2) & 3);
-      voff[i] = (int)(vd * p.Lpad + vc * 16);
+      voff[i] = (uint32_t)(vd * p.Lpad + vc * 16);
     } else {  // 128 rows x 8 chunks of 16 bytes (8 halves), k_lds_off swizzle
       const int vd = slot >> 3;
       const int vc = (slot & 7) ^ ((vd >> 1) & 7);
-      voff[i] = (int)(vd * p.Lpad * 2 + vc * 16);
+      voff[i] = (uint32_t)(vd * p.Lpad * 2 + vc * 16);
     }
   }
-  const int64_t k_step = (int64_t)kBK * p.ksl;
+  const uint32_t k_step = (uint32_t)(kBK * p.ksl);
+  const uint32_t lds_k0 = lds_addr(&lds_k[0][0]) + __builtin_amdgcn_readfirstlane(w) * 1024;
+  const uint32_t lds_v0 = lds_addr(&lds_v[0][0]) + __builtin_amdgcn_readfirstlane(w) * 1024;
   auto dma_tile = [&](int64_t t, int buf) {
-    const int8_t* kt = kbase + t * k_step;
-    const uint8_t* vt = vbase + t * kBK * kVBytes;
-    const bool clamp = t * kBK + kBK > p.Lk;
+    const uint32_t kso = (uint32_t)t * k_step, vso = (uint32_t)t * (kBK * kVBytes);
+    const uint32_t kl = lds_k0 + buf * (kBK * kD), vl = lds_v0 + buf * (kD * kBK * kVBytes);
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      // rows past Lk (last tile only) are clamped onto the last key; they are masked out anyway
-      const int8_t* src = kt + koff[i];
-      if (clamp) src = kbase + min(t * kBK + kr[i], p.Lk - 1) * p.ksl + (koff[i] - kr[i] * p.ksl);
-      lds_dma16(src, &lds_k[buf][(i * 4 + w) * 1024]);
-    }
+    for (int i = 0; i < 2; i++) lds_dma16(koff[i], krsrc, kso, kl + i * 4096);
 #pragma unroll
-    for (int i = 0; i < kVDma; i++) lds_dma16(vt + voff[i], &lds_v[buf][(i * 4 + w) * 1024]);
+    for (int i = 0; i < kVDma; i++) lds_dma16(voff[i], vrsrc, vso, vl + i * 4096);
   };
 
   v16f o[4];
@@ -563,6 +576,9 @@ static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale,
                 "output strides must be multiples of 16 bytes");
   QATTN_REQUIRE(v && aligned16(v) && q_scale && k_scale, QATTN_ERR_ARG, "null scale or V pointer");
   QATTN_REQUIRE(!causal || q_offset >= 0, QATTN_ERR_ARG, "q_offset must be >= 0");
+  // the kernel addresses one (batch, kv head) of K and V through 32-bit buffer offsets
+  QATTN_REQUIRE((Lk - 1) * k8.sl + D < (1ll << 32) && D * Lpad * 2 < (1ll << 32), QATTN_ERR_SHAPE,
+                "K/V of one (batch, head) must span less than 4 GiB");
 
   p = AttnParams{};
   p.q8 = static_cast<const int8_t*>(q8.data);
