@@ -48,6 +48,11 @@ constexpr int kThreads = 256;
 constexpr float kFp8Offset = 8.807f;  // attn_utils.cuh:35 S_FP8_OFFSET
 constexpr float kMInit = -3.0e38f;
 constexpr float kLazyTau = 1.0f;  // lazy-rescale threshold (log2 units), see the softmax below
+// The QK accumulators start at kAccBiasBits instead of 0: the int32 result bias + s, read as fp32,
+// is exactly kAccBias + s for |s| < 2^22 (here |s| <= 2^21), so the logits reach the softmax as floats
+// without an int -> float conversion per element; the bias is folded into the exp2 offset.
+constexpr int kAccBiasBits = 0x4B400000;
+constexpr float kAccBias = 12582912.0f;
 
 struct AttnParams {
   const int8_t* q8;
@@ -229,6 +234,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
 #pragma unroll
     for (int r = 0; r < 16; r++) o[i][r] = 0.f;
   float m_run = kMInit, l_run = 0.f;
+  v16i kbias;
+#pragma unroll
+  for (int r = 0; r < 16; r++) kbias[r] = kAccBiasBits;
 
   // K/V tiles run kPrefetch tiles ahead of the compute through kNBuf = kPrefetch + 1 LDS buffers:
   // iteration t issues tile t + kPrefetch into buffer (t + kPrefetch) % kNBuf, which was last read in
@@ -269,7 +277,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
 #pragma unroll
       for (int j = 0; j < 8; j++) {
         const int m = j >> 1, kb = j & 1;
-        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j], qf[m], m == 0 ? v16i{} : s[kb], 0, 0, 0);
+        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j], qf[m], m == 0 ? kbias : s[kb], 0, 0, 0);
       }
       __builtin_amdgcn_s_setprio(0);
     }
@@ -305,7 +313,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
       // <= 2^8.807 = 448 (the e4m3 maximum), so the FP8 range is honoured while the O rescale (64
       // multiplies per lane) is skipped on almost every tile.  A row whose keys in this tile are all
       // masked never moves m.
-      m_tile = mx == INT32_MIN ? kMInit : fmaf((float)mx, cs_a, -(kOffset - kLazyTau));
+      m_tile = mx == INT32_MIN ? kMInit : fmaf(__int_as_float(mx), cs_a, -fmaf(kAccBias, cs_a, kOffset - kLazyTau));
     } else {  // two scale classes per lane: max per class, scaled, then across the lane pair
       int ma = INT32_MIN, mb = INT32_MIN;
 #pragma unroll
@@ -315,8 +323,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
           if ((r & 3) < 2) ma = max(ma, s[kb][r]);
           else mb = max(mb, s[kb][r]);
         }
-      const float fa = ma == INT32_MIN ? kMInit : fmaf((float)ma, cs_a, -(kOffset - kLazyTau));
-      const float fb = mb == INT32_MIN ? kMInit : fmaf((float)mb, cs_b, -(kOffset - kLazyTau));
+      const float fa = ma == INT32_MIN ? kMInit : fmaf(__int_as_float(ma), cs_a, -fmaf(kAccBias, cs_a, kOffset - kLazyTau));
+      const float fb = mb == INT32_MIN ? kMInit : fmaf(__int_as_float(mb), cs_b, -fmaf(kAccBias, cs_b, kOffset - kLazyTau));
       float mt = fmaxf(fa, fb);
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
       m_tile = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
@@ -332,7 +340,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
         for (int r = 0; r < 16; r++) o[i][r] *= alpha;
       m_run = m_new;
     }
-    const float neg_m = -m_run;
+    const float nc_a = -fmaf(kAccBias, cs_a, m_run), nc_b = -fmaf(kAccBias, cs_b, m_run);
     // p = exp2(s * cs - m); masked logits (INT32_MIN) become p = 0 exactly (the sentinel times a tiny
     // block scale is not necessarily very negative)
     auto p4 = [&](int j, float (&pv)[4], auto mk) {
@@ -340,7 +348,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int sv = s[kb][r0 + e];
-        pv[e] = __builtin_amdgcn_exp2f(fmaf((float)sv, e < 2 ? cs_a : cs_b, neg_m));
+        pv[e] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(sv), e < 2 ? cs_a : cs_b, e < 2 ? nc_a : nc_b));
         if constexpr (decltype(mk)::value) pv[e] = sv == INT32_MIN ? 0.f : pv[e];
       }
     };
@@ -353,7 +361,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
           float pv[4];
           p4(j, pv, mk);
           lsum += (pv[0] + pv[1]) + (pv[2] + pv[3]);
-          const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], 0, false);
+          // the low word is written first; the old contents of pf[j] only fill bits that the second
+          // conversion overwrites, so no zeroed register is needed
+          const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], pf[j], false);
           pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
         }
         l_run += lsum;
