@@ -167,13 +167,29 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   // d = 32*m + 16*hf .. +16 for m = 0..3
   const int64_t wrow0 = q_first + w * 32;
   const int64_t qrow = wrow0 + lq;
+  // Q fragments: the wave's 32 rows are read row-contiguously (8 lanes x 16 B per 128-byte row, full
+  // cache lines) into a wave-private LDS stage, then each lane picks its MFMA B-operand bytes
+  // d = 32 m + 16 hf .. +16 of row lq.  Stage rows are 128 B with the 16-byte chunk c stored at
+  // chunk c ^ (row & 7), so both the row writes and the fragment reads are bank-conflict free.
+  uint8_t* stage = &lds_k[0][0] + w * 4096;  // 32 rows x 128 B per wave (lds_k is free here)
   v4i qf[4];
   {
-    const int8_t* qp = p.q8 + b * p.qsb + qrow * p.qsl + h * p.qsh + hf * 16;
+    const int8_t* qbase = p.q8 + b * p.qsb + h * p.qsh;
 #pragma unroll
-    for (int m = 0; m < 4; m++) qf[m] = qrow < p.Lq ? *reinterpret_cast<const v4i*>(qp + m * 32) : v4i{0, 0, 0, 0};
+    for (int i = 0; i < 4; i++) {
+      const int r = i * 8 + (lane >> 3), c = lane & 7;
+      const int64_t row = wrow0 + r;
+      const v4i val = row < p.Lq ? *reinterpret_cast<const v4i*>(qbase + row * p.qsl + c * 16) : v4i{0, 0, 0, 0};
+      *reinterpret_cast<v4i*>(stage + r * 128 + ((c ^ (r & 7)) << 4)) = val;
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      const int c = 2 * m + hf;
+      qf[m] = *reinterpret_cast<const v4i*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4));
+    }
     // consume the loads here: otherwise the compiler's wait for them lands at their first use inside
-    // the key loop, where it becomes a full vmcnt(0) drain of the K/V prefetch on every iteration
+    // the key loop
 #pragma unroll
     for (int m = 0; m < 4; m++) asm volatile("" ::"v"(qf[m]));
   }
@@ -242,6 +258,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   // iteration t issues tile t + kPrefetch into buffer (t + kPrefetch) % kNBuf, which was last read in
   // iteration t - 1.  The k_scales of all tiles are staged in LDS once, so the only VMEM traffic in the
   // loop is the 4 DMA instructions per tile and the vmcnt accounting below is exact.
+  __syncthreads();  // every wave has its Q fragments out of the LDS stage before the DMA reuses it
   for (int64_t i = tid; i < (t_end - t_begin) * KS; i += kThreads) lds_ks[i] = ks_ptr[t_begin * KS + i];
 #pragma unroll
   for (int d = 0; d < kPrefetch; d++)
@@ -434,8 +451,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
     l_tot = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
   }
-  if (qrow >= p.Lq) return;
   if (SPLIT) {
+    if (qrow >= p.Lq) return;
     const int64_t row = (((int64_t)split * p.B + b) * p.Hq + h) * p.Lq + qrow;
     float* wo = p.ws_o + row * kD;
 #pragma unroll
@@ -454,21 +471,38 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   }
   const float inv_l = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   const float* vs = PV == PV_FP8 ? p.v_scale + (b * p.Hkv + hk) * kD : nullptr;
-  uint16_t* orow = static_cast<uint16_t*>(p.o) + b * p.osb + qrow * p.osl + h * p.osh;
+  // O goes out through the same wave-private LDS stage (the K/V buffers are idle after the loop's last
+  // barrier), 64 channels per pass, so that every row is stored as whole 128-byte lines
+  uint16_t* obase = static_cast<uint16_t*>(p.o) + b * p.osb + h * p.osh;
 #pragma unroll
-  for (int dblk = 0; dblk < 4; dblk++)
+  for (int pass = 0; pass < 2; pass++) {
 #pragma unroll
-    for (int g = 0; g < 4; g++) {
-      const int d = dblk * 32 + g * 8 + hf * 4;
-      const v4f sc = PV == PV_FP8 ? *reinterpret_cast<const v4f*>(vs + d) : v4f{1.f, 1.f, 1.f, 1.f};
-      uint16_t hv[4];
+    for (int db = 0; db < 2; db++) {
+      const int dblk = pass * 2 + db;
 #pragma unroll
-      for (int e = 0; e < 4; e++) hv[e] = f32_to_half<IS_FP16_OUT>(o[dblk][g * 4 + e] * inv_l * sc[e]);
-      v2u packed;
-      __builtin_memcpy(&packed, hv, 8);
-      *reinterpret_cast<v2u*>(orow + d) = packed;
+      for (int g = 0; g < 4; g++) {
+        const int d = dblk * 32 + g * 8 + hf * 4;
+        const v4f sc = PV == PV_FP8 ? *reinterpret_cast<const v4f*>(vs + d) : v4f{1.f, 1.f, 1.f, 1.f};
+        uint16_t hv[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) hv[e] = f32_to_half<IS_FP16_OUT>(o[dblk][g * 4 + e] * inv_l * sc[e]);
+        v2u packed;
+        __builtin_memcpy(&packed, hv, 8);
+        const int c = db * 4 + g;  // 16-byte chunk of the staged 128-byte row (8 channels)
+        *reinterpret_cast<v2u*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4) + hf * 8) = packed;
+      }
     }
-  if (p.lse && hf == 0)
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int r = i * 8 + (lane >> 3), c = lane & 7;
+      const v4u val = *reinterpret_cast<const v4u*>(stage + r * 128 + ((c ^ (r & 7)) << 4));
+      const int64_t row = wrow0 + r;
+      if (row < p.Lq) *reinterpret_cast<v4u*>(obase + row * p.osl + pass * 64 + c * 8) = val;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+  if (p.lse && hf == 0 && qrow < p.Lq)
     p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
 }
 
