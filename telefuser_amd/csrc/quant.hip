@@ -114,20 +114,27 @@ __global__ __launch_bounds__(kQuantThreads) void quant_per_block_kernel(QuantArg
       }
     }
   }
-  // max over the TPR lanes of a row, then over the row slots of each class through LDS
-#pragma unroll
-  for (int o = 1; o < TPR; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
   __shared__ float row_max[RPP];
-  if (tid % TPR == 0) row_max[tid / TPR] = amax;
-  __syncthreads();
   auto class_max = [&](int k) {
-    float a = VARIANT == QATTN_QUANT_CUDA ? 0.0000001f : 0.f;
+    float a = 0.f;
 #pragma unroll
     for (int r = 0; r < RPP; r++)
       if (((r & 7) >> J.cls_shift) == k) a = fmaxf(a, row_max[r]);
     return a;
   };
-  amax = class_max(cls);
+  if constexpr (VARIANT == QATTN_QUANT_TRITON_THREAD) {
+    // per-thread scale classes: max over the TPR lanes of a row, then over the rows of each class
+#pragma unroll
+    for (int o = 1; o < TPR; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    if (tid % TPR == 0) row_max[tid / TPR] = amax;
+    __syncthreads();
+    amax = class_max(cls);
+  } else {  // one scale per block: wave max, then across the 4 waves
+    amax = wave_max(amax);
+    if ((tid & 63) == 0) row_max[tid >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(row_max[0], row_max[1]), fmaxf(row_max[2], row_max[3]));
+  }
 
   // IEEE division (hipcc default: correctly rounded)
   auto scale_of = [](float a) {
@@ -135,7 +142,11 @@ __global__ __launch_bounds__(kQuantThreads) void quant_per_block_kernel(QuantArg
     else return a / 127.0f;
   };
   const float scale = scale_of(amax);
-  if (tid < J.ncls) J.scale[((b * J.H + h) * J.nblk + n) * J.ncls + tid] = scale_of(class_max(tid));
+  if constexpr (VARIANT == QATTN_QUANT_TRITON_THREAD) {
+    if (tid < J.ncls) J.scale[((b * J.H + h) * J.nblk + n) * J.ncls + tid] = scale_of(class_max(tid));
+  } else if (tid == 0) {
+    J.scale[(b * J.H + h) * J.nblk + n] = scale;
+  }
   const float inv = 127.0f / amax;
 
 #pragma unroll
