@@ -4,7 +4,8 @@ Mirrors the module TeleFuser's backend registry loads into ``backends.sageattent
 (telefuser/ops/attention/backends.py:87-99, called from attention_impl.py:245-283), i.e. the public
 functions of tf-kernel/tf_kernel/sageattn2.py: ``per_block_int8`` (:96-187), ``per_channel_fp8``
 (:320-407), ``sageattn_qk_int8_pv_fp8_cuda`` (:1197-1457), ``sageattn_qk_int8_pv_fp8_cuda_sm90``
-(:1460-1693), ``sageattn_qk_int8_pv_fp16_cuda`` (:930-1194) and ``sageattn`` (:415-548).
+(:1460-1693), ``sageattn_qk_int8_pv_fp16_cuda`` (:930-1194), ``sageattn_varlen`` (:772-927) and
+``sageattn`` (:415-548).
 
 Differences from the reference, all deliberate:
   * ``qk_quant_gran`` selects the reference's quantizer: "per_thread" (the default, Triton
@@ -326,6 +327,66 @@ def sageattn_qk_int8_pv_fp16_triton(q, k, v, tensor_layout: str = "HND", quantiz
                          return_lse, kv_valid_len, q_offset, pv="half", quant_variant=variant)
 
 
+def sageattn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                    cu_seqlens_k: torch.Tensor, max_seqlen_q: int, max_seqlen_k: int, is_causal: bool = False,
+                    sm_scale: Optional[float] = None, smooth_k: bool = True, **kwargs: Any) -> torch.Tensor:
+    """Packed variable-length attention (sageattn2.py:772-927): q [total_q, Hq, D], k/v [total_k, Hkv, D],
+    sequence b spanning rows cu_seqlens[b] .. cu_seqlens[b + 1].
+
+    Same math as the reference: K smoothed by the mean over all packed keys (a half-precision subtraction),
+    per-sequence Q/K blocks of 128/64 rows quantized with the Triton rounding
+    (quant_per_block_varlen.py:22-70), V in fp16 and P rounded to fp16 for P.V
+    (attn_qk_int8_block_varlen.py:42-65; P.V accumulates in fp32 here).  ``is_causal`` masks per
+    sequence, top-left aligned.  The sequence table is read on the host (one device-to-host copy), and
+    each sequence runs as its own launches on the packed tensors' row views.
+    """
+    dtype = q.dtype
+    if not q.is_cuda:
+        raise AssertionError("Input tensors must be on cuda.")
+    if dtype not in (torch.float16, torch.bfloat16):
+        raise AssertionError("Input tensors must be in dtype of torch.float16 or torch.bfloat16")
+    if not (q.device == k.device == v.device):
+        raise AssertionError("All tensors must be on the same device.")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise AssertionError("All tensors must have the same dtype.")
+    if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape:
+        raise ValueError("q must be [total_q, Hq, D] and k/v [total_k, Hkv, D]")
+    head_dim_og = q.size(-1)
+    q, k, v = _pad_head_dim(q), _pad_head_dim(k), _pad_head_dim(v)
+    if not (q.stride(-1) == 1 and k.stride(-1) == 1 and v.stride(-1) == 1):
+        raise AssertionError("Last dim of qkv must be contiguous.")
+    if not (cu_seqlens_q.is_contiguous() and cu_seqlens_k.is_contiguous()):
+        raise AssertionError("cu_seqlens_q and cu_seqlens_k must be contiguous.")
+    hq, hkv = q.shape[1], k.shape[1]
+    if hq % hkv != 0:
+        raise ValueError(f"num_qo_heads ({hq}) must be divisible by num_kv_heads ({hkv})")
+    cq = [int(x) for x in cu_seqlens_q.tolist()]
+    ck = [int(x) for x in cu_seqlens_k.tolist()]
+    if len(cq) != len(ck) or len(cq) < 2:
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must both have batch_size + 1 entries")
+    if cq[0] != 0 or ck[0] != 0 or cq[-1] > q.shape[0] or ck[-1] > k.shape[0] or \
+            any(a > b for a, b in zip(cq, cq[1:])) or any(a > b for a, b in zip(ck, ck[1:])):
+        raise ValueError("cu_seqlens must start at 0, be non-decreasing and stay inside the packed tensors")
+    if sm_scale is None:
+        sm_scale = head_dim_og ** -0.5
+    q4, k4 = q.unsqueeze(0), k.unsqueeze(0)  # [1, total, H, D] views
+    km = k_mean(k4, "NHD") if smooth_k else None  # mean over every packed key, as k.mean(dim=0)
+    v16 = v if v.dtype == torch.float16 else v.to(torch.float16)  # the reference runs P.V in fp16
+    out = torch.zeros((q.shape[0], hq, q.shape[2]), dtype=dtype, device=q.device)
+    for b in range(len(cq) - 1):
+        lq, lk = cq[b + 1] - cq[b], ck[b + 1] - ck[b]
+        if lq == 0 or lk == 0:
+            continue  # no queries, or no keys: the rows stay zero
+        qb = q4[:, cq[b]:cq[b + 1]]
+        kb = k4[:, ck[b]:ck[b + 1]]
+        q8, qsc = quant_per_block_int8(qb, BLKQ, sm_scale=sm_scale * LOG2E, tensor_layout="NHD", variant="triton")
+        k8, ksc = quant_per_block_int8(kb, BLKK, mean=km, tensor_layout="NHD", variant="triton")
+        vt = v_tile_half(v16[ck[b]:ck[b + 1]].unsqueeze(0), tensor_layout="NHD")
+        qattn_fwd(q8, qsc, k8, ksc, vt, None, tensor_layout="NHD", out_dtype=dtype, is_causal=is_causal,
+                  out=out[cq[b]:cq[b + 1]].unsqueeze(0))
+    return out[..., :head_dim_og]
+
+
 def sageattn(q, k, v, tensor_layout: str = "HND", is_causal: bool = False, sm_scale: Optional[float] = None,
              return_lse: bool = False, **kwargs: Any):
     """Architecture dispatch of the reference (sageattn2.py:415-548): gfx950 always takes the
@@ -337,6 +398,7 @@ def sageattn(q, k, v, tensor_layout: str = "HND", is_causal: bool = False, sm_sc
 
 
 __all__ = [
+    "sageattn_varlen",
     "per_block_int8",
     "per_warp_int8",
     "per_thread_int8",

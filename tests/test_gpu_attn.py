@@ -15,6 +15,7 @@ from tests.inputs import bf16_bits, cosine, qkv
 pytestmark = pytest.mark.gpu
 COS_KERNEL = 0.99995  # same quantized operands and schedule: only exp2 ulps / fp32 sums differ
 COS_E2E = 0.999
+LOG2E = 1.44269504
 KERNEL_LAZY_TAU = 1.0  # lazy running-max threshold of qattn_fwd_kernel (kLazyTau in attn.hip)
 
 
@@ -252,3 +253,51 @@ def test_quant_granularities(oracle, gran, case):
     else:
         q, k, v = qkv(1, 300, 400, 2, 2, seed=36, k_offset_std=0.5)
         _run_and_check(oracle, q, k, v, gran=gran, pv="half")
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_sageattn_varlen(oracle, causal):
+    """Packed variable-length batch (sageattn2.py:772-927): every sequence against the oracle (Triton
+    quantizer, fp16 P.V, the kernel's schedule) and float64 truth; empty sequences stay zero."""
+    dev = require_gpu()
+    from telefuser_amd import _lib
+    from telefuser_amd import sageattn2 as sa
+
+    lq = [100, 257, 0, 64] if not causal else [130, 257, 64]
+    lk = [130, 300, 50, 64] if not causal else [130, 257, 64]
+    H, D = 2, 128
+    cq, ck = np.concatenate([[0], np.cumsum(lq)]), np.concatenate([[0], np.cumsum(lk)])
+    g = torch.Generator().manual_seed(41 + causal)
+    q = torch.randn((int(cq[-1]), H, D), generator=g).to(torch.bfloat16)
+    k = (torch.randn((int(ck[-1]), H, D), generator=g) + 0.5).to(torch.bfloat16)
+    v = torch.randn((int(ck[-1]), H, D), generator=g).to(torch.bfloat16)
+    log(f"varlen causal={causal} lq={lq} lk={lk}")
+    o = sa.sageattn_varlen(q.to(dev), k.to(dev), v.to(dev), torch.tensor(cq, dtype=torch.int32, device=dev),
+                           torch.tensor(ck, dtype=torch.int32, device=dev), max(lq), max(lk), is_causal=causal)
+    torch.cuda.synchronize()
+    og = o.float().cpu().numpy()
+    km = sa.k_mean(k.to(dev).unsqueeze(0), "NHD").cpu()  # [1, H, D], the kernel's smoothing vector
+    L = _lib.load()
+    sm = D ** -0.5
+    for b in range(len(lq)):
+        rows = slice(int(cq[b]), int(cq[b + 1]))
+        if lq[b] == 0:
+            continue
+        if lk[b] == 0:
+            assert not og[rows].any()
+            continue
+        qb, kb, vb = q[rows].unsqueeze(0), k[int(ck[b]):int(ck[b + 1])].unsqueeze(0), v[int(ck[b]):int(ck[b + 1])].unsqueeze(0)
+        q8, qs = oracle.quant_per_block_int8(bf16_bits(qb), sm_scale=sm * LOG2E, blk=128, variant="triton")
+        k8, ks = oracle.quant_per_block_int8(bf16_bits(kb), km_bits=bf16_bits(km), blk=64, variant="triton")
+        vh = vb.to(torch.float16).contiguous().view(torch.int16).numpy().view(np.uint16)
+        nkb = (lk[b] + 63) // 64
+        ns = min(L.qattn_fwd_ex_num_splits(1, lq[b], lk[b], H, 2, 1), nkb)
+        tps = (nkb + ns - 1) // ns if ns > 1 else 0
+        ref = oracle.qattn_fwd(q8, qs, k8, ks, vh_bits=vh, pv_mode=1, is_fp16=True, causal=causal,
+                               tiles_per_split=tps, lazy_tau=KERNEL_LAZY_TAU)
+        truth = oracle.attn_fp64(bf16_bits(qb), bf16_bits(kb), bf16_bits(vb), sm, causal=causal)
+        got = og[rows][None]
+        c, ct = cosine(got, ref), cosine(got, truth)
+        log(f"  seq {b}: lq={lq[b]} lk={lk[b]} cos_oracle={c:.6f} cos_truth={ct:.6f}")
+        assert c >= COS_KERNEL
+        assert ct >= COS_E2E
