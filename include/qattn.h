@@ -218,6 +218,23 @@ int qattn_fwd_ex(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* 
                  const int32_t* kv_valid, float* lse, int num_splits, void* workspace, size_t workspace_bytes,
                  qattn_stream_t stream);
 
+/*
+ * Block-sparse quantized attention: like qattn_fwd_pv16, but a query block (128 rows) only visits the
+ * key tiles (64 keys) whose mask byte is non-zero - the k_block_id skip of the reference's
+ * sparse_int8_attn forward (telefuser/kernel/triton/sparse_int8_attn.py:22-280, called from
+ * sparse_sageattn, telefuser/ops/attention/sparse_sage.py:25-80).
+ *   tile_mask: int8, element (b, kv head hk, query block i, key tile j) at
+ *              tile_mask[(b * Hkv + hk) * mask_sbh + i * mask_sq + j]  (key tiles contiguous)
+ * A query row whose blocks are all masked gets a zero output.  The KV split count must come from
+ * qattn_fwd_block_sparse_num_splits (a workgroup holds the ids of at most 1024 active tiles).
+ */
+int qattn_fwd_block_sparse_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq);
+int qattn_fwd_block_sparse(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const uint16_t* v16,
+                           int v_dtype, int64_t Lpad, qattn_seq o, int out_dtype, int64_t B, int64_t Lq, int64_t Lk,
+                           int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int causal, const int8_t* tile_mask,
+                           int64_t mask_sbh, int64_t mask_sq, float* lse, int num_splits, void* workspace,
+                           size_t workspace_bytes, qattn_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -42,7 +42,7 @@ def lib():
         L.oq_per_channel_fp8.argtypes = [vp, i32, i64, i64, i64, i64, i64, i64, i64, f32, vp, i64, vp]
         L.oq_qattn_fwd.argtypes = [vp, i64, i64, i64, vp, i64, vp, i64, i64, i64, vp, i64, vp, i64, vp, vp, i32,
                                    i64, i64, i64, i64, i64, i64, i64, i64, i64, f64, i32, i32, i64, vp, i64, i64,
-                                   i64, i64, f64, i32, i32, i32, vp, vp]
+                                   i64, i64, f64, i32, i32, i32, vp, i64, i64, vp, vp]
         L.oq_quant_per_thread_int8.argtypes = [vp, i32, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, i32, vp,
                                                i64, i64, i64, vp]
         L.oq_attn_fp64.argtypes = [vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, f64, i32, i64, vp, vp]
@@ -137,12 +137,13 @@ def per_channel_fp8(v_bits, scale_max=448.0, layout="NHD", is_fp16=False, pad=64
 def qattn_fwd(q8, q_scale, k8, k_scale, v8=None, v_scale=None, vh_bits=None, *, blkq=128, blkk=64,
               qk_mult=1.0, pv_mode=0, causal=False, q_offset=0, kv_valid=None, is_fp16=False, heads=None,
               qrows_limit=0, want_lse=False, tiles_per_split=0, lazy_tau=-1.0, lsum_rounded=False, q_gran=1,
-              k_gran=1):
+              k_gran=1, tile_mask=None):
     """Quantized attention in the reference's tile order.  q8/k8 NHD int8; returns fp32 O NHD
     (and log2-domain LSE [B, Hq, Lq] when want_lse).  lazy_tau >= 0 / tiles_per_split > 0 restate the
     device kernel's lazy running-max rule / KV-split schedule and lsum_rounded its row sum over the
     rounded P (defaults: the reference's schedule).  q_gran / k_gran: scale granularity codes of the reference
-    (1 per block, 2 per warp, 3 per thread) - see oq_qattn_fwd."""
+    (1 per block, 2 per warp, 3 per thread) - see oq_qattn_fwd.  tile_mask: int8 [B, Hkv, ceil(Lq/128),
+    ceil(Lk/64)] block-sparse mask (0 = skip the key tile for that query block)."""
     q8 = np.ascontiguousarray(q8)
     k8 = np.ascontiguousarray(k8)
     B, Lq, Hq, D = q8.shape
@@ -160,13 +161,17 @@ def qattn_fwd(q8, q_scale, k8, k_scale, v8=None, v_scale=None, vh_bits=None, *, 
     else:
         vh_bits = _bits(vh_bits)
     kvv = None if kv_valid is None else np.ascontiguousarray(np.asarray(kv_valid, np.int32))
+    tm, tm_s1, tm_s2 = None, 0, 0
+    if tile_mask is not None:
+        tm = np.ascontiguousarray(tile_mask, dtype=np.int8)
+        tm_s1, tm_s2 = tm.shape[2] * tm.shape[3], tm.shape[3]
     h0, h1 = (0, Hq) if heads is None else heads
     lib().oq_qattn_fwd(_p(q8), Lq * Hq * D, Hq * D, D, _p(q_scale), blkq, _p(k8), Lk * Hkv * D, Hkv * D, D,
                        _p(k_scale), blkk, _p(v8) if pv_mode == 0 else None, Lpad,
                        _p(v_scale) if pv_mode == 0 else None, _p(vh_bits), int(is_fp16), Lk * Hkv * D, Hkv * D, D,
                        B, Lq, Lk, Hq, Hkv, D, float(qk_mult), int(pv_mode), int(causal), int(q_offset), _p(kvv), h0,
                        h1, int(qrows_limit), int(tiles_per_split), float(lazy_tau), int(lsum_rounded), int(q_gran),
-                       int(k_gran), _p(out),
+                       int(k_gran), _p(tm), tm_s1, tm_s2, _p(out),
                        _p(lse))
     return (out, lse) if want_lse else out
 

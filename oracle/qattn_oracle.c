@@ -376,7 +376,8 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
                   int64_t vsb, int64_t vsl, int64_t vsh, int64_t B, int64_t Lq, int64_t Lk, int64_t Hq,
                   int64_t Hkv, int64_t D, double qk_mult, int pv_mode, int causal, int64_t q_offset,
                   const int32_t* kv_valid, int64_t h_begin, int64_t h_end, int64_t qrows_limit, int64_t tiles_per_split,
-                  double lazy_tau, int lsum_rounded, int q_gran, int k_gran, float* out, float* lse2) {
+                  double lazy_tau, int lsum_rounded, int q_gran, int k_gran, const int8_t* tile_mask, int64_t tm_s1,
+                  int64_t tm_s2, float* out, float* lse2) {
   const int64_t RB = 128; /* query rows per work item */
   int64_t nQB = (Lq + blkq - 1) / blkq;
   int64_t nKB = (Lk + blkk - 1) / blkk;
@@ -407,12 +408,20 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
         int* hasacc = (int*)calloc((size_t)nr, sizeof(int));
         double* vt = (double*)malloc(sizeof(double) * blkk * D);
         double s[1024];
+        /* key tiles this query block visits, in order: all of them, or the ones the block-sparse mask
+         * keeps (sparse_int8_attn.py:57-58); KV splits group consecutive visited tiles */
+        int64_t* act = (int64_t*)malloc(sizeof(int64_t) * (nKB > 0 ? nKB : 1));
+        int64_t nact = 0;
+        for (int64_t t = 0; t < nKB && t * blkk < valid; t++)
+          if (!tile_mask || tile_mask[(b * Hkv + hk) * tm_s1 + (i0 / RB) * tm_s2 + t]) act[nact++] = t;
+        const int64_t tps = tiles_per_split < nKB ? tiles_per_split : (nKB > 0 ? nKB : 1);
         for (int64_t r = 0; r < nr; r++) macc[r] = -INFINITY;
-        for (int64_t t0 = 0; t0 < nKB; t0 += tiles_per_split) {
-          int64_t t1 = t0 + tiles_per_split < nKB ? t0 + tiles_per_split : nKB;
+        for (int64_t a0 = 0; a0 < nact; a0 += tps) {
+          int64_t a1 = a0 + tps < nact ? a0 + tps : nact;
           for (int64_t r = 0; r < nr; r++) { m[r] = -5000000.0; dsum[r] = 0.0; has[r] = 0; }
           memset(o, 0, sizeof(double) * nr * D);
-          for (int64_t t = t0; t < t1 && t * blkk < valid; t++) {
+          for (int64_t ai = a0; ai < a1; ai++) {
+            const int64_t t = act[ai];
             int64_t k0 = t * blkk, kend = k0 + blkk < valid ? k0 + blkk : valid;
             const float* ksrow = k_scale + (b * Hkv + hk) * nKS;
             for (int64_t j = k0; j < kend; j++)
@@ -484,7 +493,7 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
           }
           if (lse2) lse2[(b * Hq + h) * Lq + i] = hasacc[r] && dacc[r] > 0 ? (float)(log2(dacc[r]) + macc[r]) : -INFINITY;
         }
-        free(o); free(oacc); free(m); free(dsum); free(macc); free(dacc); free(has); free(hasacc); free(vt);
+        free(o); free(oacc); free(m); free(dsum); free(macc); free(dacc); free(has); free(hasacc); free(vt); free(act);
       }
 }
 

@@ -41,6 +41,8 @@ constexpr int kNBuf = kPrefetch + 1;
 // k_scales staged in LDS per workgroup (floats).  Sized so that two workgroups per CU still fit in the
 // 160 KiB of LDS next to the K/V buffers: 24 + 24 + 30 KiB (FP8 V) or 24 + 48 + 6 KiB (half V).
 template <int PV> constexpr int ks_lds_floats() { return PV == 0 ? 7680 : 1536; }
+// block-sparse launches (half P.V only) stage the active tiles' ids next to their scales
+constexpr int kSpMaxTiles = 1024;
 // per-thread K scales: 4 per 64-key tile (one per mma lane-pair class), otherwise 1
 constexpr int ks_per_tile(bool kt) { return kt ? 4 : 1; }
 constexpr int kBK = 64;
@@ -68,6 +70,8 @@ struct AttnParams {
   int64_t osb, osl, osh;
   float* lse;  // [B, Hq, Lq] or null
   const int32_t* kv_valid;
+  const int8_t* tile_mask;  // block-sparse: [B, Hkv, nQB, nKB] (strides tm_s1 per (b, kv head), tm_s2 per Q block)
+  int64_t tm_s1, tm_s2;
   float* ws_o;   // split partials [split][B][Hq][Lq][D]
   float* ws_ml;  // [split][B][Hq][Lq][2]
   int64_t B, Lq, Lk, Hq, Hkv, nQB, nKB;
@@ -129,15 +133,18 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // P rounded to the half dtype of V x V as given (the Triton / SAGE_ATTN_2_8_16 style), fp32 accumulation.
 enum PvKind { PV_FP8 = 0, PV_BF16 = 1, PV_FP16 = 2 };
 
-template <bool IS_FP16_OUT, bool SPLIT, int PV, bool KT>
+template <bool IS_FP16_OUT, bool SPLIT, int PV, bool KT, bool SP = false>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(AttnParams p) {
+  static_assert(!SP || (PV != PV_FP8 && !KT), "block-sparse launches use half P.V and per-block scales");
   constexpr int KS = ks_per_tile(KT);
   constexpr int kVBytes = PV == PV_FP8 ? 1 : 2;    // bytes per V element
   constexpr int kVDma = 2 * kVBytes;                // V DMA instructions per wave per tile
   constexpr float kOffset = PV == PV_FP8 ? kFp8Offset : 0.f;
   __shared__ __align__(16) uint8_t lds_k[kNBuf][kBK * kD];
   __shared__ __align__(16) uint8_t lds_v[kNBuf][kD * kBK * kVBytes];
-  __shared__ float lds_ks[ks_lds_floats<PV>()];  // k_scales of this workgroup's key tiles
+  __shared__ float lds_ks[SP ? kSpMaxTiles : ks_lds_floats<PV>()];  // k_scales of this workgroup's key tiles
+  __shared__ int16_t lds_tid[SP ? kSpMaxTiles : 1];                  // block-sparse: ids of the active tiles
+  __shared__ int lds_nact;
 
   const int64_t tile_id = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t qb = tile_id % p.nQB;
@@ -157,11 +164,34 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   if (p.kv_valid) kv_end = min(kv_end, (int64_t)p.kv_valid[b]);
   if (p.causal) kv_end = min(kv_end, q_first + kBQ + p.q_offset);
   const int64_t n_tiles = kv_end > 0 ? (kv_end + kBK - 1) / kBK : 0;
-  int64_t t_begin = 0, t_end = n_tiles;
-  if (SPLIT) {
-    t_begin = (int64_t)split * p.tiles_per_split;
-    t_end = min(n_tiles, t_begin + p.tiles_per_split);
+  // The loop runs over "slots": every key tile (dense), or the tiles the block-sparse mask keeps for
+  // this query block, in key order (sparse_int8_attn.py:57-58 skips a tile whose k_block_id is 0).
+  int64_t t_begin = SPLIT ? (int64_t)split * p.tiles_per_split : 0;
+  int64_t n_slots = n_tiles;
+  if constexpr (SP) {
+    if (w == 0) {  // wave 0 compacts the mask row with ballots; only this split's slots are stored
+      const int8_t* mrow = p.tile_mask + (b * p.Hkv + hk) * p.tm_s1 + qb * p.tm_s2;
+      int64_t cnt = 0;
+      for (int64_t base = 0; base < n_tiles; base += 64) {
+        const int64_t t = base + lane;
+        const bool act = t < n_tiles && mrow[t] != 0;
+        const uint64_t bal = __ballot(act);
+        const int64_t slot = cnt + __popcll(bal & ((1ull << lane) - 1ull));
+        if (act && slot >= t_begin && slot < t_begin + (SPLIT ? p.tiles_per_split : kSpMaxTiles))
+          lds_tid[slot - t_begin] = (int16_t)t;
+        cnt += __popcll(bal);
+      }
+      if (lane == 0) lds_nact = (int)cnt;
+    }
+    __syncthreads();
+    n_slots = lds_nact;
   }
+  const int64_t t_end = SPLIT ? min(n_slots, t_begin + p.tiles_per_split) : n_slots;
+  // key tile of slot t (wave-uniform)
+  auto tile_of = [&](int64_t t) -> int64_t {
+    if constexpr (SP) return __builtin_amdgcn_readfirstlane((int)lds_tid[t - t_begin]);
+    else return t;
+  };
 
   // Q fragment (B operand of S^T = K.Q^T): lane owns query row lq of this wave, bytes
   // d = 32*m + 16*hf .. +16 for m = 0..3
@@ -259,17 +289,21 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   // iteration t - 1.  The k_scales of all tiles are staged in LDS once, so the only VMEM traffic in the
   // loop is the 4 DMA instructions per tile and the vmcnt accounting below is exact.
   __syncthreads();  // every wave has its Q fragments out of the LDS stage before the DMA reuses it
-  for (int64_t i = tid; i < (t_end - t_begin) * KS; i += kThreads) lds_ks[i] = ks_ptr[t_begin * KS + i];
+  if constexpr (SP) {
+    for (int64_t i = tid; i < t_end - t_begin; i += kThreads) lds_ks[i] = ks_ptr[lds_tid[i]];
+  } else {
+    for (int64_t i = tid; i < (t_end - t_begin) * KS; i += kThreads) lds_ks[i] = ks_ptr[t_begin * KS + i];
+  }
 #pragma unroll
   for (int d = 0; d < kPrefetch; d++)
-    if (t_begin + d < t_end) dma_tile(t_begin + d, d);
+    if (t_begin + d < t_end) dma_tile(tile_of(t_begin + d), d);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
   int buf = 0;
   for (int64_t t = t_begin; t < t_end; t++) {
     const bool issue = t + kPrefetch < t_end;
-    if (issue) dma_tile(t + kPrefetch, buf == 0 ? kNBuf - 1 : buf - 1);
+    if (issue) dma_tile(tile_of(t + kPrefetch), buf == 0 ? kNBuf - 1 : buf - 1);
     // logit scale(s) of this lane: with per-thread K scales, key kappa of the tile belongs to class
     // (kappa % 8) / 2 = 2 hf + (r & 3) / 2 for accumulator element r, so a lane needs two of them
     float cs_a, cs_b;
@@ -300,7 +334,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
     }
 
     // ---- masking (tail tile, key padding, causal diagonal) ----
-    const int64_t k0 = t * kBK;
+    const int64_t k0 = tile_of(t) * kBK;
     const bool masked = (k0 + kBK > kv_end) || (p.causal && k0 + kBK - 1 > wrow0 + p.q_offset);
     if (masked) {
       const int64_t qlim = p.causal ? qrow + p.q_offset : INT64_MAX;
@@ -574,7 +608,7 @@ extern "C" size_t qattn_fwd_workspace_size(int64_t B, int64_t Lq, int64_t Hq, in
   return (size_t)num_splits * B * Hq * Lq * (D + 2) * sizeof(float);
 }
 
-template <int PV, bool KT>
+template <int PV, bool KT, bool SP = false>
 static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, size_t workspace_bytes, hipStream_t st,
                       int64_t D) {
   const int64_t grid = p.B * p.Hq * p.nQB * ns;
@@ -587,14 +621,14 @@ static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, siz
                   qattn_fwd_workspace_size(p.B, p.Lq, p.Hq, D, ns));
     p.ws_o = static_cast<float*>(workspace);
     p.ws_ml = p.ws_o + (int64_t)ns * p.B * p.Hq * p.Lq * D;
-    if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, true, PV, KT><<<grid, kThreads, 0, st>>>(p);
-    else qattn_fwd_kernel<true, true, PV, KT><<<grid, kThreads, 0, st>>>(p);
+    if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, true, PV, KT, SP><<<grid, kThreads, 0, st>>>(p);
+    else qattn_fwd_kernel<true, true, PV, KT, SP><<<grid, kThreads, 0, st>>>(p);
     const int64_t rows = p.B * p.Hq * p.Lq;
     if (out_dtype == QATTN_BF16) qattn_combine_kernel<false><<<(rows + 3) / 4, 256, 0, st>>>(p);
     else qattn_combine_kernel<true><<<(rows + 3) / 4, 256, 0, st>>>(p);
   } else {
-    if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, false, PV, KT><<<grid, kThreads, 0, st>>>(p);
-    else qattn_fwd_kernel<true, false, PV, KT><<<grid, kThreads, 0, st>>>(p);
+    if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, false, PV, KT, SP><<<grid, kThreads, 0, st>>>(p);
+    else qattn_fwd_kernel<true, false, PV, KT, SP><<<grid, kThreads, 0, st>>>(p);
   }
   return check_launch("qattn_fwd");
 }
@@ -602,7 +636,7 @@ static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, siz
 static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale,
                      const void* v, int64_t Lpad, qattn_seq o, int out_dtype, int64_t B, int64_t Lq, int64_t Lk,
                      int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int causal, int64_t q_offset,
-                     const int32_t* kv_valid, float* lse, int num_splits, int pv, int gran) {
+                     const int32_t* kv_valid, float* lse, int num_splits, int pv, int gran, bool sparse = false) {
   QATTN_REQUIRE(out_dtype == QATTN_BF16 || out_dtype == QATTN_FP16, QATTN_ERR_DTYPE, "out dtype must be bf16 or fp16");
   QATTN_REQUIRE(D == kD, QATTN_ERR_HEAD_DIM, "qattn_fwd needs head_dim 128 (pad smaller heads), got %lld",
                 (long long)D);
@@ -649,7 +683,7 @@ static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale,
   p.causal = causal ? 1 : 0;
   p.qk_mult = qk_mult;
 
-  const int64_t max_tiles = max_tiles_per_split(pv, gran == QATTN_GRAN_THREAD);
+  const int64_t max_tiles = sparse ? kSpMaxTiles : max_tiles_per_split(pv, gran == QATTN_GRAN_THREAD);
   ns = num_splits > 0 ? num_splits : num_splits_for(B, Lq, Lk, Hq, max_tiles);
   ns = (int)std::min<int64_t>(ns, p.nKB);
   if (ns < 1) ns = 1;
@@ -709,4 +743,33 @@ extern "C" int qattn_fwd_pv16(qattn_seq q8, const float* q_scale, qattn_seq k8, 
   return qattn_fwd_ex(q8, q_scale, k8, k_scale, v16, v_dtype == QATTN_BF16 ? QATTN_V_BF16 : QATTN_V_FP16, Lpad,
                       nullptr, o, out_dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult, QATTN_GRAN_BLOCK, causal, q_offset,
                       kv_valid, lse, num_splits, workspace, workspace_bytes, stream);
+}
+
+extern "C" int qattn_fwd_block_sparse_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq) {
+  return num_splits_for(B, Lq, Lk, Hq, kSpMaxTiles);
+}
+
+extern "C" int qattn_fwd_block_sparse(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale,
+                                      const uint16_t* v16, int v_dtype, int64_t Lpad, qattn_seq o, int out_dtype,
+                                      int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D,
+                                      float qk_mult, int causal, const int8_t* tile_mask, int64_t mask_sbh,
+                                      int64_t mask_sq, float* lse, int num_splits, void* workspace,
+                                      size_t workspace_bytes, qattn_stream_t stream) {
+  QATTN_REQUIRE(v_dtype == QATTN_BF16 || v_dtype == QATTN_FP16, QATTN_ERR_DTYPE, "V dtype must be bf16 or fp16");
+  QATTN_REQUIRE(tile_mask != nullptr, QATTN_ERR_ARG, "tile_mask is null");
+  QATTN_REQUIRE(mask_sbh >= 0 && mask_sq >= 0, QATTN_ERR_STRIDE, "negative mask stride");
+  AttnParams p;
+  int ns = 1;
+  const int pv = v_dtype == QATTN_BF16 ? PV_BF16 : PV_FP16;
+  const int rc = setup_fwd(p, ns, q8, q_scale, k8, k_scale, v16, Lpad, o, out_dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult,
+                           causal, 0, nullptr, lse, num_splits, pv, QATTN_GRAN_BLOCK, true);
+  if (rc < 0) return QATTN_OK;
+  if (rc) return rc;
+  p.v_scale = nullptr;
+  p.tile_mask = tile_mask;
+  p.tm_s1 = mask_sbh;
+  p.tm_s2 = mask_sq;
+  hipStream_t st = (hipStream_t)stream;
+  if (pv == PV_BF16) return launch_fwd<PV_BF16, false, true>(p, out_dtype, ns, workspace, workspace_bytes, st, D);
+  return launch_fwd<PV_FP16, false, true>(p, out_dtype, ns, workspace, workspace_bytes, st, D);
 }

@@ -301,3 +301,62 @@ def test_sageattn_varlen(oracle, causal):
         log(f"  seq {b}: lq={lq[b]} lk={lk[b]} cos_oracle={c:.6f} cos_truth={ct:.6f}")
         assert c >= COS_KERNEL
         assert ct >= COS_E2E
+
+
+@pytest.mark.parametrize("case", ["nhd", "hnd_gqa_causal", "split"])
+def test_block_sparse(oracle, case):
+    """sparse_sageattn (sparse_sage.py:25-80, sparse_int8_attn.py k_block_id skip) against the oracle with
+    the same tile mask and against a float64 block-masked softmax; fully masked query blocks are zero."""
+    dev = require_gpu()
+    from telefuser_amd import _lib
+    from telefuser_amd import sageattn2 as sa
+    from telefuser_amd.sparse_sage import sparse_sageattn
+
+    B, Lq, Lk, Hq, Hkv, layout, causal = {"nhd": (1, 300, 700, 2, 2, "NHD", False),
+                                          "hnd_gqa_causal": (2, 384, 384, 4, 2, "HND", True),
+                                          "split": (1, 128, 4000, 2, 2, "NHD", False)}[case]
+    q, k, v = qkv(B, Lq, Lk, Hq, Hkv, seed=51, k_offset_std=0.5)
+    nqb, nkb = (Lq + 127) // 128, (Lk + 63) // 64
+    g = torch.Generator().manual_seed(52)
+    mask = (torch.rand((B, Hkv, nqb, nkb), generator=g) < 0.5).to(torch.int8)
+    mask[0, 0, 0] = 0  # a query block with no keys at all
+    log(f"block-sparse {case}: density {float(mask.float().mean()):.2f}")
+    args = [t.to(dev) for t in (q, k, v)]
+    if layout == "HND":
+        args = [t.transpose(1, 2).contiguous() for t in args]
+    o = sparse_sageattn(*args, mask_id=mask.to(dev), is_causal=causal, tensor_layout=layout)
+    torch.cuda.synchronize()
+    if layout == "HND":
+        o = o.transpose(1, 2)
+    og = o.float().cpu().numpy()
+    # oracle on the same quantized operands (Triton rounding, K smoothing), kernel schedule
+    km = sa.k_mean(k.to(dev), "NHD").cpu()
+    q8, qs = oracle.quant_per_block_int8(bf16_bits(q), sm_scale=128 ** -0.5 * LOG2E, blk=128, variant="triton")
+    k8, ks = oracle.quant_per_block_int8(bf16_bits(k), km_bits=bf16_bits(km), blk=64, variant="triton")
+    vh = v.to(torch.float16).contiguous().view(torch.int16).numpy().view(np.uint16)
+    L = _lib.load()
+    ns = min(L.qattn_fwd_block_sparse_num_splits(B, Lq, Lk, Hq), nkb)
+    tps = (nkb + ns - 1) // ns if ns > 1 else 0
+    ref = oracle.qattn_fwd(q8, qs, k8, ks, vh_bits=vh, pv_mode=1, is_fp16=True, causal=causal, tiles_per_split=tps,
+                           lazy_tau=KERNEL_LAZY_TAU, tile_mask=mask.numpy())
+    c = cosine(og, ref)
+    # float64 truth with the block mask
+    qf, kf, vf = (t.double().numpy() for t in (q, k, v))
+    rep = Hq // Hkv
+    truth = np.zeros_like(og, dtype=np.float64)
+    for bb in range(B):
+        for h in range(Hq):
+            s = qf[bb, :, h] @ kf[bb, :, h // rep].T * 128 ** -0.5
+            keep = np.repeat(np.repeat(mask[bb, h // rep].numpy().astype(bool), 128, 0), 64, 1)[:Lq, :Lk]
+            if causal:
+                keep &= np.tril(np.ones((Lq, Lk), bool))
+            s = np.where(keep, s, -np.inf)
+            mx = s.max(axis=1, keepdims=True)
+            p = np.where(keep, np.exp(s - np.where(np.isfinite(mx), mx, 0)), 0)
+            den = p.sum(axis=1, keepdims=True)
+            truth[bb, :, h] = np.where(den > 0, (p @ vf[bb, :, h // rep]) / np.where(den > 0, den, 1), 0)
+    ct = cosine(og, truth)
+    log(f"  cos_oracle={c:.6f} cos_truth={ct:.6f} max_abs_truth={float(np.abs(og - truth).max()):.4g}")
+    assert not og[0, :min(128, Lq), :rep].any()  # query block 0 of kv head 0 had no tiles
+    assert c >= COS_KERNEL
+    assert ct >= COS_E2E

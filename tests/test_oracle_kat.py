@@ -531,3 +531,28 @@ def test_attention_oracle_granularity_indexing(oracle):
     vf = oracle.e4m3_to_f32(v8[0, 0, :, :300]).T.astype(np.float64) * vs[0, 0][None, :]
     ref = (p @ vf) / p.sum(axis=1, keepdims=True)
     assert cosine(o3[0, :, 0], ref) > 0.9995
+
+
+def test_block_sparse_tile_mask(oracle):
+    """A skipped key tile is exactly a tile removed from K, V and the key scales
+    (sparse_int8_attn.py:57-58); an all-ones mask is the dense computation; a fully masked query block
+    gives zeros."""
+    q, k, v = qkv(1, 256, 384, 2, 2, seed=12, k_offset_std=0.5)
+    qb, kb, vb = bf16_bits(q), bf16_bits(k), bf16_bits(v)
+    q8, qs = oracle.quant_per_block_int8(qb, sm_scale=128 ** -0.5 * LOG2E, blk=128)
+    k8, ks = oracle.quant_per_block_int8(kb, blk=64)
+    vh = vb  # bf16 V, half P.V (the sparse kernel's mode)
+    dense = oracle.qattn_fwd(q8, qs, k8, ks, vh_bits=vh, pv_mode=1)
+    ones = np.ones((1, 2, 2, 6), np.int8)
+    assert np.array_equal(oracle.qattn_fwd(q8, qs, k8, ks, vh_bits=vh, pv_mode=1, tile_mask=ones), dense)
+    mask = ones.copy()
+    mask[0, :, 0, 2] = 0  # query block 0 skips keys 128..191 in both heads
+    mask[0, 1, 1, :] = 0  # head 1, query block 1: nothing
+    got = oracle.qattn_fwd(q8, qs, k8, ks, vh_bits=vh, pv_mode=1, tile_mask=mask)
+    keep = np.r_[0:128, 192:384]
+    ref = oracle.qattn_fwd(q8[:, :128], qs[:, :, :1], np.ascontiguousarray(k8[:, keep]),
+                           np.ascontiguousarray(ks[:, :, [0, 1, 3, 4, 5]]), vh_bits=np.ascontiguousarray(vh[:, keep]),
+                           pv_mode=1)
+    assert np.array_equal(got[:, :128], ref)
+    assert np.array_equal(got[:, 128:, 0], dense[:, 128:, 0])
+    assert not got[:, 128:, 1].any()
