@@ -235,6 +235,29 @@ int qattn_fwd_block_sparse(qattn_seq q8, const float* q_scale, qattn_seq k8, con
                            int64_t mask_sbh, int64_t mask_sq, float* lse, int num_splits, void* workspace,
                            size_t workspace_bytes, qattn_stream_t stream);
 
+/*
+ * Fused prologue of the Wan self-attention projections (the step before the path:
+ * telefuser/models/wan_video_dit.py:196-207 norm_q/norm_k -> rope_apply -> attention):
+ *   x: linear output [B, L, H*D] viewed as a sequence tensor [B, L, H, D] (row of H*D contiguous values)
+ *   rstd: qattn_row_rstd of x (RMSNorm over the whole H*D row; fp64-exact sum of squares, fp32 after)
+ *   y = half((x * rstd) * w), then interleaved RoPE on y with cos/sin [L, D/2] fp32 (rows cs_stride
+ *   floats): (y1, y2) -> half(fma(-y2, sin, y1*cos)), half(fma(y1, sin, y2*cos))
+ *   (telefuser/kernel/triton/norm.py:469-507 and rotary.py:21-88), then per-block INT8 quantization as
+ *   qattn_quant_qk_per_block_int8 (Q blocks of 128 with sm_scale folded, K blocks of 64 with k_mean).
+ * The normalized / rotated bf16 tensors are never written.  qattn_norm_rope_seq_mean gives the K mean
+ * of the rotated values (smoothing vector) in one pass over x.
+ */
+int qattn_row_rstd(const void* x, int dtype, int64_t rows, int64_t row_stride, int64_t n, float eps, float* rstd,
+                   qattn_stream_t stream);
+int qattn_norm_rope_seq_mean(qattn_seq x, int dtype, int64_t B, int64_t L, int64_t H, int64_t D, const float* rstd,
+                             const void* w, const float* cs, const float* sn, int64_t cs_stride, void* mean,
+                             void* workspace, size_t workspace_bytes, qattn_stream_t stream);
+int qattn_norm_rope_quant_qk(qattn_seq xq, qattn_seq xk, int dtype, int64_t B, int64_t L, int64_t H, int64_t D,
+                             const float* rstd_q, const float* rstd_k, const void* wq, const void* wk, const float* cs,
+                             const float* sn, int64_t cs_stride, const void* k_mean, qattn_seq q_out,
+                             qattn_seq k_out, float* q_scale, float* k_scale, float sm_scale, int variant,
+                             qattn_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -43,6 +43,7 @@ def lib():
         L.oq_qattn_fwd.argtypes = [vp, i64, i64, i64, vp, i64, vp, i64, i64, i64, vp, i64, vp, i64, vp, vp, i32,
                                    i64, i64, i64, i64, i64, i64, i64, i64, i64, f64, i32, i32, i64, vp, i64, i64,
                                    i64, i64, f64, i32, i32, i32, vp, i64, i64, vp, vp]
+        L.oq_norm_rope.argtypes = [vp, i32, i64, i64, i64, i64, vp, vp, vp, f32, vp]
         L.oq_quant_per_thread_int8.argtypes = [vp, i32, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, i32, vp,
                                                i64, i64, i64, vp]
         L.oq_attn_fp64.argtypes = [vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, f64, i32, i64, vp, vp]
@@ -106,6 +107,20 @@ def quant_per_block_int8(x_bits, km_bits=None, sm_scale=None, blk=128, layout="N
                                              kmh, float(sm_scale if sm_scale is not None else 1.0), blk, _p(out), sb,
                                              sl, sh, _p(scale))
     return out, scale
+
+
+def norm_rope(x_bits, w_bits, cos, sin, head_dim, eps=1e-6, is_fp16=False):
+    """RMSNorm over the last dim then interleaved RoPE per head (see oq_norm_rope).  x_bits [B, L, N]
+    half bits, w_bits [N], cos/sin [L, head_dim/2] fp32.  Returns half bits [B, L, N]."""
+    x_bits = np.ascontiguousarray(_bits(x_bits))
+    B, L, N = x_bits.shape
+    w = np.ascontiguousarray(_bits(w_bits))
+    cs = np.ascontiguousarray(cos, dtype=np.float32)
+    sn = np.ascontiguousarray(sin, dtype=np.float32)
+    assert cs.shape == (L, head_dim // 2) and sn.shape == cs.shape and w.shape == (N,)
+    out = np.zeros_like(x_bits)
+    lib().oq_norm_rope(_p(x_bits), int(is_fp16), B, L, N, head_dim, _p(w), _p(cs), _p(sn), float(eps), _p(out))
+    return out
 
 
 def quant_per_thread_int8(x_bits, km_bits=None, is_key=False, layout="NHD", is_fp16=False):

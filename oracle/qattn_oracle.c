@@ -291,6 +291,50 @@ void oq_quant_per_thread_int8(const uint16_t* in, int is_fp16, int64_t B, int64_
         }
 }
 
+/*
+ * Prologue of the Wan self-attention projections (telefuser/models/wan_video_dit.py:196-207):
+ * RMSNorm over the whole row of N = H*D values, then interleaved RoPE per head.
+ *   norm (Triton norm_infer, telefuser/kernel/triton/norm.py:469-507): var = sum(x^2) / N,
+ *     rstd = 1 / sqrt(var + eps), y = (x * rstd) * w stored in x's dtype.  The sum is taken exactly (fp64:
+ *     the squares of half values and their sum are exact for any realistic row) and var rounded to fp32
+ *     - the reference's fp32 tree sum differs from it in the last bits: parity of this step is pinned
+ *     to the mathematics, not to that reduction order;
+ *   rope (telefuser/kernel/triton/rotary.py:21-88): pairs (y[2i], y[2i+1]) of each head with cos/sin[l][i]
+ *     (fp32): o1 = fma(-y2, sin, y1*cos), o2 = fma(y1, sin, y2*cos), stored in x's dtype.
+ * x, out: [B, L, N] contiguous half bits; w: [N]; cs, sn: [L, D/2] fp32.
+ */
+void oq_norm_rope(const uint16_t* x, int is_fp16, int64_t B, int64_t L, int64_t N, int64_t D, const uint16_t* w,
+                  const float* cs, const float* sn, float eps, uint16_t* out) {
+#pragma omp parallel for collapse(2) schedule(static)
+  for (int64_t b = 0; b < B; b++)
+    for (int64_t l = 0; l < L; l++) {
+      const uint16_t* xr = x + (b * L + l) * N;
+      uint16_t* orow = out + (b * L + l) * N;
+      double acc = 0.0;
+      for (int64_t i = 0; i < N; i++) {
+        const double v = load_h(xr + i, is_fp16);
+        acc += v * v;
+      }
+      volatile float var = (float)(acc / (double)N);
+      volatile float den = sqrtf(var + eps);
+      const float rstd = 1.0f / den;
+      for (int64_t i = 0; i < N; i += 2) {
+        float y[2];
+        for (int e = 0; e < 2; e++) {
+          volatile float xr_ = load_h(xr + i + e, is_fp16) * rstd;
+          volatile float yw = xr_ * load_h(w + i + e, is_fp16);
+          y[e] = is_fp16 ? oq_f16_to_f32(oq_f32_to_f16(yw)) : oq_bf16_to_f32(oq_f32_to_bf16(yw));
+        }
+        const int64_t pair = (i % D) / 2;
+        const float c = cs[l * (D / 2) + pair], s = sn[l * (D / 2) + pair];
+        volatile float a = y[0] * c, bb = y[1] * c;
+        const float o1 = fmaf(-y[1], s, a), o2 = fmaf(y[0], s, bb);
+        orow[i] = is_fp16 ? oq_f32_to_f16(o1) : oq_f32_to_bf16(o1);
+        orow[i + 1] = is_fp16 ? oq_f32_to_f16(o2) : oq_f32_to_bf16(o2);
+      }
+    }
+}
+
 /* ------------------------------------------------------------------------------------------ */
 /* per-channel FP8 V quantizer                                                                 */
 /* ------------------------------------------------------------------------------------------ */

@@ -99,7 +99,11 @@ def load() -> ctypes.CDLL:
     L.qattn_fwd_block_sparse_num_splits.restype = i32
     L.qattn_fwd_block_sparse.argtypes = [S, vp, S, vp, vp, i32, i64, S, i32, i64, i64, i64, i64, i64, i64, f32, i32,
                                          vp, i64, i64, vp, i32, vp, sz, vp]
-    for name in ("qattn_fwd_block_sparse", "qattn_quant_qk_per_warp_int8", "qattn_quant_qk_per_thread_int8", "qattn_fwd_ex",
+    L.qattn_row_rstd.argtypes = [vp, i32, i64, i64, i64, f32, vp, vp]
+    L.qattn_norm_rope_seq_mean.argtypes = [S, i32, i64, i64, i64, i64, vp, vp, vp, vp, i64, vp, vp, sz, vp]
+    L.qattn_norm_rope_quant_qk.argtypes = [S, S, i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, i64, vp, S, S, vp,
+                                           vp, f32, i32, vp]
+    for name in ("qattn_row_rstd", "qattn_norm_rope_seq_mean", "qattn_norm_rope_quant_qk", "qattn_fwd_block_sparse", "qattn_quant_qk_per_warp_int8", "qattn_quant_qk_per_thread_int8", "qattn_fwd_ex",
                  "qattn_v_fp8_cache_update", "qattn_quant_per_block_int8", "qattn_quant_qk_per_block_int8", "qattn_seq_mean",
                  "qattn_per_channel_fp8", "qattn_fwd", "qattn_v_tile_half", "qattn_fwd_pv16"):
         getattr(L, name).restype = i32

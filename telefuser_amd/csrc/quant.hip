@@ -15,6 +15,45 @@ namespace qattn {
 // per-block INT8 quantizer
 // ------------------------------------------------------------------------------------------------
 
+// Prologue of the Wan self-attention projections, applied on the fly to a 16-byte chunk (8 elements,
+// 4 rotation pairs) of head h, row l of the linear output x:
+//   RMSNorm over the full H*D row: y = half((x * rstd[b, l]) * w[h*D + d])  (norm_infer,
+//     telefuser/kernel/triton/norm.py:469-507: x * rstd in fp32, times the weight, stored in x's dtype)
+//   interleaved RoPE on the stored y: (y1, y2) -> half(fma(-y2, sin, y1*cos)), half(fma(y1, sin, y2*cos))
+//     (telefuser/kernel/triton/rotary.py:21-88), cos/sin as fp32 per (row, pair)
+// rstd == nullptr: no prologue (the chunk is used as loaded).
+struct NormRope {
+  const float* rstd;     // [B * L]
+  const uint16_t* w;     // [H * D], x's dtype
+  const float* cs;       // [L, D / 2] rows of cs_stride floats
+  const float* sn;
+  int64_t cs_stride;
+};
+
+template <bool IS_FP16>
+__device__ __forceinline__ void norm_rope8(const NormRope& nr, int64_t b, int64_t L, int64_t l, int64_t h, int D,
+                                           int dc, uint16_t (&hv)[8]) {
+  const float r = nr.rstd[b * L + l];
+  const v4u wr = *reinterpret_cast<const v4u*>(nr.w + h * D + dc * 8);
+  uint16_t wv[8];
+  __builtin_memcpy(wv, &wr, 16);
+  const v4f c4 = *reinterpret_cast<const v4f*>(nr.cs + l * nr.cs_stride + dc * 4);
+  const v4f s4 = *reinterpret_cast<const v4f*>(nr.sn + l * nr.cs_stride + dc * 4);
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const float xr = half_to_f32<IS_FP16>(hv[e]) * r;
+    y[e] = half_to_f32<IS_FP16>(f32_to_half<IS_FP16>(xr * half_to_f32<IS_FP16>(wv[e])));
+  }
+#pragma unroll
+  for (int p = 0; p < 4; p++) {
+    const float y1 = y[2 * p], y2 = y[2 * p + 1];
+    const float a = y1 * c4[p], bb = y2 * c4[p];
+    hv[2 * p] = f32_to_half<IS_FP16>(fmaf(-y2, s4[p], a));
+    hv[2 * p + 1] = f32_to_half<IS_FP16>(fmaf(y1, s4[p], bb));
+  }
+}
+
 struct QuantJob {
   const uint16_t* in;
   int64_t sb, sl, sh;
@@ -29,6 +68,7 @@ struct QuantJob {
   int64_t nwg;  // B * H * nblk
   int ncls;     // scale classes per block: 1 (per block), 8 (per-thread Q), 4 (per-thread K)
   int cls_shift;  // class of row r = (r % 8) >> cls_shift  (3, 0, 1 for the cases above)
+  NormRope nr;    // optional RMSNorm + RoPE prologue on the loaded chunks
 };
 
 struct QuantArgs {
@@ -92,6 +132,7 @@ __global__ __launch_bounds__(kQuantThreads) void quant_per_block_kernel(QuantArg
       v4u raw = *reinterpret_cast<const v4u*>(J.in + b * J.sb + l * J.sl + h * J.sh + dc * 8);
       uint16_t hv[8];
       __builtin_memcpy(hv, &raw, 16);
+      if (J.nr.rstd) norm_rope8<IS_FP16>(J.nr, b, J.L, l, h, D, dc, hv);
       float mv[8];
       if (J.mean) {
         v4u mraw = *reinterpret_cast<const v4u*>(J.mean + (b * J.H + h) * D + dc * 8);
@@ -175,7 +216,7 @@ __global__ __launch_bounds__(kQuantThreads) void quant_per_block_kernel(QuantArg
 constexpr int kColChunk = 256;  // sequence rows per workgroup
 
 template <bool IS_FP16, int MODE, int D>  // MODE 0: sum, 1: max |x|
-__global__ __launch_bounds__(256) void col_partial_kernel(const uint16_t* in, int64_t sb, int64_t sl, int64_t sh,
+__global__ __launch_bounds__(256) void col_partial_kernel(NormRope nr, const uint16_t* in, int64_t sb, int64_t sl, int64_t sh,
                                                           int64_t L, int64_t H, int64_t nchunk, float* part) {
   constexpr int TPR = D / 8;
   constexpr int RPP = 256 / TPR;  // rows per pass
@@ -191,6 +232,7 @@ __global__ __launch_bounds__(256) void col_partial_kernel(const uint16_t* in, in
       v4u raw = *reinterpret_cast<const v4u*>(in + b * sb + l * sl + h * sh + dc * 8);
       uint16_t hv[8];
       __builtin_memcpy(hv, &raw, 16);
+      if (nr.rstd) norm_rope8<IS_FP16>(nr, b, L, l, h, D, dc, hv);
 #pragma unroll
       for (int e = 0; e < 8; e++) {
         float v = half_to_f32<IS_FP16>(hv[e]);
@@ -364,6 +406,37 @@ __global__ __launch_bounds__(256) void v_tile_half_kernel(const uint16_t* in, in
 }
 
 // ------------------------------------------------------------------------------------------------
+// RMSNorm statistics: rstd = 1 / sqrt(mean(x^2) + eps) per row, one wave per row.  The squares of half
+// values are exact in fp64 and so is their sum for any realistic row, which makes the mean independent
+// of the summation order; var is then rounded to fp32 and the rest is IEEE fp32 (sqrt, division).
+// ------------------------------------------------------------------------------------------------
+template <bool IS_FP16>
+__global__ __launch_bounds__(256) void row_rstd_kernel(const uint16_t* x, int64_t rows, int64_t row_stride, int64_t n,
+                                                       float eps, float* rstd) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const uint16_t* xr = x + row * row_stride;
+  double acc = 0.0;
+  for (int64_t c = lane; c * 8 < n; c += 64) {
+    const v4u raw = *reinterpret_cast<const v4u*>(xr + c * 8);
+    uint16_t hv[8];
+    __builtin_memcpy(hv, &raw, 16);
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const double v = (double)half_to_f32<IS_FP16>(hv[e]);
+      acc += v * v;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+  if (lane == 0) {
+    const float var = (float)(acc / (double)n);
+    rstd[row] = 1.0f / sqrtf(var + eps);
+  }
+}
+
+// ------------------------------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------------------------------
 
@@ -390,6 +463,7 @@ static bool fill_job(QuantJob& J, const qattn_seq& in, const qattn_seq& out, int
   J.nwg = B * H * J.nblk;
   J.ncls = 1;
   J.cls_shift = 3;
+  J.nr = NormRope{};
   return true;
 }
 
@@ -537,10 +611,10 @@ extern "C" size_t qattn_seq_mean_workspace_size(int64_t B, int64_t L, int64_t H,
 
 template <int MODE>
 static void launch_col(const qattn_seq& in, int dtype, int64_t B, int64_t L, int64_t H, int64_t D, int64_t nchunk,
-                       float* part, hipStream_t st) {
+                       float* part, hipStream_t st, const NormRope& nr = NormRope{}) {
   dim3 grid((unsigned)nchunk, (unsigned)H, (unsigned)B);
   const uint16_t* p = static_cast<const uint16_t*>(in.data);
-#define QATTN_COL(F16, DD) col_partial_kernel<F16, MODE, DD><<<grid, 256, 0, st>>>(p, in.sb, in.sl, in.sh, L, H, nchunk, part)
+#define QATTN_COL(F16, DD) col_partial_kernel<F16, MODE, DD><<<grid, 256, 0, st>>>(nr, p, in.sb, in.sl, in.sh, L, H, nchunk, part)
   if (dtype == QATTN_BF16) { if (D == 128) QATTN_COL(false, 128); else QATTN_COL(false, 64); }
   else { if (D == 128) QATTN_COL(true, 128); else QATTN_COL(true, 64); }
 #undef QATTN_COL
@@ -673,4 +747,83 @@ extern "C" int qattn_v_fp8_cache_update(qattn_seq v, int dtype, int64_t B, int64
     else v_fp8_kernel<true, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, fill, H, recp, v8, Lpad, filt);
   }
   return check_launch("v_fp8_cache_update");
+}
+
+extern "C" int qattn_row_rstd(const void* x, int dtype, int64_t rows, int64_t row_stride, int64_t n, float eps,
+                              float* rstd, qattn_stream_t stream) {
+  QATTN_REQUIRE(dtype == QATTN_BF16 || dtype == QATTN_FP16, QATTN_ERR_DTYPE, "dtype must be bf16 (0) or fp16 (1)");
+  QATTN_REQUIRE(rows >= 0 && n > 0 && n % 8 == 0, QATTN_ERR_SHAPE, "row length must be a positive multiple of 8");
+  if (rows == 0) return QATTN_OK;
+  QATTN_REQUIRE(x && aligned16(x) && row_stride % 8 == 0, QATTN_ERR_ALIGN, "rows must be 16-byte aligned");
+  QATTN_REQUIRE(rstd != nullptr, QATTN_ERR_ARG, "rstd is null");
+  hipStream_t st = (hipStream_t)stream;
+  const unsigned grid = (unsigned)((rows + 3) / 4);
+  const uint16_t* p = static_cast<const uint16_t*>(x);
+  if (dtype == QATTN_BF16) row_rstd_kernel<false><<<grid, 256, 0, st>>>(p, rows, row_stride, n, eps, rstd);
+  else row_rstd_kernel<true><<<grid, 256, 0, st>>>(p, rows, row_stride, n, eps, rstd);
+  return check_launch("row_rstd");
+}
+
+static int make_norm_rope(NormRope& nr, const float* rstd, const void* w, const float* cs, const float* sn,
+                          int64_t cs_stride, int64_t D) {
+  QATTN_REQUIRE(rstd && w && cs && sn, QATTN_ERR_ARG, "norm/rope operands must be non-null");
+  QATTN_REQUIRE(aligned16(w) && aligned16(cs) && aligned16(sn) && cs_stride % 4 == 0 && cs_stride >= D / 2,
+                QATTN_ERR_ALIGN, "weight / cos / sin must be 16-byte aligned with cos/sin rows of >= D/2 floats");
+  nr.rstd = rstd;
+  nr.w = static_cast<const uint16_t*>(w);
+  nr.cs = cs;
+  nr.sn = sn;
+  nr.cs_stride = cs_stride;
+  return QATTN_OK;
+}
+
+extern "C" int qattn_norm_rope_seq_mean(qattn_seq x, int dtype, int64_t B, int64_t L, int64_t H, int64_t D,
+                                        const float* rstd, const void* w, const float* cs, const float* sn,
+                                        int64_t cs_stride, void* mean, void* workspace, size_t workspace_bytes,
+                                        qattn_stream_t stream) {
+  int rc;
+  if ((rc = check_common(dtype, D, QATTN_QUANT_CUDA, 64))) return rc;
+  QATTN_REQUIRE(B > 0 && L > 0 && H > 0, QATTN_ERR_SHAPE, "norm_rope_seq_mean needs non-empty input");
+  if ((rc = check_seq("x", x, 2))) return rc;
+  NormRope nr{};
+  if ((rc = make_norm_rope(nr, rstd, w, cs, sn, cs_stride, D))) return rc;
+  QATTN_REQUIRE(mean != nullptr, QATTN_ERR_ARG, "mean is null");
+  QATTN_REQUIRE(workspace && workspace_bytes >= qattn_seq_mean_workspace_size(B, L, H, D), QATTN_ERR_WORKSPACE,
+                "norm_rope_seq_mean workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t nchunk = col_chunks(L);
+  float* part = static_cast<float*>(workspace);
+  launch_col<0>(x, dtype, B, L, H, D, nchunk, part, st, nr);
+  uint16_t* m = static_cast<uint16_t*>(mean);
+  if (dtype == QATTN_BF16) {
+    if (D == 128) mean_finalize_kernel<false, 128><<<B * H, 128, 0, st>>>(part, nchunk, L, m);
+    else mean_finalize_kernel<false, 64><<<B * H, 64, 0, st>>>(part, nchunk, L, m);
+  } else {
+    if (D == 128) mean_finalize_kernel<true, 128><<<B * H, 128, 0, st>>>(part, nchunk, L, m);
+    else mean_finalize_kernel<true, 64><<<B * H, 64, 0, st>>>(part, nchunk, L, m);
+  }
+  return check_launch("norm_rope_seq_mean");
+}
+
+extern "C" int qattn_norm_rope_quant_qk(qattn_seq xq, qattn_seq xk, int dtype, int64_t B, int64_t L, int64_t H,
+                                        int64_t D, const float* rstd_q, const float* rstd_k, const void* wq,
+                                        const void* wk, const float* cs, const float* sn, int64_t cs_stride,
+                                        const void* k_mean, qattn_seq q_out, qattn_seq k_out, float* q_scale,
+                                        float* k_scale, float sm_scale, int variant, qattn_stream_t stream) {
+  int rc;
+  if ((rc = check_common(dtype, D, variant, 64))) return rc;
+  QATTN_REQUIRE(B >= 0 && L >= 0 && H >= 0, QATTN_ERR_SHAPE, "negative size");
+  if (B * L * H == 0) return QATTN_OK;
+  if ((rc = check_seq("xq", xq, 2)) || (rc = check_seq("xk", xk, 2)) || (rc = check_seq("q_out", q_out, 1)) ||
+      (rc = check_seq("k_out", k_out, 1)))
+    return rc;
+  QATTN_REQUIRE(q_scale && k_scale, QATTN_ERR_ARG, "scale is null");
+  QATTN_REQUIRE(k_mean == nullptr || aligned16(k_mean), QATTN_ERR_ALIGN, "k_mean must be 16-byte aligned");
+  QuantArgs a{};
+  a.njobs = 2;
+  fill_job(a.job[0], xq, q_out, B, L, H, nullptr, q_scale, sm_scale, 1, 128);
+  fill_job(a.job[1], xk, k_out, B, L, H, k_mean, k_scale, 1.0f, 0, 64);
+  if ((rc = make_norm_rope(a.job[0].nr, rstd_q, wq, cs, sn, cs_stride, D))) return rc;
+  if ((rc = make_norm_rope(a.job[1].nr, rstd_k, wk, cs, sn, cs_stride, D))) return rc;
+  return run_quant(a, dtype, D, variant, (hipStream_t)stream);
 }

@@ -556,3 +556,54 @@ def test_block_sparse_tile_mask(oracle):
     assert np.array_equal(got[:, :128], ref)
     assert np.array_equal(got[:, 128:, 0], dense[:, 128:, 0])
     assert not got[:, 128:, 1].any()
+
+
+# ------------------------------------------------------------------------------------------------
+# RMSNorm + RoPE prologue (norm.py:469-507, rotary.py:21-88)
+# ------------------------------------------------------------------------------------------------
+
+def _norm_rope_inputs(L=40, H=2, D=128, seed=3):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn((1, L, H * D), generator=g) * 3).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn((H * D,), generator=g)).to(torch.bfloat16)
+    ang = torch.rand((L, D // 2), generator=g, dtype=torch.float64) * 6.3
+    return x, w, ang.cos().float().numpy(), ang.sin().float().numpy()
+
+
+def test_norm_rope_known_answers(oracle):
+    D = 128
+    # constant row 2.0, unit weight, no rotation: var = 4, y = bf16(2 / sqrt(4 + 1e-6)) = 1.0
+    x = np.full((1, 1, 2 * D), 0x4000, np.uint16)  # bf16 2.0
+    w = np.full((2 * D,), 0x3F80, np.uint16)       # bf16 1.0
+    one, zero = np.ones((1, D // 2), np.float32), np.zeros((1, D // 2), np.float32)
+    out = oracle.norm_rope(x, w, one, zero, D)
+    assert (out == 0x3F80).all()
+    # a quarter turn maps each pair (y1, y2) to (-y2, y1) exactly
+    xb, wb, _, _ = _norm_rope_inputs(L=3)
+    c0, s1 = np.zeros((3, D // 2), np.float32), np.ones((3, D // 2), np.float32)
+    plain = oracle.norm_rope(bf16_bits(xb), bf16_bits(wb), np.ones_like(c0), c0, D)
+    turned = oracle.norm_rope(bf16_bits(xb), bf16_bits(wb), c0, s1, D)
+    pf, tf = oracle.bf16_bits_to_f32(plain), oracle.bf16_bits_to_f32(turned)
+    assert np.array_equal(tf[..., 0::2], -pf[..., 1::2]) and np.array_equal(tf[..., 1::2], pf[..., 0::2])
+
+
+def test_norm_rope_scale_invariance_and_torch(oracle):
+    """RMSNorm is invariant to scaling the row by a power of two (exactly, in floating point); the output
+    agrees with a float32 torch restatement of the two Triton kernels (whose only difference is the
+    reduction order of the mean of squares) on all but a handful of bf16 values, by at most one ulp."""
+    D = 128
+    x, w, cs, sn = _norm_rope_inputs()
+    a = oracle.norm_rope(bf16_bits(x), bf16_bits(w), cs, sn, D)
+    b = oracle.norm_rope(bf16_bits(x * 8), bf16_bits(w), cs, sn, D)
+    assert np.array_equal(a, b)
+    xf = x.float()
+    rstd = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)
+    y = ((xf * rstd) * w.float()).to(torch.bfloat16).float().reshape(1, 40, 2, D // 2, 2)
+    c, s = torch.from_numpy(cs)[None, :, None, :], torch.from_numpy(sn)[None, :, None, :]
+    o1 = torch.addcmul(y[..., 0] * c, -y[..., 1], s)
+    o2 = torch.addcmul(y[..., 1] * c, y[..., 0], s)
+    ref = bf16_bits(torch.stack([o1, o2], -1).reshape(1, 40, 2 * D))
+    diff = np.abs(oracle.bf16_bits_to_f32(a) - oracle.bf16_bits_to_f32(ref))
+    rel = diff / np.maximum(np.abs(oracle.bf16_bits_to_f32(ref)), 1e-30)
+    assert (a != ref).mean() < 0.01
+    assert rel.max() <= 2 ** -7
