@@ -118,6 +118,56 @@ def _stream_bench(steps: int = 20, warmup: int = 3) -> dict:
             "speedup": round(out["reference_dict"] / out["quantized_ring"], 3)}
 
 
+def _prologue_bench(reps: int = 10) -> dict:
+    """C2 shape, Q and K from the linear outputs to INT8: the reference's sequence (RMSNorm kernel, RoPE
+    kernel, then K mean + per-block quantization of the materialised bf16 Q/K; norm and rope as torch
+    fp32 ops here) against the fused prologue (row statistics, rotated-K mean, one quantizer launch)."""
+    import torch
+
+    from telefuser_amd import sageattn2 as sa
+    from telefuser_amd.prologue import norm_rope_quant_qk
+
+    B, L, H, D = 1, 32760, 12, 128
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(7)
+    xq, xk = (torch.randn((B, L, H * D), generator=g, device=dev).to(torch.bfloat16) for _ in range(2))
+    wq = wk = torch.ones(H * D, dtype=torch.bfloat16, device=dev)
+    ang = torch.rand((L, 1, D // 2), generator=g, device=dev, dtype=torch.float64) * 6.3
+    fc, fs = ang.cos(), ang.sin()
+    cs, sn = fc.reshape(1, L, 1, -1).float(), fs.reshape(1, L, 1, -1).float()
+
+    def unfused():
+        out = []
+        for x, w in ((xq, wq), (xk, wk)):
+            xf = x.float()
+            y = ((xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)) * w.float()).to(torch.bfloat16)
+            y = y.float().reshape(B, L, H, D // 2, 2)
+            o = torch.stack([y[..., 0] * cs - y[..., 1] * sn, y[..., 0] * sn + y[..., 1] * cs], -1)
+            out.append(o.reshape(B, L, H, D).to(torch.bfloat16))
+        km = sa.k_mean(out[1], "NHD")
+        return sa.per_block_int8(out[0], out[1], km, sm_scale=D ** -0.5, tensor_layout="NHD")
+
+    def fused():
+        return norm_rope_quant_qk(xq, xk, wq, wk, fc, fs, H)
+
+    res = {}
+    for name, f in (("unfused_ms", unfused), ("fused_ms", fused)):
+        for _ in range(2):
+            f()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            f()
+        b.record()
+        torch.cuda.synchronize()
+        res[name] = round(a.elapsed_time(b) / reps, 4)
+    bytes_min = 2 * B * L * H * D * 2 + 2 * B * L * H * D  # read bf16 Q and K once, write int8 Q and K
+    res["fused_GB/s_vs_single_pass_bytes"] = round(bytes_min / (res["fused_ms"] * 1e-3) / 1e9, 1)
+    res["workload"] = "wan2.1-1.3b_480p Q/K prologue (B=1, L=32760, H=12, D=128)"
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -127,6 +177,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-sdpa", action="store_true")
     ap.add_argument("--no-stream", action="store_true", help="skip the streaming KV-cache comparison")
+    ap.add_argument("--no-prologue", action="store_true", help="skip the fused-prologue comparison")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -254,6 +305,9 @@ def main() -> int:
     if not args.no_stream:
         print("[bench] streaming KV-cache comparison", file=sys.stderr, flush=True)
         line["streaming_kv_cache"] = _stream_bench()
+    if not args.no_prologue:
+        print("[bench] fused prologue comparison", file=sys.stderr, flush=True)
+        line["prologue"] = _prologue_bench()
     if not args.no_cpu_baseline:
         print("[bench] timing the CPU baseline", file=sys.stderr, flush=True)
         line["cpu_baseline"] = _cpu_baseline(cfg)
