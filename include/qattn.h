@@ -212,6 +212,15 @@ int qattn_v_fp8_cache_update(qattn_seq v, int dtype, int64_t B, int64_t fill, in
  * qattn_fwd_ex_num_splits (or pass an explicit num_splits >= it).
  */
 int qattn_fwd_ex_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int v_kind, int qk_quant_gran);
+/*
+ * Query blocks (128 rows) one workgroup of qattn_fwd_ex streams through a single K/V pipeline for an
+ * automatic-split call with these sizes (1 = one block per workgroup).  Short, non-causal FP8 P.V key
+ * ranges (at most 64 key tiles) over grids larger than the resident 512 workgroups use several, so the
+ * per-workgroup start-up and the epilogue overlap the next block's work; the result does not depend on
+ * it.  No counterpart in the reference (its launch is one CTA per query block).
+ */
+int qattn_fwd_ex_blocks_per_workgroup(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int v_kind, int qk_quant_gran,
+                                      int causal);
 int qattn_fwd_ex(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const void* v, int v_kind,
                  int64_t Lpad, const float* v_scale, qattn_seq o, int out_dtype, int64_t B, int64_t Lq, int64_t Lk,
                  int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int qk_quant_gran, int causal, int64_t q_offset,

@@ -33,6 +33,7 @@ EXPORTED = (
     "qattn_per_channel_fp8",
     "qattn_fwd_workspace_size",
     "qattn_fwd_num_splits",
+    "qattn_fwd_ex_blocks_per_workgroup",
     "qattn_fwd",
     "qattn_v_tile_half",
     "qattn_fwd_pv16",
@@ -93,6 +94,8 @@ def load() -> ctypes.CDLL:
     L.qattn_quant_qk_per_thread_int8.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, vp]
     L.qattn_fwd_ex_num_splits.argtypes = [i64, i64, i64, i64, i32, i32]
     L.qattn_fwd_ex_num_splits.restype = i32
+    L.qattn_fwd_ex_blocks_per_workgroup.argtypes = [i64, i64, i64, i64, i32, i32, i32]
+    L.qattn_fwd_ex_blocks_per_workgroup.restype = i32
     L.qattn_fwd_ex.argtypes = [S, vp, S, vp, vp, i32, i64, vp, S, i32, i64, i64, i64, i64, i64, i64, f32, i32, i32,
                                i64, vp, vp, i32, vp, sz, vp]
     L.qattn_fwd_block_sparse_num_splits.argtypes = [i64, i64, i64, i64]

@@ -43,6 +43,10 @@ constexpr int kNBuf = kPrefetch + 1;
 template <int PV> constexpr int ks_lds_floats() { return PV == 0 ? 7680 : 1536; }
 // block-sparse launches (half P.V only) stage the active tiles' ids next to their scales
 constexpr int kSpMaxTiles = 1024;
+// multi-block launches (one workgroup streams up to kMqMaxBlocks query blocks of one head through one
+// K/V pipeline): short key ranges only, so their k_scales and q_scales are staged whole in LDS
+constexpr int kMqMaxTiles = 64;
+constexpr int kMqMaxBlocks = 64;
 // per-thread K scales: 4 per 64-key tile (one per mma lane-pair class), otherwise 1
 constexpr int ks_per_tile(bool kt) { return kt ? 4 : 1; }
 constexpr int kBK = 64;
@@ -81,6 +85,8 @@ struct AttnParams {
   int group;
   int nsplit;
   int tiles_per_split;
+  int qpw;       // multi-block launches: query blocks per workgroup
+  int64_t nQC;   // multi-block launches: workgroups per (batch, head)
   int causal;
   float qk_mult;
 };
@@ -125,6 +131,23 @@ __device__ __forceinline__ void lds_dma16(uint32_t voff, v4u rsrc, uint32_t soff
       : "memory", "m0");
 }
 
+// two floats -> two round-to-nearest-even halves (bf16: v_cvt_pk_bf16_f32), low word first
+template <bool IS_FP16>
+__device__ __forceinline__ uint32_t pack_half2(float a, float b) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+  uint32_t r;
+  if constexpr (IS_FP16) {
+    const h2 v = __builtin_convertvector(f2{a, b}, h2);
+    __builtin_memcpy(&r, &v, 4);
+  } else {
+    const b2 v = __builtin_convertvector(f2{a, b}, b2);
+    __builtin_memcpy(&r, &v, 4);
+  }
+  return r;
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
 }
@@ -133,24 +156,41 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // P rounded to the half dtype of V x V as given (the Triton / SAGE_ATTN_2_8_16 style), fp32 accumulation.
 enum PvKind { PV_FP8 = 0, PV_BF16 = 1, PV_FP16 = 2 };
 
-template <bool IS_FP16_OUT, bool SPLIT, int PV, bool KT, bool SP = false>
+template <bool IS_FP16_OUT, bool SPLIT, int PV, bool KT, bool SP = false, bool MQ = false>
 __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(AttnParams p) {
   static_assert(!SP || (PV != PV_FP8 && !KT), "block-sparse launches use half P.V and per-block scales");
+  static_assert(!MQ || (PV == PV_FP8 && !SPLIT && !SP), "multi-block launches: FP8 P.V, no split, dense");
   constexpr int KS = ks_per_tile(KT);
   constexpr int kVBytes = PV == PV_FP8 ? 1 : 2;    // bytes per V element
   constexpr int kVDma = 2 * kVBytes;                // V DMA instructions per wave per tile
   constexpr float kOffset = PV == PV_FP8 ? kFp8Offset : 0.f;
   __shared__ __align__(16) uint8_t lds_k[kNBuf][kBK * kD];
   __shared__ __align__(16) uint8_t lds_v[kNBuf][kD * kBK * kVBytes];
-  __shared__ float lds_ks[SP ? kSpMaxTiles : ks_lds_floats<PV>()];  // k_scales of this workgroup's key tiles
+  __shared__ float lds_ks[SP ? kSpMaxTiles : MQ ? kMqMaxTiles * 4 : ks_lds_floats<PV>()];  // k_scales of its key tiles
+  // multi-block launches: a wave-private 4 KiB region per wave that receives the next query block's Q
+  // rows by DMA and then stages the finished block's O rows; and the q_scales of all its blocks
+  __shared__ __align__(16) uint8_t lds_qo[MQ ? 4 * 4096 : 16];
+  __shared__ float lds_qs[MQ ? kMqMaxBlocks * 32 : 1];
+  __shared__ __align__(16) float lds_vs[PV == PV_FP8 ? kD : 4];  // v_scale of this head (epilogue)
   __shared__ int16_t lds_tid[SP ? kSpMaxTiles : 1];                  // block-sparse: ids of the active tiles
   __shared__ int lds_nact;
 
   const int64_t tile_id = xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t qb = tile_id % p.nQB;
-  int64_t rest = tile_id / p.nQB;
-  const int split = (int)(rest % p.nsplit);
-  rest /= p.nsplit;
+  int64_t qb, qb_end;  // query blocks [qb, qb_end) of this workgroup
+  int64_t rest;
+  int split = 0;
+  if constexpr (MQ) {
+    qb = (tile_id % p.nQC) * p.qpw;
+    qb_end = min(p.nQB, qb + p.qpw);
+    rest = tile_id / p.nQC;
+  } else {
+    qb = tile_id % p.nQB;
+    qb_end = qb + 1;
+    rest = tile_id / p.nQB;
+    split = (int)(rest % p.nsplit);
+    rest /= p.nsplit;
+  }
+  const int64_t qb0 = qb;
   const int64_t h = rest % p.Hq;
   const int64_t b = rest / p.Hq;
   const int64_t hk = h / p.group;
@@ -159,7 +199,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   const int w = tid >> 6, lane = tid & 63, lq = lane & 31, hf = lane >> 5;
 
   // key range of this workgroup
-  const int64_t q_first = qb * kBQ;
+  int64_t q_first = qb * kBQ;
   int64_t kv_end = p.Lk;
   if (p.kv_valid) kv_end = min(kv_end, (int64_t)p.kv_valid[b]);
   if (p.causal) kv_end = min(kv_end, q_first + kBQ + p.q_offset);
@@ -195,13 +235,13 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
 
   // Q fragment (B operand of S^T = K.Q^T): lane owns query row lq of this wave, bytes
   // d = 32*m + 16*hf .. +16 for m = 0..3
-  const int64_t wrow0 = q_first + w * 32;
-  const int64_t qrow = wrow0 + lq;
+  int64_t wrow0 = q_first + w * 32;
+  int64_t qrow = wrow0 + lq;
   // Q fragments: the wave's 32 rows are read row-contiguously (8 lanes x 16 B per 128-byte row, full
   // cache lines) into a wave-private LDS stage, then each lane picks its MFMA B-operand bytes
   // d = 32 m + 16 hf .. +16 of row lq.  Stage rows are 128 B with the 16-byte chunk c stored at
   // chunk c ^ (row & 7), so both the row writes and the fragment reads are bank-conflict free.
-  uint8_t* stage = &lds_k[0][0] + w * 4096;  // 32 rows x 128 B per wave (lds_k is free here)
+  uint8_t* stage = (MQ ? &lds_qo[0] : &lds_k[0][0]) + w * 4096;  // 32 rows x 128 B per wave (lds_k is free here)
   v4i qf[4];
   {
     const int8_t* qbase = p.q8 + b * p.qsb + h * p.qsh;
@@ -228,17 +268,22 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   const int64_t qsi = p.qgran == QATTN_GRAN_THREAD ? (qb * 4 + w) * 8 + (lq & 7)
                       : p.qgran == QATTN_GRAN_WARP ? qb * 4 + w
                                                    : qb;
-  const float qs = p.q_scale[(b * p.Hq + h) * p.nQS + qsi] * p.qk_mult;
+  float qs = p.q_scale[(b * p.Hq + h) * p.nQS + qsi] * p.qk_mult;
+  // q_scale entries per query block, and this lane's entry within its block
+  const int qs_per = p.qgran == QATTN_GRAN_THREAD ? 32 : p.qgran == QATTN_GRAN_WARP ? 4 : 1;
+  const int qs_sub = p.qgran == QATTN_GRAN_THREAD ? w * 8 + (lq & 7) : p.qgran == QATTN_GRAN_WARP ? w : 0;
   const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
 
   // global -> LDS copies go through the LDS-DMA path (buffer_load_dwordx4 ... lds): lane j of a wave
   // writes the 16 bytes at LDS slot (wave base + 16 j), so the XOR swizzle is applied on the global
   // side: the lane that owns LDS slot (row, chunk c') fetches global chunk c = c' ^ swizzle(row).
   // Each wave moves 2 x 1 KiB of K and kVDma x 1 KiB of V per tile; no VGPRs are spent on staging.
-  // K rows at or past Lk fall outside the K buffer range and arrive as zeros (masked anyway).
+  // The K resource of a tile starts at the tile's first row, so K rows at or past Lk fall outside its
+  // range and arrive as zeros (masked anyway) without being read (the range check covers the
+  // per-lane offset, not the scalar one).
   const int8_t* kbase = p.k8 + b * p.ksb + hk * p.ksh;
   const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad * kVBytes;
-  const v4u krsrc = make_rsrc(kbase, (uint32_t)((p.Lk - 1) * p.ksl + kD));
+  const int64_t kbytes = (p.Lk - 1) * p.ksl + kD;
   const v4u vrsrc = make_rsrc(vbase, (uint32_t)((int64_t)kD * p.Lpad * kVBytes));
   // per-lane byte offsets relative to the tile start (first K row / first V column)
   uint32_t koff[2], voff[kVDma];
@@ -262,16 +307,37 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
       voff[i] = (uint32_t)(vd * p.Lpad * 2 + vc * 16);
     }
   }
-  const uint32_t k_step = (uint32_t)(kBK * p.ksl);
+  const int64_t k_step = kBK * p.ksl;
   const uint32_t lds_k0 = lds_addr(&lds_k[0][0]) + __builtin_amdgcn_readfirstlane(w) * 1024;
   const uint32_t lds_v0 = lds_addr(&lds_v[0][0]) + __builtin_amdgcn_readfirstlane(w) * 1024;
   auto dma_tile = [&](int64_t t, int buf) {
-    const uint32_t kso = (uint32_t)t * k_step, vso = (uint32_t)t * (kBK * kVBytes);
+    const int64_t kso = t * k_step;
+    const v4u krsrc = make_rsrc(kbase + kso, (uint32_t)(kbytes - kso));
+    const uint32_t vso = (uint32_t)t * (kBK * kVBytes);
     const uint32_t kl = lds_k0 + buf * (kBK * kD), vl = lds_v0 + buf * (kD * kBK * kVBytes);
 #pragma unroll
-    for (int i = 0; i < 2; i++) lds_dma16(koff[i], krsrc, kso, kl + i * 4096);
+    for (int i = 0; i < 2; i++) lds_dma16(koff[i], krsrc, 0, kl + i * 4096);
 #pragma unroll
     for (int i = 0; i < kVDma; i++) lds_dma16(voff[i], vrsrc, vso, vl + i * 4096);
+  };
+  // multi-block launches: the wave's 32 rows of the next query block go by DMA into its region of
+  // lds_qo, in the stage layout (LDS slot (r, c') receives global chunk c' ^ (r & 7)); the resource
+  // covers exactly the rows below Lq, the others arrive as zeros
+  uint32_t qoff[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int slot = i * 64 + lane, r = slot >> 3;
+    qoff[i] = (uint32_t)(r * p.qsl + (((slot & 7) ^ (r & 7)) << 4));
+  }
+  const int8_t* qhead = p.q8 + b * p.qsb + h * p.qsh;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  auto dma_q = [&](int64_t blk) {
+    const int64_t r0 = blk * kBQ + wu * 32;
+    const int64_t nr = min((int64_t)32, p.Lq - r0);
+    const v4u qr = make_rsrc(qhead + (nr > 0 ? r0 * p.qsl : 0), nr > 0 ? (uint32_t)((nr - 1) * p.qsl + kD) : 0u);
+    const uint32_t ql = lds_addr(&lds_qo[0]) + wu * 4096;
+#pragma unroll
+    for (int i = 0; i < 4; i++) lds_dma16(qoff[i], qr, 0, ql + i * 1024);
   };
 
   v16f o[4];
@@ -294,16 +360,109 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   } else {
     for (int64_t i = tid; i < (t_end - t_begin) * KS; i += kThreads) lds_ks[i] = ks_ptr[t_begin * KS + i];
   }
+  if constexpr (PV == PV_FP8 && !SPLIT)
+    if (tid < kD) lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * kD + tid];
+  if constexpr (MQ) {
+    const float* qsp = p.q_scale + (b * p.Hq + h) * p.nQS + qb0 * qs_per;
+    for (int64_t i = tid; i < (qb_end - qb0) * qs_per; i += kThreads) lds_qs[i] = qsp[i];
+  }
+  // The loop runs over (query block, key tile) pairs: a multi-block launch walks the same key tiles once
+  // per query block, and its DMA stream runs on across the block boundaries.
+  const int64_t n_kt = t_end - t_begin;
+  const int64_t total = MQ ? (qb_end - qb0) * n_kt : n_kt;
 #pragma unroll
   for (int d = 0; d < kPrefetch; d++)
-    if (t_begin + d < t_end) dma_tile(tile_of(t_begin + d), d);
+    if (d < total) dma_tile(tile_of(t_begin + (MQ ? d % n_kt : d)), d);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
+  // ---- epilogue of the current query block: O / l * v_scale out through the wave's LDS stage ----
+  auto finish = [&]() {
+    float l_tot;
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
+      l_tot = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+    if (SPLIT) {
+      if (qrow >= p.Lq) return;
+      const int64_t row = (((int64_t)split * p.B + b) * p.Hq + h) * p.Lq + qrow;
+      float* wo = p.ws_o + row * kD;
+#pragma unroll
+      for (int dblk = 0; dblk < 4; dblk++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int d = dblk * 32 + g * 8 + hf * 4;
+          *reinterpret_cast<v4f*>(wo + d) =
+              v4f{o[dblk][g * 4 + 0], o[dblk][g * 4 + 1], o[dblk][g * 4 + 2], o[dblk][g * 4 + 3]};
+        }
+      if (hf == 0) {
+        p.ws_ml[row * 2 + 0] = m_run;
+        p.ws_ml[row * 2 + 1] = l_tot;
+      }
+      return;
+    }
+    const float inv_l = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    // O goes out through the wave-private LDS stage (the K/V buffers are idle after the loop's last
+    // barrier; multi-block launches use their own region), 64 channels per pass, so that every row is
+    // stored as whole 128-byte lines
+    uint16_t* obase = static_cast<uint16_t*>(p.o) + b * p.osb + h * p.osh;
+#pragma unroll
+    for (int pass = 0; pass < 2; pass++) {
+#pragma unroll
+      for (int db = 0; db < 2; db++) {
+        const int dblk = pass * 2 + db;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int d = dblk * 32 + g * 8 + hf * 4;
+          const v4f sc = PV == PV_FP8 ? *reinterpret_cast<const v4f*>(&lds_vs[d]) : v4f{1.f, 1.f, 1.f, 1.f};
+          float f[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) f[e] = o[dblk][g * 4 + e] * inv_l * sc[e];
+          const v2u packed{pack_half2<IS_FP16_OUT>(f[0], f[1]), pack_half2<IS_FP16_OUT>(f[2], f[3])};
+          const int c = db * 4 + g;  // 16-byte chunk of the staged 128-byte row (8 channels)
+          *reinterpret_cast<v2u*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4) + hf * 8) = packed;
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int r = i * 8 + (lane >> 3), c = lane & 7;
+        const v4u val = *reinterpret_cast<const v4u*>(stage + r * 128 + ((c ^ (r & 7)) << 4));
+        const int64_t row = wrow0 + r;
+        if (row < p.Lq) *reinterpret_cast<v4u*>(obase + row * p.osl + pass * 64 + c * 8) = val;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    if (p.lse && hf == 0 && qrow < p.Lq)
+      p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
+  };
+  [[maybe_unused]] auto next_block = [&]() {
+    qb++;
+    q_first = qb * kBQ;
+    wrow0 = q_first + w * 32;
+    qrow = wrow0 + lq;
+    qs = lds_qs[(qb - qb0) * qs_per + qs_sub] * p.qk_mult;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) o[i][r] = 0.f;
+    m_run = kMInit;
+    l_run = 0.f;
+  };
+
   int buf = 0;
-  for (int64_t t = t_begin; t < t_end; t++) {
-    const bool issue = t + kPrefetch < t_end;
-    if (issue) dma_tile(tile_of(t + kPrefetch), buf == 0 ? kNBuf - 1 : buf - 1);
+  int64_t t = t_begin;                            // key slot being computed
+  int64_t pt = t_begin + (MQ && total > 0 ? kPrefetch % n_kt : kPrefetch);  // next slot to fetch
+  for (int64_t it = 0; it < total; it++) {
+    const bool issue = it + kPrefetch < total;
+    // (issued before this iteration's K/V DMA, so the iteration's final vmcnt wait covers it)
+    if constexpr (MQ)
+      if (t == 0 && qb + 1 < qb_end) dma_q(qb + 1);
+    if (issue) {
+      dma_tile(tile_of(pt), buf == 0 ? kNBuf - 1 : buf - 1);
+      pt++;
+      if (MQ && pt == t_end) pt = t_begin;
+    }
     // logit scale(s) of this lane: with per-thread K scales, key kappa of the tile belongs to class
     // (kappa % 8) / 2 = 2 hf + (r & 3) / 2 for accumulator element r, so a lane needs two of them
     float cs_a, cs_b;
@@ -337,14 +496,16 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
     const int64_t k0 = tile_of(t) * kBK;
     const bool masked = (k0 + kBK > kv_end) || (p.causal && k0 + kBK - 1 > wrow0 + p.q_offset);
     if (masked) {
-      const int64_t qlim = p.causal ? qrow + p.q_offset : INT64_MAX;
+      // element r of block kb holds key k0 + c + 4 hf with c = 32 kb + 8 (r / 4) + r % 4; it is masked
+      // when key >= kv_end or (causal) key > qrow + q_offset, i.e. when c >= lim for this lane's lim
+      int lim = (int)min(kv_end - k0, (int64_t)kBK);
+      if (p.causal) lim = min(lim, (int)max(min(qrow + p.q_offset + 1 - k0, (int64_t)kBK), (int64_t)-1));
+      lim -= hf * 4;
 #pragma unroll
       for (int kb = 0; kb < 2; kb++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int64_t key = k0 + kb * 32 + (r >> 2) * 8 + hf * 4 + (r & 3);
-          if (key >= kv_end || key > qlim) s[kb][r] = INT32_MIN;
-        }
+        for (int r = 0; r < 16; r++)
+          if (kb * 32 + (r >> 2) * 8 + (r & 3) >= lim) s[kb][r] = INT32_MIN;
     }
 
     // ---- online softmax ----
@@ -477,67 +638,34 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     buf = buf + 1 == kNBuf ? 0 : buf + 1;
-  }
-
-  // ---- epilogue ----
-  float l_tot;
-  {
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
-    l_tot = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-  }
-  if (SPLIT) {
-    if (qrow >= p.Lq) return;
-    const int64_t row = (((int64_t)split * p.B + b) * p.Hq + h) * p.Lq + qrow;
-    float* wo = p.ws_o + row * kD;
+    t++;
+    if constexpr (MQ) {
+      if (t == t_end && qb + 1 < qb_end) {
+        // block boundary: the next block's Q rows (landed with this iteration's wait) leave the region
+        // before the finished block's O goes out through it
+        v4i qn[4];
 #pragma unroll
-    for (int dblk = 0; dblk < 4; dblk++)
+        for (int m = 0; m < 4; m++) {
+          const int c = 2 * m + hf;
+          qn[m] = *reinterpret_cast<const v4i*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4));
+        }
+        finish();
 #pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const int d = dblk * 32 + g * 8 + hf * 4;
-        *reinterpret_cast<v4f*>(wo + d) =
-            v4f{o[dblk][g * 4 + 0], o[dblk][g * 4 + 1], o[dblk][g * 4 + 2], o[dblk][g * 4 + 3]};
-      }
-    if (hf == 0) {
-      p.ws_ml[row * 2 + 0] = m_run;
-      p.ws_ml[row * 2 + 1] = l_tot;
-    }
-    return;
-  }
-  const float inv_l = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  const float* vs = PV == PV_FP8 ? p.v_scale + (b * p.Hkv + hk) * kD : nullptr;
-  // O goes out through the same wave-private LDS stage (the K/V buffers are idle after the loop's last
-  // barrier), 64 channels per pass, so that every row is stored as whole 128-byte lines
-  uint16_t* obase = static_cast<uint16_t*>(p.o) + b * p.osb + h * p.osh;
-#pragma unroll
-  for (int pass = 0; pass < 2; pass++) {
-#pragma unroll
-    for (int db = 0; db < 2; db++) {
-      const int dblk = pass * 2 + db;
-#pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const int d = dblk * 32 + g * 8 + hf * 4;
-        const v4f sc = PV == PV_FP8 ? *reinterpret_cast<const v4f*>(vs + d) : v4f{1.f, 1.f, 1.f, 1.f};
-        uint16_t hv[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) hv[e] = f32_to_half<IS_FP16_OUT>(o[dblk][g * 4 + e] * inv_l * sc[e]);
-        v2u packed;
-        __builtin_memcpy(&packed, hv, 8);
-        const int c = db * 4 + g;  // 16-byte chunk of the staged 128-byte row (8 channels)
-        *reinterpret_cast<v2u*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4) + hf * 8) = packed;
+        for (int m = 0; m < 4; m++) qf[m] = qn[m];
+        next_block();
+        t = t_begin;
       }
     }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int r = i * 8 + (lane >> 3), c = lane & 7;
-      const v4u val = *reinterpret_cast<const v4u*>(stage + r * 128 + ((c ^ (r & 7)) << 4));
-      const int64_t row = wrow0 + r;
-      if (row < p.Lq) *reinterpret_cast<v4u*>(obase + row * p.osl + pass * 64 + c * 8) = val;
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
-  if (p.lse && hf == 0 && qrow < p.Lq)
-    p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
+  if constexpr (MQ) {
+    // no key tiles at all (kv_valid 0): every block of the workgroup gets the empty-row output
+    if (total == 0)
+      while (qb + 1 < qb_end) {
+        finish();
+        next_block();
+      }
+  }
+  finish();
 }
 
 // Merge the KV-split partials: one wave per query row, 2 channels per lane.
@@ -603,6 +731,17 @@ extern "C" int qattn_fwd_ex_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_
   return num_splits_for(B, Lq, Lk, Hq, max_tiles_per_split(v_kind, qk_quant_gran == QATTN_GRAN_THREAD));
 }
 
+static int blocks_per_workgroup(int64_t bh, int64_t nqb, int64_t nkb);
+
+extern "C" int qattn_fwd_ex_blocks_per_workgroup(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int v_kind,
+                                                 int qk_quant_gran, int causal) {
+  if (v_kind != QATTN_V_FP8 || causal || B <= 0 || Lq <= 0 || Lk <= 0 || Hq <= 0) return 1;
+  const int64_t nkb = (Lk + kBK - 1) / kBK, nqb = (Lq + kBQ - 1) / kBQ;
+  if (nkb > kMqMaxTiles) return 1;
+  if (num_splits_for(B, Lq, Lk, Hq, max_tiles_per_split(PV_FP8, qk_quant_gran == QATTN_GRAN_THREAD)) != 1) return 1;
+  return blocks_per_workgroup(B * Hq, nqb, nkb);
+}
+
 extern "C" size_t qattn_fwd_workspace_size(int64_t B, int64_t Lq, int64_t Hq, int64_t D, int num_splits) {
   if (num_splits <= 1) return 0;
   return (size_t)num_splits * B * Hq * Lq * (D + 2) * sizeof(float);
@@ -611,6 +750,18 @@ extern "C" size_t qattn_fwd_workspace_size(int64_t B, int64_t Lq, int64_t Hq, in
 template <int PV, bool KT, bool SP = false>
 static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, size_t workspace_bytes, hipStream_t st,
                       int64_t D) {
+  if constexpr (PV == PV_FP8 && !SP) {
+    if (ns == 1 && p.qpw > 1) {
+      p.nsplit = 1;
+      p.tiles_per_split = (int)p.nKB;
+      p.nQC = (p.nQB + p.qpw - 1) / p.qpw;
+      const int64_t g = p.B * p.Hq * p.nQC;
+      QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
+      if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, false, PV, KT, false, true><<<g, kThreads, 0, st>>>(p);
+      else qattn_fwd_kernel<true, false, PV, KT, false, true><<<g, kThreads, 0, st>>>(p);
+      return check_launch("qattn_fwd");
+    }
+  }
   const int64_t grid = p.B * p.Hq * p.nQB * ns;
   QATTN_REQUIRE(grid < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
   p.nsplit = ns;
@@ -631,6 +782,26 @@ static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, siz
     else qattn_fwd_kernel<true, false, PV, KT, SP><<<grid, kThreads, 0, st>>>(p);
   }
   return check_launch("qattn_fwd");
+}
+
+// Short key ranges: one workgroup streams several query blocks of a head through one K/V pipeline, so
+// the per-workgroup start-up (Q load, scale staging, first DMA round trip) and the epilogue overlap the
+// next block's work.  Picks the blocks per workgroup that minimise the modelled makespan: full rounds
+// of 512 resident workgroups (256 CUs x 2), each block costing its key tiles plus about one tile of
+// epilogue, each workgroup about four tiles of start-up.
+static int blocks_per_workgroup(int64_t bh, int64_t nqb, int64_t nkb) {
+  int best = 1;
+  double best_cost = 1e300;
+  for (int64_t q = 1; q <= std::min<int64_t>(nqb, kMqMaxBlocks); q++) {
+    const int64_t wgs = bh * ((nqb + q - 1) / q);
+    const int64_t rounds = (wgs + 511) / 512;
+    const double cost = (double)rounds * (double)(q * (nkb + 1) + 4);
+    if (cost < best_cost) {
+      best_cost = cost;
+      best = (int)q;
+    }
+  }
+  return best;
 }
 
 static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale,
@@ -689,6 +860,9 @@ static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale,
   if (ns < 1) ns = 1;
   // a workgroup stages the k_scales of at most max_tiles key tiles
   ns = (int)std::max<int64_t>(ns, (p.nKB + max_tiles - 1) / max_tiles);
+  p.qpw = 1;
+  if (ns == 1 && !sparse && !causal && pv == PV_FP8 && p.nKB <= kMqMaxTiles && q8.sl >= kD)
+    p.qpw = blocks_per_workgroup(B * Hq, p.nQB, p.nKB);
   return QATTN_OK;
 }
 

@@ -360,3 +360,62 @@ def test_block_sparse(oracle, case):
     assert not og[0, :min(128, Lq), :rep].any()  # query block 0 of kv head 0 had no tiles
     assert c >= COS_KERNEL
     assert ct >= COS_E2E
+
+
+@pytest.mark.parametrize("case", ["block_nhd_bf16", "thread_hnd_fp16"])
+def test_multi_block_workgroups(oracle, case):
+    """Short key ranges over a large grid run several query blocks per workgroup through one K/V pipeline.
+    The per-block arithmetic is unchanged, so every head must match, bit for bit, a launch of a few heads
+    (small grid: one block per workgroup) on the same quantized operands; one (batch, head) is also checked
+    against the oracle.  Covers key padding down to zero keys, a ragged last query block and the lse."""
+    dev = require_gpu()
+    from telefuser_amd import _lib
+    from telefuser_amd import sageattn2 as sa
+
+    gran, layout, dt = ("per_block", "NHD", torch.bfloat16) if case == "block_nhd_bf16" else \
+        ("per_thread", "HND", torch.float16)
+    B, Lq, Lk, H, D = 2, 16300, 500, 20, 128
+    kv_valid = [300, 0]
+    L = _lib.load()
+    qpw = L.qattn_fwd_ex_blocks_per_workgroup(B, Lq, Lk, H, 0, GRAN_CODE[gran], 0)
+    log(f"multi-block {case}: B={B} Lq={Lq} Lk={Lk} H={H} kv_valid={kv_valid} blocks/workgroup={qpw}")
+    assert qpw > 1
+    assert L.qattn_fwd_ex_blocks_per_workgroup(1, 256, Lk, 2, 0, GRAN_CODE[gran], 0) == 1
+    g = torch.Generator(device=dev).manual_seed(41)
+    shape = (B, Lq, H, D) if layout == "NHD" else (B, H, Lq, D)
+    kshape = (B, Lk, H, D) if layout == "NHD" else (B, H, Lk, D)
+    q = torch.randn(shape, generator=g, device=dev).to(dt)
+    k = (torch.randn(kshape, generator=g, device=dev) + 0.5).to(dt)
+    v = torch.randn(kshape, generator=g, device=dev).to(dt)
+    km = sa.k_mean(k, layout)
+    qk_mult = 1.0
+    if gran == "per_block":
+        q8, qs, k8, ks = sa.per_block_int8(q, k, km, sm_scale=D ** -0.5, tensor_layout=layout)
+    else:
+        q8, qs, k8, ks = sa.per_thread_int8(q, k, km, tensor_layout=layout)
+        qk_mult = D ** -0.5 * LOG2E
+    v8, vs, _ = sa.per_channel_fp8(v, tensor_layout=layout)
+    kw = dict(tensor_layout=layout, out_dtype=dt, kv_valid_len=kv_valid, return_lse=True, qk_mult=qk_mult,
+              qk_quant_gran=gran)
+    o, lse = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
+    hd = 2 if layout == "NHD" else 1
+    heads = [0, 7, 19]
+    idx = torch.tensor(heads, device=dev)
+    sel = lambda t, d: t.view(torch.uint8).index_select(d, idx).view(t.dtype) if t.dtype == torch.float8_e4m3fn \
+        else t.index_select(d, idx).contiguous()
+    o3, lse3 = sa.qattn_fwd(sel(q8, hd), sel(qs, 1), sel(k8, hd), sel(ks, 1), sel(v8, 1), sel(vs, 1), **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(sel(o, hd), o3), "multi-block output differs from the one-block-per-workgroup launch"
+    assert torch.equal(sel(lse, 1), lse3)
+    assert bool((o.select(0, 1) == 0).all()) and bool(torch.isneginf(lse[1]).all())
+    # batch 0, head 7 against the oracle on the same quantized operands
+    pick = lambda t: (t[:1, :, 7:8] if layout == "NHD" else t[:1, 7:8].transpose(1, 2)).contiguous().cpu().numpy()
+    ref, ref_lse = oracle.qattn_fwd(pick(q8), qs[:1, 7:8].cpu().numpy(), pick(k8), ks[:1, 7:8].cpu().numpy(),
+                                    v8=untile_v(v8[:1, 7:8]), v_scale=vs[:1, 7:8].cpu().numpy(),
+                                    kv_valid=kv_valid[:1], want_lse=True, lazy_tau=KERNEL_LAZY_TAU, qk_mult=qk_mult,
+                                    q_gran=GRAN_CODE[gran], k_gran=GRAN_CODE[gran])
+    og = pick(o.float())
+    c = cosine(og, ref)
+    log(f"  head 7 vs quantized oracle: cosine={c:.6f} max_abs={float(np.abs(og - ref).max()):.4g}")
+    assert c >= COS_KERNEL
+    assert float(np.max(np.abs(lse[:1, 7:8].cpu().numpy() - ref_lse))) < 2e-2
