@@ -108,8 +108,16 @@ __global__ __launch_bounds__(kQuantThreads) void quant_per_block_kernel(QuantArg
     j = 1;
   }
   const QuantJob& J = args.job[j];
-  const int64_t n = wg % J.nblk;
-  const int64_t h = (wg / J.nblk) % J.H;
+  // Heads interleaved inside a row (sequence-major layouts): the heads of one row block run next to
+  // each other, so concurrent workgroups read contiguous row segments; head-major layouts walk blocks.
+  int64_t n, h;
+  if (J.sh < J.sl) {
+    h = wg % J.H;
+    n = (wg / J.H) % J.nblk;
+  } else {
+    n = wg % J.nblk;
+    h = (wg / J.nblk) % J.H;
+  }
   const int64_t b = wg / (J.nblk * J.H);
   const int tid = threadIdx.x;
   const int nchunks = J.blk * TPR;
