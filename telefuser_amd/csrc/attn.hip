@@ -152,6 +152,17 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
 }
 
+// Row sums of P on the matrix pipe (FP8 P.V): D += ONES . P^T with ONES the all-ones 32 x 64 matrix in
+// fp4 (e2m1 1.0 = 0x2 per nibble, so the A operand takes 4 VGPRs) and P^T the e4m3 B operand of the
+// P.V MFMA: every row of the 32 x 32 result is the column sum of P^T, so each lane's 16 accumulators all
+// hold the running sum l of its query column (both key halves).  l is thus the sum of the e4m3-rounded P
+// (the reference's accumulate_d sums p before rounding; the difference is the mean FP8 rounding error of
+// P, far inside the attention tolerance), and 32 VALU adds per tile leave the softmax.
+__device__ __forceinline__ v16f row_sum_mfma(const v16f& acc, const v8i& pf) {
+  const v8i ones = {0x22222222, 0x22222222, 0x22222222, 0x22222222, 0, 0, 0, 0};
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, pf, acc, 4, 0, 0, 0, 0, 0);
+}
+
 // P.V flavours: e4m3 P x e4m3 V (the reference's fp8 kernel, with the 8.807 offset and v_scale), or
 // P rounded to the half dtype of V x V as given (the Triton / SAGE_ATTN_2_8_16 style), fp32 accumulation.
 enum PvKind { PV_FP8 = 0, PV_BF16 = 1, PV_FP16 = 2 };
@@ -346,6 +357,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
 #pragma unroll
     for (int r = 0; r < 16; r++) o[i][r] = 0.f;
   float m_run = kMInit, l_run = 0.f;
+  v16f lacc;  // FP8 P.V: row sums of P on the matrix pipe (row_sum_mfma); l_run for the half P.V kinds
+#pragma unroll
+  for (int r = 0; r < 16; r++) lacc[r] = 0.f;
   v16i kbias;
 #pragma unroll
   for (int r = 0; r < 16; r++) kbias[r] = kAccBiasBits;
@@ -379,7 +393,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   // ---- epilogue of the current query block: O / l * v_scale out through the wave's LDS stage ----
   auto finish = [&]() {
     float l_tot;
-    {
+    if constexpr (PV == PV_FP8) {
+      l_tot = lacc[0];
+    } else {
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
       l_tot = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     }
@@ -448,6 +464,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
       for (int r = 0; r < 16; r++) o[i][r] = 0.f;
     m_run = kMInit;
     l_run = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) lacc[r] = 0.f;
   };
 
   int buf = 0;
@@ -550,6 +568,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[i][r] *= alpha;
+      if constexpr (PV == PV_FP8)
+#pragma unroll
+        for (int r = 0; r < 16; r++) lacc[r] *= alpha;
       m_run = m_new;
     }
     const float nc_a = -fmaf(kAccBias, cs_a, m_run), nc_b = -fmaf(kAccBias, cs_b, m_run);
@@ -567,18 +588,15 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
     if constexpr (PV == PV_FP8) {
       v8i pf;  // P^T as the e4m3 B operand: byte s of the lane = slot s = 16 kb + r
       auto body = [&](auto mk) {
-        float lsum = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
           float pv[4];
           p4(j, pv, mk);
-          lsum += (pv[0] + pv[1]) + (pv[2] + pv[3]);
           // the low word is written first; the old contents of pf[j] only fill bits that the second
           // conversion overwrites, so no zeroed register is needed
           const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], pf[j], false);
           pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
         }
-        l_run += lsum;
       };
       if (masked) body(std::true_type{});
       else body(std::false_type{});
@@ -595,6 +613,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
 #pragma unroll
       for (int dblk = 0; dblk < 4; dblk++)
         o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, o[dblk], 0, 0, 0, 0, 0, 0);
+      lacc = row_sum_mfma(lacc, pf);
     } else {
       // P^T in the half dtype: chunk c (16 keys of the MFMA's K dimension) = slots 8c .. 8c+7
       typedef __attribute__((ext_vector_type(8))) __bf16 v8bf;
@@ -666,6 +685,548 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
       }
   }
   finish();
+}
+
+// ---- wide workgroups: 64 query rows per wave, one wave per SIMD ----
+//
+// qattn_fwd_kernel gives each wave 32 query rows, so every wave reads the whole 16 KiB K/V tile from
+// LDS per 1 M MFMA ops, and the dependent chain Q.K^T -> softmax -> P.V of one tile leaves the matrix
+// pipe idle during the softmax unless the other wave of the SIMD happens to be in another phase.
+// This kernel gives each wave 64 rows as two 32-row halves A and B (256 rows per workgroup, one
+// workgroup per CU, up to 512 registers per wave) and software-pipelines the halves against each other:
+//
+//   phase 1 of tile i:  VALU softmax_A(i)   ||  MFMA  Q_B.K(i)^T,  P_B(i-1).V(i-1),  rowsum P_B(i-1)
+//   phase 2 of tile i:  VALU softmax_B(i)   ||  MFMA  rowsum P_A(i),  Q_A.K(i+1)^T,  P_A(i).V(i)
+//
+// so each phase pairs ~600 cycles of softmax VALU work with 576 cycles of independent MFMA work,
+// interleaved slot by slot (scheduling fences between slots).  K(i+1) and V(i) are read from LDS into
+// registers once, in the last slots of phase 1 (after the MFMAs that used K(i) and V(i-1)), and feed
+// both halves (Q_A.K(i+1)^T and P_A(i).V(i) in phase 2, then Q_B.K(i+1)^T and P_B(i).V(i) in the next
+// phase 1), which halves the LDS reads per MFMA op and leaves phase 2 with its operands in registers.
+// Per element the arithmetic is the one
+// of qattn_fwd_kernel (same lazy running max, FP8 offset, P rounding, row sums on the matrix pipe and
+// accumulation order), so both kernels give identical results.
+//
+// K/V tiles come in by LDS DMA, three buffers each, two iterations ahead: the barrier that starts
+// iteration i makes K(i+1) and V(i) visible and frees the buffers of K(i) and V(i-1), which then
+// receive K(i+3) and V(i+2).
+// Only key tiles with no masked key for any row of the workgroup run pipelined; the rest (a tail tile,
+// a causal diagonal, short key ranges) go through a plain per-tile loop.
+constexpr int kWideRows = 256;         // query rows per workgroup
+constexpr int kWideKsFloats = 16384;   // k_scales staged per workgroup (64 KiB)
+
+// o *= a for a 16-register tuple held in AGPRs, in place (read, multiply, write back one register at a
+// time), so the tuple never needs a VGPR copy
+__device__ __forceinline__ void agpr_scale16(v16f& o, float a) {
+  float t;
+#define QATTN_AS(i) "v_accvgpr_read_b32 %[t], %[o" #i "]\n\tv_mul_f32 %[t], %[t], %[a]\n\tv_accvgpr_write_b32 %[o" #i "], %[t]\n\t"
+  asm volatile(QATTN_AS(0) QATTN_AS(1) QATTN_AS(2) QATTN_AS(3) QATTN_AS(4) QATTN_AS(5) QATTN_AS(6) QATTN_AS(7)
+                   QATTN_AS(8) QATTN_AS(9) QATTN_AS(10) QATTN_AS(11) QATTN_AS(12) QATTN_AS(13) QATTN_AS(14) QATTN_AS(15)
+               : [t] "=&v"(t), [o0] "+a"(o[0]), [o1] "+a"(o[1]), [o2] "+a"(o[2]), [o3] "+a"(o[3]), [o4] "+a"(o[4]),
+                 [o5] "+a"(o[5]), [o6] "+a"(o[6]), [o7] "+a"(o[7]), [o8] "+a"(o[8]), [o9] "+a"(o[9]),
+                 [o10] "+a"(o[10]), [o11] "+a"(o[11]), [o12] "+a"(o[12]), [o13] "+a"(o[13]), [o14] "+a"(o[14]),
+                 [o15] "+a"(o[15])
+               : [a] "v"(a));
+#undef QATTN_AS
+}
+
+template <bool KT>
+struct WideHalf {
+  v16f o[4];
+  v16f lacc;
+  v16i s[2];
+  v8i pf;
+  v4i qf[4];
+  float qs;      // q_scale x qk_mult of this lane's row
+  float m;       // running max (log2 domain, offset included)
+  float alpha;   // pending O rescale
+  bool grew;     // some lane of the wave moved m with the last softmax
+};
+
+// (the body is a device function so that its lambdas are never instantiated by the host pass)
+template <bool IS_FP16_OUT, bool KT>
+__device__ __forceinline__ void qattn_fwd_wide(const AttnParams& p) {
+  constexpr int KS = ks_per_tile(KT);
+  __shared__ __align__(16) uint8_t lds_kv[2 * kNBuf * kBK * kD];  // K buffers 0..2, then V buffers 0..2
+  __shared__ float lds_ks[kWideKsFloats];
+  __shared__ __align__(16) float lds_vs[kD];
+  uint8_t* const lds_k = lds_kv;
+  uint8_t* const lds_v = lds_kv + kNBuf * kBK * kD;
+
+  const int64_t nQW = (p.Lq + kWideRows - 1) / kWideRows;
+  const int64_t tile_id = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t qw = tile_id % nQW;
+  const int64_t rest = tile_id / nQW;
+  const int64_t h = rest % p.Hq;
+  const int64_t b = rest / p.Hq;
+  const int64_t hk = h / p.group;
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, lane = tid & 63, lq = lane & 31, hf = lane >> 5;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+
+  const int64_t q_first = qw * kWideRows;
+  int64_t kv_end = p.Lk;
+  if (p.kv_valid) kv_end = min(kv_end, (int64_t)p.kv_valid[b]);
+  if (p.causal) kv_end = min(kv_end, q_first + kWideRows + p.q_offset);
+  const int64_t n_tiles = kv_end > 0 ? (kv_end + kBK - 1) / kBK : 0;
+  const int64_t R0 = q_first + w * 64;  // first row of half A; half B starts at R0 + 32
+
+  WideHalf<KT> A, B;
+  // Q fragments of both halves through a wave-private 8 KiB stage (row-contiguous 128-byte loads; the
+  // 16-byte chunk c of stage row r sits at chunk c ^ (r & 7))
+  {
+    uint8_t* stage = lds_kv + w * 8192;
+    const int8_t* qbase = p.q8 + b * p.qsb + h * p.qsh;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int r = i * 8 + (lane >> 3), c = lane & 7;
+      const int64_t row = R0 + r;
+      const v4i val = row < p.Lq ? *reinterpret_cast<const v4i*>(qbase + row * p.qsl + c * 16) : v4i{0, 0, 0, 0};
+      *reinterpret_cast<v4i*>(stage + r * 128 + ((c ^ (r & 7)) << 4)) = val;
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    // straight into AGPRs: the Q fragments are only ever read by the QK MFMAs
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      const int c = 2 * m + hf;
+      const uint32_t a0 = lds_addr(stage) + (uint32_t)(lq * 128 + ((c ^ (lq & 7)) << 4));
+      asm volatile("ds_read_b128 %0, %1" : "=a"(A.qf[m]) : "v"(a0) : "memory");
+      asm volatile("ds_read_b128 %0, %1 offset:4096" : "=a"(B.qf[m]) : "v"(a0) : "memory");
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+a"(A.qf[0]), "+a"(A.qf[1]), "+a"(A.qf[2]), "+a"(A.qf[3]), "+a"(B.qf[0]),
+                 "+a"(B.qf[1]), "+a"(B.qf[2]), "+a"(B.qf[3])::"memory");
+  }
+  // q_scale of this lane's row in each half: per 128-row block, per 32-row warp block or per row class
+  auto qscale = [&](int64_t R) -> float {
+    const int64_t Rc = min(R, p.Lq - 1);  // rows past Lq compute on zeros and are never stored
+    const int64_t qsi = p.qgran == QATTN_GRAN_THREAD ? (Rc / 32) * 8 + (lq & 7)
+                        : p.qgran == QATTN_GRAN_WARP ? Rc / 32
+                                                     : Rc / kBQ;
+    return p.q_scale[(b * p.Hq + h) * p.nQS + qsi] * p.qk_mult;
+  };
+  A.qs = qscale(R0);
+  B.qs = qscale(R0 + 32);
+  auto init_half = [&](WideHalf<KT>& X) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) X.o[i][r] = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) X.lacc[r] = 0.f;
+    X.m = kMInit;
+    X.alpha = 1.f;
+    X.grew = false;
+  };
+  init_half(A);
+  init_half(B);
+  v16i kbias;
+#pragma unroll
+  for (int r = 0; r < 16; r++) kbias[r] = kAccBiasBits;
+  asm volatile("" : "+v"(kbias));  // keep the bias in VGPRs (MFMA srcC), not rematerialised per use
+
+  __syncthreads();  // Q stage reads done before the DMA reuses the region
+  const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
+  for (int64_t i = tid; i < n_tiles * KS; i += kThreads) lds_ks[i] = ks_ptr[i];
+  if (tid < kD) lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * kD + tid];
+
+  // DMA: per-lane offsets relative to the tile start, as in qattn_fwd_kernel
+  const int8_t* kbase = p.k8 + b * p.ksb + hk * p.ksh;
+  const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad;
+  const int64_t kbytes = (p.Lk - 1) * p.ksl + kD;
+  const v4u vrsrc = make_rsrc(vbase, (uint32_t)((int64_t)kD * p.Lpad));
+  uint32_t koff[2], voff[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int slot = (i * 4 + w) * 64 + lane;
+    const int kr = slot >> 3;
+    const int kc = (slot & 7) ^ ((kr >> 1) & 7);
+    koff[i] = (uint32_t)(kr * p.ksl + kc * 16);
+    const int vd = slot >> 2;
+    const int vc = (slot & 3) ^ ((vd >> 2) & 3);
+    voff[i] = (uint32_t)(vd * p.Lpad + vc * 16);
+  }
+  const int64_t k_step = kBK * p.ksl;
+  const uint32_t lds_k0 = lds_addr(lds_k) + wu * 1024;
+  const uint32_t lds_v0 = lds_addr(lds_v) + wu * 1024;
+  auto dma_k = [&](int64_t t, int kb) {
+    const int64_t kso = t * k_step;
+    const v4u krsrc = make_rsrc(kbase + kso, (uint32_t)(kbytes - kso));
+#pragma unroll
+    for (int j = 0; j < 2; j++) lds_dma16(koff[j], krsrc, 0, lds_k0 + kb * (kBK * kD) + j * 4096);
+  };
+  auto dma_v = [&](int64_t t, int vb) {
+#pragma unroll
+    for (int j = 0; j < 2; j++) lds_dma16(voff[j], vrsrc, (uint32_t)t * kBK, lds_v0 + vb * (kD * kBK) + j * 4096);
+  };
+  auto read_k = [&](int kb, int j) -> v4i {
+    return *reinterpret_cast<const v4i*>(lds_k + kb * (kBK * kD) + k_lds_off((j & 1) * 32 + lq, 2 * (j >> 1) + hf));
+  };
+  auto read_v = [&](int vb, int dblk) -> v8i {
+    const int d = dblk * 32 + lq;
+    const v4i a0 = *reinterpret_cast<const v4i*>(lds_v + vb * (kD * kBK) + v_lds_off(d, 2 * hf));
+    const v4i a1 = *reinterpret_cast<const v4i*>(lds_v + vb * (kD * kBK) + v_lds_off(d, 2 * hf + 1));
+    return v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+  };
+  // The QK MFMAs go through inline asm so that the logits land in VGPRs (the softmax reads them there);
+  // the P.V and row-sum MFMAs are builtins, whose accumulators (O, l) the compiler keeps in AGPRs.  The
+  // compiler sees no MFMA in the asm, so it inserts no wait states after it: every VALU read of a logit
+  // is either a phase or more behind its MFMA or preceded by drain_s().
+  auto qk_mfma = [&](WideHalf<KT>& X, const v4i (&kf)[8], int j) {
+    if (j < 2)
+      asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %3" : "=&v"(X.s[j & 1]) : "v"(kf[j]), "a"(X.qf[j >> 1]), "v"(kbias));
+    else
+      asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(X.s[j & 1]) : "v"(kf[j]), "a"(X.qf[j >> 1]));
+  };
+  auto pv_mfma = [&](WideHalf<KT>& X, const v8i (&vf)[4], int d) {
+    X.o[d] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[d], X.pf, X.o[d], 0, 0, 0, 0, 0, 0);
+  };
+  auto rsum_mfma = [&](WideHalf<KT>& X) { X.lacc = row_sum_mfma(X.lacc, X.pf); };
+  // 24 wait states after the last MFMA: covers a 16-pass MFMA result read by the VALU or by
+  // v_accvgpr_read.  The results are threaded through the asm so no read is scheduled above it.
+  auto drain_s = [](WideHalf<KT>& X) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(X.s[0]), "+v"(X.s[1]));
+  };
+  auto drain_o = [](WideHalf<KT>& X) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+                 : "+a"(X.o[0]), "+a"(X.o[1]), "+a"(X.o[2]), "+a"(X.o[3]), "+a"(X.lacc));
+  };
+  // LDS reads of K/V fragments complete before an MFMA reads them: the compiler's wait-count pass does not
+  // see the register uses of the inline-asm MFMAs, so the wait is explicit and threads the fragments
+  auto lds_wait_k = [](v4i (&kf)[8]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3]), "+v"(kf[4]), "+v"(kf[5]), "+v"(kf[6]), "+v"(kf[7])
+                 :: "memory");
+  };
+  auto lds_wait_v = [](v8i (&vf)[4]) {
+    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vf[0]), "+v"(vf[1]), "+v"(vf[2]), "+v"(vf[3])::"memory");
+  };
+  auto rescale = [&](WideHalf<KT>& X) {
+    drain_o(X);
+#pragma unroll
+    for (int d = 0; d < 4; d++) agpr_scale16(X.o[d], X.alpha);
+    agpr_scale16(X.lacc, X.alpha);
+    // AGPR writes before the next MFMA reads them as srcC
+    asm volatile("s_nop 3" : "+a"(X.o[0]), "+a"(X.o[1]), "+a"(X.o[2]), "+a"(X.o[3]), "+a"(X.lacc));
+  };
+  auto scales = [&](const WideHalf<KT>& X, int64_t t, float& cs_a, float& cs_b) {
+    if constexpr (KT) {
+      cs_a = X.qs * lds_ks[t * 4 + 2 * hf];
+      cs_b = X.qs * lds_ks[t * 4 + 2 * hf + 1];
+    } else {
+      cs_a = cs_b = X.qs * lds_ks[t];
+    }
+  };
+  // softmax of an unmasked tile in chunks: c0 / c1 row max (c1 also moves m lazily and sets alpha),
+  // c2..c9 exp2 and e4m3 packing of 4 logits of each lane
+  struct SmState { int mx, ma, mb; float cs_a, cs_b, nc_a, nc_b; };
+  auto sm_chunk = [&](WideHalf<KT>& X, SmState& st, int c) {
+    if (c <= 1) {
+      const int kb = c;
+      if constexpr (!KT) {
+        int m0 = kb == 0 ? max(X.s[0][0], X.s[0][1]) : max(st.mx, X.s[1][0]);
+#pragma unroll
+        for (int r = kb == 0 ? 2 : 1; r < 16; r++) m0 = max(m0, X.s[kb][r]);
+        st.mx = m0;
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          if ((r & 3) < 2) st.ma = max(st.ma, X.s[kb][r]);
+          else st.mb = max(st.mb, X.s[kb][r]);
+        }
+      }
+      if (c == 1) {
+        float m_tile;
+        if constexpr (!KT) {
+          const auto sw = __builtin_amdgcn_permlane32_swap(st.mx, st.mx, false, false);
+          const int m2 = max((int)sw[0], (int)sw[1]);
+          m_tile = fmaf(__int_as_float(m2), st.cs_a, -fmaf(kAccBias, st.cs_a, kFp8Offset - kLazyTau));
+        } else {
+          const float fa = fmaf(__int_as_float(st.ma), st.cs_a, -fmaf(kAccBias, st.cs_a, kFp8Offset - kLazyTau));
+          const float fb = fmaf(__int_as_float(st.mb), st.cs_b, -fmaf(kAccBias, st.cs_b, kFp8Offset - kLazyTau));
+          const float mt = fmaxf(fa, fb);
+          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+          m_tile = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+        }
+        const bool grow = m_tile > X.m + kLazyTau;
+        X.grew = __any(grow);
+        const float m_new = grow ? m_tile : X.m;
+        X.alpha = __builtin_amdgcn_exp2f(X.m - m_new);
+        X.m = m_new;
+        st.nc_a = -fmaf(kAccBias, st.cs_a, X.m);
+        st.nc_b = -fmaf(kAccBias, st.cs_b, X.m);
+      }
+    } else {
+      const int j = c - 2, kb = j >> 2, r0 = (j & 3) * 4;
+      float pv4[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++)
+        pv4[e] = __builtin_amdgcn_exp2f(
+            fmaf(__int_as_float(X.s[kb][r0 + e]), e < 2 ? st.cs_a : st.cs_b, e < 2 ? st.nc_a : st.nc_b));
+      const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv4[0], pv4[1], X.pf[j], false);
+      X.pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv4[2], pv4[3], packed, true);
+    }
+  };
+  auto sm_init = [&](const WideHalf<KT>& X, int64_t t) {
+    SmState st;
+    st.mx = 0;
+    st.ma = st.mb = INT32_MIN;
+    st.nc_a = st.nc_b = 0.f;
+    scales(X, t, st.cs_a, st.cs_b);
+    return st;
+  };
+
+  // ---------------- pipelined tiles ----------------
+  int64_t full = kv_end / kBK;
+  if (p.causal) full = min(full, (q_first + p.q_offset + 1) / kBK);
+  full = min(full, n_tiles);
+  const int n = full >= 2 ? (int)full : 0;
+  int64_t t_simple = n;  // first tile of the plain loop
+
+  if (n >= 2) {
+    dma_k(0, 0);
+    dma_k(1, 1);
+    dma_v(0, 0);
+    if (n > 2) dma_k(2, 2);
+    dma_v(1, 1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    v4i kf[8];  // K(i) in phase 1 (Q_B.K(i)^T), K(i+1) from phase 2 on (Q_A.K(i+1)^T, then Q_B next tile)
+    v8i vf[4];  // V(i-1) in phase 1 (P_B(i-1).V), V(i) from phase 2 on
+#pragma unroll
+    for (int j = 0; j < 8; j++) kf[j] = read_k(0, j);
+    lds_wait_k(kf);
+#pragma unroll
+    for (int j = 0; j < 8; j++) qk_mfma(A, kf, j);
+    drain_s(A);
+    int issued = 0;  // DMA instructions issued at the previous iteration's barrier
+    auto iter = [&](int i, auto first, auto last) {
+      constexpr bool kFirst = decltype(first)::value, kLast = decltype(last)::value;
+      // ---- start: K(i+1) and V(i) have landed (only the previous iteration's DMAs may still be in
+      // flight); after the barrier the buffers of K(i) and V(i-1) take K(i+3) and V(i+2) ----
+      if (issued == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      else if (issued == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      issued = 0;
+      if (i + 3 < n) {
+        dma_k(i + 3, i % kNBuf);
+        issued += 2;
+      }
+      if (i + 2 < n) {
+        dma_v(i + 2, (i + 2) % kNBuf);
+        issued += 2;
+      }
+      if (!kFirst && B.grew) rescale(B);
+      // ---- phase 1: softmax_A(i) || Q_B.K(i)^T, P_B(i-1).V(i-1), rowsum P_B(i-1); then the fragments
+      // of K(i+1) and V(i) replace those of K(i) and V(i-1) once their last MFMA has gone ----
+      {
+        SmState st = sm_init(A, i);
+        // MFMA ids per slot: 0..7 QK_B fragment j, 8..11 PV_B block d, 12 rowsum_B, -1 none
+        constexpr int kM[10][2] = {{0, 1}, {2, 3}, {8, -1}, {4, 5}, {9, -1}, {6, 7}, {10, -1}, {11, -1}, {12, -1}, {-1, -1}};
+        const int kb = (i + 1) % kNBuf, vb = i % kNBuf;
+#pragma unroll
+        for (int k = 0; k < 10; k++) {
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int e = 0; e < 2; e++) {
+            const int id = kM[k][e];
+            if (id < 0) continue;
+            if (id < 8) qk_mfma(B, kf, id);
+            else if (!kFirst && id < 12) pv_mfma(B, vf, id - 8);
+            else if (!kFirst) rsum_mfma(B);
+          }
+          if ((k == 6 || k == 7) && !kLast) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) kf[(k - 6) * 4 + j] = read_k(kb, (k - 6) * 4 + j);
+          }
+          if (k == 8 || k == 9) {
+#pragma unroll
+            for (int d = 0; d < 2; d++) vf[(k - 8) * 2 + d] = read_v(vb, (k - 8) * 2 + d);
+          }
+          sm_chunk(A, st, k);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      asm volatile("" ::"v"(A.pf), "v"(A.m), "v"(B.s[0]), "v"(B.s[1]));
+      if (A.grew) rescale(A);
+      lds_wait_k(kf);
+      lds_wait_v(vf);
+      asm volatile("s_nop 1" : "+v"(A.pf));  // VALU writes of P_A before the MFMAs read them
+      // ---- phase 2: softmax_B(i) || rowsum P_A(i), Q_A.K(i+1)^T, P_A(i).V(i) ----
+      {
+        SmState st = sm_init(B, i);
+        constexpr int kM[10][2] = {{12, -1}, {0, 1}, {2, 3}, {8, -1}, {4, 5}, {9, -1}, {6, 7}, {10, -1}, {11, -1}, {-1, -1}};
+#pragma unroll
+        for (int k = 0; k < 10; k++) {
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int e = 0; e < 2; e++) {
+            const int id = kM[k][e];
+            if (id < 0) continue;
+            if (id < 8) {
+              if (!kLast) qk_mfma(A, kf, id);
+            } else if (id < 12) {
+              pv_mfma(A, vf, id - 8);
+            } else {
+              rsum_mfma(A);
+            }
+          }
+          sm_chunk(B, st, k);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      asm volatile("" ::"v"(B.pf), "v"(B.m), "v"(A.s[0]), "v"(A.s[1]));
+    };
+    iter(0, std::true_type{}, std::false_type{});
+    for (int i = 1; i < n - 1; i++) iter(i, std::false_type{}, std::false_type{});
+    iter(n - 1, std::false_type{}, std::true_type{});
+    if (B.grew) rescale(B);
+    asm volatile("s_nop 4" : "+v"(B.pf));  // VALU writes of P_B before the MFMAs read them
+#pragma unroll
+    for (int d = 0; d < 4; d++) pv_mfma(B, vf, d);
+    rsum_mfma(B);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // the plain loop below refills the buffers
+  }
+
+  // ---------------- plain loop: masked / remaining tiles, one tile at a time ----------------
+  for (int64_t t = t_simple; t < n_tiles; t++) {
+    dma_k(t, 0);
+    dma_v(t, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    v4i kf[8];
+    v8i vf[4];
+#pragma unroll
+    for (int j = 0; j < 8; j++) kf[j] = read_k(0, j);
+#pragma unroll
+    for (int d = 0; d < 4; d++) vf[d] = read_v(0, d);
+    lds_wait_k(kf);
+    lds_wait_v(vf);
+    const int64_t k0 = t * kBK;
+    auto tile_half = [&](WideHalf<KT>& X, int half) {
+      const int64_t wrow0 = R0 + 32 * half;
+      const int64_t qrow = wrow0 + lq;
+#pragma unroll
+      for (int j = 0; j < 8; j++) qk_mfma(X, kf, j);
+      drain_s(X);
+      const bool masked = (k0 + kBK > kv_end) || (p.causal && k0 + kBK - 1 > wrow0 + p.q_offset);
+      if (masked) {
+        int lim = (int)min(kv_end - k0, (int64_t)kBK);
+        if (p.causal) lim = min(lim, (int)max(min(qrow + p.q_offset + 1 - k0, (int64_t)kBK), (int64_t)-1));
+        lim -= hf * 4;
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+          for (int r = 0; r < 16; r++)
+            if (kb * 32 + (r >> 2) * 8 + (r & 3) >= lim) X.s[kb][r] = INT32_MIN;
+      }
+      float cs_a, cs_b;
+      scales(X, t, cs_a, cs_b);
+      float m_tile;
+      if constexpr (!KT) {
+        int mx = INT32_MIN;
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) mx = max(mx, X.s[kb][r]);
+        const auto sw = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);
+        mx = max((int)sw[0], (int)sw[1]);
+        m_tile = mx == INT32_MIN ? kMInit : fmaf(__int_as_float(mx), cs_a, -fmaf(kAccBias, cs_a, kFp8Offset - kLazyTau));
+      } else {
+        int ma = INT32_MIN, mb = INT32_MIN;
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            if ((r & 3) < 2) ma = max(ma, X.s[kb][r]);
+            else mb = max(mb, X.s[kb][r]);
+          }
+        const float fa = ma == INT32_MIN ? kMInit : fmaf(__int_as_float(ma), cs_a, -fmaf(kAccBias, cs_a, kFp8Offset - kLazyTau));
+        const float fb = mb == INT32_MIN ? kMInit : fmaf(__int_as_float(mb), cs_b, -fmaf(kAccBias, cs_b, kFp8Offset - kLazyTau));
+        const float mt = fmaxf(fa, fb);
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+        m_tile = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      }
+      const bool grow = m_tile > X.m + kLazyTau;
+      if (__any(grow)) {
+        const float m_new = grow ? m_tile : X.m;
+        X.alpha = __builtin_amdgcn_exp2f(X.m - m_new);
+        rescale(X);
+        X.m = m_new;
+      }
+      const float nc_a = -fmaf(kAccBias, cs_a, X.m), nc_b = -fmaf(kAccBias, cs_b, X.m);
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int kb = j >> 2, r0 = (j & 3) * 4;
+        float pv4[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int sv = X.s[kb][r0 + e];
+          pv4[e] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(sv), e < 2 ? cs_a : cs_b, e < 2 ? nc_a : nc_b));
+          pv4[e] = sv == INT32_MIN ? 0.f : pv4[e];
+        }
+        const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv4[0], pv4[1], X.pf[j], false);
+        X.pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv4[2], pv4[3], packed, true);
+      }
+      asm volatile("s_nop 4" : "+v"(X.pf));  // VALU writes of P before the MFMAs read them
+#pragma unroll
+      for (int d = 0; d < 4; d++) pv_mfma(X, vf, d);
+      rsum_mfma(X);
+    };
+    tile_half(A, 0);
+    tile_half(B, 1);
+    __syncthreads();  // every wave is done with buffer 0 before the next tile's DMA
+  }
+
+  // ---------------- epilogue: O / l * v_scale through the wave's LDS stage ----------------
+  drain_o(A);
+  drain_o(B);
+  __syncthreads();  // v_scale staging visible (no key tile at all: no barrier ran yet)
+  uint8_t* stage = lds_kv + w * 8192;
+  uint16_t* obase = static_cast<uint16_t*>(p.o) + b * p.osb + h * p.osh;
+  auto store_half = [&](WideHalf<KT>& X, int half) {
+    const int64_t wrow0 = R0 + 32 * half;
+    const int64_t qrow = wrow0 + lq;
+    const float l_tot = X.lacc[0];
+    const float inv_l = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+#pragma unroll
+    for (int pass = 0; pass < 2; pass++) {
+#pragma unroll
+      for (int db = 0; db < 2; db++) {
+        const int dblk = pass * 2 + db;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int d = dblk * 32 + g * 8 + hf * 4;
+          const v4f sc = *reinterpret_cast<const v4f*>(&lds_vs[d]);
+          float f[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) f[e] = X.o[dblk][g * 4 + e] * inv_l * sc[e];
+          const v2u packed{pack_half2<IS_FP16_OUT>(f[0], f[1]), pack_half2<IS_FP16_OUT>(f[2], f[3])};
+          const int c = db * 4 + g;
+          *reinterpret_cast<v2u*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4) + hf * 8) = packed;
+        }
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int r = i * 8 + (lane >> 3), c = lane & 7;
+        const v4u val = *reinterpret_cast<const v4u*>(stage + r * 128 + ((c ^ (r & 7)) << 4));
+        const int64_t row = wrow0 + r;
+        if (row < p.Lq) *reinterpret_cast<v4u*>(obase + row * p.osl + pass * 64 + c * 8) = val;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    if (p.lse && hf == 0 && qrow < p.Lq)
+      p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + X.m : -INFINITY;
+  };
+  store_half(A, 0);
+  store_half(B, 1);
+}
+
+template <bool IS_FP16_OUT, bool KT>
+__global__ __launch_bounds__(kThreads) void qattn_fwd_wide_kernel(AttnParams p) {
+  qattn_fwd_wide<IS_FP16_OUT, KT>(p);
 }
 
 // Merge the KV-split partials: one wave per query row, 2 channels per lane.
@@ -747,6 +1308,17 @@ extern "C" size_t qattn_fwd_workspace_size(int64_t B, int64_t Lq, int64_t Hq, in
   return (size_t)num_splits * B * Hq * Lq * (D + 2) * sizeof(float);
 }
 
+// QATTN_WIDE=1 in the environment selects the wide kernel (64 query rows per wave, software-pipelined
+// halves) for dense FP8 launches; it is bit-identical to qattn_fwd_kernel and, as measured on MI355X,
+// not yet faster, so it is opt-in
+static bool wide_enabled() {
+  static const bool on = [] {
+    const char* e = getenv("QATTN_WIDE");
+    return e && e[0] == '1';
+  }();
+  return on;
+}
+
 template <int PV, bool KT, bool SP = false>
 static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, size_t workspace_bytes, hipStream_t st,
                       int64_t D) {
@@ -777,6 +1349,15 @@ static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, siz
     const int64_t rows = p.B * p.Hq * p.Lq;
     if (out_dtype == QATTN_BF16) qattn_combine_kernel<false><<<(rows + 3) / 4, 256, 0, st>>>(p);
     else qattn_combine_kernel<true><<<(rows + 3) / 4, 256, 0, st>>>(p);
+  } else if constexpr (PV == PV_FP8 && !SP) {
+    if (wide_enabled() && p.nKB * ks_per_tile(KT) <= kWideKsFloats) {
+      const int64_t g = p.B * p.Hq * ((p.Lq + kWideRows - 1) / kWideRows);
+      if (out_dtype == QATTN_BF16) qattn_fwd_wide_kernel<false, KT><<<g, kThreads, 0, st>>>(p);
+      else qattn_fwd_wide_kernel<true, KT><<<g, kThreads, 0, st>>>(p);
+    } else {
+      if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, false, PV, KT, SP><<<grid, kThreads, 0, st>>>(p);
+      else qattn_fwd_kernel<true, false, PV, KT, SP><<<grid, kThreads, 0, st>>>(p);
+    }
   } else {
     if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, false, PV, KT, SP><<<grid, kThreads, 0, st>>>(p);
     else qattn_fwd_kernel<true, false, PV, KT, SP><<<grid, kThreads, 0, st>>>(p);

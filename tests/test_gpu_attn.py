@@ -17,6 +17,8 @@ COS_KERNEL = 0.99995  # same quantized operands and schedule: only exp2 ulps / f
 COS_E2E = 0.999
 LOG2E = 1.44269504
 KERNEL_LAZY_TAU = 1.0  # lazy running-max threshold of qattn_fwd_kernel (kLazyTau in attn.hip)
+# FP8 P.V kernels sum the e4m3-rounded P on the matrix pipe (row_sum_mfma in attn.hip); the oracle restates it
+KERNEL_LSUM_ROUNDED = True
 
 
 GRAN_CODE = {"per_block": 1, "per_warp": 2, "per_thread": 3}
@@ -68,7 +70,7 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
                                     ks.cpu().numpy(), **vargs, causal=causal, q_offset=q_offset,
                                     kv_valid=kv_valid, want_lse=True, tiles_per_split=tps,
                                     lazy_tau=KERNEL_LAZY_TAU, qk_mult=qk_mult, q_gran=GRAN_CODE[gran],
-                                    k_gran=GRAN_CODE[gran])
+                                    k_gran=GRAN_CODE[gran], lsum_rounded=KERNEL_LSUM_ROUNDED and pv == "fp8")
     c = cosine(og, ref)
     err = float(np.abs(og - ref).max())
     lerr = float(np.nanmax(np.abs(lse.cpu().numpy() - ref_lse)))
@@ -413,7 +415,7 @@ def test_multi_block_workgroups(oracle, case):
     ref, ref_lse = oracle.qattn_fwd(pick(q8), qs[:1, 7:8].cpu().numpy(), pick(k8), ks[:1, 7:8].cpu().numpy(),
                                     v8=untile_v(v8[:1, 7:8]), v_scale=vs[:1, 7:8].cpu().numpy(),
                                     kv_valid=kv_valid[:1], want_lse=True, lazy_tau=KERNEL_LAZY_TAU, qk_mult=qk_mult,
-                                    q_gran=GRAN_CODE[gran], k_gran=GRAN_CODE[gran])
+                                    q_gran=GRAN_CODE[gran], k_gran=GRAN_CODE[gran], lsum_rounded=KERNEL_LSUM_ROUNDED)
     og = pick(o.float())
     c = cosine(og, ref)
     log(f"  head 7 vs quantized oracle: cosine={c:.6f} max_abs={float(np.abs(og - ref).max()):.4g}")
