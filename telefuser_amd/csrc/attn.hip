@@ -916,62 +916,83 @@ __device__ __forceinline__ void qattn_fwd_wide(const AttnParams& p) {
       cs_a = cs_b = X.qs * lds_ks[t];
     }
   };
-  // softmax of an unmasked tile in chunks: c0 / c1 row max (c1 also moves m lazily and sets alpha),
-  // c2..c9 exp2 and e4m3 packing of 4 logits of each lane
-  struct SmState { int mx, ma, mb; float cs_a, cs_b, nc_a, nc_b; };
-  auto sm_chunk = [&](WideHalf<KT>& X, SmState& st, int c) {
-    if (c <= 1) {
-      const int kb = c;
+  // Softmax of one unmasked tile as a VALU stream of 19 items.  Items 0 and 1: the row max as four
+  // independent chains (over s[0], then s[1]; for per-thread K scales chains 0-1 hold class a and 2-3
+  // class b), then (item 1) the exchange with the lane holding the other key half, the lazy running-max
+  // update and alpha, and the first fma.  Items 2..17 run three stages of the 16 two-logit groups g at
+  // once - fma of g + 1, exp2 of g, e4m3 packing of g - 1 - so that no item waits on its own results;
+  // item 18 packs the last group.  Group g is logits r0 = 2g mod 16, r0 + 1 of block g / 8, which share one
+  // scale class, and lands in byte pair (g & 1) of pf[g / 2].
+  struct Sm {
+    int c[4];
+    float cs_a, cs_b, nc_a, nc_b;
+    float x[2][2], e[2][2];
+  };
+  auto sm_item = [&](WideHalf<KT>& X, Sm& st, int k) {
+    // chain q covers elements {0,1,4,5} + 8 (q & 1) + 2 (q >> 1) of each 16-logit block
+    auto el = [](int q, int i) { return ((i >> 1) * 4) + (i & 1) + 8 * (q & 1) + 2 * (q >> 1); };
+    if (k == 0) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) st.c[q] = max(max(X.s[0][el(q, 0)], X.s[0][el(q, 1)]), max(X.s[0][el(q, 2)], X.s[0][el(q, 3)]));
+      return;
+    }
+    if (k == 1) {
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        st.c[q] = max(max(st.c[q], X.s[1][el(q, 0)]), max(max(X.s[1][el(q, 1)], X.s[1][el(q, 2)]), X.s[1][el(q, 3)]));
+      float m_tile;
       if constexpr (!KT) {
-        int m0 = kb == 0 ? max(X.s[0][0], X.s[0][1]) : max(st.mx, X.s[1][0]);
-#pragma unroll
-        for (int r = kb == 0 ? 2 : 1; r < 16; r++) m0 = max(m0, X.s[kb][r]);
-        st.mx = m0;
+        int mx = max(max(st.c[0], st.c[1]), max(st.c[2], st.c[3]));
+        const auto sw = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);
+        mx = max((int)sw[0], (int)sw[1]);
+        m_tile = fmaf(__int_as_float(mx), st.cs_a, -fmaf(kAccBias, st.cs_a, kFp8Offset - kLazyTau));
       } else {
+        const int ma = max(st.c[0], st.c[1]), mb = max(st.c[2], st.c[3]);
+        const float fa = fmaf(__int_as_float(ma), st.cs_a, -fmaf(kAccBias, st.cs_a, kFp8Offset - kLazyTau));
+        const float fb = fmaf(__int_as_float(mb), st.cs_b, -fmaf(kAccBias, st.cs_b, kFp8Offset - kLazyTau));
+        const float mt = fmaxf(fa, fb);
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+        m_tile = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      }
+      const bool grow = m_tile > X.m + kLazyTau;
+      X.grew = __any(grow);
+      const float m_new = grow ? m_tile : X.m;
+      X.alpha = __builtin_amdgcn_exp2f(X.m - m_new);
+      X.m = m_new;
+      st.nc_a = -fmaf(kAccBias, st.cs_a, X.m);
+      st.nc_b = -fmaf(kAccBias, st.cs_b, X.m);
+    }
+    auto F = [&](int g) {
+      const int kb = g >> 3, r0 = (2 * g) & 15;
+      const bool ca = (r0 & 3) < 2;
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-          if ((r & 3) < 2) st.ma = max(st.ma, X.s[kb][r]);
-          else st.mb = max(st.mb, X.s[kb][r]);
-        }
-      }
-      if (c == 1) {
-        float m_tile;
-        if constexpr (!KT) {
-          const auto sw = __builtin_amdgcn_permlane32_swap(st.mx, st.mx, false, false);
-          const int m2 = max((int)sw[0], (int)sw[1]);
-          m_tile = fmaf(__int_as_float(m2), st.cs_a, -fmaf(kAccBias, st.cs_a, kFp8Offset - kLazyTau));
-        } else {
-          const float fa = fmaf(__int_as_float(st.ma), st.cs_a, -fmaf(kAccBias, st.cs_a, kFp8Offset - kLazyTau));
-          const float fb = fmaf(__int_as_float(st.mb), st.cs_b, -fmaf(kAccBias, st.cs_b, kFp8Offset - kLazyTau));
-          const float mt = fmaxf(fa, fb);
-          const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
-          m_tile = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-        }
-        const bool grow = m_tile > X.m + kLazyTau;
-        X.grew = __any(grow);
-        const float m_new = grow ? m_tile : X.m;
-        X.alpha = __builtin_amdgcn_exp2f(X.m - m_new);
-        X.m = m_new;
-        st.nc_a = -fmaf(kAccBias, st.cs_a, X.m);
-        st.nc_b = -fmaf(kAccBias, st.cs_b, X.m);
-      }
+      for (int e = 0; e < 2; e++)
+        st.x[g & 1][e] = fmaf(__int_as_float(X.s[kb][r0 + e]), ca ? st.cs_a : st.cs_b, ca ? st.nc_a : st.nc_b);
+    };
+    auto E = [&](int g) {
+#pragma unroll
+      for (int e = 0; e < 2; e++) st.e[g & 1][e] = __builtin_amdgcn_exp2f(st.x[g & 1][e]);
+    };
+    auto C = [&](int g) {
+      if (g & 1) X.pf[g >> 1] = __builtin_amdgcn_cvt_pk_fp8_f32(st.e[1][0], st.e[1][1], X.pf[g >> 1], true);
+      else X.pf[g >> 1] = __builtin_amdgcn_cvt_pk_fp8_f32(st.e[0][0], st.e[0][1], X.pf[g >> 1], false);
+    };
+    if (k == 1) {
+      F(0);
+    } else if (k <= 17) {
+      const int g = k - 2;
+      if (g >= 1) C(g - 1);
+      E(g);
+      if (g + 1 <= 15) F(g + 1);
     } else {
-      const int j = c - 2, kb = j >> 2, r0 = (j & 3) * 4;
-      float pv4[4];
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-        pv4[e] = __builtin_amdgcn_exp2f(
-            fmaf(__int_as_float(X.s[kb][r0 + e]), e < 2 ? st.cs_a : st.cs_b, e < 2 ? st.nc_a : st.nc_b));
-      const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv4[0], pv4[1], X.pf[j], false);
-      X.pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv4[2], pv4[3], packed, true);
+      C(15);
     }
   };
-  auto sm_init = [&](const WideHalf<KT>& X, int64_t t) {
-    SmState st;
-    st.mx = 0;
-    st.ma = st.mb = INT32_MIN;
+  auto sm_init = [&](float cs_a, float cs_b) {
+    Sm st;
+    st.cs_a = cs_a;
+    st.cs_b = cs_b;
     st.nc_a = st.nc_b = 0.f;
-    scales(X, t, st.cs_a, st.cs_b);
     return st;
   };
 
@@ -999,6 +1020,13 @@ __device__ __forceinline__ void qattn_fwd_wide(const AttnParams& p) {
     for (int j = 0; j < 8; j++) qk_mfma(A, kf, j);
     drain_s(A);
     int issued = 0;  // DMA instructions issued at the previous iteration's barrier
+    // MFMA per VALU item (-1: none), issued at the start of the item.  Ids: 0..7 Q.K^T fragment j,
+    // 8..11 P.V block d, 12 row sum.  Greedy placement: an MFMA goes into the first item that starts
+    // after the previous MFMA has left the matrix pipe (QK 32 cycles, PV and row sum 64; items are
+    // ~33 cycles of VALU work, the two max items ~40 and ~95), so the wave never stalls on a busy
+    // pipe and the matrix work (576 cycles) hides under the softmax stream (~670 cycles).
+    constexpr int kMf1[19] = {0, 1, 2, 3, 8, -1, 4, 9, -1, 5, 10, -1, 6, 7, 11, -1, 12, -1, -1};
+    constexpr int kMf2[19] = {12, 0, 1, 2, 3, 8, -1, 4, 9, -1, 5, 10, -1, 6, 7, 11, -1, -1, -1};
     auto iter = [&](int i, auto first, auto last) {
       constexpr bool kFirst = decltype(first)::value, kLast = decltype(last)::value;
       // ---- start: K(i+1) and V(i) have landed (only the previous iteration's DMAs may still be in
@@ -1016,62 +1044,57 @@ __device__ __forceinline__ void qattn_fwd_wide(const AttnParams& p) {
         dma_v(i + 2, (i + 2) % kNBuf);
         issued += 2;
       }
+      float csA_a, csA_b, csB_a, csB_b;
+      scales(A, i, csA_a, csA_b);
+      scales(B, i, csB_a, csB_b);
       if (!kFirst && B.grew) rescale(B);
-      // ---- phase 1: softmax_A(i) || Q_B.K(i)^T, P_B(i-1).V(i-1), rowsum P_B(i-1); then the fragments
-      // of K(i+1) and V(i) replace those of K(i) and V(i-1) once their last MFMA has gone ----
+      // ---- phase 1: softmax_A(i) || Q_B.K(i)^T, P_B(i-1).V(i-1), rowsum P_B(i-1).  The fragments of
+      // K(i+1) and V(i) replace those of K(i) and V(i-1) two items after their last MFMA ----
       {
-        SmState st = sm_init(A, i);
-        // MFMA ids per slot: 0..7 QK_B fragment j, 8..11 PV_B block d, 12 rowsum_B, -1 none
-        constexpr int kM[10][2] = {{0, 1}, {2, 3}, {8, -1}, {4, 5}, {9, -1}, {6, 7}, {10, -1}, {11, -1}, {12, -1}, {-1, -1}};
+        Sm st = sm_init(csA_a, csA_b);
         const int kb = (i + 1) % kNBuf, vb = i % kNBuf;
 #pragma unroll
-        for (int k = 0; k < 10; k++) {
+        for (int k = 0; k < 19; k++) {
           __builtin_amdgcn_sched_barrier(0);
+          const int id = kMf1[k];
+          if (id >= 0 && id < 8) qk_mfma(B, kf, id);
+          else if (id >= 8 && id < 12 && !kFirst) pv_mfma(B, vf, id - 8);
+          else if (id == 12 && !kFirst) rsum_mfma(B);
+          if (!kLast && (k == 5 || k == 15)) {
 #pragma unroll
-          for (int e = 0; e < 2; e++) {
-            const int id = kM[k][e];
-            if (id < 0) continue;
-            if (id < 8) qk_mfma(B, kf, id);
-            else if (!kFirst && id < 12) pv_mfma(B, vf, id - 8);
-            else if (!kFirst) rsum_mfma(B);
+            for (int j = 0; j < 4; j++) kf[(k == 15) * 4 + j] = read_k(kb, (k == 15) * 4 + j);
           }
-          if ((k == 6 || k == 7) && !kLast) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) kf[(k - 6) * 4 + j] = read_k(kb, (k - 6) * 4 + j);
+          if (k == 6 || k == 9 || k == 12 || k == 16) {
+            const int d = k == 6 ? 0 : k == 9 ? 1 : k == 12 ? 2 : 3;
+            vf[d] = read_v(vb, d);
           }
-          if (k == 8 || k == 9) {
-#pragma unroll
-            for (int d = 0; d < 2; d++) vf[(k - 8) * 2 + d] = read_v(vb, (k - 8) * 2 + d);
-          }
-          sm_chunk(A, st, k);
+          sm_item(A, st, k);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
       asm volatile("" ::"v"(A.pf), "v"(A.m), "v"(B.s[0]), "v"(B.s[1]));
       if (A.grew) rescale(A);
-      lds_wait_k(kf);
-      lds_wait_v(vf);
-      asm volatile("s_nop 1" : "+v"(A.pf));  // VALU writes of P_A before the MFMAs read them
       // ---- phase 2: softmax_B(i) || rowsum P_A(i), Q_A.K(i+1)^T, P_A(i).V(i) ----
       {
-        SmState st = sm_init(B, i);
-        constexpr int kM[10][2] = {{12, -1}, {0, 1}, {2, 3}, {8, -1}, {4, 5}, {9, -1}, {6, 7}, {10, -1}, {11, -1}, {-1, -1}};
+        Sm st = sm_init(csB_a, csB_b);
 #pragma unroll
-        for (int k = 0; k < 10; k++) {
+        for (int k = 0; k < 19; k++) {
           __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-          for (int e = 0; e < 2; e++) {
-            const int id = kM[k][e];
-            if (id < 0) continue;
-            if (id < 8) {
-              if (!kLast) qk_mfma(A, kf, id);
-            } else if (id < 12) {
-              pv_mfma(A, vf, id - 8);
-            } else {
-              rsum_mfma(A);
-            }
+          // LDS reads complete before the inline-asm MFMAs use them: K fragments 0..3 were read before
+          // the 12 other reads of phase 1 (V 0..2, K 4..7, V 3), K 4..7 before V 3 (two reads)
+          if (!kLast && k == 1)
+            asm volatile("s_waitcnt lgkmcnt(12)" : "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3])::"memory");
+          if (!kLast && k == 7)
+            asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(kf[4]), "+v"(kf[5]), "+v"(kf[6]), "+v"(kf[7])::"memory");
+          const int id = kMf2[k];
+          if (id >= 0 && id < 8) {
+            if (!kLast) qk_mfma(A, kf, id);
+          } else if (id >= 8 && id < 12) {
+            pv_mfma(A, vf, id - 8);
+          } else if (id == 12) {
+            rsum_mfma(A);
           }
-          sm_chunk(B, st, k);
+          sm_item(B, st, k);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -1081,7 +1104,6 @@ __device__ __forceinline__ void qattn_fwd_wide(const AttnParams& p) {
     for (int i = 1; i < n - 1; i++) iter(i, std::false_type{}, std::false_type{});
     iter(n - 1, std::false_type{}, std::true_type{});
     if (B.grew) rescale(B);
-    asm volatile("s_nop 4" : "+v"(B.pf));  // VALU writes of P_B before the MFMAs read them
 #pragma unroll
     for (int d = 0; d < 4; d++) pv_mfma(B, vf, d);
     rsum_mfma(B);
