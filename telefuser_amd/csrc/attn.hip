@@ -1020,6 +1020,9 @@ __device__ __forceinline__ void qattn_fwd_wide(const AttnParams& p) {
     for (int j = 0; j < 8; j++) qk_mfma(A, kf, j);
     drain_s(A);
     int issued = 0;  // DMA instructions issued at the previous iteration's barrier
+    float cs[4];     // logit scales (class a, b) of halves A and B for the tile being computed
+    scales(A, 0, cs[0], cs[1]);
+    scales(B, 0, cs[2], cs[3]);
     // MFMA per VALU item (-1: none), issued at the start of the item.  Ids: 0..7 Q.K^T fragment j,
     // 8..11 P.V block d, 12 row sum.  Greedy placement: an MFMA goes into the first item that starts
     // after the previous MFMA has left the matrix pipe (QK 32 cycles, PV and row sum 64; items are
@@ -1044,9 +1047,8 @@ __device__ __forceinline__ void qattn_fwd_wide(const AttnParams& p) {
         dma_v(i + 2, (i + 2) % kNBuf);
         issued += 2;
       }
-      float csA_a, csA_b, csB_a, csB_b;
-      scales(A, i, csA_a, csA_b);
-      scales(B, i, csB_a, csB_b);
+      // this tile's logit scales were read during the previous iteration (scales of tile 0: prologue)
+      const float csA_a = cs[0], csA_b = cs[1], csB_a = cs[2], csB_b = cs[3];
       if (!kFirst && B.grew) rescale(B);
       // ---- phase 1: softmax_A(i) || Q_B.K(i)^T, P_B(i-1).V(i-1), rowsum P_B(i-1).  The fragments of
       // K(i+1) and V(i) replace those of K(i) and V(i-1) two items after their last MFMA ----
@@ -1086,6 +1088,10 @@ __device__ __forceinline__ void qattn_fwd_wide(const AttnParams& p) {
             asm volatile("s_waitcnt lgkmcnt(12)" : "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3])::"memory");
           if (!kLast && k == 7)
             asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(kf[4]), "+v"(kf[5]), "+v"(kf[6]), "+v"(kf[7])::"memory");
+          if (!kLast && k == 17) {  // the next tile's scales (their LDS latency is hidden by the last items)
+            scales(A, i + 1, cs[0], cs[1]);
+            scales(B, i + 1, cs[2], cs[3]);
+          }
           const int id = kMf2[k];
           if (id >= 0 && id < 8) {
             if (!kLast) qk_mfma(A, kf, id);
