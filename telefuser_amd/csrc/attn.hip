@@ -1336,15 +1336,12 @@ extern "C" size_t qattn_fwd_workspace_size(int64_t B, int64_t Lq, int64_t Hq, in
   return (size_t)num_splits * B * Hq * Lq * (D + 2) * sizeof(float);
 }
 
-// QATTN_WIDE=1 in the environment selects the wide kernel (64 query rows per wave, software-pipelined
-// halves) for dense FP8 launches; it is bit-identical to qattn_fwd_kernel and, as measured on MI355X,
-// not yet faster, so it is opt-in
+// QATTN_WIDE=1 in the environment (read at every launch) selects the wide kernel (64 query rows per
+// wave, software-pipelined halves) for dense FP8 launches; it is bit-identical to qattn_fwd_kernel and,
+// as measured on MI355X, not faster yet, so it is opt-in
 static bool wide_enabled() {
-  static const bool on = [] {
-    const char* e = getenv("QATTN_WIDE");
-    return e && e[0] == '1';
-  }();
-  return on;
+  const char* e = getenv("QATTN_WIDE");
+  return e && e[0] == '1';
 }
 
 template <int PV, bool KT, bool SP = false>

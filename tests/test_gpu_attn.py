@@ -421,3 +421,54 @@ def test_multi_block_workgroups(oracle, case):
     log(f"  head 7 vs quantized oracle: cosine={c:.6f} max_abs={float(np.abs(og - ref).max()):.4g}")
     assert c >= COS_KERNEL
     assert float(np.max(np.abs(lse[:1, 7:8].cpu().numpy() - ref_lse))) < 2e-2
+
+
+@pytest.mark.parametrize("case", ["ragged", "padding", "causal", "gqa_hnd_thread", "long"])
+def test_wide_kernel_matches(oracle, case, monkeypatch):
+    """The opt-in wide kernel (QATTN_WIDE=1: 64 query rows per wave, software-pipelined halves) runs the
+    same per-element arithmetic and accumulation order as qattn_fwd_kernel, so its output and LSE must be
+    identical, bit for bit, on the same quantized operands; checked on ragged lengths (a masked tail tile
+    through its plain loop), key padding, top-left causal, GQA + HND + per-thread scales and a key range
+    long enough for the steady-state pipeline.  One case is also checked against the oracle."""
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    B, Lq, Lk, Hq, Hkv, layout, causal, kv_valid, gran = {
+        "ragged": (2, 1000, 777, 3, 3, "NHD", False, None, "per_block"),
+        "padding": (1, 600, 512, 4, 4, "NHD", False, [300], "per_block"),
+        "causal": (1, 1024, 1024, 2, 2, "NHD", True, None, "per_block"),
+        "gqa_hnd_thread": (1, 2000, 1500, 4, 2, "HND", False, None, "per_thread"),
+        "long": (1, 700, 8200, 2, 2, "NHD", False, None, "per_block"),
+    }[case]
+    log(f"wide vs default: {case} B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} layout={layout} causal={causal} "
+        f"kv_valid={kv_valid} gran={gran}")
+    q, k, v = qkv(B, Lq, Lk, Hq, Hkv, seed=4242, k_offset_std=0.5)
+    qd, kd, vd = (t.to(dev) for t in (q, k, v))
+    if layout == "HND":
+        qd, kd, vd = (t.transpose(1, 2).contiguous() for t in (qd, kd, vd))
+    km = sa.k_mean(kd, layout)
+    qk_mult = 1.0
+    if gran == "per_block":
+        q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=128 ** -0.5, tensor_layout=layout)
+    else:
+        q8, qs, k8, ks = sa.per_thread_int8(qd, kd, km, tensor_layout=layout)
+        qk_mult = 128 ** -0.5 * LOG2E
+    v8, vs, _ = sa.per_channel_fp8(vd, tensor_layout=layout)
+    kw = dict(tensor_layout=layout, out_dtype=torch.bfloat16, is_causal=causal, kv_valid_len=kv_valid,
+              return_lse=True, qk_mult=qk_mult, qk_quant_gran=gran, num_splits=1)
+    monkeypatch.setenv("QATTN_WIDE", "0")
+    o0, l0 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
+    monkeypatch.setenv("QATTN_WIDE", "1")
+    o1, l1 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
+    o2, l2 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2), "wide kernel is not deterministic"
+    assert torch.equal(o0, o1), f"wide kernel differs: max {float((o0.float() - o1.float()).abs().max()):.4g}"
+    assert torch.equal(l0, l1)
+    if case == "long":
+        ref = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
+                               ks.cpu().numpy(), v8=untile_v(v8), v_scale=vs.cpu().numpy(),
+                               lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED)
+        c = cosine(o1.float().cpu().numpy(), ref)
+        log(f"  wide kernel vs quantized oracle: cosine={c:.6f}")
+        assert c >= COS_KERNEL
