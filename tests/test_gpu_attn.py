@@ -472,3 +472,60 @@ def test_wide_kernel_matches(oracle, case, monkeypatch):
         c = cosine(o1.float().cpu().numpy(), ref)
         log(f"  wide kernel vs quantized oracle: cosine={c:.6f}")
         assert c >= COS_KERNEL
+
+
+@pytest.mark.parametrize("name", ["c3", "c4", "c5"])
+def test_full_size_configs(oracle, name):
+    """BASELINE configs 3-5 at full size through the drop-in's quantize + attention path (the bench's own
+    inputs and calls): 14B 720p self attention (L = 75600, H = 40, K mean offset), the 14B text cross
+    attention (Lk = 512 with zero-padded, masked keys) and the streaming chunk over a 32760-key window
+    (KV split, restated by the oracle).  Checked on a subset that the CPU finishes in seconds: 192 query rows (the first 128 and
+    the last 64) of the first and last head, against float64 truth (cosine >= 0.999) and against the
+    oracle on the very quantized operands of the launch (cosine >= 0.99995); the whole output must be
+    finite."""
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+    from telefuser_amd.workloads import CONFIGS, make_inputs
+
+    cfg = CONFIGS[name]
+    log(f"full size {name}: B={cfg.B} Lq={cfg.Lq} Lk={cfg.Lk} H={cfg.Hq} pad={cfg.pad_range}")
+    q, k, v, kvv = make_inputs(cfg, dev)
+    sm = cfg.D ** -0.5
+    km = sa.k_mean(k, "NHD")
+    q8, qs, k8, ks = sa.per_block_int8(q, k, km, sm_scale=sm, tensor_layout="NHD")
+    v8, vs, _ = sa.per_channel_fp8(v, tensor_layout="NHD")
+    o = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout="NHD", out_dtype=q.dtype, kv_valid_len=kvv)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(o.float()).all())
+    rows = torch.cat([torch.arange(0, 128), torch.arange(cfg.Lq - 64, cfg.Lq)])
+    v8_plain = untile_v(v8)
+    from telefuser_amd import _lib
+    nkb = (cfg.Lk + 63) // 64
+    ns = min(_lib.load().qattn_fwd_num_splits(cfg.B, cfg.Lq, cfg.Lk, cfg.Hq), nkb)
+    tps = (nkb + ns - 1) // ns if ns > 1 else 0  # the launch's KV-split schedule, restated on the CPU
+    log(f"  kv splits={ns}")
+    for h in (0, cfg.Hq - 1):
+        og = o[:, rows, h:h + 1].float().cpu().numpy()
+        truth = oracle.attn_fp64(bf16_bits(q[:, rows, h:h + 1].cpu()), bf16_bits(k[:, :, h:h + 1].cpu()),
+                                 bf16_bits(v[:, :, h:h + 1].cpu()), sm, kv_valid=kvv)
+        # the oracle restates per-block quantized rows with their own block's q_scale: rows 0..127 are query
+        # block 0, the last 64 rows lie inside the last (ragged) block, which is handed over whole
+        q8h = q8[:, :, h:h + 1].cpu()
+        qsh = qs[:, h:h + 1].cpu().numpy()
+        nqb = qsh.shape[-1]
+        ref_first = oracle.qattn_fwd(q8h[:, :128].contiguous().numpy(), qsh[..., :1].copy(),
+                                     k8[:, :, h:h + 1].contiguous().cpu().numpy(), ks[:, h:h + 1].cpu().numpy(),
+                                     v8=np.ascontiguousarray(v8_plain[:, h:h + 1]), v_scale=vs[:, h:h + 1].cpu().numpy(),
+                                     kv_valid=kvv, lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED,
+                                     tiles_per_split=tps)
+        last0 = (nqb - 1) * 128  # first row of the last query block
+        ref_last = oracle.qattn_fwd(q8h[:, last0:].contiguous().numpy(), qsh[..., nqb - 1:].copy(),
+                                    k8[:, :, h:h + 1].contiguous().cpu().numpy(), ks[:, h:h + 1].cpu().numpy(),
+                                    v8=np.ascontiguousarray(v8_plain[:, h:h + 1]), v_scale=vs[:, h:h + 1].cpu().numpy(),
+                                    kv_valid=kvv, lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED,
+                                    tiles_per_split=tps)
+        ref = np.concatenate([ref_first, ref_last[:, -64:]], axis=1)
+        ct, ck = cosine(og, truth), cosine(og, ref)
+        log(f"  head {h}: cos_truth={ct:.6f} cos_oracle={ck:.6f} max_abs_truth={float(np.abs(og - truth).max()):.4g}")
+        assert ct >= COS_E2E
+        assert ck >= COS_KERNEL
