@@ -168,6 +168,16 @@ def _prologue_bench(reps: int = 10) -> dict:
     return res
 
 
+def _attn_kernel_name(cfg) -> str:
+    """Kernel that a dense, unsplit FP8 launch of `cfg` runs (the library's own selection rule: the
+    ping-pong kernel when its grid of one workgroup per two query blocks fills the 256 CUs, unless
+    QATTN_PP says otherwise)."""
+    grid = cfg.B * cfg.Hq * ((-(-cfg.Lq // 128) + 1) // 2)
+    env = os.environ.get("QATTN_PP", "")
+    use_pp = env == "1" if env else grid >= 256
+    return "qattn_fwd_pp_kernel" if use_pp else "qattn_fwd_kernel"
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -295,7 +305,7 @@ def main() -> int:
         "pct_mfma_peak": round(100 * value / peak, 2),
         "roofline": {"bound": "mfma", "achieved": round(attn_tops, 2), "peak": peak, "unit": "TFLOP/s",
                      "frac": round(attn_tops / peak, 4), "traffic": traffic,
-                     "kernel": "qattn_fwd_kernel", "kernel_ms": round(attn_ms, 4),
+                     "kernel": _attn_kernel_name(cfg), "kernel_ms": round(attn_ms, 4),
                      "algorithmic_ops_per_launch": ops},
         "quantizer": {"kernel": "quant_per_block_kernel (Q+K)", "ms": round(quant_ms, 4),
                       "GB/s": round(quant_bytes / (quant_ms * 1e-3) / 1e9, 1), "peak_GB/s": 8000},

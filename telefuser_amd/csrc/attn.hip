@@ -207,7 +207,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   const int64_t hk = h / p.group;
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, lane = tid & 63, lq = lane & 31, hf = lane >> 5;
+  // (wave index in a scalar register, so that every per-wave quantity and branch stays scalar)
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31, hf = lane >> 5;
 
   // key range of this workgroup
   int64_t q_first = qb * kBQ;
@@ -1257,6 +1258,336 @@ __global__ __launch_bounds__(kThreads) void qattn_fwd_wide_kernel(AttnParams p) 
   qattn_fwd_wide<IS_FP16_OUT, KT>(p);
 }
 
+// ---- ping-pong workgroups: two groups of four waves, one wave of each group per SIMD ----
+//
+// In qattn_fwd_kernel the two waves of a SIMD belong to different workgroups and fall into step with
+// each other: both run their softmax on the VALU, then both run their MFMAs, so a SIMD spends the sum
+// of the two phases per tile.  Here one workgroup holds two query blocks of the same head (group 0 =
+// waves 0-3, group 1 = waves 4-7; wave w runs on SIMD w % 4) and the groups alternate through workgroup
+// barriers, half a tile apart:
+//
+//   group 0:  M(0) | V(0) | M(1) | V(1) | ...        M(t) = P(t-1).V(t-1), row sum, Q.K(t)^T (matrix pipe)
+//   group 1:    -  | M(0) | V(0) | M(1) | ...        V(t) = mask, softmax, P(t) to e4m3  (VALU)
+//
+// so at every step one wave of a SIMD feeds the matrix pipe while the other runs the VALU softmax, and
+// a SIMD spends about max(MFMA, VALU) per step instead of their sum.  Per element the arithmetic is
+// that of qattn_fwd_kernel (32 rows per wave, same MFMA chains, lazy running max, FP8 offset, row sums
+// on the matrix pipe), so both kernels give identical results.
+//
+// K/V tiles come in by LDS DMA, four buffers, two tiles ahead: every wave moves 1 KiB of K and 1 KiB of
+// V of tile t + 2 at the start of its stage M(t) and has its share of tile t + 1 landed by the end of
+// M(t); tile t is read as K in M(t) and as V during V(t) (operands of M(t + 1)), so its buffer is free
+// once both groups have finished M(t + 1).
+constexpr int kPPThreads = 512;
+constexpr int kPPNBuf = 4;
+
+// workgroup barrier that the compiler neither crosses with memory operations nor schedules around
+__device__ __forceinline__ void pp_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <bool IS_FP16_OUT, bool KT>
+__device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
+  constexpr int KS = ks_per_tile(KT);
+  constexpr int NB = kPPNBuf;
+  __shared__ __align__(16) uint8_t lds_k[NB][kBK * kD];
+  __shared__ __align__(16) uint8_t lds_v[NB][kD * kBK];
+  auto buf_of = [](int t) { return (int)((unsigned)t % (unsigned)NB); };
+  __shared__ float lds_ks[ks_lds_floats<PV_FP8>()];
+  __shared__ __align__(16) float lds_vs[kD];
+
+  const int64_t nQP = (p.nQB + 1) / 2;
+  const int64_t tile_id = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t qp = tile_id % nQP;
+  const int64_t rest = tile_id / nQP;
+  const int64_t h = rest % p.Hq;
+  const int64_t b = rest / p.Hq;
+  const int64_t hk = h / p.group;
+
+  const int tid = threadIdx.x;
+  // (wave index in a scalar register, so that every per-wave quantity and branch stays scalar)
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31, hf = lane >> 5;
+  const int grp = w >> 2, wl = w & 3;
+  const int64_t qb = qp * 2 + grp;  // == nQB for the empty second group of an odd block count
+  const int64_t q_first = qb * kBQ;
+  const int64_t wrow0 = q_first + wl * 32;
+  const int64_t qrow = wrow0 + lq;
+
+  // key range of this group, and of the workgroup (its last non-empty group)
+  int64_t kv_lim = p.Lk;
+  if (p.kv_valid) kv_lim = min(kv_lim, (int64_t)p.kv_valid[b]);
+  int64_t kv_end = kv_lim, kv_end_wg = kv_lim;
+  if (p.causal) {
+    kv_end = min(kv_lim, q_first + kBQ + p.q_offset);
+    kv_end_wg = min(kv_lim, min(qp * 2 + 1, p.nQB - 1) * kBQ + kBQ + p.q_offset);
+  }
+  // (wave-uniform values in scalar registers: kv_valid comes through a vector load)
+  const int kv_end_s = __builtin_amdgcn_readfirstlane((int)kv_end);
+  // last key that the wave's first row may see (causal), clamped so that adding a row index stays in range
+  constexpr int kNoDiag = INT32_MAX - 128;
+  const int diag_s = p.causal ? __builtin_amdgcn_readfirstlane((int)min(wrow0 + p.q_offset, (int64_t)kNoDiag)) : kNoDiag;
+  const int n_tiles = __builtin_amdgcn_readfirstlane(kv_end_wg > 0 ? (int)((kv_end_wg + kBK - 1) / kBK) : 0);
+
+  // Q fragments through the wave-private LDS stage (rows row-contiguous, chunk c of row r at c ^ (r & 7))
+  uint8_t* stage = &lds_k[0][0] + w * 4096;
+  v4i qf[4];
+  {
+    const int8_t* qbase = p.q8 + b * p.qsb + h * p.qsh;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int r = i * 8 + (lane >> 3), c = lane & 7;
+      const int64_t row = wrow0 + r;
+      const v4i val = row < p.Lq ? *reinterpret_cast<const v4i*>(qbase + row * p.qsl + c * 16) : v4i{0, 0, 0, 0};
+      *reinterpret_cast<v4i*>(stage + r * 128 + ((c ^ (r & 7)) << 4)) = val;
+    }
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      const int c = 2 * m + hf;
+      qf[m] = *reinterpret_cast<const v4i*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4));
+    }
+#pragma unroll
+    for (int m = 0; m < 4; m++) asm volatile("" ::"v"(qf[m]));
+  }
+  const int64_t qbs = min(qb, p.nQB - 1);
+  const int64_t qsi = p.qgran == QATTN_GRAN_THREAD ? (qbs * 4 + wl) * 8 + (lq & 7)
+                      : p.qgran == QATTN_GRAN_WARP ? qbs * 4 + wl
+                                                   : qbs;
+  const float qs = p.q_scale[(b * p.Hq + h) * p.nQS + qsi] * p.qk_mult;
+  const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
+
+  // LDS DMA: wave w moves LDS slots 64 w .. 64 w + 63 (16 B each) of the K tile and of the V tile
+  const int8_t* kbase = p.k8 + b * p.ksb + hk * p.ksh;
+  const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad;
+  const int64_t kbytes = (p.Lk - 1) * p.ksl + kD;
+  const v4u vrsrc = make_rsrc(vbase, (uint32_t)((int64_t)kD * p.Lpad));
+  uint32_t koff, voff;
+  {
+    const int slot = w * 64 + lane;
+    const int kr = slot >> 3;
+    koff = (uint32_t)(kr * p.ksl + (((slot & 7) ^ ((kr >> 1) & 7)) << 4));
+    const int vd = slot >> 2;
+    voff = (uint32_t)(vd * p.Lpad + (((slot & 3) ^ ((vd >> 2) & 3)) << 4));
+  }
+  const int64_t k_step = kBK * p.ksl;
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const uint32_t lds_k0 = lds_addr(&lds_k[0][0]) + wu * 1024;
+  const uint32_t lds_v0 = lds_addr(&lds_v[0][0]) + wu * 1024;
+  auto dma_tile = [&](int t) {
+    const int buf = buf_of(t);
+    const int64_t kso = (int64_t)t * k_step;
+    lds_dma16(koff, make_rsrc(kbase + kso, (uint32_t)(kbytes - kso)), 0, lds_k0 + buf * (kBK * kD));
+    lds_dma16(voff, vrsrc, (uint32_t)t * kBK, lds_v0 + buf * (kD * kBK));
+  };
+
+  v16f o[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) o[i][r] = 0.f;
+  float m_run = kMInit;
+  v16f lacc;
+#pragma unroll
+  for (int r = 0; r < 16; r++) lacc[r] = 0.f;
+  v16i kbias;
+#pragma unroll
+  for (int r = 0; r < 16; r++) kbias[r] = kAccBiasBits;
+
+  __syncthreads();  // Q fragments are out of the LDS stage before the DMA reuses it
+  for (int64_t i = tid; i < n_tiles * KS; i += kPPThreads) lds_ks[i] = ks_ptr[i];
+  if (tid < kD) lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * kD + tid];
+  for (int t = 0; t < min(n_tiles, 2); t++) dma_tile(t);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  v16i s[2];
+  v8i pf, vf[4];
+  v4i kf[8];
+  float cs_a, cs_b;  // logit scales of the tile in the softmax
+  auto read_k = [&](int t) {
+    const int buf = buf_of(t);
+#pragma unroll
+    for (int j = 0; j < 8; j++)
+      kf[j] = *reinterpret_cast<const v4i*>(&lds_k[buf][k_lds_off((j & 1) * 32 + lq, 2 * (j >> 1) + hf)]);
+  };
+  auto read_cs = [&](int t) {
+    if constexpr (KT) {
+      cs_a = qs * lds_ks[t * 4 + 2 * hf];
+      cs_b = qs * lds_ks[t * 4 + 2 * hf + 1];
+    } else {
+      cs_a = cs_b = qs * lds_ks[t];
+    }
+  };
+  auto read_v = [&](int t) {
+    const int buf = buf_of(t);
+#pragma unroll
+    for (int dblk = 0; dblk < 4; dblk++) {
+      const int d = dblk * 32 + lq;
+      const v4i a0 = *reinterpret_cast<const v4i*>(&lds_v[buf][v_lds_off(d, 2 * hf)]);
+      const v4i a1 = *reinterpret_cast<const v4i*>(&lds_v[buf][v_lds_off(d, 2 * hf + 1)]);
+      vf[dblk] = v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+    }
+  };
+  // stage M: P(t-1).V(t-1) and its row sum (operands from the previous stage V), then S^T(t) = K(t).Q^T
+  auto pv = [&]() {
+#pragma unroll
+    for (int dblk = 0; dblk < 4; dblk++)
+      o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, o[dblk], 0, 0, 0, 0, 0, 0);
+    lacc = row_sum_mfma(lacc, pf);
+  };
+  auto qk = [&]() {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int m = j >> 1, kb = j & 1;
+      s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j], qf[m], m == 0 ? kbias : s[kb], 0, 0, 0);
+    }
+  };
+  auto stage_m = [&](int t) {
+    if (t > 0) read_v(t - 1);
+    read_k(t);
+    if (t > 0) pv();
+    qk();
+    // the logit scales of the tile, for the softmax of the next stage
+    read_cs(t);
+  };
+  // stage V: V(t) fragments out of LDS (operands of the next stage M), mask, online softmax, P(t) to e4m3
+  auto stage_v = [&](int t) {
+    const int k0 = t * kBK;
+    const bool masked = (k0 + kBK > kv_end_s) || (k0 + kBK - 1 > diag_s);
+    if (masked) {
+      int lim = max(min(kv_end_s - k0, kBK), -1);
+      lim = min(lim, max(min(diag_s + lq + 1 - k0, kBK), -1));
+      lim -= hf * 4;
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++)
+          if (kb * 32 + (r >> 2) * 8 + (r & 3) >= lim) s[kb][r] = INT32_MIN;
+    }
+    float m_tile;
+    if constexpr (!KT) {
+      int mx = max(s[0][0], s[0][1]);
+#pragma unroll
+      for (int r = 2; r < 16; r++) mx = max(mx, s[0][r]);
+#pragma unroll
+      for (int r = 0; r < 16; r++) mx = max(mx, s[1][r]);
+      const auto sw = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);
+      mx = max((int)sw[0], (int)sw[1]);
+      m_tile = mx == INT32_MIN ? kMInit : fmaf(__int_as_float(mx), cs_a, -fmaf(kAccBias, cs_a, kFp8Offset - kLazyTau));
+    } else {
+      int ma = INT32_MIN, mb = INT32_MIN;
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          if ((r & 3) < 2) ma = max(ma, s[kb][r]);
+          else mb = max(mb, s[kb][r]);
+        }
+      const float fa = ma == INT32_MIN ? kMInit : fmaf(__int_as_float(ma), cs_a, -fmaf(kAccBias, cs_a, kFp8Offset - kLazyTau));
+      const float fb = mb == INT32_MIN ? kMInit : fmaf(__int_as_float(mb), cs_b, -fmaf(kAccBias, cs_b, kFp8Offset - kLazyTau));
+      const float mt = fmaxf(fa, fb);
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+      m_tile = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
+    const bool grow = m_tile > m_run + kLazyTau;
+    if (__any(grow)) {
+      const float m_new = grow ? m_tile : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[i][r] *= alpha;
+#pragma unroll
+      for (int r = 0; r < 16; r++) lacc[r] *= alpha;
+      m_run = m_new;
+    }
+    const float nc_a = -fmaf(kAccBias, cs_a, m_run), nc_b = -fmaf(kAccBias, cs_b, m_run);
+    auto body = [&](auto mk) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const int kb = j >> 2, r0 = (j & 3) * 4;
+        float pv[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const int sv = s[kb][r0 + e];
+          pv[e] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(sv), e < 2 ? cs_a : cs_b, e < 2 ? nc_a : nc_b));
+          if constexpr (decltype(mk)::value) pv[e] = sv == INT32_MIN ? 0.f : pv[e];
+        }
+        const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], pf[j], false);
+        pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
+      }
+    };
+    if (masked) body(std::true_type{});
+    else body(std::false_type{});
+  };
+
+  if (grp == 1) pp_barrier();
+  for (int t = 0; t < n_tiles; t++) {
+    const bool issue = t + 2 < n_tiles;
+    if (issue) dma_tile(t + 2);
+    // the matrix stage runs at raised wave priority: the vector-stage wave of the SIMD then cannot
+    // delay the issue of its MFMAs (measured faster than equal priorities)
+    __builtin_amdgcn_s_setprio(1);
+    stage_m(t);
+    __builtin_amdgcn_s_setprio(0);
+    // this wave's share of tile t + 1 has landed (tile t + 2 may stay in flight)
+    if (issue) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    pp_barrier();
+    stage_v(t);
+    pp_barrier();
+  }
+  if (grp == 0) pp_barrier();
+  if (n_tiles > 0) {
+    read_v(n_tiles - 1);
+#pragma unroll
+    for (int dblk = 0; dblk < 4; dblk++)
+      o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, o[dblk], 0, 0, 0, 0, 0, 0);
+    lacc = row_sum_mfma(lacc, pf);
+  }
+
+  // ---- epilogue: O / l * v_scale out through the wave's LDS stage (the K buffers are idle now) ----
+  const float l_tot = lacc[0];
+  const float inv_l = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  uint16_t* obase = static_cast<uint16_t*>(p.o) + b * p.osb + h * p.osh;
+#pragma unroll
+  for (int pass = 0; pass < 2; pass++) {
+#pragma unroll
+    for (int db = 0; db < 2; db++) {
+      const int dblk = pass * 2 + db;
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int d = dblk * 32 + g * 8 + hf * 4;
+        const v4f sc = *reinterpret_cast<const v4f*>(&lds_vs[d]);
+        float f[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) f[e] = o[dblk][g * 4 + e] * inv_l * sc[e];
+        const v2u packed{pack_half2<IS_FP16_OUT>(f[0], f[1]), pack_half2<IS_FP16_OUT>(f[2], f[3])};
+        const int c = db * 4 + g;
+        *reinterpret_cast<v2u*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4) + hf * 8) = packed;
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int r = i * 8 + (lane >> 3), c = lane & 7;
+      const v4u val = *reinterpret_cast<const v4u*>(stage + r * 128 + ((c ^ (r & 7)) << 4));
+      const int64_t row = wrow0 + r;
+      if (row < p.Lq) *reinterpret_cast<v4u*>(obase + row * p.osl + pass * 64 + c * 8) = val;
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  }
+  if (p.lse && hf == 0 && qrow < p.Lq)
+    p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
+}
+
+template <bool IS_FP16_OUT, bool KT>
+__global__ __launch_bounds__(kPPThreads) void qattn_fwd_pp_kernel(AttnParams p) {
+  qattn_fwd_pp<IS_FP16_OUT, KT>(p);
+}
+
 // Merge the KV-split partials: one wave per query row, 2 channels per lane.
 template <bool IS_FP16_OUT>
 __global__ __launch_bounds__(256) void qattn_combine_kernel(AttnParams p) {
@@ -1344,6 +1675,15 @@ static bool wide_enabled() {
   return e && e[0] == '1';
 }
 
+// Dense FP8 launches without a KV split go to the ping-pong kernel when its grid (one workgroup per
+// two query blocks, one workgroup per CU) fills the 256 CUs; QATTN_PP=0 / QATTN_PP=1 in the environment
+// (read at every launch) turns it off / on regardless of the grid size.
+static bool pp_enabled(int64_t grid) {
+  const char* e = getenv("QATTN_PP");
+  if (e && e[0]) return e[0] == '1';
+  return grid >= 256;
+}
+
 template <int PV, bool KT, bool SP = false>
 static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, size_t workspace_bytes, hipStream_t st,
                       int64_t D) {
@@ -1375,7 +1715,12 @@ static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, siz
     if (out_dtype == QATTN_BF16) qattn_combine_kernel<false><<<(rows + 3) / 4, 256, 0, st>>>(p);
     else qattn_combine_kernel<true><<<(rows + 3) / 4, 256, 0, st>>>(p);
   } else if constexpr (PV == PV_FP8 && !SP) {
-    if (wide_enabled() && p.nKB * ks_per_tile(KT) <= kWideKsFloats) {
+    const int64_t g = p.B * p.Hq * ((p.nQB + 1) / 2);
+    if (pp_enabled(g)) {
+      QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
+      if (out_dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT><<<g, kPPThreads, 0, st>>>(p);
+      else qattn_fwd_pp_kernel<true, KT><<<g, kPPThreads, 0, st>>>(p);
+    } else if (wide_enabled() && p.nKB * ks_per_tile(KT) <= kWideKsFloats) {
       const int64_t g = p.B * p.Hq * ((p.Lq + kWideRows - 1) / kWideRows);
       if (out_dtype == QATTN_BF16) qattn_fwd_wide_kernel<false, KT><<<g, kThreads, 0, st>>>(p);
       else qattn_fwd_wide_kernel<true, KT><<<g, kThreads, 0, st>>>(p);

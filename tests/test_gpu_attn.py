@@ -423,13 +423,24 @@ def test_multi_block_workgroups(oracle, case):
     assert float(np.max(np.abs(lse[:1, 7:8].cpu().numpy() - ref_lse))) < 2e-2
 
 
-@pytest.mark.parametrize("case", ["ragged", "padding", "causal", "gqa_hnd_thread", "long"])
-def test_wide_kernel_matches(oracle, case, monkeypatch):
-    """The opt-in wide kernel (QATTN_WIDE=1: 64 query rows per wave, software-pipelined halves) runs the
-    same per-element arithmetic and accumulation order as qattn_fwd_kernel, so its output and LSE must be
-    identical, bit for bit, on the same quantized operands; checked on ragged lengths (a masked tail tile
-    through its plain loop), key padding, top-left causal, GQA + HND + per-thread scales and a key range
-    long enough for the steady-state pipeline.  One case is also checked against the oracle."""
+ALT_KERNELS = {  # opt-in kernels for dense FP8 launches: environment settings
+    "wide": {"QATTN_WIDE": "1", "QATTN_PP": "0"},
+    "pingpong": {"QATTN_WIDE": "0", "QATTN_PP": "1"},
+    "pingpong_kpre": {"QATTN_WIDE": "0", "QATTN_PP": "2"},
+}
+
+
+@pytest.mark.parametrize("kernel", list(ALT_KERNELS))
+@pytest.mark.parametrize("case", ["ragged", "padding", "causal", "causal_odd", "gqa_hnd_thread", "long"])
+def test_alt_kernel_matches(oracle, kernel, case, monkeypatch):
+    """The alternative dense FP8 kernels run the same per-element arithmetic and accumulation order as
+    qattn_fwd_kernel, so their output and LSE must be identical, bit for bit, on the same quantized
+    operands: the wide kernel (QATTN_WIDE=1: 64 query rows per wave, software-pipelined halves) and the
+    ping-pong kernel (QATTN_PP=1 or 2: two 4-wave groups per workgroup alternating matrix and vector
+    stages; 2 reads V one stage earlier).  Checked on ragged lengths (masked tail tiles), key padding per
+    batch, top-left causal, causal with an odd number of query blocks and more keys than queries, GQA +
+    HND + per-thread scales and a key range long enough for the steady-state pipeline.  The long case is
+    also checked against the oracle."""
     dev = require_gpu()
     from telefuser_amd import sageattn2 as sa
 
@@ -437,10 +448,11 @@ def test_wide_kernel_matches(oracle, case, monkeypatch):
         "ragged": (2, 1000, 777, 3, 3, "NHD", False, None, "per_block"),
         "padding": (1, 600, 512, 4, 4, "NHD", False, [300], "per_block"),
         "causal": (1, 1024, 1024, 2, 2, "NHD", True, None, "per_block"),
+        "causal_odd": (2, 1100, 1300, 2, 2, "NHD", True, [1300, 900], "per_block"),
         "gqa_hnd_thread": (1, 2000, 1500, 4, 2, "HND", False, None, "per_thread"),
         "long": (1, 700, 8200, 2, 2, "NHD", False, None, "per_block"),
     }[case]
-    log(f"wide vs default: {case} B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} layout={layout} causal={causal} "
+    log(f"{kernel} vs default: {case} B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} layout={layout} causal={causal} "
         f"kv_valid={kv_valid} gran={gran}")
     q, k, v = qkv(B, Lq, Lk, Hq, Hkv, seed=4242, k_offset_std=0.5)
     qd, kd, vd = (t.to(dev) for t in (q, k, v))
@@ -457,20 +469,22 @@ def test_wide_kernel_matches(oracle, case, monkeypatch):
     kw = dict(tensor_layout=layout, out_dtype=torch.bfloat16, is_causal=causal, kv_valid_len=kv_valid,
               return_lse=True, qk_mult=qk_mult, qk_quant_gran=gran, num_splits=1)
     monkeypatch.setenv("QATTN_WIDE", "0")
+    monkeypatch.setenv("QATTN_PP", "0")
     o0, l0 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
-    monkeypatch.setenv("QATTN_WIDE", "1")
+    for key, val in ALT_KERNELS[kernel].items():
+        monkeypatch.setenv(key, val)
     o1, l1 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
     o2, l2 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
     torch.cuda.synchronize()
-    assert torch.equal(o1, o2) and torch.equal(l1, l2), "wide kernel is not deterministic"
-    assert torch.equal(o0, o1), f"wide kernel differs: max {float((o0.float() - o1.float()).abs().max()):.4g}"
+    assert torch.equal(o1, o2) and torch.equal(l1, l2), f"{kernel} kernel is not deterministic"
+    assert torch.equal(o0, o1), f"{kernel} kernel differs: max {float((o0.float() - o1.float()).abs().max()):.4g}"
     assert torch.equal(l0, l1)
     if case == "long":
         ref = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
                                ks.cpu().numpy(), v8=untile_v(v8), v_scale=vs.cpu().numpy(),
                                lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED)
         c = cosine(o1.float().cpu().numpy(), ref)
-        log(f"  wide kernel vs quantized oracle: cosine={c:.6f}")
+        log(f"  {kernel} kernel vs quantized oracle: cosine={c:.6f}")
         assert c >= COS_KERNEL
 
 
