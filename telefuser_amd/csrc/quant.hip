@@ -343,7 +343,11 @@ __global__ __launch_bounds__(256) void v_fp8_kernel(const uint16_t* in, int64_t 
                                                     int64_t L, int64_t H, const float* recp, uint8_t* v8,
                                                     int64_t Lpad, VTileFilter filt) {
   constexpr int TPR = D / 8;
-  __shared__ __align__(16) uint8_t tile[D][64];
+  // The tile as 4-byte words: word w of channel d holds the tile-permuted key slots 4w .. 4w + 3.  Its
+  // 16-byte chunks (4 words) are XOR-swizzled by the channel group (d / 8) & 3, so that the word stores
+  // of a wave (16 channel groups x 4 key quads) spread over the banks and each chunk is still read back
+  // with one 16-byte load.
+  __shared__ __align__(16) uint32_t tile[D][16];
   const int64_t t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
   if (filt.grown && !filt.grown[b * H + h]) {
@@ -352,36 +356,38 @@ __global__ __launch_bounds__(256) void v_fp8_kernel(const uint16_t* in, int64_t 
     if (!hit) return;  // uniform over the workgroup
   }
   const float* rc = recp + (b * H + h) * D;
+  // thread: key quad q (keys 4q .. 4q + 3 of the tile, which occupy consecutive slots) x 8 channels
+  for (int c = tid; c < 16 * TPR; c += 256) {
+    const int q = c / TPR, dc = c % TPR;
+    uint16_t hv[4][8];
 #pragma unroll
-  for (int i = 0; i < 64 * TPR / 256; i++) {
-    const int c = tid + i * 256;
-    const int row = c / TPR, dc = c % TPR;
-    const int64_t l = t * 64 + row;
-    uint16_t hv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (l < L) {
-      v4u raw = *reinterpret_cast<const v4u*>(in + b * sb + l * sl + h * sh + dc * 8);
-      __builtin_memcpy(hv, &raw, 16);
+    for (int r = 0; r < 4; r++) {
+      const int64_t l = t * 64 + 4 * q + r;
+      v4u raw = {0u, 0u, 0u, 0u};
+      if (l < L) raw = *reinterpret_cast<const v4u*>(in + b * sb + l * sl + h * sh + dc * 8);
+      __builtin_memcpy(hv[r], &raw, 16);
     }
-    const int pos = vtile_pos(row);
+    const int wi = vtile_pos(4 * q) >> 2;
+    const int sw = (dc & 3) << 2;
 #pragma unroll
     for (int e = 0; e < 8; e++) {
       const int d = dc * 8 + e;
-      const float y = half_to_f32<IS_FP16>(hv[e]) * rc[d];
-      tile[d][pos] = f32_to_e4m3_sat(y);
+      const float s = rc[d];
+      uint32_t word = 0;
+#pragma unroll
+      for (int r = 0; r < 4; r++) word |= (uint32_t)f32_to_e4m3_sat(half_to_f32<IS_FP16>(hv[r][e]) * s) << (8 * r);
+      tile[d][wi ^ sw] = word;
     }
   }
   __syncthreads();
-#pragma unroll
-  for (int i = 0; i < D * 4 / 256; i++) {
-    const int c = tid + i * 256;
+  for (int c = tid; c < D * 4; c += 256) {
     const int d = c / 4, cc = c % 4;
+    const int sc = cc ^ ((d >> 3) & 3);
     *reinterpret_cast<v4u*>(v8 + ((b * H + h) * D + d) * Lpad + t * 64 + cc * 16) =
-        *reinterpret_cast<const v4u*>(&tile[d][cc * 16]);
+        *reinterpret_cast<const v4u*>(&tile[d][sc * 4]);
   }
 }
 
-
-// V (half) -> the same transposed, tile-permuted layout in its own dtype, for the bf16/fp16 P.V path
 template <int D>
 __global__ __launch_bounds__(256) void v_tile_half_kernel(const uint16_t* in, int64_t sb, int64_t sl, int64_t sh,
                                                           int64_t L, int64_t H, uint16_t* v16, int64_t Lpad) {
