@@ -234,18 +234,30 @@ __global__ __launch_bounds__(256) void col_partial_kernel(NormRope nr, const uin
   float acc[8];
 #pragma unroll
   for (int e = 0; e < 8; e++) acc[e] = 0.f;
-  for (int r = r0; r < kColChunk; r += RPP) {
-    const int64_t l = c * kColChunk + r;
-    if (l < L) {
-      v4u raw = *reinterpret_cast<const v4u*>(in + b * sb + l * sl + h * sh + dc * 8);
-      uint16_t hv[8];
-      __builtin_memcpy(hv, &raw, 16);
-      if (nr.rstd) norm_rope8<IS_FP16>(nr, b, L, l, h, D, dc, hv);
+  // rows r0, r0 + RPP, ... of the chunk, loaded four at a time (four loads in flight per thread) and
+  // accumulated in row order
+  constexpr int kU = 4;
+  for (int r = r0; r < kColChunk; r += kU * RPP) {
+    v4u raw[kU];
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        float v = half_to_f32<IS_FP16>(hv[e]);
-        if constexpr (MODE == 0) acc[e] += v;
-        else acc[e] = fmaxf(acc[e], fabsf(v));
+    for (int u = 0; u < kU; u++) {
+      const int64_t l = c * kColChunk + r + u * RPP;
+      raw[u] = v4u{0u, 0u, 0u, 0u};
+      if (r + u * RPP < kColChunk && l < L) raw[u] = *reinterpret_cast<const v4u*>(in + b * sb + l * sl + h * sh + dc * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < kU; u++) {
+      const int64_t l = c * kColChunk + r + u * RPP;
+      if (r + u * RPP < kColChunk && l < L) {
+        uint16_t hv[8];
+        __builtin_memcpy(hv, &raw[u], 16);
+        if (nr.rstd) norm_rope8<IS_FP16>(nr, b, L, l, h, D, dc, hv);
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          float v = half_to_f32<IS_FP16>(hv[e]);
+          if constexpr (MODE == 0) acc[e] += v;
+          else acc[e] = fmaxf(acc[e], fabsf(v));
+        }
       }
     }
   }
@@ -265,6 +277,14 @@ template <int MODE, int D>
 __device__ __forceinline__ float reduce_chunks(const float* part, int64_t bh, int64_t nchunk, int d) {
   float a[4] = {0.f, 0.f, 0.f, 0.f};
   int64_t c = 0;
+  // 32 chunks per step: all loads first, then the same accumulation order as one chunk at a time
+  for (; c + 32 <= nchunk; c += 32) {
+    float x[32];
+#pragma unroll
+    for (int u = 0; u < 32; u++) x[u] = part[(bh * nchunk + c + u) * D + d];
+#pragma unroll
+    for (int u = 0; u < 32; u++) a[u & 3] = MODE == 0 ? a[u & 3] + x[u] : fmaxf(a[u & 3], x[u]);
+  }
   for (; c + 4 <= nchunk; c += 4)
 #pragma unroll
     for (int u = 0; u < 4; u++) {
