@@ -431,16 +431,17 @@ ALT_KERNELS = {  # opt-in kernels for dense FP8 launches: environment settings
 
 
 @pytest.mark.parametrize("kernel", list(ALT_KERNELS))
-@pytest.mark.parametrize("case", ["ragged", "padding", "causal", "causal_odd", "gqa_hnd_thread", "long"])
+@pytest.mark.parametrize("case", ["ragged", "padding", "causal", "causal_odd", "gqa_hnd_thread", "fp16_warp_gqa",
+                                  "long"])
 def test_alt_kernel_matches(oracle, kernel, case, monkeypatch):
     """The alternative dense FP8 kernels run the same per-element arithmetic and accumulation order as
     qattn_fwd_kernel, so their output and LSE must be identical, bit for bit, on the same quantized
     operands: the wide kernel (QATTN_WIDE=1: 64 query rows per wave, software-pipelined halves) and the
-    ping-pong kernel (QATTN_PP=1 or 2: two 4-wave groups per workgroup alternating matrix and vector
-    stages; 2 reads V one stage earlier).  Checked on ragged lengths (masked tail tiles), key padding per
+    ping-pong kernel (QATTN_PP=1: two 4-wave groups per workgroup alternating matrix and vector stages,
+    forced here whatever the grid size).  Checked on ragged lengths (masked tail tiles), key padding per
     batch, top-left causal, causal with an odd number of query blocks and more keys than queries, GQA +
-    HND + per-thread scales and a key range long enough for the steady-state pipeline.  The long case is
-    also checked against the oracle."""
+    HND + per-thread scales, GQA + per-warp scales + fp16 output, and a key range long enough for the
+    steady-state pipeline.  The long case is also checked against the oracle."""
     dev = require_gpu()
     from telefuser_amd import sageattn2 as sa
 
@@ -450,6 +451,7 @@ def test_alt_kernel_matches(oracle, kernel, case, monkeypatch):
         "causal": (1, 1024, 1024, 2, 2, "NHD", True, None, "per_block"),
         "causal_odd": (2, 1100, 1300, 2, 2, "NHD", True, [1300, 900], "per_block"),
         "gqa_hnd_thread": (1, 2000, 1500, 4, 2, "HND", False, None, "per_thread"),
+        "fp16_warp_gqa": (1, 900, 1100, 6, 2, "NHD", False, None, "per_warp"),
         "long": (1, 700, 8200, 2, 2, "NHD", False, None, "per_block"),
     }[case]
     log(f"{kernel} vs default: {case} B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} layout={layout} causal={causal} "
@@ -463,10 +465,12 @@ def test_alt_kernel_matches(oracle, kernel, case, monkeypatch):
     if gran == "per_block":
         q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=128 ** -0.5, tensor_layout=layout)
     else:
-        q8, qs, k8, ks = sa.per_thread_int8(qd, kd, km, tensor_layout=layout)
+        quant = sa.per_thread_int8 if gran == "per_thread" else sa.per_warp_int8
+        q8, qs, k8, ks = quant(qd, kd, km, tensor_layout=layout)
         qk_mult = 128 ** -0.5 * LOG2E
     v8, vs, _ = sa.per_channel_fp8(vd, tensor_layout=layout)
-    kw = dict(tensor_layout=layout, out_dtype=torch.bfloat16, is_causal=causal, kv_valid_len=kv_valid,
+    out_dtype = torch.float16 if case == "fp16_warp_gqa" else torch.bfloat16
+    kw = dict(tensor_layout=layout, out_dtype=out_dtype, is_causal=causal, kv_valid_len=kv_valid,
               return_lse=True, qk_mult=qk_mult, qk_quant_gran=gran, num_splits=1)
     monkeypatch.setenv("QATTN_WIDE", "0")
     monkeypatch.setenv("QATTN_PP", "0")
