@@ -431,15 +431,15 @@ ALT_KERNELS = {  # opt-in kernels for dense FP8 launches: environment settings
 
 
 @pytest.mark.parametrize("kernel", list(ALT_KERNELS))
-@pytest.mark.parametrize("case", ["ragged", "padding", "causal", "causal_odd", "gqa_hnd_thread", "fp16_warp_gqa",
-                                  "long"])
+@pytest.mark.parametrize("case", ["ragged", "padding", "empty_batch", "causal", "causal_odd", "gqa_hnd_thread",
+                                  "fp16_warp_gqa", "long"])
 def test_alt_kernel_matches(oracle, kernel, case, monkeypatch):
     """The alternative dense FP8 kernels run the same per-element arithmetic and accumulation order as
     qattn_fwd_kernel, so their output and LSE must be identical, bit for bit, on the same quantized
     operands: the wide kernel (QATTN_WIDE=1: 64 query rows per wave, software-pipelined halves) and the
     ping-pong kernel (QATTN_PP=1: two 4-wave groups per workgroup alternating matrix and vector stages,
     forced here whatever the grid size).  Checked on ragged lengths (masked tail tiles), key padding per
-    batch, top-left causal, causal with an odd number of query blocks and more keys than queries, GQA +
+    batch (one batch with no valid key at all), top-left causal, causal with an odd number of query blocks and more keys than queries, GQA +
     HND + per-thread scales, GQA + per-warp scales + fp16 output, and a key range long enough for the
     steady-state pipeline.  The long case is also checked against the oracle."""
     dev = require_gpu()
@@ -448,6 +448,7 @@ def test_alt_kernel_matches(oracle, kernel, case, monkeypatch):
     B, Lq, Lk, Hq, Hkv, layout, causal, kv_valid, gran = {
         "ragged": (2, 1000, 777, 3, 3, "NHD", False, None, "per_block"),
         "padding": (1, 600, 512, 4, 4, "NHD", False, [300], "per_block"),
+        "empty_batch": (2, 700, 600, 2, 2, "NHD", False, [600, 0], "per_block"),
         "causal": (1, 1024, 1024, 2, 2, "NHD", True, None, "per_block"),
         "causal_odd": (2, 1100, 1300, 2, 2, "NHD", True, [1300, 900], "per_block"),
         "gqa_hnd_thread": (1, 2000, 1500, 4, 2, "HND", False, None, "per_thread"),
@@ -483,6 +484,8 @@ def test_alt_kernel_matches(oracle, kernel, case, monkeypatch):
     assert torch.equal(o1, o2) and torch.equal(l1, l2), f"{kernel} kernel is not deterministic"
     assert torch.equal(o0, o1), f"{kernel} kernel differs: max {float((o0.float() - o1.float()).abs().max()):.4g}"
     assert torch.equal(l0, l1)
+    if case == "empty_batch":  # no valid key: zero output, LSE -inf
+        assert bool((o1[1] == 0).all()) and bool(torch.isneginf(l1[1]).all())
     if case == "long":
         ref = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
                                ks.cpu().numpy(), v8=untile_v(v8), v_scale=vs.cpu().numpy(),
