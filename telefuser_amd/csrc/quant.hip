@@ -76,7 +76,7 @@ struct QuantArgs {
   int njobs;
 };
 
-constexpr int kQuantThreads = 256;
+constexpr int kQuantThreads = 512;
 // Rounding of the Triton per-thread quantizer (quant_per_thread.py:63-70): scale = amax/127 + 1e-7,
 // half-rounded K - km, round half away.  Used with per-thread scale classes only.
 constexpr int QATTN_QUANT_TRITON_THREAD = 2;
@@ -178,11 +178,13 @@ __global__ __launch_bounds__(kQuantThreads) void quant_per_block_kernel(QuantArg
     if (tid % TPR == 0) row_max[tid / TPR] = amax;
     __syncthreads();
     amax = class_max(cls);
-  } else {  // one scale per block: wave max, then across the 4 waves
+  } else {  // one scale per block: wave max, then across the waves
     amax = wave_max(amax);
     if ((tid & 63) == 0) row_max[tid >> 6] = amax;
     __syncthreads();
-    amax = fmaxf(fmaxf(row_max[0], row_max[1]), fmaxf(row_max[2], row_max[3]));
+    amax = row_max[0];
+#pragma unroll
+    for (int w = 1; w < kQuantThreads / 64; w++) amax = fmaxf(amax, row_max[w]);
   }
 
   // IEEE division (hipcc default: correctly rounded)
