@@ -76,10 +76,13 @@ struct QuantArgs {
   int njobs;
 };
 
-constexpr int kQuantThreads = 512;
 // Rounding of the Triton per-thread quantizer (quant_per_thread.py:63-70): scale = amax/127 + 1e-7,
 // half-rounded K - km, round half away.  Used with per-thread scale classes only.
 constexpr int QATTN_QUANT_TRITON_THREAD = 2;
+// threads per quantizer workgroup: 512 (4 chunks of 16 bytes per thread at 128 rows; measured faster than
+// 256 and 1024) for one scale per block, 256 for the per-thread scale classes (their class maxima loop
+// over the rows of a pass, twice as many at 512)
+template <int VARIANT> constexpr int quant_threads() { return VARIANT == QATTN_QUANT_TRITON_THREAD ? 256 : 512; }
 
 // Round-half-away-from-zero of the Triton kernel: t + 0.5*sign, truncate; NaN -> 0.
 __device__ __forceinline__ int8_t s8_half_away(float t) {
@@ -97,7 +100,8 @@ __device__ __forceinline__ int8_t s8_rne_sat(float t) {
 }
 
 template <bool IS_FP16, int VARIANT, int D>
-__global__ __launch_bounds__(kQuantThreads) void quant_per_block_kernel(QuantArgs args) {
+__global__ __launch_bounds__(quant_threads<VARIANT>()) void quant_per_block_kernel(QuantArgs args) {
+  constexpr int kQuantThreads = quant_threads<VARIANT>();
   constexpr int TPR = D / 8;                       // threads (16-byte chunks) per row
   constexpr int MAXC = 128 * TPR / kQuantThreads;  // chunks per thread at blk = 128
 
@@ -505,8 +509,8 @@ static bool fill_job(QuantJob& J, const qattn_seq& in, const qattn_seq& out, int
 
 template <int D>
 static void launch_quant(const QuantArgs& a, int dtype, int variant, int64_t nwg, hipStream_t st) {
-  dim3 grid((unsigned)nwg), block(kQuantThreads);
-#define QATTN_QK(F16, V) quant_per_block_kernel<F16, V, D><<<grid, block, 0, st>>>(a)
+  dim3 grid((unsigned)nwg);
+#define QATTN_QK(F16, V) quant_per_block_kernel<F16, V, D><<<grid, quant_threads<V>(), 0, st>>>(a)
   if (dtype == QATTN_BF16) {
     if (variant == QATTN_QUANT_CUDA) QATTN_QK(false, QATTN_QUANT_CUDA);
     else if (variant == QATTN_QUANT_TRITON) QATTN_QK(false, QATTN_QUANT_TRITON);
