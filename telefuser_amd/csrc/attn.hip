@@ -1358,18 +1358,23 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   const float qs = p.q_scale[(b * p.Hq + h) * p.nQS + qsi] * p.qk_mult;
   const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
 
-  // LDS DMA: wave w moves LDS slots 64 w .. 64 w + 63 (16 B each) of the K tile and of the V tile
+  // K/V tiles in LDS, fragment-major: 1 KiB block j holds MFMA operand fragment j of all 64 lanes (lane l
+  // at 16 l), so a lane reads its fragments at one per-tile base address plus constant offsets (no
+  // per-fragment address arithmetic) and every read is a contiguous, conflict-free 1 KiB.
+  //   K block j (0..7): lane l gets K row (j & 1) * 32 + l % 32, bytes 16 (2 (j >> 1) + l / 32) .. + 16
+  //   V block 2 dblk + h (h = 0, 1): lane l gets V^T row dblk * 32 + l % 32, bytes 16 (2 (l / 32) + h) .. + 16
+  //     of the tile (the two halves of the lane's P.V A operand)
+  // LDS DMA: wave w fills block w of the K tile and block w of the V tile.
   const int8_t* kbase = p.k8 + b * p.ksb + hk * p.ksh;
   const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad;
   const int64_t kbytes = (p.Lk - 1) * p.ksl + kD;
   const v4u vrsrc = make_rsrc(vbase, (uint32_t)((int64_t)kD * p.Lpad));
   uint32_t koff, voff;
   {
-    const int slot = w * 64 + lane;
-    const int kr = slot >> 3;
-    koff = (uint32_t)(kr * p.ksl + (((slot & 7) ^ ((kr >> 1) & 7)) << 4));
-    const int vd = slot >> 2;
-    voff = (uint32_t)(vd * p.Lpad + (((slot & 3) ^ ((vd >> 2) & 3)) << 4));
+    const int kr = (w & 1) * 32 + lq, kc = 2 * (w >> 1) + hf;
+    koff = (uint32_t)(kr * p.ksl + kc * 16);
+    const int vd = (w >> 1) * 32 + lq, vc = 2 * hf + (w & 1);
+    voff = (uint32_t)(vd * p.Lpad + vc * 16);
   }
   const int64_t k_step = kBK * p.ksl;
   const int wu = __builtin_amdgcn_readfirstlane(w);
@@ -1407,10 +1412,9 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   v4i kf[8];
   float cs_a, cs_b;  // logit scales of the tile in the softmax
   auto read_k = [&](int t) {
-    const int buf = buf_of(t);
+    const uint8_t* kb = &lds_k[buf_of(t)][lane * 16];
 #pragma unroll
-    for (int j = 0; j < 8; j++)
-      kf[j] = *reinterpret_cast<const v4i*>(&lds_k[buf][k_lds_off((j & 1) * 32 + lq, 2 * (j >> 1) + hf)]);
+    for (int j = 0; j < 8; j++) kf[j] = *reinterpret_cast<const v4i*>(kb + j * 1024);
   };
   auto read_cs = [&](int t) {
     if constexpr (KT) {
@@ -1421,12 +1425,11 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     }
   };
   auto read_v = [&](int t) {
-    const int buf = buf_of(t);
+    const uint8_t* vb = &lds_v[buf_of(t)][lane * 16];
 #pragma unroll
     for (int dblk = 0; dblk < 4; dblk++) {
-      const int d = dblk * 32 + lq;
-      const v4i a0 = *reinterpret_cast<const v4i*>(&lds_v[buf][v_lds_off(d, 2 * hf)]);
-      const v4i a1 = *reinterpret_cast<const v4i*>(&lds_v[buf][v_lds_off(d, 2 * hf + 1)]);
+      const v4i a0 = *reinterpret_cast<const v4i*>(vb + (2 * dblk) * 1024);
+      const v4i a1 = *reinterpret_cast<const v4i*>(vb + (2 * dblk + 1) * 1024);
       vf[dblk] = v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
     }
   };
