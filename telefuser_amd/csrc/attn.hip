@@ -97,7 +97,8 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t n) {
   return xcd * q + (xcd < r ? xcd : r) + idx;
 }
 
-// LDS layouts (bytes):
+// Row-major, XOR-swizzled LDS layouts of the wide kernel (bytes; the other kernels keep their tiles
+// fragment-major, see their DMA set-up):
 //   K tile: 64 rows x 128 B, 16-byte chunk c of row r at r*128 + ((c ^ ((r >> 1) & 7)) * 16)
 //   V tile: 128 rows (d) x 64 B, chunk c (0..3) of row d at d*64 + ((c ^ ((d >> 2) & 3)) * 16)
 __device__ __forceinline__ int k_lds_off(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
@@ -287,9 +288,14 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
 
   // global -> LDS copies go through the LDS-DMA path (buffer_load_dwordx4 ... lds): lane j of a wave
-  // writes the 16 bytes at LDS slot (wave base + 16 j), so the XOR swizzle is applied on the global
-  // side: the lane that owns LDS slot (row, chunk c') fetches global chunk c = c' ^ swizzle(row).
-  // Each wave moves 2 x 1 KiB of K and kVDma x 1 KiB of V per tile; no VGPRs are spent on staging.
+  // writes the 16 bytes at LDS slot (wave base + 16 j).  The tiles are fragment-major: 1 KiB block f holds
+  // MFMA operand fragment f of all 64 lanes (lane l at 16 l), so a lane reads its fragments at one base
+  // address plus constant offsets, each read a contiguous, conflict-free 1 KiB:
+  //   K block j (0..7): lane l gets K row (j & 1) * 32 + l % 32, bytes 16 (2 (j >> 1) + l / 32) .. + 16
+  //   FP8 V block 2 dblk + h: lane l gets V^T row dblk * 32 + l % 32, bytes 16 (2 (l / 32) + h) .. + 16
+  //   half V block 4 dblk + c: lane l gets V^T row dblk * 32 + l % 32, bytes 16 (4 (l / 32) + c) .. + 16
+  // DMA instruction i of wave w fills block 4 i + w.  Each wave moves 2 x 1 KiB of K and kVDma x 1 KiB of V
+  // per tile; no VGPRs are spent on staging.
   // The K resource of a tile starts at the tile's first row, so K rows at or past Lk fall outside its
   // range and arrive as zeros (masked anyway) without being read (the range check covers the
   // per-lane offset, not the scalar one).
@@ -301,23 +307,14 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   uint32_t koff[2], voff[kVDma];
 #pragma unroll
   for (int i = 0; i < 2; i++) {
-    const int slot = (i * 4 + w) * 64 + lane;
-    const int kr = slot >> 3;
-    const int kc = (slot & 7) ^ ((kr >> 1) & 7);
-    koff[i] = (uint32_t)(kr * p.ksl + kc * 16);
+    const int j = i * 4 + w;
+    koff[i] = (uint32_t)(((j & 1) * 32 + lq) * p.ksl + (2 * (j >> 1) + hf) * 16);
   }
 #pragma unroll
   for (int i = 0; i < kVDma; i++) {
-    const int slot = (i * 4 + w) * 64 + lane;
-    if constexpr (PV == PV_FP8) {  // 128 rows x 4 chunks, v_lds_off swizzle
-      const int vd = slot >> 2;
-      const int vc = (slot & 3) ^ ((vd >> 2) & 3);
-      voff[i] = (uint32_t)(vd * p.Lpad + vc * 16);
-    } else {  // 128 rows x 8 chunks of 16 bytes (8 halves), k_lds_off swizzle
-      const int vd = slot >> 3;
-      const int vc = (slot & 7) ^ ((vd >> 1) & 7);
-      voff[i] = (uint32_t)(vd * p.Lpad * 2 + vc * 16);
-    }
+    const int f = i * 4 + w;
+    if constexpr (PV == PV_FP8) voff[i] = (uint32_t)(((f >> 1) * 32 + lq) * p.Lpad + (2 * hf + (f & 1)) * 16);
+    else voff[i] = (uint32_t)(((f >> 2) * 32 + lq) * p.Lpad * 2 + (4 * hf + (f & 3)) * 16);
   }
   const int64_t k_step = kBK * p.ksl;
   const uint32_t lds_k0 = lds_addr(&lds_k[0][0]) + __builtin_amdgcn_readfirstlane(w) * 1024;
@@ -498,7 +495,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
       v4i kf[8];  // all K fragments first: the LDS latency is paid once per tile
 #pragma unroll
       for (int j = 0; j < 8; j++)
-        kf[j] = *reinterpret_cast<const v4i*>(&lds_k[buf][k_lds_off((j & 1) * 32 + lq, 2 * (j >> 1) + hf)]);
+        kf[j] = *reinterpret_cast<const v4i*>(&lds_k[buf][j * 1024 + lane * 16]);
       // The QK MFMAs run at raised wave priority: when the other wave of the SIMD is in its softmax
       // VALU phase, the scheduler then keeps the matrix pipe fed from this wave (measured ~6 % faster
       // than equal priorities).
@@ -606,9 +603,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
       v8i vf[4];
 #pragma unroll
       for (int dblk = 0; dblk < 4; dblk++) {
-        const int d = dblk * 32 + lq;
-        const v4i a0 = *reinterpret_cast<const v4i*>(&lds_v[buf][v_lds_off(d, 2 * hf)]);
-        const v4i a1 = *reinterpret_cast<const v4i*>(&lds_v[buf][v_lds_off(d, 2 * hf + 1)]);
+        const v4i a0 = *reinterpret_cast<const v4i*>(&lds_v[buf][(2 * dblk) * 1024 + lane * 16]);
+        const v4i a1 = *reinterpret_cast<const v4i*>(&lds_v[buf][(2 * dblk + 1) * 1024 + lane * 16]);
         vf[dblk] = v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
       }
 #pragma unroll
@@ -640,11 +636,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
       // ---- O^T += V^T . P^T (half MFMA 32x32x16, 4 K-chunks per 32-channel block) ----
 #pragma unroll
       for (int dblk = 0; dblk < 4; dblk++) {
-        const int d = dblk * 32 + lq;
         HV vf[4];
 #pragma unroll
         for (int c = 0; c < 4; c++)
-          vf[c] = *reinterpret_cast<const HV*>(&lds_v[buf][k_lds_off(d, hf * 4 + c)]);
+          vf[c] = *reinterpret_cast<const HV*>(&lds_v[buf][(4 * dblk + c) * 1024 + lane * 16]);
 #pragma unroll
         for (int c = 0; c < 4; c++) {
           if constexpr (PV == PV_BF16) o[dblk] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[c], ph[c], o[dblk], 0, 0, 0);
