@@ -11,7 +11,7 @@
 //   out  = O / l * v_scale[d]
 //
 // MI355X design (not a translation of the NVIDIA tiling):
-//   * workgroup = 4 wave64s = 128 query rows (one Q quantization block, so one q_scale);
+//   * qattn_fwd_kernel: workgroup = 4 wave64s = 128 query rows (one Q quantization block, so one q_scale);
 //     each wave owns 32 rows.  Key tiles of 64 keys (one K quantization block, one k_scale).
 //   * S^T = K . Q^T with v_mfma_i32_32x32x32_i8 (A = K from LDS, B = Q held in VGPRs for the whole
 //     loop).  In the 32x32 result each lane owns one query column and 16 key rows, so the row max
@@ -19,9 +19,12 @@
 //   * O^T = V^T . P^T with v_mfma_f32_32x32x64_f8f6f4 (A = V^T from LDS, B = P^T straight from the
 //     softmax registers).  The FP8 V quantizer stores every 64-key tile in exactly the key order the
 //     B operand inherits from the S^T layout, so P never goes through LDS.
-//   * K tiles are double-buffered and V tiles triple-buffered in LDS (40 KiB) with XOR-swizzled 16-byte chunks; the next
-//     tile is fetched by LDS DMA (global_load_lds_dwordx4) issued before the current tile's
-//     MFMA/softmax work, so staging costs neither VGPRs nor VALU slots.
+//   * K/V tiles are multi-buffered in LDS, fragment-major (each 1 KiB block holds one MFMA operand
+//     fragment of all 64 lanes), and fetched by LDS DMA (buffer_load_dwordx4 ... lds) issued before the
+//     current tile's MFMA/softmax work, so staging costs neither VGPRs nor VALU slots and a lane reads
+//     its fragments from one base address plus constant offsets.
+//   * Large dense launches run the ping-pong kernel (two 4-wave groups per workgroup, 256 rows, whose
+//     waves alternate matrix and vector stages on each SIMD); the per-element arithmetic is the same.
 //   * blockIdx -> tile mapping is XCD-aware: the hardware deals workgroups round-robin over the 8
 //     XCDs, so consecutive tiles of one (batch, head) are gathered onto one XCD and share its L2.
 //   * Optional KV split (flash-decoding style) for grids that cannot fill 256 CUs; a combine kernel
