@@ -21,8 +21,26 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 
+def _cpu_info() -> dict:
+    """Host CPU facts for the CPU-baseline report: model, usable cores (affinity) and OpenMP settings."""
+    model = "?"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": model, "affinity_cpus": len(os.sched_getaffinity(0)), "os_cpu_count": os.cpu_count(),
+            "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
+
+
 def _cpu_baseline(cfg, budget_s: float = 12.0) -> dict:
-    """Time the CPU restatement of the reference math (oracle/) on one head of the workload."""
+    """Time the CPU restatement of the reference math (oracle/, gcc -O3, OpenMP) on a bounded sample of the
+    workload's first head: one fixed single-thread slice (attention only: 128 queries x all keys) for a
+    per-thread rate, then the whole call path (K mean + quantizers + attention) on all threads, growing
+    the query rows until one pass takes about budget_s / 2.  Reports the threads that actually ran."""
     import numpy as np
     import torch
 
@@ -31,50 +49,54 @@ def _cpu_baseline(cfg, budget_s: float = 12.0) -> dict:
 
     oracle.build()
     q, k, v, _ = make_inputs(cfg, "cpu", call=0)
-    h = 0
-    qb = q[:, :, h:h + 1].contiguous().view(torch.int16).numpy().view(np.uint16)
-    kb = k[:, :, h:h + 1].contiguous().view(torch.int16).numpy().view(np.uint16)
-    vb = v[:, :, h:h + 1].contiguous().view(torch.int16).numpy().view(np.uint16)
+    qb = q[:, :, :1].contiguous().view(torch.int16).numpy().view(np.uint16)
+    kb = k[:, :, :1].contiguous().view(torch.int16).numpy().view(np.uint16)
+    vb = v[:, :, :1].contiguous().view(torch.int16).numpy().view(np.uint16)
     sm = cfg.D ** -0.5
-    # grow the sample (queries first, then heads) until one pass takes about budget_s / 2 .. budget_s
-    rows, heads = 256, 1
-    while True:
-        qh, kh, vh = (np.ascontiguousarray(x[:, :, :heads]) for x in (qb, kb, vb))
+    km = oracle.k_mean_bits(kb)
+    k8, ks = oracle.quant_per_block_int8(kb, km_bits=km, blk=64)
+    v8, vs = oracle.per_channel_fp8(vb)
+    q8, qs = oracle.quant_per_block_int8(np.ascontiguousarray(qb[:, :128]), sm_scale=sm * oracle.LOG2E, blk=128)
+    threads_all = oracle.num_threads()
+    oracle.set_threads(1)
+    try:
+        one = oracle.parallel_threads()
         t0 = time.perf_counter()
-        km = oracle.k_mean_bits(kh)
-        q8, qs = oracle.quant_per_block_int8(np.ascontiguousarray(qh[:, :rows]), sm_scale=sm * oracle.LOG2E, blk=128)
-        k8, ks = oracle.quant_per_block_int8(kh, km_bits=km, blk=64)
-        v8, vs = oracle.per_channel_fp8(vh)
         oracle.qattn_fwd(q8, qs, k8, ks, v8, vs)
-        dt = time.perf_counter() - t0
-        if dt * 2 > budget_s:
-            break
-        if rows < cfg.Lq:
-            rows = min(cfg.Lq, rows * 4)
-        elif heads < cfg.Hkv:
-            heads = min(cfg.Hkv, heads * 2)
-        else:
-            break
-    calls = 1
-    if dt * 2 < budget_s:  # the whole call is short: time repeated calls (as the layers of a step would)
-        calls = max(1, int(budget_s / max(dt, 1e-3)))
+        dt1 = time.perf_counter() - t0
+    finally:
+        oracle.set_threads(threads_all)
+    ns_pair_1t = dt1 / (128 * cfg.Lk) * 1e9
+    observed = oracle.parallel_threads()
+
+    def whole(rows):
+        qh = np.ascontiguousarray(qb[:, :rows])
         t0 = time.perf_counter()
-        for _ in range(calls):
-            km = oracle.k_mean_bits(kh)
-            q8, qs = oracle.quant_per_block_int8(np.ascontiguousarray(qh[:, :rows]), sm_scale=sm * oracle.LOG2E,
-                                                 blk=128)
-            k8, ks = oracle.quant_per_block_int8(kh, km_bits=km, blk=64)
-            v8, vs = oracle.per_channel_fp8(vh)
-            oracle.qattn_fwd(q8, qs, k8, ks, v8, vs)
-        dt = time.perf_counter() - t0
-    ops = 4.0 * rows * heads * cfg.Lk * cfg.D * calls
+        kmh = oracle.k_mean_bits(kb)
+        q8h, qsh = oracle.quant_per_block_int8(qh, sm_scale=sm * oracle.LOG2E, blk=128)
+        k8h, ksh = oracle.quant_per_block_int8(kb, km_bits=kmh, blk=64)
+        v8h, vsh = oracle.per_channel_fp8(vb)
+        oracle.qattn_fwd(q8h, qsh, k8h, ksh, v8h, vsh)
+        return time.perf_counter() - t0
+
+    rows = 128 * observed
+    dt = whole(rows)
+    while dt * 2 < budget_s and rows < cfg.Lq:
+        rows = min(cfg.Lq, rows * 2 if dt * 4 < budget_s else int(rows * budget_s / 2 / dt))
+        dt = whole(rows)
+    pairs = rows * cfg.Lk
+    ops = 4.0 * pairs * cfg.D
     return {
         "value": round(ops / dt / 1e12, 6),
         "unit": "TOPS",
-        "cores": oracle.num_threads(),
+        "cores": observed,
         "kind": "port",
-        "sample": f"{calls} call(s) of {heads} of {cfg.Hq} heads, first {rows} of {cfg.Lq} queries x all "
-                  f"{cfg.Lk} keys (K mean + Q/K/V quantizers + attention), {dt:.2f} s",
+        "sample": f"head 0 of {cfg.Hq}, first {rows} of {cfg.Lq} queries x all {cfg.Lk} keys (K mean + Q/K/V "
+                  f"quantizers + attention) on {observed} threads in {dt:.2f} s",
+        "ns_per_query_key_pair_per_thread": round(dt / pairs * 1e9 * observed, 2),
+        "single_thread": {"sample": f"attention only, 128 queries x {cfg.Lk} keys", "s": round(dt1, 3),
+                          "ns_per_query_key_pair": round(ns_pair_1t, 2), "threads_observed": one},
+        "host": dict(_cpu_info(), omp_max_threads=threads_all, omp_threads_observed=observed),
     }
 
 
@@ -168,14 +190,93 @@ def _prologue_bench(reps: int = 10) -> dict:
     return res
 
 
-def _attn_kernel_name(cfg) -> str:
-    """Kernel that a dense, unsplit FP8 launch of `cfg` runs (the library's own selection rule: the
-    ping-pong kernel when its grid of one workgroup per two query blocks fills the 256 CUs, unless
-    QATTN_PP says otherwise)."""
-    grid = cfg.B * cfg.Hq * ((-(-cfg.Lq // 128) + 1) // 2)
-    env = os.environ.get("QATTN_PP", "")
-    use_pp = env == "1" if env else grid >= 256
-    return "qattn_fwd_pp_kernel" if use_pp else "qattn_fwd_kernel"
+def _config_bench(name: str, calls: int = 5, warmup: int = 2) -> dict:
+    """One BASELINE config through the same drop-in sequence as the headline step (K mean, per-block Q/K
+    quantizer, V fp8, attention), inputs resident in HBM: ms per call, the attention launch alone (HIP
+    events on the launch stream) and its roofline fraction.  C4's attention launch is bounded by HBM
+    (int8 Q + K + e4m3 V read once, bf16 O written), the others by the dense INT8/FP8 MFMA peak."""
+    import torch
+
+    from telefuser_amd import _lib
+    from telefuser_amd import sageattn2 as sa
+    from telefuser_amd.workloads import CONFIGS, make_inputs, peak_ops
+
+    cfg = CONFIGS[name]
+    dev = torch.device("cuda:0")
+    q, k, v, kvv = make_inputs(cfg, dev, call=0)
+    sm = cfg.D ** -0.5
+    L = _lib.load()
+    t_attn = []
+
+    def call(record):
+        km = sa.k_mean(k, "NHD")
+        q8, qs, k8, ks = sa.per_block_int8(q, k, km, sm_scale=sm, tensor_layout="NHD")
+        v8, vs, _ = sa.per_channel_fp8(v, tensor_layout="NHD")
+        s = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        o = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout="NHD", out_dtype=q.dtype, kv_valid_len=kvv)
+        e1.record(s)
+        if record:
+            t_attn.append((e0, e1))
+        return o
+
+    for _ in range(warmup):
+        call(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        call(True)
+    torch.cuda.synchronize()
+    ms_call = (time.perf_counter() - t0) * 1e3 / calls
+    kernel = _lib.KERNEL_NAMES.get(L.qattn_last_kernel(), "?")
+    splits = L.qattn_fwd_num_splits(cfg.B, cfg.Lq, cfg.Lk, cfg.Hq)
+    ms_attn = sum(a.elapsed_time(b) for a, b in t_attn) / len(t_attn)
+    ops = cfg.ops()
+    res = {"workload": cfg.name, "calls": calls, "ms_per_call": round(ms_call, 4), "attn_ms": round(ms_attn, 4),
+           "attn_kernel": kernel + (f" + qattn_combine_kernel ({splits} KV splits)" if splits > 1 else ""),
+           "attn_TOPS": round(ops / (ms_attn * 1e-3) / 1e12, 2),
+           "call_TOPS": round(ops / (ms_call * 1e-3) / 1e12, 2),
+           "mfma_frac": round(ops / (ms_attn * 1e-3) / peak_ops("fp8"), 4)}
+    if name == "c4":
+        # algorithmic HBM bytes of the attention launch: int8 Q + int8 K + e4m3 V read once, bf16 O written
+        byts = cfg.B * cfg.Hq * cfg.Lq * cfg.D * (1 + 2) + 2 * cfg.B * cfg.Hkv * cfg.Lk * cfg.D
+        res["bound"] = "hbm"
+        res["attn_GB/s"] = round(byts / (ms_attn * 1e-3) / 1e9, 1)
+        res["hbm_frac"] = round(byts / (ms_attn * 1e-3) / 8e12, 4)
+        res["algorithmic_bytes_per_launch"] = byts
+    else:
+        res["bound"] = "mfma"
+    del q, k, v
+    torch.cuda.empty_cache()
+    return res
+
+
+def _telefuser_call_path(steps: int = 10, warmup: int = 3) -> dict:
+    """C2 through the entry TeleFuser's attention() actually calls for SAGE_ATTN_2_8_8
+    (attention_impl.py:249-258): sageattn_qk_int8_pv_fp8_cuda with qk_quant_gran="per_thread" and
+    pv_accum_dtype="fp32+fp32", bf16 NHD in and out, 30-layer inputs resident in HBM."""
+    import torch
+
+    from telefuser_amd import _lib
+    from telefuser_amd import sageattn2 as sa
+    from telefuser_amd.workloads import CONFIGS, make_inputs
+
+    cfg = CONFIGS["c2"]
+    dev = torch.device("cuda:0")
+    q, k, v, _ = make_inputs(cfg, dev, call=0)
+    kw = dict(tensor_layout="NHD", is_causal=False, qk_quant_gran="per_thread", pv_accum_dtype="fp32+fp32")
+    for _ in range(warmup):
+        sa.sageattn_qk_int8_pv_fp8_cuda(q, k, v, **kw)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        sa.sageattn_qk_int8_pv_fp8_cuda(q, k, v, **kw)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    return {"entry": "sageattn_qk_int8_pv_fp8_cuda(qk_quant_gran='per_thread', pv_accum_dtype='fp32+fp32')",
+            "workload": cfg.name, "ms_per_call": round(ms, 4), "TOPS": round(cfg.ops() / (ms * 1e-3) / 1e12, 2),
+            "attn_kernel": _lib.KERNEL_NAMES.get(_lib.load().qattn_last_kernel(), "?")}
 
 
 def main() -> int:
@@ -188,9 +289,14 @@ def main() -> int:
     ap.add_argument("--no-sdpa", action="store_true")
     ap.add_argument("--no-stream", action="store_true", help="skip the streaming KV-cache comparison")
     ap.add_argument("--no-prologue", action="store_true", help="skip the fused-prologue comparison")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C3 / C4 / C5 and per-thread call-path legs")
+    ap.add_argument("--profile", action="store_true",
+                    help="headline C2 steps only (no SDPA, streaming, prologue, config or CPU legs): for rocprofv3")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
+    if args.profile:
+        args.no_sdpa = args.no_stream = args.no_prologue = args.no_configs = args.no_cpu_baseline = True
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); the path shards "
               "per head across GPUs with no collectives inside the op", file=sys.stderr)
@@ -254,6 +360,7 @@ def main() -> int:
         step(i, True)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    kernel_ran = _lib.KERNEL_NAMES.get(_lib.load().qattn_last_kernel(), "?")
     ms_per_step = elapsed * 1e3 / args.steps
     attn_ms = sum(a.elapsed_time(b) for a, b in ev["attn"]) / len(ev["attn"])
     quant_ms = sum(a.elapsed_time(b) for a, b in ev["quant"]) / len(ev["quant"])
@@ -281,11 +388,16 @@ def main() -> int:
         torch.cuda.synchronize()
         sdpa_ms = a.elapsed_time(b) / 5
 
-    traffic = None
+    # HBM bytes per launch come from two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of this file with
+    # --profile, committed as a summary: reported with the commit and kernel they were measured on
+    traffic, traffic_src = None, None
     tpath = os.path.join(ROOT, "profiles", f"attn_{args.config}_traffic.txt")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            tj = json.load(f)
+        if tj.get("kernel") == kernel_ran:
+            traffic = tj.get("hbm_bytes_per_launch")
+            traffic_src = f"profiles/{tj.get('source', os.path.basename(tpath))} (measured at {tj.get('commit', '?')})"
 
     line = {
         "metric": "quant-attn TOPS & % MFMA peak; ms/call at Wan2.1 480p shape",
@@ -304,14 +416,23 @@ def main() -> int:
                    "causal": False, "calls": args.steps, "parallelism": "single GPU"},
         "pct_mfma_peak": round(100 * value / peak, 2),
         "roofline": {"bound": "mfma", "achieved": round(attn_tops, 2), "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(attn_tops / peak, 4), "traffic": traffic,
-                     "kernel": _attn_kernel_name(cfg), "kernel_ms": round(attn_ms, 4),
+                     "frac": round(attn_tops / peak, 4), "traffic": traffic, "traffic_source": traffic_src,
+                     "kernel": kernel_ran, "kernel_ms": round(attn_ms, 4),
                      "algorithmic_ops_per_launch": ops},
         "quantizer": {"kernel": "quant_per_block_kernel (Q+K)", "ms": round(quant_ms, 4),
                       "GB/s": round(quant_bytes / (quant_ms * 1e-3) / 1e9, 1), "peak_GB/s": 8000},
         "sdpa_bf16_ms": None if sdpa_ms is None else round(sdpa_ms, 4),
         "speedup_vs_sdpa": None if sdpa_ms is None else round(sdpa_ms / ms_per_step, 3),
     }
+    if not args.no_configs:
+        del inputs
+        torch.cuda.empty_cache()
+        print("[bench] TeleFuser call path (per-thread scales)", file=sys.stderr, flush=True)
+        line["telefuser_call_path"] = _telefuser_call_path()
+        line["configs"] = {}
+        for name, calls in (("c3", 3), ("c4", 10), ("c5", 10)):
+            print(f"[bench] config {name}", file=sys.stderr, flush=True)
+            line["configs"][name] = _config_bench(name, calls=calls)
     if not args.no_stream:
         print("[bench] streaming KV-cache comparison", file=sys.stderr, flush=True)
         line["streaming_kv_cache"] = _stream_bench()

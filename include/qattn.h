@@ -221,6 +221,30 @@ int qattn_fwd_ex_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int v
  */
 int qattn_fwd_ex_blocks_per_workgroup(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int v_kind, int qk_quant_gran,
                                       int causal);
+/*
+ * Which kernel a qattn_fwd_ex launch runs (no counterpart in the reference, whose launch is one CTA
+ * kernel per query block; for benchmarks and tests):
+ *   QATTN_KERNEL_ONE_BLOCK:   one query block (128 rows, 4 waves) per workgroup; KV-split, half-P.V and
+ *                             block-sparse launches always run it
+ *   QATTN_KERNEL_MULTI_BLOCK: several query blocks of a head per workgroup through one K/V pipeline
+ *                             (short, non-causal FP8 key ranges; see qattn_fwd_ex_blocks_per_workgroup)
+ *   QATTN_KERNEL_PINGPONG:    two query blocks per workgroup (8 waves) whose wave groups alternate
+ *                             matrix and vector stages; dense unsplit FP8 launches whose grid fills the chip
+ * All three give identical results for a launch they can run.  qattn_fwd_ex_kernel returns the kernel the
+ * automatic rule picks for these sizes; qattn_set_kernel(k) forces k for the calling thread's later
+ * FP8, dense, unsplit launches (QATTN_KERNEL_AUTO restores the rule; MULTI_BLOCK only where it applies)
+ * and returns the previous setting; qattn_last_kernel() is the kernel of the calling thread's last launch.
+ */
+enum qattn_kernel {
+  QATTN_KERNEL_AUTO = 0,
+  QATTN_KERNEL_ONE_BLOCK = 1,
+  QATTN_KERNEL_MULTI_BLOCK = 2,
+  QATTN_KERNEL_PINGPONG = 3
+};
+int qattn_fwd_ex_kernel(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int v_kind, int qk_quant_gran, int causal,
+                        int num_splits);
+int qattn_set_kernel(int kernel);
+int qattn_last_kernel(void);
 int qattn_fwd_ex(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const void* v, int v_kind,
                  int64_t Lpad, const float* v_scale, qattn_seq o, int out_dtype, int64_t B, int64_t Lq, int64_t Lk,
                  int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int qk_quant_gran, int causal, int64_t q_offset,

@@ -58,6 +58,8 @@ def lib():
         L.oq_f32_to_s8_half_away.argtypes = [f32]
         L.oq_f32_to_s8_half_away.restype = ctypes.c_int8
         L.oq_num_threads.restype = i32
+        L.oq_parallel_threads.restype = i32
+        L.oq_set_threads.argtypes = [i32]
         L.oq_cvt_array.argtypes = [vp, i64, i32, vp]
         _lib = L
     return _lib
@@ -248,3 +250,12 @@ def cvt_array(x: np.ndarray, kind: str) -> np.ndarray:
 
 def num_threads() -> int:
     return lib().oq_num_threads()
+
+
+def parallel_threads() -> int:
+    """Threads that run an OpenMP parallel region of the oracle right now."""
+    return lib().oq_parallel_threads()
+
+
+def set_threads(n: int) -> None:
+    lib().oq_set_threads(int(n))

@@ -585,6 +585,28 @@ int oq_num_threads(void) {
 #endif
 }
 
+/* Threads that actually run an OpenMP parallel region (for the CPU-baseline report), and a setter for the
+ * thread count of later regions (n <= 0 leaves it unchanged). */
+int oq_parallel_threads(void) {
+  int n = 1;
+#ifdef _OPENMP
+#pragma omp parallel
+  {
+#pragma omp single
+    n = omp_get_num_threads();
+  }
+#endif
+  return n;
+}
+
+void oq_set_threads(int n) {
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+#else
+  (void)n;
+#endif
+}
+
 /* Element-wise conversions over an array (kind 0: e4m3 bytes, 1: bf16 bits, 2: s8 RNE-sat,
  * 3: s8 half-away (Triton), 4: fp16 bits).  Lets tests sweep millions of values in one call. */
 void oq_cvt_array(const float* x, int64_t n, int kind, void* out) {

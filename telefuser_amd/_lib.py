@@ -21,6 +21,9 @@ QATTN_QUANT_CUDA = 0
 QATTN_QUANT_TRITON = 1
 QATTN_GRAN_BLOCK, QATTN_GRAN_WARP, QATTN_GRAN_THREAD = 1, 2, 3
 QATTN_V_FP8, QATTN_V_BF16, QATTN_V_FP16 = 0, 1, 2
+QATTN_KERNEL_AUTO, QATTN_KERNEL_ONE_BLOCK, QATTN_KERNEL_MULTI_BLOCK, QATTN_KERNEL_PINGPONG = 0, 1, 2, 3
+KERNEL_NAMES = {QATTN_KERNEL_ONE_BLOCK: "qattn_fwd_kernel", QATTN_KERNEL_MULTI_BLOCK: "qattn_fwd_kernel (multi-block)",
+                QATTN_KERNEL_PINGPONG: "qattn_fwd_pp_kernel"}
 
 EXPORTED = (
     "qattn_last_error",
@@ -34,6 +37,9 @@ EXPORTED = (
     "qattn_fwd_workspace_size",
     "qattn_fwd_num_splits",
     "qattn_fwd_ex_blocks_per_workgroup",
+    "qattn_fwd_ex_kernel",
+    "qattn_set_kernel",
+    "qattn_last_kernel",
     "qattn_fwd",
     "qattn_v_tile_half",
     "qattn_fwd_pv16",
@@ -96,6 +102,12 @@ def load() -> ctypes.CDLL:
     L.qattn_fwd_ex_num_splits.restype = i32
     L.qattn_fwd_ex_blocks_per_workgroup.argtypes = [i64, i64, i64, i64, i32, i32, i32]
     L.qattn_fwd_ex_blocks_per_workgroup.restype = i32
+    L.qattn_fwd_ex_kernel.argtypes = [i64, i64, i64, i64, i32, i32, i32, i32]
+    L.qattn_fwd_ex_kernel.restype = i32
+    L.qattn_set_kernel.argtypes = [i32]
+    L.qattn_set_kernel.restype = i32
+    L.qattn_last_kernel.argtypes = []
+    L.qattn_last_kernel.restype = i32
     L.qattn_fwd_ex.argtypes = [S, vp, S, vp, vp, i32, i64, vp, S, i32, i64, i64, i64, i64, i64, i64, f32, i32, i32,
                                i64, vp, vp, i32, vp, sz, vp]
     L.qattn_fwd_block_sparse_num_splits.argtypes = [i64, i64, i64, i64]

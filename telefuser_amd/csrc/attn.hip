@@ -100,13 +100,6 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t n) {
   return xcd * q + (xcd < r ? xcd : r) + idx;
 }
 
-// Row-major, XOR-swizzled LDS layouts of the wide kernel (bytes; the other kernels keep their tiles
-// fragment-major, see their DMA set-up):
-//   K tile: 64 rows x 128 B, 16-byte chunk c of row r at r*128 + ((c ^ ((r >> 1) & 7)) * 16)
-//   V tile: 128 rows (d) x 64 B, chunk c (0..3) of row d at d*64 + ((c ^ ((d >> 2) & 3)) * 16)
-__device__ __forceinline__ int k_lds_off(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
-__device__ __forceinline__ int v_lds_off(int d, int c) { return d * 64 + ((c ^ ((d >> 2) & 3)) << 4); }
-
 // Buffer resource (V#) for raw, unswizzled byte addressing of [base, base + bytes): loads whose offset
 // is at or past `bytes` return zeros instead of touching memory.
 __device__ __forceinline__ v4u make_rsrc(const void* base, uint32_t bytes) {
@@ -686,576 +679,6 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   finish();
 }
 
-// ---- wide workgroups: 64 query rows per wave, one wave per SIMD ----
-//
-// qattn_fwd_kernel gives each wave 32 query rows, so every wave reads the whole 16 KiB K/V tile from
-// LDS per 1 M MFMA ops, and the dependent chain Q.K^T -> softmax -> P.V of one tile leaves the matrix
-// pipe idle during the softmax unless the other wave of the SIMD happens to be in another phase.
-// This kernel gives each wave 64 rows as two 32-row halves A and B (256 rows per workgroup, one
-// workgroup per CU, up to 512 registers per wave) and software-pipelines the halves against each other:
-//
-//   phase 1 of tile i:  VALU softmax_A(i)   ||  MFMA  Q_B.K(i)^T,  P_B(i-1).V(i-1),  rowsum P_B(i-1)
-//   phase 2 of tile i:  VALU softmax_B(i)   ||  MFMA  rowsum P_A(i),  Q_A.K(i+1)^T,  P_A(i).V(i)
-//
-// so each phase pairs ~600 cycles of softmax VALU work with 576 cycles of independent MFMA work,
-// interleaved slot by slot (scheduling fences between slots).  K(i+1) and V(i) are read from LDS into
-// registers once, in the last slots of phase 1 (after the MFMAs that used K(i) and V(i-1)), and feed
-// both halves (Q_A.K(i+1)^T and P_A(i).V(i) in phase 2, then Q_B.K(i+1)^T and P_B(i).V(i) in the next
-// phase 1), which halves the LDS reads per MFMA op and leaves phase 2 with its operands in registers.
-// Per element the arithmetic is the one
-// of qattn_fwd_kernel (same lazy running max, FP8 offset, P rounding, row sums on the matrix pipe and
-// accumulation order), so both kernels give identical results.
-//
-// K/V tiles come in by LDS DMA, three buffers each, two iterations ahead: the barrier that starts
-// iteration i makes K(i+1) and V(i) visible and frees the buffers of K(i) and V(i-1), which then
-// receive K(i+3) and V(i+2).
-// Only key tiles with no masked key for any row of the workgroup run pipelined; the rest (a tail tile,
-// a causal diagonal, short key ranges) go through a plain per-tile loop.
-constexpr int kWideRows = 256;         // query rows per workgroup
-constexpr int kWideKsFloats = 16384;   // k_scales staged per workgroup (64 KiB)
-
-// o *= a for a 16-register tuple held in AGPRs, in place (read, multiply, write back one register at a
-// time), so the tuple never needs a VGPR copy
-__device__ __forceinline__ void agpr_scale16(v16f& o, float a) {
-  float t;
-#define QATTN_AS(i) "v_accvgpr_read_b32 %[t], %[o" #i "]\n\tv_mul_f32 %[t], %[t], %[a]\n\tv_accvgpr_write_b32 %[o" #i "], %[t]\n\t"
-  asm volatile(QATTN_AS(0) QATTN_AS(1) QATTN_AS(2) QATTN_AS(3) QATTN_AS(4) QATTN_AS(5) QATTN_AS(6) QATTN_AS(7)
-                   QATTN_AS(8) QATTN_AS(9) QATTN_AS(10) QATTN_AS(11) QATTN_AS(12) QATTN_AS(13) QATTN_AS(14) QATTN_AS(15)
-               : [t] "=&v"(t), [o0] "+a"(o[0]), [o1] "+a"(o[1]), [o2] "+a"(o[2]), [o3] "+a"(o[3]), [o4] "+a"(o[4]),
-                 [o5] "+a"(o[5]), [o6] "+a"(o[6]), [o7] "+a"(o[7]), [o8] "+a"(o[8]), [o9] "+a"(o[9]),
-                 [o10] "+a"(o[10]), [o11] "+a"(o[11]), [o12] "+a"(o[12]), [o13] "+a"(o[13]), [o14] "+a"(o[14]),
-                 [o15] "+a"(o[15])
-               : [a] "v"(a));
-#undef QATTN_AS
-}
-
-template <bool KT>
-struct WideHalf {
-  v16f o[4];
-  v16f lacc;
-  v16i s[2];
-  v8i pf;
-  v4i qf[4];
-  float qs;      // q_scale x qk_mult of this lane's row
-  float m;       // running max (log2 domain, offset included)
-  float alpha;   // pending O rescale
-  bool grew;     // some lane of the wave moved m with the last softmax
-};
-
-// (the body is a device function so that its lambdas are never instantiated by the host pass)
-template <bool IS_FP16_OUT, bool KT>
-__device__ __forceinline__ void qattn_fwd_wide(const AttnParams& p) {
-  constexpr int KS = ks_per_tile(KT);
-  __shared__ __align__(16) uint8_t lds_kv[2 * kNBuf * kBK * kD];  // K buffers 0..2, then V buffers 0..2
-  __shared__ float lds_ks[kWideKsFloats];
-  __shared__ __align__(16) float lds_vs[kD];
-  uint8_t* const lds_k = lds_kv;
-  uint8_t* const lds_v = lds_kv + kNBuf * kBK * kD;
-
-  const int64_t nQW = (p.Lq + kWideRows - 1) / kWideRows;
-  const int64_t tile_id = xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t qw = tile_id % nQW;
-  const int64_t rest = tile_id / nQW;
-  const int64_t h = rest % p.Hq;
-  const int64_t b = rest / p.Hq;
-  const int64_t hk = h / p.group;
-  const int tid = threadIdx.x;
-  const int w = tid >> 6, lane = tid & 63, lq = lane & 31, hf = lane >> 5;
-  const int wu = __builtin_amdgcn_readfirstlane(w);
-
-  const int64_t q_first = qw * kWideRows;
-  int64_t kv_end = p.Lk;
-  if (p.kv_valid) kv_end = min(kv_end, (int64_t)p.kv_valid[b]);
-  if (p.causal) kv_end = min(kv_end, q_first + kWideRows + p.q_offset);
-  const int64_t n_tiles = kv_end > 0 ? (kv_end + kBK - 1) / kBK : 0;
-  const int64_t R0 = q_first + w * 64;  // first row of half A; half B starts at R0 + 32
-
-  WideHalf<KT> A, B;
-  // Q fragments of both halves through a wave-private 8 KiB stage (row-contiguous 128-byte loads; the
-  // 16-byte chunk c of stage row r sits at chunk c ^ (r & 7))
-  {
-    uint8_t* stage = lds_kv + w * 8192;
-    const int8_t* qbase = p.q8 + b * p.qsb + h * p.qsh;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const int r = i * 8 + (lane >> 3), c = lane & 7;
-      const int64_t row = R0 + r;
-      const v4i val = row < p.Lq ? *reinterpret_cast<const v4i*>(qbase + row * p.qsl + c * 16) : v4i{0, 0, 0, 0};
-      *reinterpret_cast<v4i*>(stage + r * 128 + ((c ^ (r & 7)) << 4)) = val;
-    }
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
-    // straight into AGPRs: the Q fragments are only ever read by the QK MFMAs
-#pragma unroll
-    for (int m = 0; m < 4; m++) {
-      const int c = 2 * m + hf;
-      const uint32_t a0 = lds_addr(stage) + (uint32_t)(lq * 128 + ((c ^ (lq & 7)) << 4));
-      asm volatile("ds_read_b128 %0, %1" : "=a"(A.qf[m]) : "v"(a0) : "memory");
-      asm volatile("ds_read_b128 %0, %1 offset:4096" : "=a"(B.qf[m]) : "v"(a0) : "memory");
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+a"(A.qf[0]), "+a"(A.qf[1]), "+a"(A.qf[2]), "+a"(A.qf[3]), "+a"(B.qf[0]),
-                 "+a"(B.qf[1]), "+a"(B.qf[2]), "+a"(B.qf[3])::"memory");
-  }
-  // q_scale of this lane's row in each half: per 128-row block, per 32-row warp block or per row class
-  auto qscale = [&](int64_t R) -> float {
-    const int64_t Rc = min(R, p.Lq - 1);  // rows past Lq compute on zeros and are never stored
-    const int64_t qsi = p.qgran == QATTN_GRAN_THREAD ? (Rc / 32) * 8 + (lq & 7)
-                        : p.qgran == QATTN_GRAN_WARP ? Rc / 32
-                                                     : Rc / kBQ;
-    return p.q_scale[(b * p.Hq + h) * p.nQS + qsi] * p.qk_mult;
-  };
-  A.qs = qscale(R0);
-  B.qs = qscale(R0 + 32);
-  auto init_half = [&](WideHalf<KT>& X) {
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) X.o[i][r] = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; r++) X.lacc[r] = 0.f;
-    X.m = kMInit;
-    X.alpha = 1.f;
-    X.grew = false;
-  };
-  init_half(A);
-  init_half(B);
-  v16i kbias;
-#pragma unroll
-  for (int r = 0; r < 16; r++) kbias[r] = kAccBiasBits;
-  asm volatile("" : "+v"(kbias));  // keep the bias in VGPRs (MFMA srcC), not rematerialised per use
-
-  __syncthreads();  // Q stage reads done before the DMA reuses the region
-  const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
-  for (int64_t i = tid; i < n_tiles * KS; i += kThreads) lds_ks[i] = ks_ptr[i];
-  if (tid < kD) lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * kD + tid];
-
-  // DMA: per-lane offsets relative to the tile start, as in qattn_fwd_kernel
-  const int8_t* kbase = p.k8 + b * p.ksb + hk * p.ksh;
-  const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad;
-  const int64_t kbytes = (p.Lk - 1) * p.ksl + kD;
-  const v4u vrsrc = make_rsrc(vbase, (uint32_t)((int64_t)kD * p.Lpad));
-  uint32_t koff[2], voff[2];
-#pragma unroll
-  for (int i = 0; i < 2; i++) {
-    const int slot = (i * 4 + w) * 64 + lane;
-    const int kr = slot >> 3;
-    const int kc = (slot & 7) ^ ((kr >> 1) & 7);
-    koff[i] = (uint32_t)(kr * p.ksl + kc * 16);
-    const int vd = slot >> 2;
-    const int vc = (slot & 3) ^ ((vd >> 2) & 3);
-    voff[i] = (uint32_t)(vd * p.Lpad + vc * 16);
-  }
-  const int64_t k_step = kBK * p.ksl;
-  const uint32_t lds_k0 = lds_addr(lds_k) + wu * 1024;
-  const uint32_t lds_v0 = lds_addr(lds_v) + wu * 1024;
-  auto dma_k = [&](int64_t t, int kb) {
-    const int64_t kso = t * k_step;
-    const v4u krsrc = make_rsrc(kbase + kso, (uint32_t)(kbytes - kso));
-#pragma unroll
-    for (int j = 0; j < 2; j++) lds_dma16(koff[j], krsrc, 0, lds_k0 + kb * (kBK * kD) + j * 4096);
-  };
-  auto dma_v = [&](int64_t t, int vb) {
-#pragma unroll
-    for (int j = 0; j < 2; j++) lds_dma16(voff[j], vrsrc, (uint32_t)t * kBK, lds_v0 + vb * (kD * kBK) + j * 4096);
-  };
-  auto read_k = [&](int kb, int j) -> v4i {
-    return *reinterpret_cast<const v4i*>(lds_k + kb * (kBK * kD) + k_lds_off((j & 1) * 32 + lq, 2 * (j >> 1) + hf));
-  };
-  auto read_v = [&](int vb, int dblk) -> v8i {
-    const int d = dblk * 32 + lq;
-    const v4i a0 = *reinterpret_cast<const v4i*>(lds_v + vb * (kD * kBK) + v_lds_off(d, 2 * hf));
-    const v4i a1 = *reinterpret_cast<const v4i*>(lds_v + vb * (kD * kBK) + v_lds_off(d, 2 * hf + 1));
-    return v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-  };
-  // The QK MFMAs go through inline asm so that the logits land in VGPRs (the softmax reads them there);
-  // the P.V and row-sum MFMAs are builtins, whose accumulators (O, l) the compiler keeps in AGPRs.  The
-  // compiler sees no MFMA in the asm, so it inserts no wait states after it: every VALU read of a logit
-  // is either a phase or more behind its MFMA or preceded by drain_s().
-  auto qk_mfma = [&](WideHalf<KT>& X, const v4i (&kf)[8], int j) {
-    if (j < 2)
-      asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %3" : "=&v"(X.s[j & 1]) : "v"(kf[j]), "a"(X.qf[j >> 1]), "v"(kbias));
-    else
-      asm volatile("v_mfma_i32_32x32x32_i8 %0, %1, %2, %0" : "+v"(X.s[j & 1]) : "v"(kf[j]), "a"(X.qf[j >> 1]));
-  };
-  auto pv_mfma = [&](WideHalf<KT>& X, const v8i (&vf)[4], int d) {
-    X.o[d] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[d], X.pf, X.o[d], 0, 0, 0, 0, 0, 0);
-  };
-  auto rsum_mfma = [&](WideHalf<KT>& X) { X.lacc = row_sum_mfma(X.lacc, X.pf); };
-  // 24 wait states after the last MFMA: covers a 16-pass MFMA result read by the VALU or by
-  // v_accvgpr_read.  The results are threaded through the asm so no read is scheduled above it.
-  auto drain_s = [](WideHalf<KT>& X) {
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" : "+v"(X.s[0]), "+v"(X.s[1]));
-  };
-  auto drain_o = [](WideHalf<KT>& X) {
-    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
-                 : "+a"(X.o[0]), "+a"(X.o[1]), "+a"(X.o[2]), "+a"(X.o[3]), "+a"(X.lacc));
-  };
-  // LDS reads of K/V fragments complete before an MFMA reads them: the compiler's wait-count pass does not
-  // see the register uses of the inline-asm MFMAs, so the wait is explicit and threads the fragments
-  auto lds_wait_k = [](v4i (&kf)[8]) {
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3]), "+v"(kf[4]), "+v"(kf[5]), "+v"(kf[6]), "+v"(kf[7])
-                 :: "memory");
-  };
-  auto lds_wait_v = [](v8i (&vf)[4]) {
-    asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(vf[0]), "+v"(vf[1]), "+v"(vf[2]), "+v"(vf[3])::"memory");
-  };
-  auto rescale = [&](WideHalf<KT>& X) {
-    drain_o(X);
-#pragma unroll
-    for (int d = 0; d < 4; d++) agpr_scale16(X.o[d], X.alpha);
-    agpr_scale16(X.lacc, X.alpha);
-    // AGPR writes before the next MFMA reads them as srcC
-    asm volatile("s_nop 3" : "+a"(X.o[0]), "+a"(X.o[1]), "+a"(X.o[2]), "+a"(X.o[3]), "+a"(X.lacc));
-  };
-  auto scales = [&](const WideHalf<KT>& X, int64_t t, float& cs_a, float& cs_b) {
-    if constexpr (KT) {
-      cs_a = X.qs * lds_ks[t * 4 + 2 * hf];
-      cs_b = X.qs * lds_ks[t * 4 + 2 * hf + 1];
-    } else {
-      cs_a = cs_b = X.qs * lds_ks[t];
-    }
-  };
-  // Softmax of one unmasked tile as a VALU stream of 19 items.  Items 0 and 1: the row max as four
-  // independent chains (over s[0], then s[1]; for per-thread K scales chains 0-1 hold class a and 2-3
-  // class b), then (item 1) the exchange with the lane holding the other key half, the lazy running-max
-  // update and alpha, and the first fma.  Items 2..17 run three stages of the 16 two-logit groups g at
-  // once - fma of g + 1, exp2 of g, e4m3 packing of g - 1 - so that no item waits on its own results;
-  // item 18 packs the last group.  Group g is logits r0 = 2g mod 16, r0 + 1 of block g / 8, which share one
-  // scale class, and lands in byte pair (g & 1) of pf[g / 2].
-  struct Sm {
-    int c[4];
-    float cs_a, cs_b, nc_a, nc_b;
-    float x[2][2], e[2][2];
-  };
-  auto sm_item = [&](WideHalf<KT>& X, Sm& st, int k) {
-    // chain q covers elements {0,1,4,5} + 8 (q & 1) + 2 (q >> 1) of each 16-logit block
-    auto el = [](int q, int i) { return ((i >> 1) * 4) + (i & 1) + 8 * (q & 1) + 2 * (q >> 1); };
-    if (k == 0) {
-#pragma unroll
-      for (int q = 0; q < 4; q++) st.c[q] = max(max(X.s[0][el(q, 0)], X.s[0][el(q, 1)]), max(X.s[0][el(q, 2)], X.s[0][el(q, 3)]));
-      return;
-    }
-    if (k == 1) {
-#pragma unroll
-      for (int q = 0; q < 4; q++)
-        st.c[q] = max(max(st.c[q], X.s[1][el(q, 0)]), max(max(X.s[1][el(q, 1)], X.s[1][el(q, 2)]), X.s[1][el(q, 3)]));
-      float m_tile;
-      if constexpr (!KT) {
-        int mx = max(max(st.c[0], st.c[1]), max(st.c[2], st.c[3]));
-        const auto sw = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);
-        mx = max((int)sw[0], (int)sw[1]);
-        m_tile = fmaf(__int_as_float(mx), st.cs_a, -fmaf(kAccBias, st.cs_a, kFp8Offset - kLazyTau));
-      } else {
-        const int ma = max(st.c[0], st.c[1]), mb = max(st.c[2], st.c[3]);
-        const float fa = fmaf(__int_as_float(ma), st.cs_a, -fmaf(kAccBias, st.cs_a, kFp8Offset - kLazyTau));
-        const float fb = fmaf(__int_as_float(mb), st.cs_b, -fmaf(kAccBias, st.cs_b, kFp8Offset - kLazyTau));
-        const float mt = fmaxf(fa, fb);
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
-        m_tile = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-      }
-      const bool grow = m_tile > X.m + kLazyTau;
-      X.grew = __any(grow);
-      const float m_new = grow ? m_tile : X.m;
-      X.alpha = __builtin_amdgcn_exp2f(X.m - m_new);
-      X.m = m_new;
-      st.nc_a = -fmaf(kAccBias, st.cs_a, X.m);
-      st.nc_b = -fmaf(kAccBias, st.cs_b, X.m);
-    }
-    auto F = [&](int g) {
-      const int kb = g >> 3, r0 = (2 * g) & 15;
-      const bool ca = (r0 & 3) < 2;
-#pragma unroll
-      for (int e = 0; e < 2; e++)
-        st.x[g & 1][e] = fmaf(__int_as_float(X.s[kb][r0 + e]), ca ? st.cs_a : st.cs_b, ca ? st.nc_a : st.nc_b);
-    };
-    auto E = [&](int g) {
-#pragma unroll
-      for (int e = 0; e < 2; e++) st.e[g & 1][e] = __builtin_amdgcn_exp2f(st.x[g & 1][e]);
-    };
-    auto C = [&](int g) {
-      if (g & 1) X.pf[g >> 1] = __builtin_amdgcn_cvt_pk_fp8_f32(st.e[1][0], st.e[1][1], X.pf[g >> 1], true);
-      else X.pf[g >> 1] = __builtin_amdgcn_cvt_pk_fp8_f32(st.e[0][0], st.e[0][1], X.pf[g >> 1], false);
-    };
-    if (k == 1) {
-      F(0);
-    } else if (k <= 17) {
-      const int g = k - 2;
-      if (g >= 1) C(g - 1);
-      E(g);
-      if (g + 1 <= 15) F(g + 1);
-    } else {
-      C(15);
-    }
-  };
-  auto sm_init = [&](float cs_a, float cs_b) {
-    Sm st;
-    st.cs_a = cs_a;
-    st.cs_b = cs_b;
-    st.nc_a = st.nc_b = 0.f;
-    return st;
-  };
-
-  // ---------------- pipelined tiles ----------------
-  int64_t full = kv_end / kBK;
-  if (p.causal) full = min(full, (q_first + p.q_offset + 1) / kBK);
-  full = min(full, n_tiles);
-  const int n = full >= 2 ? (int)full : 0;
-  int64_t t_simple = n;  // first tile of the plain loop
-
-  if (n >= 2) {
-    dma_k(0, 0);
-    dma_k(1, 1);
-    dma_v(0, 0);
-    if (n > 2) dma_k(2, 2);
-    dma_v(1, 1);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    v4i kf[8];  // K(i) in phase 1 (Q_B.K(i)^T), K(i+1) from phase 2 on (Q_A.K(i+1)^T, then Q_B next tile)
-    v8i vf[4];  // V(i-1) in phase 1 (P_B(i-1).V), V(i) from phase 2 on
-#pragma unroll
-    for (int j = 0; j < 8; j++) kf[j] = read_k(0, j);
-    lds_wait_k(kf);
-#pragma unroll
-    for (int j = 0; j < 8; j++) qk_mfma(A, kf, j);
-    drain_s(A);
-    int issued = 0;  // DMA instructions issued at the previous iteration's barrier
-    float cs[4];     // logit scales (class a, b) of halves A and B for the tile being computed
-    scales(A, 0, cs[0], cs[1]);
-    scales(B, 0, cs[2], cs[3]);
-    // MFMA per VALU item (-1: none), issued at the start of the item.  Ids: 0..7 Q.K^T fragment j,
-    // 8..11 P.V block d, 12 row sum.  Greedy placement: an MFMA goes into the first item that starts
-    // after the previous MFMA has left the matrix pipe (QK 32 cycles, PV and row sum 64; items are
-    // ~33 cycles of VALU work, the two max items ~40 and ~95), so the wave never stalls on a busy
-    // pipe and the matrix work (576 cycles) hides under the softmax stream (~670 cycles).
-    constexpr int kMf1[19] = {0, 1, 2, 3, 8, -1, 4, 9, -1, 5, 10, -1, 6, 7, 11, -1, 12, -1, -1};
-    constexpr int kMf2[19] = {12, 0, 1, 2, 3, 8, -1, 4, 9, -1, 5, 10, -1, 6, 7, 11, -1, -1, -1};
-    auto iter = [&](int i, auto first, auto last) {
-      constexpr bool kFirst = decltype(first)::value, kLast = decltype(last)::value;
-      // ---- start: K(i+1) and V(i) have landed (only the previous iteration's DMAs may still be in
-      // flight); after the barrier the buffers of K(i) and V(i-1) take K(i+3) and V(i+2) ----
-      if (issued == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-      else if (issued == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-      __syncthreads();
-      issued = 0;
-      if (i + 3 < n) {
-        dma_k(i + 3, i % kNBuf);
-        issued += 2;
-      }
-      if (i + 2 < n) {
-        dma_v(i + 2, (i + 2) % kNBuf);
-        issued += 2;
-      }
-      // this tile's logit scales were read during the previous iteration (scales of tile 0: prologue)
-      const float csA_a = cs[0], csA_b = cs[1], csB_a = cs[2], csB_b = cs[3];
-      if (!kFirst && B.grew) rescale(B);
-      // ---- phase 1: softmax_A(i) || Q_B.K(i)^T, P_B(i-1).V(i-1), rowsum P_B(i-1).  The fragments of
-      // K(i+1) and V(i) replace those of K(i) and V(i-1) two items after their last MFMA ----
-      {
-        Sm st = sm_init(csA_a, csA_b);
-        const int kb = (i + 1) % kNBuf, vb = i % kNBuf;
-#pragma unroll
-        for (int k = 0; k < 19; k++) {
-          __builtin_amdgcn_sched_barrier(0);
-          const int id = kMf1[k];
-          if (id >= 0 && id < 8) qk_mfma(B, kf, id);
-          else if (id >= 8 && id < 12 && !kFirst) pv_mfma(B, vf, id - 8);
-          else if (id == 12 && !kFirst) rsum_mfma(B);
-          if (!kLast && (k == 5 || k == 15)) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) kf[(k == 15) * 4 + j] = read_k(kb, (k == 15) * 4 + j);
-          }
-          if (k == 6 || k == 9 || k == 12 || k == 16) {
-            const int d = k == 6 ? 0 : k == 9 ? 1 : k == 12 ? 2 : 3;
-            vf[d] = read_v(vb, d);
-          }
-          sm_item(A, st, k);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      asm volatile("" ::"v"(A.pf), "v"(A.m), "v"(B.s[0]), "v"(B.s[1]));
-      if (A.grew) rescale(A);
-      // ---- phase 2: softmax_B(i) || rowsum P_A(i), Q_A.K(i+1)^T, P_A(i).V(i) ----
-      {
-        Sm st = sm_init(csB_a, csB_b);
-#pragma unroll
-        for (int k = 0; k < 19; k++) {
-          __builtin_amdgcn_sched_barrier(0);
-          // LDS reads complete before the inline-asm MFMAs use them: K fragments 0..3 were read before
-          // the 12 other reads of phase 1 (V 0..2, K 4..7, V 3), K 4..7 before V 3 (two reads)
-          if (!kLast && k == 1)
-            asm volatile("s_waitcnt lgkmcnt(12)" : "+v"(kf[0]), "+v"(kf[1]), "+v"(kf[2]), "+v"(kf[3])::"memory");
-          if (!kLast && k == 7)
-            asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(kf[4]), "+v"(kf[5]), "+v"(kf[6]), "+v"(kf[7])::"memory");
-          if (!kLast && k == 17) {  // the next tile's scales (their LDS latency is hidden by the last items)
-            scales(A, i + 1, cs[0], cs[1]);
-            scales(B, i + 1, cs[2], cs[3]);
-          }
-          const int id = kMf2[k];
-          if (id >= 0 && id < 8) {
-            if (!kLast) qk_mfma(A, kf, id);
-          } else if (id >= 8 && id < 12) {
-            pv_mfma(A, vf, id - 8);
-          } else if (id == 12) {
-            rsum_mfma(A);
-          }
-          sm_item(B, st, k);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      asm volatile("" ::"v"(B.pf), "v"(B.m), "v"(A.s[0]), "v"(A.s[1]));
-    };
-    iter(0, std::true_type{}, std::false_type{});
-    for (int i = 1; i < n - 1; i++) iter(i, std::false_type{}, std::false_type{});
-    iter(n - 1, std::false_type{}, std::true_type{});
-    if (B.grew) rescale(B);
-#pragma unroll
-    for (int d = 0; d < 4; d++) pv_mfma(B, vf, d);
-    rsum_mfma(B);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();  // the plain loop below refills the buffers
-  }
-
-  // ---------------- plain loop: masked / remaining tiles, one tile at a time ----------------
-  for (int64_t t = t_simple; t < n_tiles; t++) {
-    dma_k(t, 0);
-    dma_v(t, 0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    v4i kf[8];
-    v8i vf[4];
-#pragma unroll
-    for (int j = 0; j < 8; j++) kf[j] = read_k(0, j);
-#pragma unroll
-    for (int d = 0; d < 4; d++) vf[d] = read_v(0, d);
-    lds_wait_k(kf);
-    lds_wait_v(vf);
-    const int64_t k0 = t * kBK;
-    auto tile_half = [&](WideHalf<KT>& X, int half) {
-      const int64_t wrow0 = R0 + 32 * half;
-      const int64_t qrow = wrow0 + lq;
-#pragma unroll
-      for (int j = 0; j < 8; j++) qk_mfma(X, kf, j);
-      drain_s(X);
-      const bool masked = (k0 + kBK > kv_end) || (p.causal && k0 + kBK - 1 > wrow0 + p.q_offset);
-      if (masked) {
-        int lim = (int)min(kv_end - k0, (int64_t)kBK);
-        if (p.causal) lim = min(lim, (int)max(min(qrow + p.q_offset + 1 - k0, (int64_t)kBK), (int64_t)-1));
-        lim -= hf * 4;
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-          for (int r = 0; r < 16; r++)
-            if (kb * 32 + (r >> 2) * 8 + (r & 3) >= lim) X.s[kb][r] = INT32_MIN;
-      }
-      float cs_a, cs_b;
-      scales(X, t, cs_a, cs_b);
-      float m_tile;
-      if constexpr (!KT) {
-        int mx = INT32_MIN;
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) mx = max(mx, X.s[kb][r]);
-        const auto sw = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);
-        mx = max((int)sw[0], (int)sw[1]);
-        m_tile = mx == INT32_MIN ? kMInit : fmaf(__int_as_float(mx), cs_a, -fmaf(kAccBias, cs_a, kFp8Offset - kLazyTau));
-      } else {
-        int ma = INT32_MIN, mb = INT32_MIN;
-#pragma unroll
-        for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) {
-            if ((r & 3) < 2) ma = max(ma, X.s[kb][r]);
-            else mb = max(mb, X.s[kb][r]);
-          }
-        const float fa = ma == INT32_MIN ? kMInit : fmaf(__int_as_float(ma), cs_a, -fmaf(kAccBias, cs_a, kFp8Offset - kLazyTau));
-        const float fb = mb == INT32_MIN ? kMInit : fmaf(__int_as_float(mb), cs_b, -fmaf(kAccBias, cs_b, kFp8Offset - kLazyTau));
-        const float mt = fmaxf(fa, fb);
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
-        m_tile = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-      }
-      const bool grow = m_tile > X.m + kLazyTau;
-      if (__any(grow)) {
-        const float m_new = grow ? m_tile : X.m;
-        X.alpha = __builtin_amdgcn_exp2f(X.m - m_new);
-        rescale(X);
-        X.m = m_new;
-      }
-      const float nc_a = -fmaf(kAccBias, cs_a, X.m), nc_b = -fmaf(kAccBias, cs_b, X.m);
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const int kb = j >> 2, r0 = (j & 3) * 4;
-        float pv4[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int sv = X.s[kb][r0 + e];
-          pv4[e] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(sv), e < 2 ? cs_a : cs_b, e < 2 ? nc_a : nc_b));
-          pv4[e] = sv == INT32_MIN ? 0.f : pv4[e];
-        }
-        const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv4[0], pv4[1], X.pf[j], false);
-        X.pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv4[2], pv4[3], packed, true);
-      }
-      asm volatile("s_nop 4" : "+v"(X.pf));  // VALU writes of P before the MFMAs read them
-#pragma unroll
-      for (int d = 0; d < 4; d++) pv_mfma(X, vf, d);
-      rsum_mfma(X);
-    };
-    tile_half(A, 0);
-    tile_half(B, 1);
-    __syncthreads();  // every wave is done with buffer 0 before the next tile's DMA
-  }
-
-  // ---------------- epilogue: O / l * v_scale through the wave's LDS stage ----------------
-  drain_o(A);
-  drain_o(B);
-  __syncthreads();  // v_scale staging visible (no key tile at all: no barrier ran yet)
-  uint8_t* stage = lds_kv + w * 8192;
-  uint16_t* obase = static_cast<uint16_t*>(p.o) + b * p.osb + h * p.osh;
-  auto store_half = [&](WideHalf<KT>& X, int half) {
-    const int64_t wrow0 = R0 + 32 * half;
-    const int64_t qrow = wrow0 + lq;
-    const float l_tot = X.lacc[0];
-    const float inv_l = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-#pragma unroll
-    for (int pass = 0; pass < 2; pass++) {
-#pragma unroll
-      for (int db = 0; db < 2; db++) {
-        const int dblk = pass * 2 + db;
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const int d = dblk * 32 + g * 8 + hf * 4;
-          const v4f sc = *reinterpret_cast<const v4f*>(&lds_vs[d]);
-          float f[4];
-#pragma unroll
-          for (int e = 0; e < 4; e++) f[e] = X.o[dblk][g * 4 + e] * inv_l * sc[e];
-          const v2u packed{pack_half2<IS_FP16_OUT>(f[0], f[1]), pack_half2<IS_FP16_OUT>(f[2], f[3])};
-          const int c = db * 4 + g;
-          *reinterpret_cast<v2u*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4) + hf * 8) = packed;
-        }
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int r = i * 8 + (lane >> 3), c = lane & 7;
-        const v4u val = *reinterpret_cast<const v4u*>(stage + r * 128 + ((c ^ (r & 7)) << 4));
-        const int64_t row = wrow0 + r;
-        if (row < p.Lq) *reinterpret_cast<v4u*>(obase + row * p.osl + pass * 64 + c * 8) = val;
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    }
-    if (p.lse && hf == 0 && qrow < p.Lq)
-      p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + X.m : -INFINITY;
-  };
-  store_half(A, 0);
-  store_half(B, 1);
-}
-
-template <bool IS_FP16_OUT, bool KT>
-__global__ __launch_bounds__(kThreads) void qattn_fwd_wide_kernel(AttnParams p) {
-  qattn_fwd_wide<IS_FP16_OUT, KT>(p);
-}
-
 // ---- ping-pong workgroups: two groups of four waves, one wave of each group per SIMD ----
 //
 // In qattn_fwd_kernel the two waves of a SIMD belong to different workgroups and fall into step with
@@ -1668,28 +1091,39 @@ extern "C" size_t qattn_fwd_workspace_size(int64_t B, int64_t Lq, int64_t Hq, in
   return (size_t)num_splits * B * Hq * Lq * (D + 2) * sizeof(float);
 }
 
-// QATTN_WIDE=1 in the environment (read at every launch) selects the wide kernel (64 query rows per
-// wave, software-pipelined halves) for dense FP8 launches; it is bit-identical to qattn_fwd_kernel and,
-// as measured on MI355X, not faster yet, so it is opt-in
-static bool wide_enabled() {
-  const char* e = getenv("QATTN_WIDE");
-  return e && e[0] == '1';
+// Kernel selection.  Dense FP8 launches without a KV split run the ping-pong kernel when its grid (one
+// workgroup per two query blocks, one workgroup per CU) fills the 256 CUs, the multi-block variant of
+// qattn_fwd_kernel for short key ranges (blocks_per_workgroup > 1), and qattn_fwd_kernel otherwise;
+// split, half-P.V and block-sparse launches always run qattn_fwd_kernel.  A thread-local override
+// (qattn_set_kernel) forces one of the applicable kernels, so tests can compare them on small shapes.
+static thread_local int t_kernel_override = QATTN_KERNEL_AUTO;
+static thread_local int t_last_kernel = QATTN_KERNEL_AUTO;
+
+extern "C" int qattn_set_kernel(int kernel) {
+  const int prev = t_kernel_override;
+  if (kernel >= QATTN_KERNEL_AUTO && kernel <= QATTN_KERNEL_PINGPONG) t_kernel_override = kernel;
+  return prev;
 }
 
-// Dense FP8 launches without a KV split go to the ping-pong kernel when its grid (one workgroup per
-// two query blocks, one workgroup per CU) fills the 256 CUs; QATTN_PP=0 / QATTN_PP=1 in the environment
-// (read at every launch) turns it off / on regardless of the grid size.
-static bool pp_enabled(int64_t grid) {
-  const char* e = getenv("QATTN_PP");
-  if (e && e[0]) return e[0] == '1';
-  return grid >= 256;
+extern "C" int qattn_last_kernel(void) { return t_last_kernel; }
+
+// the kernel a launch runs, given its split count and whether the multi-block layout applies
+static int pick_kernel(int pv, bool sparse, int ns, int causal, int64_t B, int64_t Hq, int64_t nQB, int qpw_auto,
+                       bool mq_ok) {
+  if (pv != PV_FP8 || sparse || ns > 1) return QATTN_KERNEL_ONE_BLOCK;
+  const int ov = t_kernel_override;
+  if (ov == QATTN_KERNEL_PINGPONG || ov == QATTN_KERNEL_ONE_BLOCK) return ov;
+  if (ov == QATTN_KERNEL_MULTI_BLOCK && mq_ok && !causal) return QATTN_KERNEL_MULTI_BLOCK;
+  if (qpw_auto > 1) return QATTN_KERNEL_MULTI_BLOCK;
+  return B * Hq * ((nQB + 1) / 2) >= 256 ? QATTN_KERNEL_PINGPONG : QATTN_KERNEL_ONE_BLOCK;
 }
 
 template <int PV, bool KT, bool SP = false>
 static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, size_t workspace_bytes, hipStream_t st,
-                      int64_t D) {
+                      int64_t D, int kernel) {
+  t_last_kernel = kernel;
   if constexpr (PV == PV_FP8 && !SP) {
-    if (ns == 1 && p.qpw > 1) {
+    if (kernel == QATTN_KERNEL_MULTI_BLOCK) {
       p.nsplit = 1;
       p.tiles_per_split = (int)p.nKB;
       p.nQC = (p.nQB + p.qpw - 1) / p.qpw;
@@ -1697,6 +1131,15 @@ static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, siz
       QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
       if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, false, PV, KT, false, true><<<g, kThreads, 0, st>>>(p);
       else qattn_fwd_kernel<true, false, PV, KT, false, true><<<g, kThreads, 0, st>>>(p);
+      return check_launch("qattn_fwd");
+    }
+    if (kernel == QATTN_KERNEL_PINGPONG) {
+      p.nsplit = 1;
+      p.tiles_per_split = (int)p.nKB;
+      const int64_t g = p.B * p.Hq * ((p.nQB + 1) / 2);
+      QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
+      if (out_dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT><<<g, kPPThreads, 0, st>>>(p);
+      else qattn_fwd_pp_kernel<true, KT><<<g, kPPThreads, 0, st>>>(p);
       return check_launch("qattn_fwd");
     }
   }
@@ -1715,20 +1158,6 @@ static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, siz
     const int64_t rows = p.B * p.Hq * p.Lq;
     if (out_dtype == QATTN_BF16) qattn_combine_kernel<false><<<(rows + 3) / 4, 256, 0, st>>>(p);
     else qattn_combine_kernel<true><<<(rows + 3) / 4, 256, 0, st>>>(p);
-  } else if constexpr (PV == PV_FP8 && !SP) {
-    const int64_t g = p.B * p.Hq * ((p.nQB + 1) / 2);
-    if (pp_enabled(g)) {
-      QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
-      if (out_dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT><<<g, kPPThreads, 0, st>>>(p);
-      else qattn_fwd_pp_kernel<true, KT><<<g, kPPThreads, 0, st>>>(p);
-    } else if (wide_enabled() && p.nKB * ks_per_tile(KT) <= kWideKsFloats) {
-      const int64_t g = p.B * p.Hq * ((p.Lq + kWideRows - 1) / kWideRows);
-      if (out_dtype == QATTN_BF16) qattn_fwd_wide_kernel<false, KT><<<g, kThreads, 0, st>>>(p);
-      else qattn_fwd_wide_kernel<true, KT><<<g, kThreads, 0, st>>>(p);
-    } else {
-      if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, false, PV, KT, SP><<<grid, kThreads, 0, st>>>(p);
-      else qattn_fwd_kernel<true, false, PV, KT, SP><<<grid, kThreads, 0, st>>>(p);
-    }
   } else {
     if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, false, PV, KT, SP><<<grid, kThreads, 0, st>>>(p);
     else qattn_fwd_kernel<true, false, PV, KT, SP><<<grid, kThreads, 0, st>>>(p);
@@ -1756,10 +1185,36 @@ static int blocks_per_workgroup(int64_t bh, int64_t nqb, int64_t nkb) {
   return best;
 }
 
+// Split count, query blocks per workgroup and kernel of a launch (rows of 128 queries, tiles of 64 keys).
+static void plan_fwd(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int pv, int gran, int causal, bool sparse,
+                     int num_splits, int& ns, int& qpw, int& kernel) {
+  const int64_t nQB = (Lq + kBQ - 1) / kBQ, nKB = (Lk + kBK - 1) / kBK;
+  const int64_t max_tiles = sparse ? kSpMaxTiles : max_tiles_per_split(pv, gran == QATTN_GRAN_THREAD);
+  ns = num_splits > 0 ? num_splits : num_splits_for(B, Lq, Lk, Hq, max_tiles);
+  ns = (int)std::min<int64_t>(ns, nKB);
+  if (ns < 1) ns = 1;
+  // a workgroup stages the k_scales of at most max_tiles key tiles
+  ns = (int)std::max<int64_t>(ns, (nKB + max_tiles - 1) / max_tiles);
+  const bool mq_ok = ns == 1 && !sparse && !causal && pv == PV_FP8 && nKB <= kMqMaxTiles;
+  const int qpw_auto = mq_ok ? blocks_per_workgroup(B * Hq, nQB, nKB) : 1;
+  kernel = pick_kernel(pv, sparse, ns, causal, B, Hq, nQB, qpw_auto, mq_ok);
+  qpw = kernel == QATTN_KERNEL_MULTI_BLOCK ? qpw_auto : 1;
+}
+
+extern "C" int qattn_fwd_ex_kernel(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int v_kind, int qk_quant_gran,
+                                   int causal, int num_splits) {
+  if (B <= 0 || Lq <= 0 || Lk <= 0 || Hq <= 0) return QATTN_KERNEL_AUTO;
+  const int pv = v_kind == QATTN_V_FP8 ? PV_FP8 : v_kind == QATTN_V_BF16 ? PV_BF16 : PV_FP16;
+  int ns, qpw, kernel;
+  plan_fwd(B, Lq, Lk, Hq, pv, qk_quant_gran, causal, false, num_splits, ns, qpw, kernel);
+  return kernel;
+}
+
 static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale,
                      const void* v, int64_t Lpad, qattn_seq o, int out_dtype, int64_t B, int64_t Lq, int64_t Lk,
                      int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int causal, int64_t q_offset,
-                     const int32_t* kv_valid, float* lse, int num_splits, int pv, int gran, bool sparse = false) {
+                     const int32_t* kv_valid, float* lse, int num_splits, int pv, int gran, int& kernel,
+                     bool sparse = false) {
   QATTN_REQUIRE(out_dtype == QATTN_BF16 || out_dtype == QATTN_FP16, QATTN_ERR_DTYPE, "out dtype must be bf16 or fp16");
   QATTN_REQUIRE(D == kD, QATTN_ERR_HEAD_DIM, "qattn_fwd needs head_dim 128 (pad smaller heads), got %lld",
                 (long long)D);
@@ -1806,23 +1261,15 @@ static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale,
   p.causal = causal ? 1 : 0;
   p.qk_mult = qk_mult;
 
-  const int64_t max_tiles = sparse ? kSpMaxTiles : max_tiles_per_split(pv, gran == QATTN_GRAN_THREAD);
-  ns = num_splits > 0 ? num_splits : num_splits_for(B, Lq, Lk, Hq, max_tiles);
-  ns = (int)std::min<int64_t>(ns, p.nKB);
-  if (ns < 1) ns = 1;
-  // a workgroup stages the k_scales of at most max_tiles key tiles
-  ns = (int)std::max<int64_t>(ns, (p.nKB + max_tiles - 1) / max_tiles);
-  p.qpw = 1;
-  if (ns == 1 && !sparse && !causal && pv == PV_FP8 && p.nKB <= kMqMaxTiles && q8.sl >= kD)
-    p.qpw = blocks_per_workgroup(B * Hq, p.nQB, p.nKB);
+  plan_fwd(B, Lq, Lk, Hq, pv, gran, causal, sparse, num_splits, ns, p.qpw, kernel);
   return QATTN_OK;
 }
 
 template <int PV>
 static int launch_gran(AttnParams& p, int gran, int out_dtype, int ns, void* ws, size_t wsb, hipStream_t st,
-                       int64_t D) {
-  if (gran == QATTN_GRAN_THREAD) return launch_fwd<PV, true>(p, out_dtype, ns, ws, wsb, st, D);
-  return launch_fwd<PV, false>(p, out_dtype, ns, ws, wsb, st, D);
+                       int64_t D, int kernel) {
+  if (gran == QATTN_GRAN_THREAD) return launch_fwd<PV, true>(p, out_dtype, ns, ws, wsb, st, D, kernel);
+  return launch_fwd<PV, false>(p, out_dtype, ns, ws, wsb, st, D, kernel);
 }
 
 extern "C" int qattn_fwd_ex(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const void* v,
@@ -1833,21 +1280,21 @@ extern "C" int qattn_fwd_ex(qattn_seq q8, const float* q_scale, qattn_seq k8, co
   QATTN_REQUIRE(v_kind == QATTN_V_FP8 || v_kind == QATTN_V_BF16 || v_kind == QATTN_V_FP16, QATTN_ERR_DTYPE,
                 "v_kind must be 0 (fp8), 1 (bf16) or 2 (fp16), got %d", v_kind);
   AttnParams p;
-  int ns = 1;
+  int ns = 1, kernel = QATTN_KERNEL_AUTO;
   const int pv = v_kind == QATTN_V_FP8 ? PV_FP8 : v_kind == QATTN_V_BF16 ? PV_BF16 : PV_FP16;
   const int rc = setup_fwd(p, ns, q8, q_scale, k8, k_scale, v, Lpad, o, out_dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult,
-                           causal, q_offset, kv_valid, lse, num_splits, pv, qk_quant_gran);
+                           causal, q_offset, kv_valid, lse, num_splits, pv, qk_quant_gran, kernel);
   if (rc < 0) return QATTN_OK;
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
   if (pv == PV_FP8) {
     QATTN_REQUIRE(v_scale, QATTN_ERR_ARG, "v_scale is null");
     p.v_scale = v_scale;
-    return launch_gran<PV_FP8>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D);
+    return launch_gran<PV_FP8>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D, kernel);
   }
   p.v_scale = nullptr;
-  if (pv == PV_BF16) return launch_gran<PV_BF16>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D);
-  return launch_gran<PV_FP16>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D);
+  if (pv == PV_BF16) return launch_gran<PV_BF16>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D, kernel);
+  return launch_gran<PV_FP16>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D, kernel);
 }
 
 extern "C" int qattn_fwd(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const uint8_t* v8,
@@ -1885,10 +1332,10 @@ extern "C" int qattn_fwd_block_sparse(qattn_seq q8, const float* q_scale, qattn_
   QATTN_REQUIRE(tile_mask != nullptr, QATTN_ERR_ARG, "tile_mask is null");
   QATTN_REQUIRE(mask_sbh >= 0 && mask_sq >= 0, QATTN_ERR_STRIDE, "negative mask stride");
   AttnParams p;
-  int ns = 1;
+  int ns = 1, kernel = QATTN_KERNEL_AUTO;
   const int pv = v_dtype == QATTN_BF16 ? PV_BF16 : PV_FP16;
   const int rc = setup_fwd(p, ns, q8, q_scale, k8, k_scale, v16, Lpad, o, out_dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult,
-                           causal, 0, nullptr, lse, num_splits, pv, QATTN_GRAN_BLOCK, true);
+                           causal, 0, nullptr, lse, num_splits, pv, QATTN_GRAN_BLOCK, kernel, true);
   if (rc < 0) return QATTN_OK;
   if (rc) return rc;
   p.v_scale = nullptr;
@@ -1896,6 +1343,6 @@ extern "C" int qattn_fwd_block_sparse(qattn_seq q8, const float* q_scale, qattn_
   p.tm_s1 = mask_sbh;
   p.tm_s2 = mask_sq;
   hipStream_t st = (hipStream_t)stream;
-  if (pv == PV_BF16) return launch_fwd<PV_BF16, false, true>(p, out_dtype, ns, workspace, workspace_bytes, st, D);
-  return launch_fwd<PV_FP16, false, true>(p, out_dtype, ns, workspace, workspace_bytes, st, D);
+  if (pv == PV_BF16) return launch_fwd<PV_BF16, false, true>(p, out_dtype, ns, workspace, workspace_bytes, st, D, kernel);
+  return launch_fwd<PV_FP16, false, true>(p, out_dtype, ns, workspace, workspace_bytes, st, D, kernel);
 }

@@ -91,3 +91,24 @@ def test_fwd_ex_granularity_validation_and_splits(lib):
     assert lib.qattn_fwd_ex_num_splits(1, 75600, 75600, 40, 0, 3) == 1  # C3 fits one split with FP8 V
     assert lib.qattn_fwd_ex_num_splits(1, 75600, 75600, 40, 1, 3) > 1   # half V leaves less LDS for scales
     assert lib.qattn_fwd_ex_num_splits(1, 4680, 32760, 12, 0, 1) == lib.qattn_fwd_num_splits(1, 4680, 32760, 12)
+
+
+def test_kernel_selection_rule(lib):
+    """qattn_fwd_ex_kernel reports the automatic choice; qattn_set_kernel overrides it per thread."""
+    one, multi, pp = 1, 2, 3
+    assert lib.qattn_fwd_ex_kernel(1, 32760, 32760, 12, 0, 1, 0, 0) == pp      # C2: 1536 ping-pong workgroups
+    assert lib.qattn_fwd_ex_kernel(1, 32760, 32760, 12, 0, 3, 0, 0) == pp      # per-thread scales, same rule
+    assert lib.qattn_fwd_ex_kernel(1, 75600, 512, 40, 0, 1, 0, 0) == multi     # C4: short key range
+    assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 12, 0, 1, 0, 0) == one      # C5: KV split
+    assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 0) == one        # C1: grid too small
+    assert lib.qattn_fwd_ex_kernel(1, 32760, 32760, 12, 1, 1, 0, 0) == one     # half P.V
+    prev = lib.qattn_set_kernel(pp)
+    try:
+        assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 1) == pp
+        assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 12, 0, 1, 0, 0) == one  # a split launch cannot
+        lib.qattn_set_kernel(multi)
+        assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 1, 1) == one    # causal: multi-block does not apply
+        assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 1) == multi
+    finally:
+        lib.qattn_set_kernel(prev)
+    assert lib.qattn_set_kernel(0) == 0

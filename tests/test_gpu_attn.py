@@ -22,6 +22,7 @@ KERNEL_LSUM_ROUNDED = True
 
 
 GRAN_CODE = {"per_block": 1, "per_warp": 2, "per_thread": 3}
+KERNEL_ONE_BLOCK, KERNEL_MULTI_BLOCK, KERNEL_PINGPONG = 1, 2, 3  # enum qattn_kernel
 
 
 def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None, num_splits=0, q_offset=0,
@@ -400,12 +401,14 @@ def test_multi_block_workgroups(oracle, case):
     kw = dict(tensor_layout=layout, out_dtype=dt, kv_valid_len=kv_valid, return_lse=True, qk_mult=qk_mult,
               qk_quant_gran=gran)
     o, lse = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
+    assert L.qattn_last_kernel() == KERNEL_MULTI_BLOCK
     hd = 2 if layout == "NHD" else 1
     heads = [0, 7, 19]
     idx = torch.tensor(heads, device=dev)
     sel = lambda t, d: t.view(torch.uint8).index_select(d, idx).view(t.dtype) if t.dtype == torch.float8_e4m3fn \
         else t.index_select(d, idx).contiguous()
     o3, lse3 = sa.qattn_fwd(sel(q8, hd), sel(qs, 1), sel(k8, hd), sel(ks, 1), sel(v8, 1), sel(vs, 1), **kw)
+    assert L.qattn_last_kernel() == KERNEL_ONE_BLOCK
     torch.cuda.synchronize()
     assert torch.equal(sel(o, hd), o3), "multi-block output differs from the one-block-per-workgroup launch"
     assert torch.equal(sel(lse, 1), lse3)
@@ -423,26 +426,19 @@ def test_multi_block_workgroups(oracle, case):
     assert float(np.max(np.abs(lse[:1, 7:8].cpu().numpy() - ref_lse))) < 2e-2
 
 
-ALT_KERNELS = {  # opt-in kernels for dense FP8 launches: environment settings
-    "wide": {"QATTN_WIDE": "1", "QATTN_PP": "0"},
-    "pingpong": {"QATTN_WIDE": "0", "QATTN_PP": "1"},
-    "pingpong_kpre": {"QATTN_WIDE": "0", "QATTN_PP": "2"},
-}
-
-
-@pytest.mark.parametrize("kernel", list(ALT_KERNELS))
 @pytest.mark.parametrize("case", ["ragged", "padding", "empty_batch", "causal", "causal_odd", "gqa_hnd_thread",
                                   "fp16_warp_gqa", "long"])
-def test_alt_kernel_matches(oracle, kernel, case, monkeypatch):
-    """The alternative dense FP8 kernels run the same per-element arithmetic and accumulation order as
-    qattn_fwd_kernel, so their output and LSE must be identical, bit for bit, on the same quantized
-    operands: the wide kernel (QATTN_WIDE=1: 64 query rows per wave, software-pipelined halves) and the
-    ping-pong kernel (QATTN_PP=1: two 4-wave groups per workgroup alternating matrix and vector stages,
-    forced here whatever the grid size).  Checked on ragged lengths (masked tail tiles), key padding per
-    batch (one batch with no valid key at all), top-left causal, causal with an odd number of query blocks and more keys than queries, GQA +
-    HND + per-thread scales, GQA + per-warp scales + fp16 output, and a key range long enough for the
+def test_pingpong_kernel_matches(oracle, case):
+    """The ping-pong kernel (two 4-wave groups per workgroup alternating matrix and vector stages) runs the
+    same per-element arithmetic and accumulation order as qattn_fwd_kernel, so its output and LSE must be
+    identical, bit for bit, on the same quantized operands.  Both kernels are forced through
+    qattn_set_kernel whatever the grid size, and qattn_last_kernel confirms which one ran.  Checked on
+    ragged lengths (masked tail tiles), key padding per batch (one batch with no valid key at all),
+    top-left causal, causal with an odd number of query blocks and more keys than queries, GQA + HND +
+    per-thread scales, GQA + per-warp scales + fp16 output, and a key range long enough for the
     steady-state pipeline.  The long case is also checked against the oracle."""
     dev = require_gpu()
+    from telefuser_amd import _lib
     from telefuser_amd import sageattn2 as sa
 
     B, Lq, Lk, Hq, Hkv, layout, causal, kv_valid, gran = {
@@ -455,7 +451,7 @@ def test_alt_kernel_matches(oracle, kernel, case, monkeypatch):
         "fp16_warp_gqa": (1, 900, 1100, 6, 2, "NHD", False, None, "per_warp"),
         "long": (1, 700, 8200, 2, 2, "NHD", False, None, "per_block"),
     }[case]
-    log(f"{kernel} vs default: {case} B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} layout={layout} causal={causal} "
+    log(f"pingpong vs one-block: {case} B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} layout={layout} causal={causal} "
         f"kv_valid={kv_valid} gran={gran}")
     q, k, v = qkv(B, Lq, Lk, Hq, Hkv, seed=4242, k_offset_std=0.5)
     qd, kd, vd = (t.to(dev) for t in (q, k, v))
@@ -473,16 +469,20 @@ def test_alt_kernel_matches(oracle, kernel, case, monkeypatch):
     out_dtype = torch.float16 if case == "fp16_warp_gqa" else torch.bfloat16
     kw = dict(tensor_layout=layout, out_dtype=out_dtype, is_causal=causal, kv_valid_len=kv_valid,
               return_lse=True, qk_mult=qk_mult, qk_quant_gran=gran, num_splits=1)
-    monkeypatch.setenv("QATTN_WIDE", "0")
-    monkeypatch.setenv("QATTN_PP", "0")
-    o0, l0 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
-    for key, val in ALT_KERNELS[kernel].items():
-        monkeypatch.setenv(key, val)
-    o1, l1 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
-    o2, l2 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
+    L = _lib.load()
+    prev = L.qattn_set_kernel(KERNEL_ONE_BLOCK)
+    try:
+        o0, l0 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
+        assert L.qattn_last_kernel() == KERNEL_ONE_BLOCK
+        L.qattn_set_kernel(KERNEL_PINGPONG)
+        o1, l1 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
+        assert L.qattn_last_kernel() == KERNEL_PINGPONG
+        o2, l2 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
+    finally:
+        L.qattn_set_kernel(prev)
     torch.cuda.synchronize()
-    assert torch.equal(o1, o2) and torch.equal(l1, l2), f"{kernel} kernel is not deterministic"
-    assert torch.equal(o0, o1), f"{kernel} kernel differs: max {float((o0.float() - o1.float()).abs().max()):.4g}"
+    assert torch.equal(o1, o2) and torch.equal(l1, l2), "ping-pong kernel is not deterministic"
+    assert torch.equal(o0, o1), f"ping-pong kernel differs: max {float((o0.float() - o1.float()).abs().max()):.4g}"
     assert torch.equal(l0, l1)
     if case == "empty_batch":  # no valid key: zero output, LSE -inf
         assert bool((o1[1] == 0).all()) and bool(torch.isneginf(l1[1]).all())
@@ -491,7 +491,7 @@ def test_alt_kernel_matches(oracle, kernel, case, monkeypatch):
                                ks.cpu().numpy(), v8=untile_v(v8), v_scale=vs.cpu().numpy(),
                                lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED)
         c = cosine(o1.float().cpu().numpy(), ref)
-        log(f"  {kernel} kernel vs quantized oracle: cosine={c:.6f}")
+        log(f"  ping-pong kernel vs quantized oracle: cosine={c:.6f}")
         assert c >= COS_KERNEL
 
 
