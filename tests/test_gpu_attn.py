@@ -369,7 +369,7 @@ def test_block_sparse(oracle, case):
 def test_multi_block_workgroups(oracle, case):
     """Short key ranges over a large grid run several query blocks per workgroup through one K/V pipeline.
     The per-block arithmetic is unchanged, so every head must match, bit for bit, a launch of a few heads
-    (small grid: one block per workgroup) on the same quantized operands; one (batch, head) is also checked
+    (forced to one block per workgroup) on the same quantized operands; one (batch, head) is also checked
     against the oracle.  Covers key padding down to zero keys, a ragged last query block and the lse."""
     dev = require_gpu()
     from telefuser_amd import _lib
@@ -407,8 +407,12 @@ def test_multi_block_workgroups(oracle, case):
     idx = torch.tensor(heads, device=dev)
     sel = lambda t, d: t.view(torch.uint8).index_select(d, idx).view(t.dtype) if t.dtype == torch.float8_e4m3fn \
         else t.index_select(d, idx).contiguous()
-    o3, lse3 = sa.qattn_fwd(sel(q8, hd), sel(qs, 1), sel(k8, hd), sel(ks, 1), sel(v8, 1), sel(vs, 1), **kw)
-    assert L.qattn_last_kernel() == KERNEL_ONE_BLOCK
+    prev = L.qattn_set_kernel(KERNEL_ONE_BLOCK)  # the reference launch: one query block per workgroup
+    try:
+        o3, lse3 = sa.qattn_fwd(sel(q8, hd), sel(qs, 1), sel(k8, hd), sel(ks, 1), sel(v8, 1), sel(vs, 1), **kw)
+        assert L.qattn_last_kernel() == KERNEL_ONE_BLOCK
+    finally:
+        L.qattn_set_kernel(prev)
     torch.cuda.synchronize()
     assert torch.equal(sel(o, hd), o3), "multi-block output differs from the one-block-per-workgroup launch"
     assert torch.equal(sel(lse, 1), lse3)
