@@ -252,6 +252,21 @@ int qattn_fwd_ex(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* 
                  qattn_stream_t stream);
 
 /*
+ * qattn_fwd_ex without a workspace argument, for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops).  No counterpart in the reference.  KV-split partials go to a
+ * device array inside the library (one per GPU, held until the process ends) of at most
+ * qattn_fwd_noalloc_max_scratch() bytes (128 MiB): a launch whose qattn_fwd_workspace_size(B, Lq, Hq, D,
+ * splits) exceeds it fails with QATTN_ERR_WORKSPACE.  Calls never allocate; calls that overlap on one GPU
+ * (different streams or threads) share that array and race.  Results equal qattn_fwd_ex's.
+ */
+size_t qattn_fwd_noalloc_max_scratch(void);
+int qattn_fwd_ex_noalloc(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const void* v,
+                         int v_kind, int64_t Lpad, const float* v_scale, qattn_seq o, int out_dtype, int64_t B,
+                         int64_t Lq, int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int qk_quant_gran,
+                         int causal, int64_t q_offset, const int32_t* kv_valid, float* lse, int num_splits,
+                         qattn_stream_t stream);
+
+/*
  * Block-sparse quantized attention: like qattn_fwd_pv16, but a query block (128 rows) only visits the
  * key tiles (64 keys) whose mask byte is non-zero - the k_block_id skip of the reference's
  * sparse_int8_attn forward (telefuser/kernel/triton/sparse_int8_attn.py:22-280, called from

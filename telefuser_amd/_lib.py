@@ -102,6 +102,11 @@ def load() -> ctypes.CDLL:
     L.qattn_fwd_ex_num_splits.restype = i32
     L.qattn_fwd_ex_blocks_per_workgroup.argtypes = [i64, i64, i64, i64, i32, i32, i32]
     L.qattn_fwd_ex_blocks_per_workgroup.restype = i32
+    L.qattn_fwd_noalloc_max_scratch.argtypes = []
+    L.qattn_fwd_noalloc_max_scratch.restype = sz
+    L.qattn_fwd_ex_noalloc.argtypes = [S, vp, S, vp, vp, i32, i64, vp, S, i32, i64, i64, i64, i64, i64, i64, f32, i32,
+                                       i32, i64, vp, vp, i32, vp]
+    L.qattn_fwd_ex_noalloc.restype = i32
     L.qattn_fwd_ex_kernel.argtypes = [i64, i64, i64, i64, i32, i32, i32, i32]
     L.qattn_fwd_ex_kernel.restype = i32
     L.qattn_set_kernel.argtypes = [i32]

@@ -30,6 +30,7 @@
 //   * Optional KV split (flash-decoding style) for grids that cannot fill 256 CUs; a combine kernel
 //     merges the partial (O, m, l) triples.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1295,6 +1296,65 @@ extern "C" int qattn_fwd_ex(qattn_seq q8, const float* q_scale, qattn_seq k8, co
   p.v_scale = nullptr;
   if (pv == PV_BF16) return launch_gran<PV_BF16>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D, kernel);
   return launch_gran<PV_FP16>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D, kernel);
+}
+
+// ---- allocation-free form of qattn_fwd_ex ----
+// KV-split launches keep their partial (O, m, l) rows in this file-scope device array instead of a caller
+// workspace.  Every GPU the library runs on holds its own copy for the life of the process; host code
+// reaches it only through the address hipGetSymbolAddress returns on that device (the array's name is a
+// host-side stand-in, not a device address).
+constexpr size_t kScratchBytes = 128ull << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+// the scratch address on the calling thread's current device, looked up once per device
+static int scratch_on_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  QATTN_REQUIRE(e == hipSuccess && dev >= 0 && dev < kMaxDevices, QATTN_ERR_LAUNCH, "hipGetDevice failed: %s",
+                hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    QATTN_REQUIRE(e == hipSuccess && ptr, QATTN_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return QATTN_OK;
+}
+
+extern "C" size_t qattn_fwd_noalloc_max_scratch(void) { return kScratchBytes; }
+
+extern "C" int qattn_fwd_ex_noalloc(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale,
+                                    const void* v, int v_kind, int64_t Lpad, const float* v_scale, qattn_seq o,
+                                    int out_dtype, int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t Hkv,
+                                    int64_t D, float qk_mult, int qk_quant_gran, int causal, int64_t q_offset,
+                                    const int32_t* kv_valid, float* lse, int num_splits, qattn_stream_t stream) {
+  QATTN_REQUIRE(v_kind == QATTN_V_FP8 || v_kind == QATTN_V_BF16 || v_kind == QATTN_V_FP16, QATTN_ERR_DTYPE,
+                "v_kind must be 0 (fp8), 1 (bf16) or 2 (fp16), got %d", v_kind);
+  AttnParams p;
+  int ns = 1, kernel = QATTN_KERNEL_AUTO;
+  const int pv = v_kind == QATTN_V_FP8 ? PV_FP8 : v_kind == QATTN_V_BF16 ? PV_BF16 : PV_FP16;
+  const int rc = setup_fwd(p, ns, q8, q_scale, k8, k_scale, v, Lpad, o, out_dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult,
+                           causal, q_offset, kv_valid, lse, num_splits, pv, qk_quant_gran, kernel);
+  if (rc < 0) return QATTN_OK;
+  if (rc) return rc;
+  const size_t need = qattn_fwd_workspace_size(B, Lq, Hq, D, ns);
+  QATTN_REQUIRE(need <= kScratchBytes, QATTN_ERR_WORKSPACE,
+                "qattn_fwd_ex_noalloc: %d KV splits need %zu bytes of scratch, more than its %zu-byte limit "
+                "(use qattn_fwd_ex with a workspace, or fewer splits)", ns, need, kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int e = scratch_on_current_device(&ws);
+    if (e) return e;
+  }
+  // the same launch as qattn_fwd_ex with this split count and the device array as its workspace
+  return qattn_fwd_ex(q8, q_scale, k8, k_scale, v, v_kind, Lpad, v_scale, o, out_dtype, B, Lq, Lk, Hq, Hkv, D,
+                      qk_mult, qk_quant_gran, causal, q_offset, kv_valid, lse, ns, ws, need, stream);
 }
 
 extern "C" int qattn_fwd(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const uint8_t* v8,
