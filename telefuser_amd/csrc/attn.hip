@@ -587,9 +587,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
         for (int j = 0; j < 8; j++) {
           float pv[4];
           p4(j, pv, mk);
-          // the low word is written first; the old contents of pf[j] only fill bits that the second
-          // conversion overwrites, so no zeroed register is needed
-          const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], pf[j], false);
+          // the low word is written first and the high word then overwrites the rest of the register,
+          // so its incoming value does not matter (an undefined one needs no copy)
+          const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], __builtin_nondeterministic_value(0), false);
           pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
         }
       };
@@ -940,7 +940,9 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
           pv[e] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(sv), e < 2 ? cs_a : cs_b, e < 2 ? nc_a : nc_b));
           if constexpr (decltype(mk)::value) pv[e] = sv == INT32_MIN ? 0.f : pv[e];
         }
-        const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], pf[j], false);
+        // the low word is written first and the high word then overwrites the rest of the register, so
+        // its incoming value does not matter: an undefined one lets the compiler skip a copy per pair
+        const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], __builtin_nondeterministic_value(0), false);
         pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
       }
     };
