@@ -103,7 +103,9 @@ def attention(
 
     q/k/v: [B, S, N, D] (BSND) or [B, N, S, D] (BNSD).  ``kv_valid_len`` (int or per-batch sequence) is
     this backend's key-padding mask for the SAGE implementations; as in the reference, ``attn_mask`` is
-    not applied by the SAGE kernels (pass ``kv_valid_len`` instead) but is honoured by SDPA.
+    not applied by the SAGE kernels (pass ``kv_valid_len`` instead) but is honoured by SDPA, and
+    ``is_causal`` is not passed to the SAGE kernels (their output is non-causal; call
+    ``sageattn2.sageattn_qk_int8_pv_fp8_cuda(..., is_causal=True)`` directly for causal SAGE attention).
     """
     if attention_config is None:
         attention_config = AttentionConfig(attn_impl=attn_impl or AttnImplType.TORCH_SDPA, scale=scale,
@@ -133,8 +135,10 @@ def attention(
             AttnImplType.SAGE_ATTN_2_8_8_SM90: sageattention.sageattn_qk_int8_pv_fp8_cuda_sm90,
         }[impl]
         pv_accum = "fp32" if impl == AttnImplType.SAGE_ATTN_2_8_16 else "fp32+fp32"
-        result = fn(q, k, v, attn_mask=attn_mask, sm_scale=scale, tensor_layout=layout, is_causal=is_causal,
-                    pv_accum_dtype=pv_accum, return_lse=return_lse, kv_valid_len=kv_valid_len, **kwargs)
+        # is_causal is not forwarded: the reference's SAGE branch calls the sage functions without it
+        # (attention_impl.py:249-283), so their output is non-causal whatever is_causal says
+        result = fn(q, k, v, attn_mask=attn_mask, sm_scale=scale, tensor_layout=layout, pv_accum_dtype=pv_accum,
+                    return_lse=return_lse, kv_valid_len=kv_valid_len, **kwargs)
         output, lse = result if return_lse else (result, None)
     elif impl in (AttnImplType.TORCH_SDPA, AttnImplType.TORCH_CUDNN) and SDPA_AVAILABLE:
         output = F.scaled_dot_product_attention(q, k, v, attn_mask=attn_mask, scale=scale, is_causal=is_causal)

@@ -190,6 +190,40 @@ def _kv_valid_tensor(kv_valid_len, b: int, device) -> Optional[torch.Tensor]:
 _GRAN = {"per_block": _lib.QATTN_GRAN_BLOCK, "per_warp": _lib.QATTN_GRAN_WARP, "per_thread": _lib.QATTN_GRAN_THREAD}
 
 
+def _check_attn_operands(q_int8, q_scale, k_int8, k_scale, v, v_scale, b, lq, lk, hq, hkv, d, gran, out, out_dtype):
+    """Shapes, dtypes and devices of qattn_fwd's operands: a scale tensor of another granularity or a V
+    tile of the wrong size would make the kernel read outside them."""
+    nqb, nkb = -(-lq // BLKQ), -(-lk // BLKK)
+    q_per = {"per_block": 1, "per_warp": 4, "per_thread": 32}[gran]
+    k_per = 4 if gran == "per_thread" else 1
+    dev = q_int8.device
+    if q_int8.dtype != torch.int8 or k_int8.dtype != torch.int8:
+        raise ValueError("q_int8 and k_int8 must be int8")
+    for name, t, shape in (("q_scale", q_scale, (b, hq, nqb * q_per)), ("k_scale", k_scale, (b, hkv, nkb * k_per))):
+        if t.dtype != torch.float32 or tuple(t.shape) != shape or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 tensor of shape {shape} for qk_quant_gran="
+                             f"{gran!r}, got {t.dtype} {tuple(t.shape)}")
+    lpad = nkb * BLKK
+    if v.dim() != 4 or tuple(v.shape[:3]) != (b, hkv, d) or v.shape[3] < lpad or v.shape[3] % BLKK or \
+            not v.is_contiguous():
+        raise ValueError(f"the V tile must be a contiguous [B, Hkv, D, Lpad] = [{b}, {hkv}, {d}, >= {lpad} (multiple "
+                         f"of 64)] tensor from per_channel_fp8 / v_tile_half, got {tuple(v.shape)}")
+    if v_scale is not None:
+        if v.element_size() != 1:
+            raise ValueError("with v_scale, V must be the e4m3 tile of per_channel_fp8")
+        if v_scale.dtype != torch.float32 or tuple(v_scale.shape) != (b, hkv, d) or not v_scale.is_contiguous():
+            raise ValueError(f"v_scale must be a contiguous float32 tensor of shape {(b, hkv, d)}, "
+                             f"got {v_scale.dtype} {tuple(v_scale.shape)}")
+    elif v.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("without v_scale, V must be the bf16 / fp16 tile of v_tile_half")
+    if out is not None and (tuple(out.shape) != tuple(q_int8.shape) or out.dtype != out_dtype):
+        raise ValueError(f"out must have q's shape {tuple(q_int8.shape)} and dtype {out_dtype}")
+    for name, t in (("q_scale", q_scale), ("k_int8", k_int8), ("k_scale", k_scale), ("V", v), ("v_scale", v_scale),
+                    ("out", out)):
+        if t is not None and t.device != dev:
+            raise ValueError(f"{name} is on {t.device}, q_int8 on {dev}")
+
+
 def qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout="HND", out_dtype=torch.bfloat16,
               qk_mult=1.0, is_causal=False, q_offset=0, kv_valid_len=None, return_lse=False, num_splits=0,
               qk_quant_gran="per_block", out: Optional[torch.Tensor] = None):
@@ -203,7 +237,11 @@ def qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout
     _, lk, hkv, _ = _dims(k_int8, tensor_layout)
     if hq % hkv != 0:
         raise ValueError(f"num_qo_heads ({hq}) must be divisible by num_kv_heads ({hkv})")
+    if qk_quant_gran not in _GRAN:
+        raise ValueError(f"qk_quant_gran must be one of {sorted(_GRAN)}, got {qk_quant_gran!r}")
     gran = _GRAN[qk_quant_gran]
+    _check_attn_operands(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, b, lq, lk, hq, hkv, d, qk_quant_gran, out,
+                         out_dtype)
     o = out if out is not None else torch.empty(q_int8.shape, dtype=out_dtype, device=q_int8.device)
     if v_scale is None:  # v_fp8 is then the half-dtype tile layout from v_tile_half
         v_kind = _lib.QATTN_V_BF16 if v_fp8.dtype == torch.bfloat16 else _lib.QATTN_V_FP16

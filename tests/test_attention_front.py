@@ -74,3 +74,14 @@ def test_sdpa_path_and_fallback_match_torch():
     # an implementation this package does not provide falls back to SDPA
     got2 = A.attention(q, k, v, attn_impl=A.AttnImplType.FLASH_ATTN_3, is_causal=True)
     assert torch.allclose(got2, want, atol=1e-6)
+
+
+def test_sage_impls_do_not_forward_is_causal(fake_sage):
+    """The reference's SAGE branch calls the sage functions without is_causal (attention_impl.py:249-283),
+    so a causal request through attention() yields the non-causal SAGE result; the front door matches."""
+    q = torch.randn(1, 8, 2, 128)
+    for impl in (A.AttnImplType.SAGE_ATTN_2_8_8, A.AttnImplType.SAGE_ATTN_2_8_16, A.AttnImplType.SAGE_ATTN_2_8_8_SM90):
+        A.attention(q, q, q, attn_impl=impl, is_causal=True)
+        assert "is_causal" not in fake_sage.calls[-1][2]
+    A.attention(q, q, q, attention_config=A.AttentionConfig(attn_impl=A.AttnImplType.SAGE_ATTN_2_8_8, is_causal=True))
+    assert "is_causal" not in fake_sage.calls[-1][2]

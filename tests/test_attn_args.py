@@ -1,0 +1,60 @@
+"""Argument checks of sageattn2.qattn_fwd, on the CPU: operands that do not match the launch's sizes and
+scale granularity are rejected before any kernel could read outside them."""
+
+import os
+
+import pytest
+import torch
+
+from telefuser_amd import _lib
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _built():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("libqattn.so not built")
+
+
+def _ops(B=1, Lq=300, Lk=200, Hq=4, Hkv=2, gran="per_block", half=False):
+    from telefuser_amd.sageattn2 import BLKK, BLKQ
+
+    nqb, nkb = -(-Lq // BLKQ), -(-Lk // BLKK)
+    q8 = torch.zeros(B, Lq, Hq, 128, dtype=torch.int8)
+    k8 = torch.zeros(B, Lk, Hkv, 128, dtype=torch.int8)
+    qs = torch.ones(B, Hq, nqb * {"per_block": 1, "per_warp": 4, "per_thread": 32}[gran])
+    ks = torch.ones(B, Hkv, nkb * (4 if gran == "per_thread" else 1))
+    if half:
+        v, vs = torch.zeros(B, Hkv, 128, nkb * BLKK, dtype=torch.bfloat16), None
+    else:
+        v, vs = torch.zeros(B, Hkv, 128, nkb * BLKK, dtype=torch.uint8), torch.ones(B, Hkv, 128)
+    return q8, qs, k8, ks, v, vs
+
+
+@pytest.mark.parametrize("bad", ["q_scale_gran", "k_scale_thread", "v_short", "v_noncontig", "v_scale_shape",
+                                 "half_with_scale", "q_dtype", "gran_name", "out_shape"])
+def test_qattn_fwd_rejects_mismatched_operands(bad):
+    from telefuser_amd import sageattn2 as sa
+
+    gran = "per_thread" if bad == "k_scale_thread" else "per_block"
+    q8, qs, k8, ks, v, vs = _ops(gran=gran)
+    kw = dict(tensor_layout="NHD", qk_quant_gran=gran)
+    if bad == "q_scale_gran":
+        kw["qk_quant_gran"] = "per_thread"  # per-block scales handed to a per-thread launch
+    elif bad == "k_scale_thread":
+        ks = ks[..., :ks.shape[-1] // 4].contiguous()
+    elif bad == "v_short":
+        v = v[..., :64].contiguous()
+    elif bad == "v_noncontig":
+        v = torch.zeros(v.shape[0], v.shape[1], v.shape[3], v.shape[2], dtype=v.dtype).transpose(2, 3)
+    elif bad == "v_scale_shape":
+        vs = vs[:, :1].contiguous()
+    elif bad == "half_with_scale":
+        v = v.to(torch.bfloat16)
+    elif bad == "q_dtype":
+        q8 = q8.to(torch.int16)
+    elif bad == "gran_name":
+        kw["qk_quant_gran"] = "per_tile"
+    elif bad == "out_shape":
+        kw["out"] = torch.empty(1, 10, 4, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        sa.qattn_fwd(q8, qs, k8, ks, v, vs, **kw)

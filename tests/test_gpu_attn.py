@@ -19,6 +19,7 @@ LOG2E = 1.44269504
 KERNEL_LAZY_TAU = 1.0  # lazy running-max threshold of qattn_fwd_kernel (kLazyTau in attn.hip)
 # FP8 P.V kernels sum the e4m3-rounded P on the matrix pipe (row_sum_mfma in attn.hip); the oracle restates it
 KERNEL_LSUM_ROUNDED = True
+LSE_ROUNDED_SUM_BOUND = 0.0931  # log2(16/15): bound of the rounded-vs-unrounded row-sum LSE difference
 
 
 GRAN_CODE = {"per_block": 1, "per_warp": 2, "per_thread": 3}
@@ -78,13 +79,20 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
     log(f"  vs quantized oracle (splits={ns}): cosine={c:.6f} max_abs={err:.4g} lse_max_abs={lerr:.3g}")
     assert c >= COS_KERNEL
     # the reference's own schedule (no split, eager running max) on the same quantized operands
-    ref0 = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
-                            ks.cpu().numpy(), **vargs, causal=causal, q_offset=q_offset, kv_valid=kv_valid,
-                            qk_mult=qk_mult, q_gran=GRAN_CODE[gran], k_gran=GRAN_CODE[gran])
+    ref0, ref0_lse = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(),
+                                      k8.contiguous().cpu().numpy(), ks.cpu().numpy(), **vargs, causal=causal,
+                                      q_offset=q_offset, kv_valid=kv_valid, qk_mult=qk_mult, q_gran=GRAN_CODE[gran],
+                                      k_gran=GRAN_CODE[gran], want_lse=True)
     c0 = cosine(og, ref0)
-    log(f"  vs reference-schedule quantized math: cosine={c0:.6f} max_abs={float(np.abs(og - ref0).max()):.4g}")
+    lerr0 = float(np.nanmax(np.abs(lse.cpu().numpy() - ref0_lse)))
+    log(f"  vs reference-schedule quantized math: cosine={c0:.6f} max_abs={float(np.abs(og - ref0).max()):.4g} "
+        f"lse_max_abs={lerr0:.3g}")
     assert c0 >= COS_E2E
     assert lerr < 2e-2
+    # The reference sums the unrounded p (accumulate_d); the FP8 kernels sum the e4m3-rounded P on the
+    # matrix pipe.  Every p is rounded by a relative error of at most 2^-4, so the row sums differ by at
+    # most a factor 1 / (1 - 2^-4) and the log2-domain LSE by at most log2(16/15) = 0.0931.
+    assert lerr0 < LSE_ROUNDED_SUM_BOUND
     if check_truth:
         bits = (lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)) if f16 else bf16_bits
         truth = oracle.attn_fp64(bits(q), bits(k), bits(v), D ** -0.5, causal=causal,
