@@ -211,7 +211,7 @@ def _config_bench(name: str, calls: int = 5, warmup: int = 2) -> dict:
     def call(record):
         km = sa.k_mean(k, "NHD")
         q8, qs, k8, ks = sa.per_block_int8(q, k, km, sm_scale=sm, tensor_layout="NHD")
-        v8, vs, _ = sa.per_channel_fp8(v, tensor_layout="NHD")
+        v8, vs, _ = sa.per_channel_fp8(v, tensor_layout="NHD", smooth_v=False)
         s = torch.cuda.current_stream()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(s)
@@ -340,7 +340,7 @@ def main() -> int:
         if record:
             e1 = torch.cuda.Event(enable_timing=True)
             e1.record()
-        v8, vs, _ = sa.per_channel_fp8(v, tensor_layout=layout)
+        v8, vs, _ = sa.per_channel_fp8(v, tensor_layout=layout, smooth_v=False)
         if record:
             e2 = torch.cuda.Event(enable_timing=True)
             e2.record()

@@ -135,6 +135,17 @@ size_t qattn_per_channel_fp8_workspace_size(int64_t B, int64_t L, int64_t H, int
 int qattn_per_channel_fp8(qattn_seq v, int dtype, int64_t B, int64_t L, int64_t H, int64_t D, float scale_max,
                           uint8_t* v8, int64_t Lpad, float* v_scale, void* workspace, size_t workspace_bytes,
                           qattn_stream_t stream);
+/*
+ * qattn_per_channel_fp8 with the reference's optional V smoothing (per_channel_fp8(smooth_v=True) ->
+ * mean_scale_fuse_quant_cuda, MeanScaleKernel<sub_mean> fused.cu:362-445): with smooth_v != 0,
+ *   v_mean = sum over the L tokens / (L rounded up to 16)        (fp32 [B, H, D], written)
+ *   amax   = max(|max - v_mean|, |min - v_mean|), max / min including the zero pad tokens up to 16
+ *   v8     = e4m3((v - v_mean) * scale_max / amax),  v_scale = amax / scale_max
+ * and the attention adds v_mean back to its output (qattn_fwd_ex2).  smooth_v == 0: qattn_per_channel_fp8.
+ */
+int qattn_per_channel_fp8_ex(qattn_seq v, int dtype, int64_t B, int64_t L, int64_t H, int64_t D, float scale_max,
+                             int smooth_v, uint8_t* v8, int64_t Lpad, float* v_scale, float* v_mean, void* workspace,
+                             size_t workspace_bytes, qattn_stream_t stream);
 
 /*
  * Quantized attention: INT8 Q.K^T on MFMA, fp32 online softmax (exp2 domain, FP8 offset 8.807),
@@ -250,6 +261,17 @@ int qattn_fwd_ex(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* 
                  int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int qk_quant_gran, int causal, int64_t q_offset,
                  const int32_t* kv_valid, float* lse, int num_splits, void* workspace, size_t workspace_bytes,
                  qattn_stream_t stream);
+/*
+ * qattn_fwd_ex plus the V-mean epilogue of the reference's fuse_v_mean kernel
+ * (qk_int8_sv_f8_accum_f32_fuse_v_scale_fuse_v_mean_attn, common_extension.cc; sm89 kernel :742-761):
+ * out = O / l * v_scale + v_mean, with v_mean fp32 [B, Hkv, D] from qattn_per_channel_fp8_ex (FP8 V
+ * only; NULL = qattn_fwd_ex).
+ */
+int qattn_fwd_ex2(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const void* v, int v_kind,
+                  int64_t Lpad, const float* v_scale, const float* v_mean, qattn_seq o, int out_dtype, int64_t B,
+                  int64_t Lq, int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int qk_quant_gran,
+                  int causal, int64_t q_offset, const int32_t* kv_valid, float* lse, int num_splits, void* workspace,
+                  size_t workspace_bytes, qattn_stream_t stream);
 
 /*
  * qattn_fwd_ex without a workspace argument, for callers that cannot allocate device memory (code under

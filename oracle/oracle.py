@@ -40,9 +40,11 @@ def lib():
         L.oq_quant_per_block_int8_triton.argtypes = [vp, i32, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, f32,
                                                      i64, vp, i64, i64, i64, vp]
         L.oq_per_channel_fp8.argtypes = [vp, i32, i64, i64, i64, i64, i64, i64, i64, f32, vp, i64, vp]
+        L.oq_per_channel_fp8_ex.argtypes = [vp, i32, i64, i64, i64, i64, i64, i64, i64, f32, i32, vp, vp, vp, i64,
+                                            vp]
         L.oq_qattn_fwd.argtypes = [vp, i64, i64, i64, vp, i64, vp, i64, i64, i64, vp, i64, vp, i64, vp, vp, i32,
                                    i64, i64, i64, i64, i64, i64, i64, i64, i64, f64, i32, i32, i64, vp, i64, i64,
-                                   i64, i64, f64, i32, i32, i32, vp, i64, i64, vp, vp]
+                                   i64, i64, f64, i32, i32, i32, vp, i64, i64, vp, i32, vp, vp]
         L.oq_norm_rope.argtypes = [vp, i32, i64, i64, i64, i64, vp, vp, vp, f32, vp]
         L.oq_quant_per_thread_int8.argtypes = [vp, i32, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, i32, vp,
                                                i64, i64, i64, vp]
@@ -139,28 +141,34 @@ def quant_per_thread_int8(x_bits, km_bits=None, is_key=False, layout="NHD", is_f
     return out, scale
 
 
-def per_channel_fp8(v_bits, scale_max=448.0, layout="NHD", is_fp16=False, pad=64):
-    """V -> (e4m3 bytes [B, H, D, Lpad] in plain key order, v_scale [B, H, D]).  fused.cu:332-445."""
+def per_channel_fp8(v_bits, scale_max=448.0, layout="NHD", is_fp16=False, pad=64, smooth=False, mean_in=None):
+    """V -> (e4m3 bytes [B, H, D, Lpad] in plain key order, v_scale [B, H, D]).  fused.cu:332-445.
+    ``smooth=True`` is the sub_mean form and also returns the fp32 mean [B, H, D] (taken from ``mean_in``
+    when given, else from a float64 sum); key slots past L are zero."""
     v_bits = _bits(v_bits)
     B, L, H, D, sb, sl, sh = _dims_nhd(v_bits, layout)
     Lpad = (L + pad - 1) // pad * pad
     v8 = np.zeros((B, H, D, Lpad), np.uint8)
     vs = np.zeros((B, H, D), np.float32)
-    lib().oq_per_channel_fp8(_p(v_bits), int(is_fp16), B, L, H, D, sb, sl, sh, float(scale_max), _p(v8), Lpad,
-                             _p(vs))
-    return v8, vs
+    mean = np.zeros((B, H, D), np.float32)
+    mi = None if mean_in is None else np.ascontiguousarray(mean_in, dtype=np.float32)
+    lib().oq_per_channel_fp8_ex(_p(v_bits), int(is_fp16), B, L, H, D, sb, sl, sh, float(scale_max), int(smooth),
+                                _p(mi), _p(mean), _p(v8), Lpad, _p(vs))
+    return (v8, vs, mean) if smooth else (v8, vs)
 
 
 def qattn_fwd(q8, q_scale, k8, k_scale, v8=None, v_scale=None, vh_bits=None, *, blkq=128, blkk=64,
               qk_mult=1.0, pv_mode=0, causal=False, q_offset=0, kv_valid=None, is_fp16=False, heads=None,
               qrows_limit=0, want_lse=False, tiles_per_split=0, lazy_tau=-1.0, lsum_rounded=False, q_gran=1,
-              k_gran=1, tile_mask=None):
+              k_gran=1, tile_mask=None, v_mean=None, pv_f16_tile=False):
     """Quantized attention in the reference's tile order.  q8/k8 NHD int8; returns fp32 O NHD
     (and log2-domain LSE [B, Hq, Lq] when want_lse).  lazy_tau >= 0 / tiles_per_split > 0 restate the
     device kernel's lazy running-max rule / KV-split schedule and lsum_rounded its row sum over the
     rounded P (defaults: the reference's schedule).  q_gran / k_gran: scale granularity codes of the reference
     (1 per block, 2 per warp, 3 per thread) - see oq_qattn_fwd.  tile_mask: int8 [B, Hkv, ceil(Lq/128),
-    ceil(Lk/64)] block-sparse mask (0 = skip the key tile for that query block)."""
+    ceil(Lk/64)] block-sparse mask (0 = skip the key tile for that query block).  v_mean: fp32 [B, Hkv, D]
+    added to the output (smoothed V).  pv_f16_tile: each tile's P.V summed as two 32-key fp16 MMAs before it
+    joins the fp32 O (the reference's "fp32+fp16" accumulation)."""
     q8 = np.ascontiguousarray(q8)
     k8 = np.ascontiguousarray(k8)
     B, Lq, Hq, D = q8.shape
@@ -188,8 +196,9 @@ def qattn_fwd(q8, q_scale, k8, k_scale, v8=None, v_scale=None, vh_bits=None, *, 
                        _p(v_scale) if pv_mode == 0 else None, _p(vh_bits), int(is_fp16), Lk * Hkv * D, Hkv * D, D,
                        B, Lq, Lk, Hq, Hkv, D, float(qk_mult), int(pv_mode), int(causal), int(q_offset), _p(kvv), h0,
                        h1, int(qrows_limit), int(tiles_per_split), float(lazy_tau), int(lsum_rounded), int(q_gran),
-                       int(k_gran), _p(tm), tm_s1, tm_s2, _p(out),
-                       _p(lse))
+                       int(k_gran), _p(tm), tm_s1, tm_s2,
+                       _p(None if v_mean is None else np.ascontiguousarray(v_mean, dtype=np.float32)),
+                       int(bool(pv_f16_tile)), _p(out), _p(lse))
     return (out, lse) if want_lse else out
 
 

@@ -347,32 +347,62 @@ void oq_norm_rope(const uint16_t* x, int is_fp16, int64_t B, int64_t L, int64_t 
  * Output here is the plain transposed layout v8[b][h][d][l] with Lpad >= L columns (pad = 0x00);
  * the device kernel's in-tile key permutation is a storage detail undone by the tests.
  */
-void oq_per_channel_fp8(const uint16_t* in, int is_fp16, int64_t B, int64_t L, int64_t H, int64_t D, int64_t sb,
-                        int64_t sl, int64_t sh, float scale_max, uint8_t* v8, int64_t Lpad, float* v_scale) {
+/* Per-channel e4m3 quantization of V (MeanScaleKernel, fused.cu:332-445).  The reference reduces over the
+ * tokens padded with zeros up to a multiple of 16 (fp8_padded_num_tokens, :362-366).  smooth != 0 is the
+ * sub_mean form (:388-411,430-436): mean = sum / ceil16(L), amax = max(|max - mean|, |min - mean|),
+ * v8 = e4m3((x - mean) * recp); the mean comes from mean_in when given (its fp32 value depends on the
+ * reduction order, which the reference leaves to its block reduction), else from a float64 sum, and is
+ * written to mean_out.  Key slots past L are written as zero. */
+void oq_per_channel_fp8_ex(const uint16_t* in, int is_fp16, int64_t B, int64_t L, int64_t H, int64_t D, int64_t sb,
+                           int64_t sl, int64_t sh, float scale_max, int smooth, const float* mean_in, float* mean_out,
+                           uint8_t* v8, int64_t Lpad, float* v_scale) {
+  const int64_t l16 = (L + 15) / 16 * 16;
 #pragma omp parallel for collapse(3) schedule(static)
   for (int64_t b = 0; b < B; b++)
     for (int64_t h = 0; h < H; h++)
       for (int64_t d = 0; d < D; d++) {
         float mx = -1000000.0f, mn = 1000000.0f;
+        double sum = 0.0;
         for (int64_t l = 0; l < L; l++) {
           float x = load_h(in + b * sb + l * sl + h * sh + d, is_fp16);
           mx = fmaxf(mx, x);
           mn = fminf(mn, x);
+          sum += x;
         }
-        if (Lpad > L) { /* the reference reduces over zero padding up to a multiple of 16 */
+        if (l16 > L) {
           mx = fmaxf(mx, 0.f);
           mn = fminf(mn, 0.f);
         }
-        volatile float amax = fmaxf(fabsf(mx), fabsf(mn));
-        v_scale[(b * H + h) * D + d] = amax / scale_max;
+        const int64_t i = (b * H + h) * D + d;
+        volatile float mean = 0.f;
+        volatile float amax;
+        if (smooth) {
+          mean = mean_in ? mean_in[i] : (float)(sum / (double)l16);
+          if (mean_out) mean_out[i] = mean;
+          volatile float a1 = mx - mean, a2 = mn - mean;
+          amax = fmaxf(fabsf(a1), fabsf(a2));
+        } else {
+          amax = fmaxf(fabsf(mx), fabsf(mn));
+        }
+        v_scale[i] = amax / scale_max;
         volatile float recp = scale_max / amax;
-        uint8_t* row = v8 + ((b * H + h) * D + d) * Lpad;
+        uint8_t* row = v8 + i * Lpad;
         for (int64_t l = 0; l < Lpad; l++) {
-          float x = l < L ? load_h(in + b * sb + l * sl + h * sh + d, is_fp16) : 0.f;
+          if (l >= L) {
+            row[l] = 0;
+            continue;
+          }
+          volatile float x = load_h(in + b * sb + l * sl + h * sh + d, is_fp16);
+          if (smooth) x = x - mean;
           volatile float y = x * recp;
           row[l] = oq_f32_to_e4m3(y);
         }
       }
+}
+
+void oq_per_channel_fp8(const uint16_t* in, int is_fp16, int64_t B, int64_t L, int64_t H, int64_t D, int64_t sb,
+                        int64_t sl, int64_t sh, float scale_max, uint8_t* v8, int64_t Lpad, float* v_scale) {
+  oq_per_channel_fp8_ex(in, is_fp16, B, L, H, D, sb, sl, sh, scale_max, 0, NULL, NULL, v8, Lpad, v_scale);
 }
 
 /* ------------------------------------------------------------------------------------------ */
@@ -421,7 +451,7 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
                   int64_t Hkv, int64_t D, double qk_mult, int pv_mode, int causal, int64_t q_offset,
                   const int32_t* kv_valid, int64_t h_begin, int64_t h_end, int64_t qrows_limit, int64_t tiles_per_split,
                   double lazy_tau, int lsum_rounded, int q_gran, int k_gran, const int8_t* tile_mask, int64_t tm_s1,
-                  int64_t tm_s2, float* out, float* lse2) {
+                  int64_t tm_s2, const float* v_mean, int pv_f16_tile, float* out, float* lse2) {
   const int64_t RB = 128; /* query rows per work item */
   int64_t nQB = (Lq + blkq - 1) / blkq;
   int64_t nKB = (Lk + blkk - 1) / blkk;
@@ -505,6 +535,8 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
               for (int64_t d = 0; d < D; d++) orow[d] *= alpha;
               m[r] = m_new;
               has[r] = 1;
+              double part[2][128];
+              if (pv_f16_tile) memset(part, 0, sizeof(part));
               for (int64_t j = k0; j < k1; j++) {
                 double p = exp2(s[j - k0] - m_new);
                 double pr = pv_mode == 0 ? oq_e4m3_to_f32(oq_f32_to_e4m3((float)p))
@@ -512,7 +544,21 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
                                         : oq_bf16_to_f32(oq_f32_to_bf16((float)p));
                 dsum[r] += lsum_rounded ? pr : p;
                 const double* vr = vt + (j - k0) * D;
-                for (int64_t d = 0; d < D; d++) orow[d] += pr * vr[d];
+                if (pv_f16_tile) {
+                  double* pp = part[(j - k0) >= 32];
+                  for (int64_t d = 0; d < D; d++) pp[d] += pr * vr[d];
+                } else {
+                  for (int64_t d = 0; d < D; d++) orow[d] += pr * vr[d];
+                }
+              }
+              if (pv_f16_tile) {
+                /* the tile's P.V as two k = 32 MMAs with an fp16 accumulator (compute_fp8_sv_inst_buf_fp16_accu,
+                 * attn_utils.cuh:886-953): each MMA's sum rounded to fp16, then added to the fp32 O */
+                for (int64_t d = 0; d < D; d++) {
+                  const float a = oq_f16_to_f32(oq_f32_to_f16((float)part[0][d]));
+                  const float b2 = oq_f16_to_f32(oq_f32_to_f16((float)(a + part[1][d])));
+                  orow[d] += b2;
+                }
               }
             }
           }
@@ -533,6 +579,7 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
           for (int64_t d = 0; d < D; d++) {
             double v = hasacc[r] && dacc[r] > 0 ? oacc[r * D + d] / dacc[r] : 0.0;
             if (pv_mode == 0) v *= (double)v_scale[(b * Hkv + hk) * D + d];
+            if (pv_mode == 0 && v_mean) v += (double)v_mean[(b * Hkv + hk) * D + d];
             orow[d] = (float)v;
           }
           if (lse2) lse2[(b * Hq + h) * Lq + i] = hasacc[r] && dacc[r] > 0 ? (float)(log2(dacc[r]) + macc[r]) : -INFINITY;

@@ -102,6 +102,11 @@ def load() -> ctypes.CDLL:
     L.qattn_fwd_ex_num_splits.restype = i32
     L.qattn_fwd_ex_blocks_per_workgroup.argtypes = [i64, i64, i64, i64, i32, i32, i32]
     L.qattn_fwd_ex_blocks_per_workgroup.restype = i32
+    L.qattn_per_channel_fp8_ex.argtypes = [S, i32, i64, i64, i64, i64, f32, i32, vp, i64, vp, vp, vp, sz, vp]
+    L.qattn_per_channel_fp8_ex.restype = i32
+    L.qattn_fwd_ex2.argtypes = [S, vp, S, vp, vp, i32, i64, vp, vp, S, i32, i64, i64, i64, i64, i64, i64, f32, i32,
+                                i32, i64, vp, vp, i32, vp, sz, vp]
+    L.qattn_fwd_ex2.restype = i32
     L.qattn_fwd_noalloc_max_scratch.argtypes = []
     L.qattn_fwd_noalloc_max_scratch.restype = sz
     L.qattn_fwd_ex_noalloc.argtypes = [S, vp, S, vp, vp, i32, i64, vp, S, i32, i64, i64, i64, i64, i64, i64, f32, i32,

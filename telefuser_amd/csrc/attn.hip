@@ -74,6 +74,7 @@ struct AttnParams {
   const float* q_scale;  // [B, Hq, nQS]: per 128-row block, per 32-row warp block, or per thread class
   const float* k_scale;  // [B, Hkv, nKS]: per 64-key tile, or 4 lane-pair classes per tile
   const float* v_scale;  // [B, Hkv, D] (FP8 P.V only)
+  const float* v_mean;   // [B, Hkv, D] or null: added to the output (smoothed V, FP8 P.V only)
   void* o;
   int64_t osb, osl, osh;
   float* lse;  // [B, Hq, Lq] or null
@@ -181,6 +182,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   __shared__ __align__(16) uint8_t lds_qo[MQ ? 4 * 4096 : 16];
   __shared__ float lds_qs[MQ ? kMqMaxBlocks * 32 : 1];
   __shared__ __align__(16) float lds_vs[PV == PV_FP8 ? kD : 4];  // v_scale of this head (epilogue)
+  __shared__ __align__(16) float lds_vm[PV == PV_FP8 ? kD : 4];  // v_mean of this head (smoothed V)
   __shared__ int16_t lds_tid[SP ? kSpMaxTiles : 1];                  // block-sparse: ids of the active tiles
   __shared__ int lds_nact;
 
@@ -370,7 +372,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
     for (int64_t i = tid; i < (t_end - t_begin) * KS; i += kThreads) lds_ks[i] = ks_ptr[t_begin * KS + i];
   }
   if constexpr (PV == PV_FP8 && !SPLIT)
-    if (tid < kD) lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * kD + tid];
+    if (tid < kD) {
+      lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * kD + tid];
+      lds_vm[tid] = p.v_mean ? p.v_mean[(b * p.Hkv + hk) * kD + tid] : 0.f;
+    }
   if constexpr (MQ) {
     const float* qsp = p.q_scale + (b * p.Hq + h) * p.nQS + qb0 * qs_per;
     for (int64_t i = tid; i < (qb_end - qb0) * qs_per; i += kThreads) lds_qs[i] = qsp[i];
@@ -429,6 +434,11 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
           float f[4];
 #pragma unroll
           for (int e = 0; e < 4; e++) f[e] = o[dblk][g * 4 + e] * inv_l * sc[e];
+          if (PV == PV_FP8 && p.v_mean) {
+            const v4f vm = *reinterpret_cast<const v4f*>(&lds_vm[d]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) f[e] += vm[e];
+          }
           const v2u packed{pack_half2<IS_FP16_OUT>(f[0], f[1]), pack_half2<IS_FP16_OUT>(f[2], f[3])};
           const int c = db * 4 + g;  // 16-byte chunk of the staged 128-byte row (8 channels)
           *reinterpret_cast<v2u*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4) + hf * 8) = packed;
@@ -719,6 +729,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   auto buf_of = [](int t) { return (int)((unsigned)t % (unsigned)NB); };
   __shared__ float lds_ks[ks_lds_floats<PV_FP8>()];
   __shared__ __align__(16) float lds_vs[kD];
+  __shared__ __align__(16) float lds_vm[kD];
 
   const int64_t nQP = (p.nQB + 1) / 2;
   const int64_t tile_id = xcd_remap(blockIdx.x, gridDim.x);
@@ -824,7 +835,10 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
 
   __syncthreads();  // Q fragments are out of the LDS stage before the DMA reuses it
   for (int64_t i = tid; i < n_tiles * KS; i += kPPThreads) lds_ks[i] = ks_ptr[i];
-  if (tid < kD) lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * kD + tid];
+  if (tid < kD) {
+    lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * kD + tid];
+    lds_vm[tid] = p.v_mean ? p.v_mean[(b * p.Hkv + hk) * kD + tid] : 0.f;
+  }
   for (int t = 0; t < min(n_tiles, 2); t++) dma_tile(t);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -991,6 +1005,11 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
         float f[4];
 #pragma unroll
         for (int e = 0; e < 4; e++) f[e] = o[dblk][g * 4 + e] * inv_l * sc[e];
+        if (p.v_mean) {
+          const v4f vm = *reinterpret_cast<const v4f*>(&lds_vm[d]);
+#pragma unroll
+          for (int e = 0; e < 4; e++) f[e] += vm[e];
+        }
         const v2u packed{pack_half2<IS_FP16_OUT>(f[0], f[1]), pack_half2<IS_FP16_OUT>(f[2], f[3])};
         const int c = db * 4 + g;
         *reinterpret_cast<v2u*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4) + hf * 8) = packed;
@@ -1041,8 +1060,14 @@ __global__ __launch_bounds__(256) void qattn_combine_kernel(AttnParams p) {
   const float inv = L > 0.f ? 1.0f / L : 0.f;
   const float* vs = p.v_scale ? p.v_scale + (b * p.Hkv + hk) * kD + lane * 2 : nullptr;
   uint16_t* orow = static_cast<uint16_t*>(p.o) + b * p.osb + qrow * p.osl + h * p.osh + lane * 2;
-  orow[0] = f32_to_half<IS_FP16_OUT>(a0 * inv * (vs ? vs[0] : 1.f));
-  orow[1] = f32_to_half<IS_FP16_OUT>(a1 * inv * (vs ? vs[1] : 1.f));
+  float r0 = a0 * inv * (vs ? vs[0] : 1.f), r1 = a1 * inv * (vs ? vs[1] : 1.f);
+  if (p.v_mean) {
+    const float* vm = p.v_mean + (b * p.Hkv + hk) * kD + lane * 2;
+    r0 += vm[0];
+    r1 += vm[1];
+  }
+  orow[0] = f32_to_half<IS_FP16_OUT>(r0);
+  orow[1] = f32_to_half<IS_FP16_OUT>(r1);
   if (p.lse && lane == 0) p.lse[(b * p.Hq + h) * p.Lq + qrow] = L > 0.f ? __builtin_log2f(L) + M : -INFINITY;
 }
 
@@ -1280,6 +1305,18 @@ extern "C" int qattn_fwd_ex(qattn_seq q8, const float* q_scale, qattn_seq k8, co
                             int64_t Lq, int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult,
                             int qk_quant_gran, int causal, int64_t q_offset, const int32_t* kv_valid, float* lse,
                             int num_splits, void* workspace, size_t workspace_bytes, qattn_stream_t stream) {
+  return qattn_fwd_ex2(q8, q_scale, k8, k_scale, v, v_kind, Lpad, v_scale, nullptr, o, out_dtype, B, Lq, Lk, Hq, Hkv,
+                       D, qk_mult, qk_quant_gran, causal, q_offset, kv_valid, lse, num_splits, workspace,
+                       workspace_bytes, stream);
+}
+
+extern "C" int qattn_fwd_ex2(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const void* v,
+                             int v_kind, int64_t Lpad, const float* v_scale, const float* v_mean, qattn_seq o,
+                             int out_dtype, int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D,
+                             float qk_mult, int qk_quant_gran, int causal, int64_t q_offset, const int32_t* kv_valid,
+                             float* lse, int num_splits, void* workspace, size_t workspace_bytes,
+                             qattn_stream_t stream) {
+  QATTN_REQUIRE(!v_mean || v_kind == QATTN_V_FP8, QATTN_ERR_ARG, "v_mean needs the FP8 V path");
   QATTN_REQUIRE(v_kind == QATTN_V_FP8 || v_kind == QATTN_V_BF16 || v_kind == QATTN_V_FP16, QATTN_ERR_DTYPE,
                 "v_kind must be 0 (fp8), 1 (bf16) or 2 (fp16), got %d", v_kind);
   AttnParams p;
@@ -1293,6 +1330,7 @@ extern "C" int qattn_fwd_ex(qattn_seq q8, const float* q_scale, qattn_seq k8, co
   if (pv == PV_FP8) {
     QATTN_REQUIRE(v_scale, QATTN_ERR_ARG, "v_scale is null");
     p.v_scale = v_scale;
+    p.v_mean = v_mean;
     return launch_gran<PV_FP8>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D, kernel);
   }
   p.v_scale = nullptr;

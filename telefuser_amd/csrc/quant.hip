@@ -229,7 +229,8 @@ __global__ __launch_bounds__(quant_threads<VARIANT>()) void quant_per_block_kern
 
 constexpr int kColChunk = 256;  // sequence rows per workgroup
 
-template <bool IS_FP16, int MODE, int D>  // MODE 0: sum, 1: max |x|
+// MODE 0: sum; 1: max |x|; 2: sum, max and min (V smoothing), stored as three D-vectors per chunk
+template <bool IS_FP16, int MODE, int D>
 __global__ __launch_bounds__(256) void col_partial_kernel(NormRope nr, const uint16_t* in, int64_t sb, int64_t sl, int64_t sh,
                                                           int64_t L, int64_t H, int64_t nchunk, float* part) {
   constexpr int TPR = D / 8;
@@ -237,9 +238,13 @@ __global__ __launch_bounds__(256) void col_partial_kernel(NormRope nr, const uin
   __shared__ float red[RPP][D + 1];
   const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, r0 = tid / TPR, dc = tid % TPR;
-  float acc[8];
+  float acc[8], amx[8], amn[8];
 #pragma unroll
-  for (int e = 0; e < 8; e++) acc[e] = 0.f;
+  for (int e = 0; e < 8; e++) {
+    acc[e] = 0.f;
+    amx[e] = -INFINITY;
+    amn[e] = INFINITY;
+  }
   // rows r0, r0 + RPP, ... of the chunk, loaded four at a time (four loads in flight per thread) and
   // accumulated in row order
   constexpr int kU = 4;
@@ -261,47 +266,60 @@ __global__ __launch_bounds__(256) void col_partial_kernel(NormRope nr, const uin
 #pragma unroll
         for (int e = 0; e < 8; e++) {
           float v = half_to_f32<IS_FP16>(hv[e]);
-          if constexpr (MODE == 0) acc[e] += v;
-          else acc[e] = fmaxf(acc[e], fabsf(v));
+          if constexpr (MODE == 1) {
+            acc[e] = fmaxf(acc[e], fabsf(v));
+          } else {
+            acc[e] += v;
+            if constexpr (MODE == 2) {
+              amx[e] = fmaxf(amx[e], v);
+              amn[e] = fminf(amn[e], v);
+            }
+          }
         }
       }
     }
   }
+  constexpr int NV = MODE == 2 ? 3 : 1;
 #pragma unroll
-  for (int e = 0; e < 8; e++) red[r0][dc * 8 + e] = acc[e];
-  __syncthreads();
-  if (tid < D) {
-    float s = red[0][tid];
-    for (int r = 1; r < RPP; r++) s = MODE == 0 ? s + red[r][tid] : fmaxf(s, red[r][tid]);
-    part[((b * H + h) * nchunk + c) * D + tid] = s;
+  for (int k = 0; k < NV; k++) {
+    if (k) __syncthreads();
+#pragma unroll
+    for (int e = 0; e < 8; e++) red[r0][dc * 8 + e] = k == 0 ? acc[e] : k == 1 ? amx[e] : amn[e];
+    __syncthreads();
+    if (tid < D) {
+      float s = red[0][tid];
+      for (int r = 1; r < RPP; r++) {
+        const float x = red[r][tid];
+        s = (MODE == 1 || k == 1) ? fmaxf(s, x) : k == 2 ? fminf(s, x) : s + x;
+      }
+      part[(((b * H + h) * nchunk + c) * NV + k) * D + tid] = s;
+    }
   }
 }
 
 // Chunk partials -> one value per (b, h, d).  One workgroup per (b, h), one thread per channel; the
 // loop over chunks keeps 4 independent loads in flight (it is latency-bound, not bandwidth-bound).
-template <int MODE, int D>
-__device__ __forceinline__ float reduce_chunks(const float* part, int64_t bh, int64_t nchunk, int d) {
-  float a[4] = {0.f, 0.f, 0.f, 0.f};
+// MODE 0: sum, 1: max, 2: min.  Chunk c's vector is at part + ((bh * nchunk + c) * NV + k) * D.
+template <int MODE, int D, int NV = 1>
+__device__ __forceinline__ float reduce_chunks(const float* part, int64_t bh, int64_t nchunk, int d, int k = 0) {
+  const float init = MODE == 0 ? 0.f : MODE == 1 ? -INFINITY : INFINITY;
+  float a[4] = {init, init, init, init};
+  auto op = [](float x, float y) { return MODE == 0 ? x + y : MODE == 1 ? fmaxf(x, y) : fminf(x, y); };
+  auto at = [&](int64_t c) { return part[((bh * nchunk + c) * NV + k) * D + d]; };
   int64_t c = 0;
   // 32 chunks per step: all loads first, then the same accumulation order as one chunk at a time
   for (; c + 32 <= nchunk; c += 32) {
     float x[32];
 #pragma unroll
-    for (int u = 0; u < 32; u++) x[u] = part[(bh * nchunk + c + u) * D + d];
+    for (int u = 0; u < 32; u++) x[u] = at(c + u);
 #pragma unroll
-    for (int u = 0; u < 32; u++) a[u & 3] = MODE == 0 ? a[u & 3] + x[u] : fmaxf(a[u & 3], x[u]);
+    for (int u = 0; u < 32; u++) a[u & 3] = op(a[u & 3], x[u]);
   }
   for (; c + 4 <= nchunk; c += 4)
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const float x = part[(bh * nchunk + c + u) * D + d];
-      a[u] = MODE == 0 ? a[u] + x : fmaxf(a[u], x);
-    }
-  for (; c < nchunk; c++) {
-    const float x = part[(bh * nchunk + c) * D + d];
-    a[0] = MODE == 0 ? a[0] + x : fmaxf(a[0], x);
-  }
-  return MODE == 0 ? (a[0] + a[1]) + (a[2] + a[3]) : fmaxf(fmaxf(a[0], a[1]), fmaxf(a[2], a[3]));
+    for (int u = 0; u < 4; u++) a[u] = op(a[u], at(c + u));
+  for (; c < nchunk; c++) a[0] = op(a[0], at(c));
+  return op(op(a[0], a[1]), op(a[2], a[3]));
 }
 
 template <bool IS_FP16, int D>
@@ -309,6 +327,28 @@ __global__ void mean_finalize_kernel(const float* part, int64_t nchunk, int64_t 
   const int64_t bh = blockIdx.x;
   const int d = threadIdx.x;
   mean[bh * D + d] = f32_to_half<IS_FP16>(reduce_chunks<0, D>(part, bh, nchunk, d) / (float)L);
+}
+
+// V smoothing (MeanScaleKernel<sub_mean>, fused.cu:362-416): the mean divides the sum by the token count
+// rounded up to 16 and the max / min cover those zero pad tokens too; amax = max(|max - mean|, |min - mean|).
+template <int D>
+__global__ void vsmooth_finalize_kernel(const float* part, int64_t nchunk, int64_t L, float scale_max, float* v_scale,
+                                        float* recp, float* v_mean) {
+  const int64_t bh = blockIdx.x;
+  const int d = threadIdx.x;
+  const float sum = reduce_chunks<0, D, 3>(part, bh, nchunk, d, 0);
+  float mx = reduce_chunks<1, D, 3>(part, bh, nchunk, d, 1);
+  float mn = reduce_chunks<2, D, 3>(part, bh, nchunk, d, 2);
+  const int64_t l16 = (L + 15) / 16 * 16;
+  if (l16 != L) {
+    mx = fmaxf(mx, 0.f);
+    mn = fminf(mn, 0.f);
+  }
+  const float mean = sum / (float)l16;
+  const float a = fmaxf(fabsf(mx - mean), fabsf(mn - mean));
+  v_mean[bh * D + d] = mean;
+  v_scale[bh * D + d] = a / scale_max;
+  recp[bh * D + d] = scale_max / a;
 }
 
 template <int D>
@@ -367,7 +407,7 @@ struct VTileFilter {
 template <bool IS_FP16, int D>
 __global__ __launch_bounds__(256) void v_fp8_kernel(const uint16_t* in, int64_t sb, int64_t sl, int64_t sh,
                                                     int64_t L, int64_t H, const float* recp, uint8_t* v8,
-                                                    int64_t Lpad, VTileFilter filt) {
+                                                    int64_t Lpad, VTileFilter filt, const float* vmean = nullptr) {
   constexpr int TPR = D / 8;
   // The tile as 4-byte words: word w of channel d holds the tile-permuted key slots 4w .. 4w + 3.  Its
   // 16-byte chunks (4 words) are XOR-swizzled by the channel group (d / 8) & 3, so that the word stores
@@ -382,6 +422,7 @@ __global__ __launch_bounds__(256) void v_fp8_kernel(const uint16_t* in, int64_t 
     if (!hit) return;  // uniform over the workgroup
   }
   const float* rc = recp + (b * H + h) * D;
+  const float* mn = vmean ? vmean + (b * H + h) * D : nullptr;
   // thread: key quad q (keys 4q .. 4q + 3 of the tile, which occupy consecutive slots) x 8 channels
   for (int c = tid; c < 16 * TPR; c += 256) {
     const int q = c / TPR, dc = c % TPR;
@@ -399,9 +440,16 @@ __global__ __launch_bounds__(256) void v_fp8_kernel(const uint16_t* in, int64_t 
     for (int e = 0; e < 8; e++) {
       const int d = dc * 8 + e;
       const float s = rc[d];
+      const float m = mn ? mn[d] : 0.f;
       uint32_t word = 0;
 #pragma unroll
-      for (int r = 0; r < 4; r++) word |= (uint32_t)f32_to_e4m3_sat(half_to_f32<IS_FP16>(hv[r][e]) * s) << (8 * r);
+      for (int r = 0; r < 4; r++) {
+        // x * recp or (x - mean) * recp as MeanScaleKernel computes it; key slots past L are zero (they
+        // are masked, and a zero byte keeps P.V finite there even for an all-zero channel's recp = inf)
+        const float x = half_to_f32<IS_FP16>(hv[r][e]);
+        const float y = t * 64 + 4 * q + r < L ? (mn ? (x - m) * s : x * s) : 0.f;
+        word |= (uint32_t)f32_to_e4m3_sat(y) << (8 * r);
+      }
       tile[d][wi ^ sw] = word;
     }
   }
@@ -685,13 +733,23 @@ extern "C" int qattn_seq_mean(qattn_seq in, int dtype, int64_t B, int64_t L, int
 }
 
 extern "C" size_t qattn_per_channel_fp8_workspace_size(int64_t B, int64_t L, int64_t H, int64_t D) {
-  return (size_t)(B * H * col_chunks(L) * D + B * H * D) * sizeof(float);
+  // (three partial vectors per chunk: enough for the smoothed form too)
+  return (size_t)(3 * B * H * col_chunks(L) * D + B * H * D) * sizeof(float);
 }
 
 extern "C" int qattn_per_channel_fp8(qattn_seq v, int dtype, int64_t B, int64_t L, int64_t H, int64_t D,
                                      float scale_max, uint8_t* v8, int64_t Lpad, float* v_scale, void* workspace,
                                      size_t workspace_bytes, qattn_stream_t stream) {
+  return qattn_per_channel_fp8_ex(v, dtype, B, L, H, D, scale_max, 0, v8, Lpad, v_scale, nullptr, workspace,
+                                  workspace_bytes, stream);
+}
+
+extern "C" int qattn_per_channel_fp8_ex(qattn_seq v, int dtype, int64_t B, int64_t L, int64_t H, int64_t D,
+                                        float scale_max, int smooth_v, uint8_t* v8, int64_t Lpad, float* v_scale,
+                                        float* v_mean, void* workspace, size_t workspace_bytes,
+                                        qattn_stream_t stream) {
   int rc;
+  QATTN_REQUIRE(!smooth_v || v_mean, QATTN_ERR_ARG, "smooth_v needs a v_mean output");
   if ((rc = check_common(dtype, D, QATTN_QUANT_CUDA, 64))) return rc;
   QATTN_REQUIRE(B > 0 && L > 0 && H > 0, QATTN_ERR_SHAPE, "per_channel_fp8 needs non-empty input");
   if ((rc = check_seq("v", v, 2))) return rc;
@@ -703,19 +761,26 @@ extern "C" int qattn_per_channel_fp8(qattn_seq v, int dtype, int64_t B, int64_t 
   hipStream_t st = (hipStream_t)stream;
   const int64_t nchunk = col_chunks(L);
   float* part = static_cast<float*>(workspace);
-  float* recp = part + B * H * nchunk * D;
-  launch_col<1>(v, dtype, B, L, H, D, nchunk, part, st);
-  if (D == 128) vscale_finalize_kernel<128><<<B * H, 128, 0, st>>>(part, nchunk, scale_max, v_scale, recp);
-  else vscale_finalize_kernel<64><<<B * H, 64, 0, st>>>(part, nchunk, scale_max, v_scale, recp);
+  float* recp = part + 3 * B * H * nchunk * D;
+  const float* mean = smooth_v ? v_mean : nullptr;
+  if (smooth_v) {
+    launch_col<2>(v, dtype, B, L, H, D, nchunk, part, st);
+    if (D == 128) vsmooth_finalize_kernel<128><<<B * H, 128, 0, st>>>(part, nchunk, L, scale_max, v_scale, recp, v_mean);
+    else vsmooth_finalize_kernel<64><<<B * H, 64, 0, st>>>(part, nchunk, L, scale_max, v_scale, recp, v_mean);
+  } else {
+    launch_col<1>(v, dtype, B, L, H, D, nchunk, part, st);
+    if (D == 128) vscale_finalize_kernel<128><<<B * H, 128, 0, st>>>(part, nchunk, scale_max, v_scale, recp);
+    else vscale_finalize_kernel<64><<<B * H, 64, 0, st>>>(part, nchunk, scale_max, v_scale, recp);
+  }
   dim3 grid((unsigned)(Lpad / 64), (unsigned)H, (unsigned)B);
   const uint16_t* p = static_cast<const uint16_t*>(v.data);
   const VTileFilter nof{nullptr, {0, 0, 0, 0}};
   if (dtype == QATTN_BF16) {
-    if (D == 128) v_fp8_kernel<false, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof);
-    else v_fp8_kernel<false, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof);
+    if (D == 128) v_fp8_kernel<false, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof, mean);
+    else v_fp8_kernel<false, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof, mean);
   } else {
-    if (D == 128) v_fp8_kernel<true, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof);
-    else v_fp8_kernel<true, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof);
+    if (D == 128) v_fp8_kernel<true, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof, mean);
+    else v_fp8_kernel<true, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof, mean);
   }
   return check_launch("per_channel_fp8");
 }

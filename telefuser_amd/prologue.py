@@ -88,7 +88,7 @@ def wan_self_attention(xq: torch.Tensor, xk: torch.Tensor, xv: torch.Tensor, wq:
     b, l, n = xq.shape
     d = n // num_heads
     q8, qs, k8, ks, _ = norm_rope_quant_qk(xq, xk, wq, wk, freqs_cos, freqs_sin, num_heads, eps)
-    v8, vs, _ = sa.per_channel_fp8(xv.reshape(b, l, num_heads, d), tensor_layout="NHD")
+    v8, vs, _ = sa.per_channel_fp8(xv.reshape(b, l, num_heads, d), tensor_layout="NHD", smooth_v=False)
     o = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout="NHD", out_dtype=xq.dtype, kv_valid_len=kv_valid_len)
     return o.reshape(b, l, n)
 

@@ -148,21 +148,24 @@ def quant_per_block_int8(x: torch.Tensor, block_size: int, sm_scale: Optional[fl
 
 
 def per_channel_fp8(v: torch.Tensor, tensor_layout: str = "HND", scale_max: float = 448.0, smooth_v: bool = True):
-    """V -> (v_fp8 [B, H, D, Lpad] float8_e4m3fn in tile layout, v_scale [B, H, D] fp32, None).
+    """V -> (v_fp8 [B, H, D, Lpad] float8_e4m3fn in tile layout, v_scale [B, H, D] fp32, vm).
 
     Same quantization as tf_kernel.sageattn2.per_channel_fp8 (sageattn2.py:320-407, MeanScaleKernel
-    fused.cu:332-445).  V smoothing (``smooth_v``) is only meaningful for fp16 accumulation and is
-    not applied (the third return value is always None)."""
+    fused.cu:332-445), including the default ``smooth_v=True``: V minus its per-channel mean (sum over
+    the tokens / tokens rounded up to 16) is quantized and ``vm`` [B, H, D] fp32 is returned (None when
+    ``smooth_v`` is False).  The attention adds ``vm`` back (qattn_fwd(..., v_mean=vm))."""
     L = _lib.load()
     b, l, h, d = _dims(v, tensor_layout)
     lpad = (l + 63) // 64 * 64
     v_fp8 = torch.empty((b, h, d, lpad), dtype=torch.float8_e4m3fn, device=v.device)
     v_scale = torch.empty((b, h, d), dtype=torch.float32, device=v.device)
+    vm = torch.empty((b, h, d), dtype=torch.float32, device=v.device) if smooth_v else None
     ws = torch.empty(L.qattn_per_channel_fp8_workspace_size(b, l, h, d), dtype=torch.uint8, device=v.device)
-    _lib.check(L.qattn_per_channel_fp8(_lib.seq(v, tensor_layout), _lib.dtype_code(v.dtype), b, l, h, d,
-                                       float(scale_max), _lib.ptr(v_fp8), lpad, _lib.ptr(v_scale), _lib.ptr(ws),
-                                       ws.numel(), _lib.stream_of(v)))
-    return v_fp8, v_scale, None
+    _lib.check(L.qattn_per_channel_fp8_ex(_lib.seq(v, tensor_layout), _lib.dtype_code(v.dtype), b, l, h, d,
+                                          float(scale_max), int(bool(smooth_v)), _lib.ptr(v_fp8), lpad,
+                                          _lib.ptr(v_scale), _lib.ptr(vm), _lib.ptr(ws), ws.numel(),
+                                          _lib.stream_of(v)))
+    return v_fp8, v_scale, vm
 
 
 def v_tile_half(v: torch.Tensor, tensor_layout: str = "HND") -> torch.Tensor:
@@ -226,7 +229,7 @@ def _check_attn_operands(q_int8, q_scale, k_int8, k_scale, v, v_scale, b, lq, lk
 
 def qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout="HND", out_dtype=torch.bfloat16,
               qk_mult=1.0, is_causal=False, q_offset=0, kv_valid_len=None, return_lse=False, num_splits=0,
-              qk_quant_gran="per_block", out: Optional[torch.Tensor] = None):
+              qk_quant_gran="per_block", out: Optional[torch.Tensor] = None, v_mean: Optional[torch.Tensor] = None):
     """Attention on already-quantized operands (the torch.ops.tf_kernel.qk_int8_sv_f8_accum_f32_fuse_v_scale
     _attn op, common_extension.cc:239-258).  With v_scale=None, v_fp8 is the half-dtype V tile from
     ``v_tile_half`` and P.V runs in that dtype (qk_int8_sv_f16_accum_f32_attn, common_extension.cc:214-218).
@@ -242,6 +245,9 @@ def qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout
     gran = _GRAN[qk_quant_gran]
     _check_attn_operands(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, b, lq, lk, hq, hkv, d, qk_quant_gran, out,
                          out_dtype)
+    if v_mean is not None and (v_scale is None or v_mean.dtype != torch.float32 or
+                               tuple(v_mean.shape) != (b, hkv, d) or not v_mean.is_contiguous()):
+        raise ValueError(f"v_mean must be a contiguous float32 tensor of shape {(b, hkv, d)} (FP8 V only)")
     o = out if out is not None else torch.empty(q_int8.shape, dtype=out_dtype, device=q_int8.device)
     if v_scale is None:  # v_fp8 is then the half-dtype tile layout from v_tile_half
         v_kind = _lib.QATTN_V_BF16 if v_fp8.dtype == torch.bfloat16 else _lib.QATTN_V_FP16
@@ -252,9 +258,9 @@ def qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout
     ns = num_splits if num_splits > 0 else L.qattn_fwd_ex_num_splits(b, lq, lk, hq, v_kind, gran)
     wsb = L.qattn_fwd_workspace_size(b, lq, hq, d, ns)
     ws = torch.empty(wsb, dtype=torch.uint8, device=q_int8.device) if wsb else None
-    _lib.check(L.qattn_fwd_ex(
+    _lib.check(L.qattn_fwd_ex2(
         _lib.seq(q_int8, tensor_layout), _lib.ptr(q_scale), _lib.seq(k_int8, tensor_layout), _lib.ptr(k_scale),
-        _lib.ptr(v_fp8), v_kind, v_fp8.shape[-1], _lib.ptr(v_scale), _lib.seq(o, tensor_layout),
+        _lib.ptr(v_fp8), v_kind, v_fp8.shape[-1], _lib.ptr(v_scale), _lib.ptr(v_mean), _lib.seq(o, tensor_layout),
         _lib.dtype_code(o.dtype), b, lq, lk, hq, hkv, d, float(qk_mult), gran, int(bool(is_causal)), int(q_offset),
         _lib.ptr(kvv), _lib.ptr(lse), ns, _lib.ptr(ws), wsb, _lib.stream_of(q_int8)))
     return (o, lse) if return_lse else o
@@ -302,15 +308,24 @@ def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv
         quant = per_thread_int8 if qk_quant_gran == "per_thread" else per_warp_int8
         q_int8, q_scale, k_int8, k_scale = quant(q, k, km, tensor_layout=tensor_layout)
         qk_mult = sm_scale * LOG2E
-    if smooth_v:
-        warnings.warn(f"pv_accum_dtype is '{pv_accum_dtype}', smooth_v will be ignored.")
+    vm = None
     if pv == "fp8":
-        v_fp8, v_scale, _ = per_channel_fp8(v, tensor_layout=tensor_layout, scale_max=448.0)
+        # sageattn2.py:1368-1383: smooth_v only with "fp32" accumulation; "fp32+fp16" quantizes V to
+        # |v8| <= 2.25 so that its fp16 tile partials cannot overflow (here P.V accumulates in fp32)
+        if pv_accum_dtype not in ("fp32", "fp32+fp32", "fp32+fp16"):
+            raise ValueError(f"pv_accum_dtype must be 'fp32', 'fp32+fp32' or 'fp32+fp16', got {pv_accum_dtype!r}")
+        if pv_accum_dtype != "fp32" and smooth_v:
+            warnings.warn(f"pv_accum_dtype is '{pv_accum_dtype}', smooth_v will be ignored.")
+            smooth_v = False
+        scale_max = 2.25 if pv_accum_dtype == "fp32+fp16" else 448.0
+        v_fp8, v_scale, vm = per_channel_fp8(v, tensor_layout=tensor_layout, scale_max=scale_max, smooth_v=smooth_v)
     else:
+        if smooth_v:
+            warnings.warn(f"pv_accum_dtype is '{pv_accum_dtype}', smooth_v will be ignored.")
         v_fp8, v_scale = v_tile_half(v, tensor_layout), None
     res = qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, tensor_layout=tensor_layout, out_dtype=dtype,
                     qk_mult=qk_mult, is_causal=is_causal, q_offset=q_offset, kv_valid_len=kv_valid_len,
-                    return_lse=return_lse, qk_quant_gran=qk_quant_gran)
+                    return_lse=return_lse, qk_quant_gran=qk_quant_gran, v_mean=vm)
     o, lse = res if return_lse else (res, None)
     o = o[..., :head_dim_og]
     if not return_lse:

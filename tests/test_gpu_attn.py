@@ -48,7 +48,7 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
         q8, qs, k8, ks = quant(qd, kd, km, tensor_layout=layout)
         qk_mult = D ** -0.5 * sa.LOG2E
     if pv == "fp8":
-        v8, vs, _ = sa.per_channel_fp8(vd, tensor_layout=layout)
+        v8, vs, _ = sa.per_channel_fp8(vd, tensor_layout=layout, smooth_v=False)
     else:
         v8, vs = sa.v_tile_half(vd, tensor_layout=layout), None
     o, lse = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout=layout, out_dtype=q.dtype, is_causal=causal,
@@ -405,7 +405,7 @@ def test_multi_block_workgroups(oracle, case):
     else:
         q8, qs, k8, ks = sa.per_thread_int8(q, k, km, tensor_layout=layout)
         qk_mult = D ** -0.5 * LOG2E
-    v8, vs, _ = sa.per_channel_fp8(v, tensor_layout=layout)
+    v8, vs, _ = sa.per_channel_fp8(v, tensor_layout=layout, smooth_v=False)
     kw = dict(tensor_layout=layout, out_dtype=dt, kv_valid_len=kv_valid, return_lse=True, qk_mult=qk_mult,
               qk_quant_gran=gran)
     o, lse = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
@@ -477,7 +477,7 @@ def test_pingpong_kernel_matches(oracle, case):
         quant = sa.per_thread_int8 if gran == "per_thread" else sa.per_warp_int8
         q8, qs, k8, ks = quant(qd, kd, km, tensor_layout=layout)
         qk_mult = 128 ** -0.5 * LOG2E
-    v8, vs, _ = sa.per_channel_fp8(vd, tensor_layout=layout)
+    v8, vs, _ = sa.per_channel_fp8(vd, tensor_layout=layout, smooth_v=False)
     out_dtype = torch.float16 if case == "fp16_warp_gqa" else torch.bfloat16
     kw = dict(tensor_layout=layout, out_dtype=out_dtype, is_causal=causal, kv_valid_len=kv_valid,
               return_lse=True, qk_mult=qk_mult, qk_quant_gran=gran, num_splits=1)
@@ -526,7 +526,7 @@ def test_full_size_configs(oracle, name):
     sm = cfg.D ** -0.5
     km = sa.k_mean(k, "NHD")
     q8, qs, k8, ks = sa.per_block_int8(q, k, km, sm_scale=sm, tensor_layout="NHD")
-    v8, vs, _ = sa.per_channel_fp8(v, tensor_layout="NHD")
+    v8, vs, _ = sa.per_channel_fp8(v, tensor_layout="NHD", smooth_v=False)
     o = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout="NHD", out_dtype=q.dtype, kv_valid_len=kvv)
     torch.cuda.synchronize()
     assert bool(torch.isfinite(o.float()).all())
@@ -562,3 +562,50 @@ def test_full_size_configs(oracle, name):
         log(f"  head {h}: cos_truth={ct:.6f} cos_oracle={ck:.6f} max_abs_truth={float(np.abs(og - truth).max()):.4g}")
         assert ct >= COS_E2E
         assert ck >= COS_KERNEL
+
+
+@pytest.mark.parametrize("mode", ["fp32_smooth_v", "fp32+fp16", "fp32+fp32_smooth_ignored"])
+def test_pv_accum_modes_and_smooth_v(oracle, mode):
+    """sageattn_qk_int8_pv_fp8_cuda's pv_accum_dtype / smooth_v semantics (sageattn2.py:1368-1445):
+    "fp32" with smooth_v quantizes V - mean and adds the mean back in the epilogue (fuse_v_mean kernel);
+    "fp32+fp16" quantizes V with scale_max 2.25 (the reference then sums each tile's P.V in fp16 - this
+    kernel sums it in fp32); with "fp32+fp32" smooth_v is ignored with a warning.  Each is checked
+    against the oracle on the same quantized operands (the fp16 tile partials restated for "fp32+fp16")
+    and against float64 truth."""
+    import warnings
+
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    B, Lq, Lk, H = 1, 700, 900, 2
+    q, k, v = qkv(B, Lq, Lk, H, H, seed=91, k_offset_std=0.5)
+    v = (v.float() + 1.5).to(torch.bfloat16)  # a channel offset that smoothing removes
+    qd, kd, vd = (t.to(dev) for t in (q, k, v))
+    pv, smooth = {"fp32_smooth_v": ("fp32", True), "fp32+fp16": ("fp32+fp16", False),
+                  "fp32+fp32_smooth_ignored": ("fp32+fp32", True)}[mode]
+    log(f"pv_accum {mode}: B={B} Lq={Lq} Lk={Lk} H={H}")
+    with warnings.catch_warnings(record=True) as wlist:
+        warnings.simplefilter("always")
+        o = sa.sageattn_qk_int8_pv_fp8_cuda(qd, kd, vd, tensor_layout="NHD", qk_quant_gran="per_thread",
+                                            pv_accum_dtype=pv, smooth_v=smooth)
+    torch.cuda.synchronize()
+    assert any("smooth_v will be ignored" in str(w.message) for w in wlist) == (mode == "fp32+fp32_smooth_ignored")
+    og = o.float().cpu().numpy()
+    # the same operands, quantized on the GPU by the module's own quantizers
+    km = sa.k_mean(kd, "NHD")
+    q8, qs, k8, ks = sa.per_thread_int8(qd, kd, km, tensor_layout="NHD")
+    use_smooth = mode == "fp32_smooth_v"
+    v8, vs, vm = sa.per_channel_fp8(vd, tensor_layout="NHD", scale_max=2.25 if pv == "fp32+fp16" else 448.0,
+                                    smooth_v=use_smooth)
+    args = (q8.cpu().numpy(), qs.cpu().numpy(), k8.cpu().numpy(), ks.cpu().numpy())
+    kw = dict(v8=untile_v(v8), v_scale=vs.cpu().numpy(), qk_mult=128 ** -0.5 * LOG2E, q_gran=3, k_gran=3,
+              v_mean=None if vm is None else vm.cpu().numpy())
+    ref_k = oracle.qattn_fwd(*args, **kw, lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED)
+    ref_r = oracle.qattn_fwd(*args, **kw, pv_f16_tile=pv == "fp32+fp16")
+    truth = oracle.attn_fp64(bf16_bits(q), bf16_bits(k), bf16_bits(v), 128 ** -0.5)
+    ck, cr, ct = cosine(og, ref_k), cosine(og, ref_r), cosine(og, truth)
+    log(f"  cos kernel-schedule oracle={ck:.6f} reference math={cr:.6f} truth={ct:.6f} "
+        f"max_abs_truth={float(np.abs(og - truth).max()):.4g}")
+    assert ck >= COS_KERNEL
+    assert cr >= COS_E2E
+    assert ct >= COS_E2E

@@ -61,7 +61,7 @@ def test_fused_wan_self_attention_matches_unfused(oracle):
     kn = to_t(oracle.norm_rope(bf16_bits(xk), bf16_bits(wk), cs, sn, D))
     vn = xv.reshape(B, L, H, D)
     o2 = sa.sageattn_qk_int8_pv_fp8_cuda(qn.to(dev), kn.to(dev), vn.to(dev), tensor_layout="NHD",
-                                         qk_quant_gran="per_block")
+                                         qk_quant_gran="per_block", pv_accum_dtype="fp32+fp32")
     torch.cuda.synchronize()
     truth = oracle.attn_fp64(bf16_bits(qn), bf16_bits(kn), bf16_bits(vn), D ** -0.5)
     a, b = o.float().cpu().numpy().reshape(B, L, H, D), o2.float().cpu().numpy()

@@ -135,8 +135,35 @@ def test_v_fp8_bit_exact(oracle, B, L, H, layout, dtype):
     _, _, v = qkv(B, 8, L, H, H, seed=77, dtype=dtype)
     if layout == "HND":
         v = v.transpose(1, 2).contiguous()
-    v8, vs, _ = sa.per_channel_fp8(v.to(dev), tensor_layout=layout)
+    v8, vs, _ = sa.per_channel_fp8(v.to(dev), tensor_layout=layout, smooth_v=False)
     torch.cuda.synchronize()
     ov8, ovs = oracle.per_channel_fp8(_as_bits(v), layout=layout, is_fp16=dtype == torch.float16)
+    assert np.array_equal(vs.cpu().numpy(), ovs)
+    assert np.array_equal(untile_v(v8), ov8)
+
+
+@pytest.mark.parametrize("B,L,H,layout,dtype,scale_max", [(1, 1024, 2, "NHD", torch.bfloat16, 448.0),
+                                                          (2, 777, 3, "NHD", torch.bfloat16, 2.25),
+                                                          (1, 300, 2, "HND", torch.float16, 448.0)])
+def test_v_fp8_smooth_bit_exact(oracle, B, L, H, layout, dtype, scale_max):
+    """per_channel_fp8(smooth_v=True), the sub_mean form of MeanScaleKernel: the mean [B, H, D] is within
+    fp32 reduction-order noise of the float64 mean; given that mean, v_scale and the e4m3 bytes are
+    bit-exact (key slots past L zero)."""
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    log(f"v_fp8 smooth B={B} L={L} H={H} {layout} {dtype} scale_max={scale_max}")
+    _, _, v = qkv(B, 8, L, H, H, seed=78, dtype=dtype)
+    v = v + 0.75  # a per-channel offset for the mean to remove
+    if layout == "HND":
+        v = v.transpose(1, 2).contiguous()
+    v = v.to(dtype)
+    v8, vs, vm = sa.per_channel_fp8(v.to(dev), tensor_layout=layout, scale_max=scale_max, smooth_v=True)
+    torch.cuda.synchronize()
+    gvm = vm.cpu().numpy()
+    _, _, fm = oracle.per_channel_fp8(_as_bits(v), layout=layout, is_fp16=dtype == torch.float16, smooth=True)
+    assert np.all(np.abs(gvm - fm) <= 1e-6 * np.maximum(1.0, np.abs(fm)))
+    ov8, ovs, _ = oracle.per_channel_fp8(_as_bits(v), layout=layout, is_fp16=dtype == torch.float16, smooth=True,
+                                         scale_max=scale_max, mean_in=gvm)
     assert np.array_equal(vs.cpu().numpy(), ovs)
     assert np.array_equal(untile_v(v8), ov8)

@@ -213,9 +213,54 @@ def test_v_fp8_known_answers(oracle):
     assert vs[0, 0, 0] == np.float32(2.0) / np.float32(448)
     assert v8[0, 0, 0, 3] == 0x7E and v8[0, 0, 0, 0] == oracle.lib().oq_f32_to_e4m3(224.0)
     assert v8[0, 0, 1, 0] == 0xFE  # -0.5 is the channel's amax -> -448
-    assert np.all(v8[0, 0, :3, 70:] == 0)  # padding of live channels (dead channels are NaN codes)
-    assert np.all(v8[0, 0, 5] == 0x7F)
+    assert np.all(v8[0, 0, :, 70:] == 0)  # key slots past L are zero in every channel
+    assert np.all(v8[0, 0, 5, :70] == 0x7F)
     assert vs[0, 0, 5] == 0.0  # all-zero channel: scale 0, recp = inf, codes NaN (as the reference)
+
+
+def test_v_fp8_smooth_known_answers(oracle):
+    """sub_mean form of MeanScaleKernel (fused.cu:362-445): mean over the tokens padded with zeros to a
+    multiple of 16, amax from max / min about that mean (pad zeros included), v8 = e4m3((v - mean) * recp)."""
+    v = np.zeros((70, 128), np.float32)
+    v[:, 0] = 2.0             # constant channel, 70 tokens (pad to 80): mean = 1.75, amax = |0 - 1.75|
+    v[:, 1] = np.linspace(-3, 1, 70)
+    v8, vs, mean = oracle.per_channel_fp8(_bits(v, (1, 70, 1, 128)), smooth=True)
+    assert mean[0, 0, 0] == np.float32(2.0 * 70 / 80)
+    assert vs[0, 0, 0] == np.float32(1.75) / np.float32(448)
+    # (2 - 1.75) * 448 / 1.75 = 64 exactly
+    assert np.all(v8[0, 0, 0, :70] == oracle.lib().oq_f32_to_e4m3(64.0))
+    assert np.all(v8[0, 0, :, 70:] == 0)
+    col = oracle.bf16_bits_to_f32(_bits(v, (1, 70, 1, 128)))[0, :, 0, 1]  # the bf16 values of channel 1
+    m1 = np.float32(col.astype(np.float64).sum() / 80)
+    assert abs(mean[0, 0, 1] - m1) <= 1e-6
+    amax1 = max(abs(np.float32(col.max()) - mean[0, 0, 1]), abs(np.float32(col.min()) - mean[0, 0, 1]))
+    assert vs[0, 0, 1] == np.float32(amax1) / np.float32(448)
+    # 64 tokens (a multiple of 16): no pad zeros join the max / min
+    w = np.full((64, 128), 3.0, np.float32)
+    w[0] = 1.0
+    _, vs2, mean2 = oracle.per_channel_fp8(_bits(w, (1, 64, 1, 128)), smooth=True)
+    assert mean2[0, 0, 0] == np.float32((63 * 3.0 + 1.0) / 64)
+    assert vs2[0, 0, 0] == np.float32(abs(1.0 - mean2[0, 0, 0])) / np.float32(448)
+    # the mean is taken from mean_in when given (the GPU's reduction order is an input of the bit-exact step)
+    _, _, mean3 = oracle.per_channel_fp8(_bits(w, (1, 64, 1, 128)), smooth=True, mean_in=np.full((1, 1, 128), 0.5))
+    assert np.all(mean3 == np.float32(0.5))
+
+
+def test_v_fp8_smooth_matches_numpy_restatement(oracle):
+    for L in (96, 333):
+        _, _, v = qkv(1, L, L, 2, 2, seed=21)
+        vb = bf16_bits(v)
+        v8, vs, mean = oracle.per_channel_fp8(vb, smooth=True, scale_max=2.25)
+        x = oracle.bf16_bits_to_f32(vb).transpose(0, 2, 3, 1).astype(np.float32)  # B H D L
+        l16 = (L + 15) // 16 * 16
+        mx, mn = x.max(-1), x.min(-1)
+        if l16 != L:
+            mx, mn = np.maximum(mx, 0), np.minimum(mn, 0)
+        amax = np.maximum(np.abs(mx - mean), np.abs(mn - mean)).astype(np.float32)
+        assert np.array_equal(vs, amax / np.float32(2.25))
+        recp = np.float32(2.25) / amax
+        want = oracle.cvt_array(((x - mean[..., None]).astype(np.float32) * recp[..., None]).astype(np.float32), "e4m3")
+        assert np.array_equal(v8[..., :L], want)
 
 
 def test_v_fp8_random_matches_torch_cast(oracle):

@@ -18,7 +18,7 @@ def _quantized(dev, B, Lq, Lk, H, seed):
     q, k, v = (t.to(dev) for t in (q, k, v))
     km = sa.k_mean(k, "NHD")
     q8, qs, k8, ks = sa.per_block_int8(q, k, km, sm_scale=128 ** -0.5, tensor_layout="NHD")
-    v8, vs, _ = sa.per_channel_fp8(v, tensor_layout="NHD")
+    v8, vs, _ = sa.per_channel_fp8(v, tensor_layout="NHD", smooth_v=False)
     return q8, qs, k8, ks, v8, vs
 
 
