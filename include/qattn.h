@@ -180,6 +180,44 @@ int qattn_v_tile_half(qattn_seq v, int dtype, int64_t B, int64_t L, int64_t H, i
                       int64_t Lpad, qattn_stream_t stream);
 
 /*
+ * Packed variable-length batches: sequence b spans rows cu_seqlens[b] .. cu_seqlens[b + 1] of a packed
+ * [total, H, D] tensor (int32 device tables of B + 1 entries, read only on the device).
+ *
+ * qattn_varlen_offsets: the per-sequence block offsets cu_qs[b] = sum over earlier sequences of
+ * ceil(len_q / 128), cu_ks[b] = cu_vt[b] = the same of ceil(len_k / 64) (each B + 1 entries); replaces the
+ * cumsum of quant_per_block_varlen.py:92-107 (tf-kernel/tf_kernel/).
+ *
+ * qattn_quant_qk_varlen_int8: per-sequence INT8 blocks of 128 Q rows and 64 K rows, with the Triton rounding
+ * of variant; q_scale [cu_qs[B], Hq] and k_scale [cu_ks[B], Hkv] (block-major, the reference's layout);
+ * k_mean [1, Hkv, D] (shared by every sequence) or NULL; q scaled by sm_scale.  max_lq / max_lk bound every
+ * sequence's length.  Replaces per_block_int8_varlen (quant_per_block_varlen.py:72-127).
+ *
+ * qattn_v_tile_half_varlen: V into the tile layout of qattn_v_tile_half as one entry [1, H, D, Lpad], sequence
+ * b's tiles at tile columns cu_vt[b] ..; Lpad >= 64 * (cu_vt[B]) (an upper bound such as
+ * 64 * (ceil(total_k / 64) + B) is fine).
+ *
+ * qattn_fwd_varlen: INT8 Q.K^T and fp16 P.V per sequence in one launch, causal top-left aligned per sequence;
+ * q8/k8/o are the packed [1, total, H, D] views (their batch stride is ignored), v16 from
+ * qattn_v_tile_half_varlen.  Rows of sequences with no keys are left untouched.  Replaces
+ * attn_qk_int8_block_varlen.forward (attn_qk_int8_block_varlen.py:157-200).
+ */
+int qattn_varlen_offsets(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t B, int32_t* cu_qs,
+                         int32_t* cu_ks, int32_t* cu_vt, qattn_stream_t stream);
+int qattn_quant_qk_varlen_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t max_lq, int64_t max_lk,
+                               int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean, const int32_t* cu_seqlens_q,
+                               const int32_t* cu_seqlens_k, const int32_t* cu_qs, const int32_t* cu_ks,
+                               qattn_seq q_out, qattn_seq k_out, float* q_scale, float* k_scale, float sm_scale,
+                               int variant, qattn_stream_t stream);
+int qattn_v_tile_half_varlen(qattn_seq v, int dtype, int64_t B, int64_t max_lk, int64_t H, int64_t D,
+                             const int32_t* cu_seqlens_k, const int32_t* cu_vt, uint16_t* v16, int64_t Lpad,
+                             qattn_stream_t stream);
+int qattn_fwd_varlen(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const uint16_t* v16,
+                     int64_t Lpad, qattn_seq o, int out_dtype, int64_t B, int64_t max_lq, int64_t max_lk, int64_t Hq,
+                     int64_t Hkv, int64_t D, float qk_mult, int causal, const int32_t* cu_seqlens_q,
+                     const int32_t* cu_seqlens_k, const int32_t* cu_qs, const int32_t* cu_ks, const int32_t* cu_vt,
+                     qattn_stream_t stream);
+
+/*
  * Quantized attention with INT8 Q.K^T and P.V in the half dtype of V (P rounded to that dtype,
  * fp32 accumulation, no FP8 offset or v_scale): the math of the reference's INT8-QK / FP16-PV kernels
  * (qk_int8_sv_f16_accum_f32_attn, common_extension.cc:214-218; Triton attn_qk_int8_per_block.py:46-101).

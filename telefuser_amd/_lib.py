@@ -43,6 +43,10 @@ EXPORTED = (
     "qattn_fwd",
     "qattn_v_tile_half",
     "qattn_fwd_pv16",
+    "qattn_varlen_offsets",
+    "qattn_quant_qk_varlen_int8",
+    "qattn_v_tile_half_varlen",
+    "qattn_fwd_varlen",
 )
 
 
@@ -128,6 +132,15 @@ def load() -> ctypes.CDLL:
     L.qattn_norm_rope_seq_mean.argtypes = [S, i32, i64, i64, i64, i64, vp, vp, vp, vp, i64, vp, vp, sz, vp]
     L.qattn_norm_rope_quant_qk.argtypes = [S, S, i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, i64, vp, S, S, vp,
                                            vp, f32, i32, vp]
+    L.qattn_varlen_offsets.argtypes = [vp, vp, i64, vp, vp, vp, vp]
+    L.qattn_quant_qk_varlen_int8.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, vp, vp, vp, vp, S, S, vp,
+                                             vp, f32, i32, vp]
+    L.qattn_v_tile_half_varlen.argtypes = [S, i32, i64, i64, i64, i64, vp, vp, vp, i64, vp]
+    L.qattn_fwd_varlen.argtypes = [S, vp, S, vp, vp, i64, S, i32, i64, i64, i64, i64, i64, i64, f32, i32, vp, vp, vp,
+                                   vp, vp, vp]
+    for name in ("qattn_varlen_offsets", "qattn_quant_qk_varlen_int8", "qattn_v_tile_half_varlen",
+                 "qattn_fwd_varlen"):
+        getattr(L, name).restype = i32
     for name in ("qattn_row_rstd", "qattn_norm_rope_seq_mean", "qattn_norm_rope_quant_qk", "qattn_fwd_block_sparse", "qattn_quant_qk_per_warp_int8", "qattn_quant_qk_per_thread_int8", "qattn_fwd_ex",
                  "qattn_v_fp8_cache_update", "qattn_quant_per_block_int8", "qattn_quant_qk_per_block_int8", "qattn_seq_mean",
                  "qattn_per_channel_fp8", "qattn_fwd", "qattn_v_tile_half", "qattn_fwd_pv16"):

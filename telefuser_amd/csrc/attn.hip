@@ -94,6 +94,14 @@ struct AttnParams {
   int64_t nQC;   // multi-block launches: workgroups per (batch, head)
   int causal;
   float qk_mult;
+  // packed variable-length batches (null otherwise): sequence b has query rows cu_q[b] .. cu_q[b + 1] and key
+  // rows cu_k[b] .. cu_k[b + 1] of the packed [1, total, H, D] tensors, its scales start at block cu_qs[b] /
+  // cu_ks[b] of [total_blocks, H] tables, and its V tiles at tile cu_vt[b] of the [1, Hkv, D, Lpad] tile layout
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  const int32_t* cu_qs;
+  const int32_t* cu_ks;
+  const int32_t* cu_vt;
 };
 
 __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t n) {
@@ -206,13 +214,37 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   const int64_t b = rest / p.Hq;
   const int64_t hk = h / p.group;
 
+  // the batch entry's view: a dense batch, or one sequence of a packed variable-length batch
+  int64_t Lq = p.Lq, Lk = p.Lk;
+  const int8_t* q8b = p.q8 + b * p.qsb;
+  const int8_t* k8b = p.k8 + b * p.ksb;
+  int64_t vcol0 = 0;  // first key column of this entry in the V tile layout
+  const float* qs_tab = p.q_scale + (b * p.Hq + h) * p.nQS;
+  const float* ks_tab = p.k_scale + (b * p.Hkv + hk) * p.nKS;
+  int64_t qs_stride = 1, ks_stride = 1;
+  uint16_t* ob = static_cast<uint16_t*>(p.o) + b * p.osb;
+  if (p.cu_q) {
+    const int64_t q0 = p.cu_q[b], k0s = p.cu_k[b];
+    Lq = p.cu_q[b + 1] - q0;
+    Lk = p.cu_k[b + 1] - k0s;
+    if (qb * kBQ >= Lq || Lk <= 0) return;  // uniform over the workgroup: no query row of this sequence here
+    q8b = p.q8 + q0 * p.qsl;
+    k8b = p.k8 + k0s * p.ksl;
+    vcol0 = (int64_t)p.cu_vt[b] * kBK;
+    qs_tab = p.q_scale + (int64_t)p.cu_qs[b] * p.Hq + h;
+    ks_tab = p.k_scale + (int64_t)p.cu_ks[b] * p.Hkv + hk;
+    qs_stride = p.Hq;
+    ks_stride = p.Hkv;
+    ob = static_cast<uint16_t*>(p.o) + q0 * p.osl;
+  }
+
   const int tid = threadIdx.x;
   // (wave index in a scalar register, so that every per-wave quantity and branch stays scalar)
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31, hf = lane >> 5;
 
   // key range of this workgroup
   int64_t q_first = qb * kBQ;
-  int64_t kv_end = p.Lk;
+  int64_t kv_end = Lk;
   if (p.kv_valid) kv_end = min(kv_end, (int64_t)p.kv_valid[b]);
   if (p.causal) kv_end = min(kv_end, q_first + kBQ + p.q_offset);
   const int64_t n_tiles = kv_end > 0 ? (kv_end + kBK - 1) / kBK : 0;
@@ -256,12 +288,12 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   uint8_t* stage = (MQ ? &lds_qo[0] : &lds_k[0][0]) + w * 4096;  // 32 rows x 128 B per wave (lds_k is free here)
   v4i qf[4];
   {
-    const int8_t* qbase = p.q8 + b * p.qsb + h * p.qsh;
+    const int8_t* qbase = q8b + h * p.qsh;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int r = i * 8 + (lane >> 3), c = lane & 7;
       const int64_t row = wrow0 + r;
-      const v4i val = row < p.Lq ? *reinterpret_cast<const v4i*>(qbase + row * p.qsl + c * 16) : v4i{0, 0, 0, 0};
+      const v4i val = row < Lq ? *reinterpret_cast<const v4i*>(qbase + row * p.qsl + c * 16) : v4i{0, 0, 0, 0};
       *reinterpret_cast<v4i*>(stage + r * 128 + ((c ^ (r & 7)) << 4)) = val;
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
@@ -280,11 +312,11 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   const int64_t qsi = p.qgran == QATTN_GRAN_THREAD ? (qb * 4 + w) * 8 + (lq & 7)
                       : p.qgran == QATTN_GRAN_WARP ? qb * 4 + w
                                                    : qb;
-  float qs = p.q_scale[(b * p.Hq + h) * p.nQS + qsi] * p.qk_mult;
+  float qs = qs_tab[qsi * qs_stride] * p.qk_mult;
   // q_scale entries per query block, and this lane's entry within its block
   const int qs_per = p.qgran == QATTN_GRAN_THREAD ? 32 : p.qgran == QATTN_GRAN_WARP ? 4 : 1;
   const int qs_sub = p.qgran == QATTN_GRAN_THREAD ? w * 8 + (lq & 7) : p.qgran == QATTN_GRAN_WARP ? w : 0;
-  const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
+  const float* ks_ptr = ks_tab;
 
   // global -> LDS copies go through the LDS-DMA path (buffer_load_dwordx4 ... lds): lane j of a wave
   // writes the 16 bytes at LDS slot (wave base + 16 j).  The tiles are fragment-major: 1 KiB block f holds
@@ -298,10 +330,11 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   // The K resource of a tile starts at the tile's first row, so K rows at or past Lk fall outside its
   // range and arrive as zeros (masked anyway) without being read (the range check covers the
   // per-lane offset, not the scalar one).
-  const int8_t* kbase = p.k8 + b * p.ksb + hk * p.ksh;
-  const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad * kVBytes;
-  const int64_t kbytes = (p.Lk - 1) * p.ksl + kD;
-  const v4u vrsrc = make_rsrc(vbase, (uint32_t)((int64_t)kD * p.Lpad * kVBytes));
+  const int8_t* kbase = k8b + hk * p.ksh;
+  const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + ((p.cu_q ? 0 : b) * p.Hkv + hk) * (int64_t)kD * p.Lpad * kVBytes +
+                         vcol0 * kVBytes;
+  const int64_t kbytes = (Lk - 1) * p.ksl + kD;
+  const v4u vrsrc = make_rsrc(vbase, (uint32_t)(((int64_t)kD * p.Lpad - vcol0) * kVBytes));
   // per-lane byte offsets relative to the tile start (first K row / first V column)
   uint32_t koff[2], voff[kVDma];
 #pragma unroll
@@ -337,11 +370,11 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
     const int slot = i * 64 + lane, r = slot >> 3;
     qoff[i] = (uint32_t)(r * p.qsl + (((slot & 7) ^ (r & 7)) << 4));
   }
-  const int8_t* qhead = p.q8 + b * p.qsb + h * p.qsh;
+  const int8_t* qhead = q8b + h * p.qsh;
   const int wu = __builtin_amdgcn_readfirstlane(w);
   auto dma_q = [&](int64_t blk) {
     const int64_t r0 = blk * kBQ + wu * 32;
-    const int64_t nr = min((int64_t)32, p.Lq - r0);
+    const int64_t nr = min((int64_t)32, Lq - r0);
     const v4u qr = make_rsrc(qhead + (nr > 0 ? r0 * p.qsl : 0), nr > 0 ? (uint32_t)((nr - 1) * p.qsl + kD) : 0u);
     const uint32_t ql = lds_addr(&lds_qo[0]) + wu * 4096;
 #pragma unroll
@@ -367,9 +400,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   // loop is the 4 DMA instructions per tile and the vmcnt accounting below is exact.
   __syncthreads();  // every wave has its Q fragments out of the LDS stage before the DMA reuses it
   if constexpr (SP) {
-    for (int64_t i = tid; i < t_end - t_begin; i += kThreads) lds_ks[i] = ks_ptr[lds_tid[i]];
+    for (int64_t i = tid; i < t_end - t_begin; i += kThreads) lds_ks[i] = ks_ptr[lds_tid[i] * ks_stride];
   } else {
-    for (int64_t i = tid; i < (t_end - t_begin) * KS; i += kThreads) lds_ks[i] = ks_ptr[t_begin * KS + i];
+    for (int64_t i = tid; i < (t_end - t_begin) * KS; i += kThreads) lds_ks[i] = ks_ptr[(t_begin * KS + i) * ks_stride];
   }
   if constexpr (PV == PV_FP8 && !SPLIT)
     if (tid < kD) {
@@ -400,7 +433,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
       l_tot = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
     }
     if (SPLIT) {
-      if (qrow >= p.Lq) return;
+      if (qrow >= Lq) return;
       const int64_t row = (((int64_t)split * p.B + b) * p.Hq + h) * p.Lq + qrow;
       float* wo = p.ws_o + row * kD;
 #pragma unroll
@@ -421,7 +454,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
     // O goes out through the wave-private LDS stage (the K/V buffers are idle after the loop's last
     // barrier; multi-block launches use their own region), 64 channels per pass, so that every row is
     // stored as whole 128-byte lines
-    uint16_t* obase = static_cast<uint16_t*>(p.o) + b * p.osb + h * p.osh;
+    uint16_t* obase = ob + h * p.osh;
 #pragma unroll
     for (int pass = 0; pass < 2; pass++) {
 #pragma unroll
@@ -450,11 +483,11 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
         const int r = i * 8 + (lane >> 3), c = lane & 7;
         const v4u val = *reinterpret_cast<const v4u*>(stage + r * 128 + ((c ^ (r & 7)) << 4));
         const int64_t row = wrow0 + r;
-        if (row < p.Lq) *reinterpret_cast<v4u*>(obase + row * p.osl + pass * 64 + c * 8) = val;
+        if (row < Lq) *reinterpret_cast<v4u*>(obase + row * p.osl + pass * 64 + c * 8) = val;
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
-    if (p.lse && hf == 0 && qrow < p.Lq)
+    if (p.lse && hf == 0 && qrow < Lq)
       p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
   };
   [[maybe_unused]] auto next_block = [&]() {
@@ -1336,6 +1369,33 @@ extern "C" int qattn_fwd_ex2(qattn_seq q8, const float* q_scale, qattn_seq k8, c
   p.v_scale = nullptr;
   if (pv == PV_BF16) return launch_gran<PV_BF16>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D, kernel);
   return launch_gran<PV_FP16>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D, kernel);
+}
+
+// ---- packed variable-length batches ----
+// One launch over every sequence of a packed batch (attn_qk_int8_block_varlen.py:68-155): the grid covers
+// max_seqlen_q rows per sequence and head, and each workgroup reads its sequence's row range, scale
+// offsets and V tile column from the device tables, so the host never reads cu_seqlens.
+extern "C" int qattn_fwd_varlen(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale,
+                                const uint16_t* v16, int64_t Lpad, qattn_seq o, int out_dtype, int64_t B,
+                                int64_t max_lq, int64_t max_lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult,
+                                int causal, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                const int32_t* cu_qs, const int32_t* cu_ks, const int32_t* cu_vt,
+                                qattn_stream_t stream) {
+  QATTN_REQUIRE(cu_seqlens_q && cu_seqlens_k && cu_qs && cu_ks && cu_vt, QATTN_ERR_ARG, "null sequence table");
+  AttnParams p;
+  int ns = 1, kernel = QATTN_KERNEL_AUTO;
+  const int rc = setup_fwd(p, ns, q8, q_scale, k8, k_scale, v16, Lpad, o, out_dtype, B, max_lq, max_lk, Hq, Hkv, D,
+                           qk_mult, causal, 0, nullptr, nullptr, 1, PV_FP16, QATTN_GRAN_BLOCK, kernel);
+  if (rc < 0) return QATTN_OK;
+  if (rc) return rc;
+  p.cu_q = cu_seqlens_q;
+  p.cu_k = cu_seqlens_k;
+  p.cu_qs = cu_qs;
+  p.cu_ks = cu_ks;
+  p.cu_vt = cu_vt;
+  p.v_scale = nullptr;
+  p.qpw = 1;
+  return launch_fwd<PV_FP16, false>(p, out_dtype, 1, nullptr, 0, (hipStream_t)stream, D, QATTN_KERNEL_ONE_BLOCK);
 }
 
 // ---- allocation-free form of qattn_fwd_ex ----

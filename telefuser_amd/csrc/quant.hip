@@ -69,6 +69,10 @@ struct QuantJob {
   int ncls;     // scale classes per block: 1 (per block), 8 (per-thread Q), 4 (per-thread K)
   int cls_shift;  // class of row r = (r % 8) >> cls_shift  (3, 0, 1 for the cases above)
   NormRope nr;    // optional RMSNorm + RoPE prologue on the loaded chunks
+  // packed variable-length input (null otherwise): entry b is rows cu_seq[b] .. cu_seq[b + 1] of batch 0, its
+  // block n's scale goes to scale[(cu_blk[b] + n) * H + h] (quant_per_block_varlen.py:22-70)
+  const int32_t* cu_seq;
+  const int32_t* cu_blk;
 };
 
 struct QuantArgs {
@@ -125,6 +129,21 @@ __global__ __launch_bounds__(quant_threads<VARIANT>()) void quant_per_block_kern
   const int64_t b = wg / (J.nblk * J.H);
   const int tid = threadIdx.x;
   const int nchunks = J.blk * TPR;
+  // this entry's rows: in_b[l * sl], l < Lb (a dense batch entry, or one packed sequence)
+  const uint16_t* in_b = J.in + b * J.sb;
+  int8_t* out_b = J.out + b * J.ob;
+  int64_t Lb = J.L;
+  float* scale_at = J.scale + ((b * J.H + h) * J.nblk + n) * J.ncls;
+  int64_t mb = b;  // batch entry of the mean (packed sequences share entry 0)
+  if (J.cu_seq) {
+    mb = 0;
+    const int64_t r0 = J.cu_seq[b];
+    Lb = J.cu_seq[b + 1] - r0;
+    if (n * J.blk >= Lb) return;  // uniform over the workgroup
+    in_b = J.in + r0 * J.sl;
+    out_b = J.out + r0 * J.ol;
+    scale_at = J.scale + ((int64_t)J.cu_blk[b] + n) * J.H + h;
+  }
 
   // the scale class of a row: rows r with equal (r % 8) / (8 / ncls) share a scale.  Every thread
   // touches rows of a single class (rows per pass, 256 / TPR, is a multiple of 8).
@@ -140,14 +159,14 @@ __global__ __launch_bounds__(quant_threads<VARIANT>()) void quant_per_block_kern
     const int64_t l = n * J.blk + row;
 #pragma unroll
     for (int e = 0; e < 8; e++) x[i][e] = 0.f;
-    if (c < nchunks && l < J.L) {
-      v4u raw = *reinterpret_cast<const v4u*>(J.in + b * J.sb + l * J.sl + h * J.sh + dc * 8);
+    if (c < nchunks && l < Lb) {
+      v4u raw = *reinterpret_cast<const v4u*>(in_b + l * J.sl + h * J.sh + dc * 8);
       uint16_t hv[8];
       __builtin_memcpy(hv, &raw, 16);
       if (J.nr.rstd) norm_rope8<IS_FP16>(J.nr, b, J.L, l, h, D, dc, hv);
       float mv[8];
       if (J.mean) {
-        v4u mraw = *reinterpret_cast<const v4u*>(J.mean + (b * J.H + h) * D + dc * 8);
+        v4u mraw = *reinterpret_cast<const v4u*>(J.mean + (mb * J.H + h) * D + dc * 8);
         uint16_t mh[8];
         __builtin_memcpy(mh, &mraw, 16);
 #pragma unroll
@@ -198,9 +217,9 @@ __global__ __launch_bounds__(quant_threads<VARIANT>()) void quant_per_block_kern
   };
   const float scale = scale_of(amax);
   if constexpr (VARIANT == QATTN_QUANT_TRITON_THREAD) {
-    if (tid < J.ncls) J.scale[((b * J.H + h) * J.nblk + n) * J.ncls + tid] = scale_of(class_max(tid));
+    if (tid < J.ncls) scale_at[tid] = scale_of(class_max(tid));
   } else if (tid == 0) {
-    J.scale[(b * J.H + h) * J.nblk + n] = scale;
+    *scale_at = scale;
   }
   const float inv = 127.0f / amax;
 
@@ -209,7 +228,7 @@ __global__ __launch_bounds__(quant_threads<VARIANT>()) void quant_per_block_kern
     const int c = tid + i * kQuantThreads;
     const int row = c / TPR, dc = c % TPR;
     const int64_t l = n * J.blk + row;
-    if (c < nchunks && l < J.L) {
+    if (c < nchunks && l < Lb) {
       int8_t qv[8];
 #pragma unroll
       for (int e = 0; e < 8; e++) {
@@ -218,7 +237,7 @@ __global__ __launch_bounds__(quant_threads<VARIANT>()) void quant_per_block_kern
       }
       v2u packed;
       __builtin_memcpy(&packed, qv, 8);
-      *reinterpret_cast<v2u*>(J.out + b * J.ob + l * J.ol + h * J.oh + dc * 8) = packed;
+      *reinterpret_cast<v2u*>(out_b + l * J.ol + h * J.oh + dc * 8) = packed;
     }
   }
 }
@@ -464,11 +483,21 @@ __global__ __launch_bounds__(256) void v_fp8_kernel(const uint16_t* in, int64_t 
 
 template <int D>
 __global__ __launch_bounds__(256) void v_tile_half_kernel(const uint16_t* in, int64_t sb, int64_t sl, int64_t sh,
-                                                          int64_t L, int64_t H, uint16_t* v16, int64_t Lpad) {
+                                                          int64_t L, int64_t H, uint16_t* v16, int64_t Lpad,
+                                                          const int32_t* cu_k = nullptr, const int32_t* cu_vt = nullptr) {
   constexpr int TPR = D / 8;
   __shared__ __align__(16) uint16_t tile[D][64];
-  const int64_t t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  int64_t t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
+  int64_t tcol = t;  // tile column in v16
+  if (cu_k) {  // packed variable-length keys: sequence b's tile t goes to tile column cu_vt[b] + t of entry 0
+    const int64_t k0 = cu_k[b];
+    L = cu_k[b + 1] - k0;
+    if (t * 64 >= L) return;
+    in += k0 * sl;
+    tcol = cu_vt[b] + t;
+    b = 0;
+  }
 #pragma unroll
   for (int i = 0; i < 64 * TPR / 256; i++) {
     const int c = tid + i * 256;
@@ -488,7 +517,7 @@ __global__ __launch_bounds__(256) void v_tile_half_kernel(const uint16_t* in, in
   for (int i = 0; i < D * 8 / 256; i++) {
     const int c = tid + i * 256;
     const int d = c / 8, cc = c % 8;
-    *reinterpret_cast<v4u*>(v16 + ((b * H + h) * D + d) * Lpad + t * 64 + cc * 8) =
+    *reinterpret_cast<v4u*>(v16 + ((b * H + h) * D + d) * Lpad + tcol * 64 + cc * 8) =
         *reinterpret_cast<const v4u*>(&tile[d][cc * 8]);
   }
 }
@@ -552,6 +581,7 @@ static bool fill_job(QuantJob& J, const qattn_seq& in, const qattn_seq& out, int
   J.ncls = 1;
   J.cls_shift = 3;
   J.nr = NormRope{};
+  J.cu_seq = J.cu_blk = nullptr;
   return true;
 }
 
@@ -931,4 +961,85 @@ extern "C" int qattn_norm_rope_quant_qk(qattn_seq xq, qattn_seq xk, int dtype, i
   if ((rc = make_norm_rope(a.job[0].nr, rstd_q, wq, cs, sn, cs_stride, D))) return rc;
   if ((rc = make_norm_rope(a.job[1].nr, rstd_k, wk, cs, sn, cs_stride, D))) return rc;
   return run_quant(a, dtype, D, variant, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------------------------------------
+// packed variable-length batches
+// ------------------------------------------------------------------------------------------------
+
+namespace qattn {
+// Block offsets of every sequence: cu_qs[b] = sum of ceil(len_q / 128), cu_ks[b] = cu_vt[b] = sum of
+// ceil(len_k / 64) over the sequences before b (the cumsum of quant_per_block_varlen.py:92-107).  One
+// thread: B is small and the loop reads B + 1 entries.
+__global__ void varlen_offsets_kernel(const int32_t* cu_q, const int32_t* cu_k, int64_t B, int32_t* cu_qs,
+                                      int32_t* cu_ks, int32_t* cu_vt) {
+  if (threadIdx.x != 0) return;
+  int32_t aq = 0, ak = 0;
+  for (int64_t b = 0; b <= B; b++) {
+    cu_qs[b] = aq;
+    cu_ks[b] = ak;
+    cu_vt[b] = ak;
+    if (b < B) {
+      aq += (cu_q[b + 1] - cu_q[b] + 127) / 128;
+      ak += (cu_k[b + 1] - cu_k[b] + 63) / 64;
+    }
+  }
+}
+}  // namespace qattn
+
+extern "C" int qattn_varlen_offsets(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t B,
+                                    int32_t* cu_qs, int32_t* cu_ks, int32_t* cu_vt, qattn_stream_t stream) {
+  QATTN_REQUIRE(B > 0, QATTN_ERR_SHAPE, "varlen batch must hold at least one sequence");
+  QATTN_REQUIRE(cu_seqlens_q && cu_seqlens_k && cu_qs && cu_ks && cu_vt, QATTN_ERR_ARG, "null pointer");
+  varlen_offsets_kernel<<<1, 64, 0, (hipStream_t)stream>>>(cu_seqlens_q, cu_seqlens_k, B, cu_qs, cu_ks, cu_vt);
+  return check_launch("varlen_offsets");
+}
+
+extern "C" int qattn_quant_qk_varlen_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t max_lq,
+                                          int64_t max_lk, int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean,
+                                          const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                          const int32_t* cu_qs, const int32_t* cu_ks, qattn_seq q_out,
+                                          qattn_seq k_out, float* q_scale, float* k_scale, float sm_scale,
+                                          int variant, qattn_stream_t stream) {
+  int rc;
+  if ((rc = check_common(dtype, D, variant, 128))) return rc;
+  QATTN_REQUIRE(B > 0 && max_lq >= 0 && max_lk >= 0 && Hq > 0 && Hkv > 0, QATTN_ERR_SHAPE, "bad sizes");
+  QATTN_REQUIRE(cu_seqlens_q && cu_seqlens_k && cu_qs && cu_ks && q_scale && k_scale, QATTN_ERR_ARG, "null pointer");
+  if ((rc = check_seq("q", q, 2)) || (rc = check_seq("q_out", q_out, 1)) || (rc = check_seq("k", k, 2)) ||
+      (rc = check_seq("k_out", k_out, 1)))
+    return rc;
+  QATTN_REQUIRE(k_mean == nullptr || aligned16(k_mean), QATTN_ERR_ALIGN, "k_mean must be 16-byte aligned");
+  QuantArgs a{};
+  a.njobs = 0;
+  if (max_lq > 0) {
+    QuantJob& J = a.job[a.njobs++];
+    fill_job(J, q, q_out, B, max_lq, Hq, nullptr, q_scale, sm_scale, 1, 128);
+    J.cu_seq = cu_seqlens_q;
+    J.cu_blk = cu_qs;
+  }
+  if (max_lk > 0) {
+    QuantJob& J = a.job[a.njobs++];
+    fill_job(J, k, k_out, B, max_lk, Hkv, k_mean, k_scale, 1.0f, 0, 64);
+    J.cu_seq = cu_seqlens_k;
+    J.cu_blk = cu_ks;
+  }
+  if (a.njobs == 0) return QATTN_OK;
+  return run_quant(a, dtype, D, variant, (hipStream_t)stream);
+}
+
+extern "C" int qattn_v_tile_half_varlen(qattn_seq v, int dtype, int64_t B, int64_t max_lk, int64_t H, int64_t D,
+                                        const int32_t* cu_seqlens_k, const int32_t* cu_vt, uint16_t* v16,
+                                        int64_t Lpad, qattn_stream_t stream) {
+  int rc;
+  if ((rc = check_common(dtype, D, QATTN_QUANT_CUDA, 64))) return rc;
+  QATTN_REQUIRE(B > 0 && max_lk > 0 && H > 0, QATTN_ERR_SHAPE, "v_tile_half_varlen needs non-empty input");
+  if ((rc = check_seq("v", v, 2))) return rc;
+  QATTN_REQUIRE(Lpad % 64 == 0, QATTN_ERR_SHAPE, "Lpad must be a multiple of 64");
+  QATTN_REQUIRE(v16 && aligned16(v16) && cu_seqlens_k && cu_vt, QATTN_ERR_ARG, "null or misaligned pointer");
+  hipStream_t st = (hipStream_t)stream;
+  dim3 grid((unsigned)((max_lk + 63) / 64), (unsigned)H, (unsigned)B);
+  const uint16_t* p = static_cast<const uint16_t*>(v.data);
+  if (D == 128) v_tile_half_kernel<128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, max_lk, H, v16, Lpad, cu_seqlens_k, cu_vt);
+  else v_tile_half_kernel<64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, max_lk, H, v16, Lpad, cu_seqlens_k, cu_vt);
+  return check_launch("v_tile_half_varlen");
 }

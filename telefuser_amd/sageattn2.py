@@ -390,15 +390,18 @@ def sageattn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlen
     per-sequence Q/K blocks of 128/64 rows quantized with the Triton rounding
     (quant_per_block_varlen.py:22-70), V in fp16 and P rounded to fp16 for P.V
     (attn_qk_int8_block_varlen.py:42-65; P.V accumulates in fp32 here).  ``is_causal`` masks per
-    sequence, top-left aligned.  The sequence table is read on the host (one device-to-host copy), and
-    each sequence runs as its own launches on the packed tensors' row views.
+    sequence, top-left aligned.  The whole batch is four launches (block offsets, Q/K quantizer, V tiles,
+    attention) whose workgroups read the sequence tables on the device: the host never reads cu_seqlens,
+    and sizes its buffers from the packed lengths and max_seqlen_q / max_seqlen_k alone.  As in the
+    reference, the tables must be valid (start at 0, non-decreasing, within the packed tensors, every
+    length at most its max_seqlen); rows of sequences without keys are zero.
     """
     dtype = q.dtype
     if not q.is_cuda:
         raise AssertionError("Input tensors must be on cuda.")
     if dtype not in (torch.float16, torch.bfloat16):
         raise AssertionError("Input tensors must be in dtype of torch.float16 or torch.bfloat16")
-    if not (q.device == k.device == v.device):
+    if not (q.device == k.device == v.device == cu_seqlens_q.device == cu_seqlens_k.device):
         raise AssertionError("All tensors must be on the same device.")
     if not (q.dtype == k.dtype == v.dtype):
         raise AssertionError("All tensors must have the same dtype.")
@@ -410,33 +413,53 @@ def sageattn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlen
         raise AssertionError("Last dim of qkv must be contiguous.")
     if not (cu_seqlens_q.is_contiguous() and cu_seqlens_k.is_contiguous()):
         raise AssertionError("cu_seqlens_q and cu_seqlens_k must be contiguous.")
-    hq, hkv = q.shape[1], k.shape[1]
+    if cu_seqlens_q.dim() != 1 or cu_seqlens_q.shape != cu_seqlens_k.shape or cu_seqlens_q.numel() < 2:
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must both have batch_size + 1 entries")
+    hq, hkv, d = q.shape[1], k.shape[1], q.shape[2]
     if hq % hkv != 0:
         raise ValueError(f"num_qo_heads ({hq}) must be divisible by num_kv_heads ({hkv})")
-    cq = [int(x) for x in cu_seqlens_q.tolist()]
-    ck = [int(x) for x in cu_seqlens_k.tolist()]
-    if len(cq) != len(ck) or len(cq) < 2:
-        raise ValueError("cu_seqlens_q and cu_seqlens_k must both have batch_size + 1 entries")
-    if cq[0] != 0 or ck[0] != 0 or cq[-1] > q.shape[0] or ck[-1] > k.shape[0] or \
-            any(a > b for a, b in zip(cq, cq[1:])) or any(a > b for a, b in zip(ck, ck[1:])):
-        raise ValueError("cu_seqlens must start at 0, be non-decreasing and stay inside the packed tensors")
+    max_seqlen_q, max_seqlen_k = int(max_seqlen_q), int(max_seqlen_k)
+    if max_seqlen_q < 0 or max_seqlen_k < 0 or max_seqlen_q > q.shape[0] or max_seqlen_k > k.shape[0]:
+        raise ValueError("max_seqlen_q / max_seqlen_k must lie within the packed tensors")
     if sm_scale is None:
         sm_scale = head_dim_og ** -0.5
-    q4, k4 = q.unsqueeze(0), k.unsqueeze(0)  # [1, total, H, D] views
+    L = _lib.load()
+    st = _lib.stream_of(q)
+    dev = q.device
+    bsz = cu_seqlens_q.numel() - 1
+    out = torch.zeros((q.shape[0], hq, d), dtype=dtype, device=dev)
+    if max_seqlen_q == 0 or max_seqlen_k == 0 or q.shape[0] == 0 or k.shape[0] == 0:
+        return out[..., :head_dim_og]
+    cq = cu_seqlens_q if cu_seqlens_q.dtype == torch.int32 else cu_seqlens_q.to(torch.int32)
+    ck = cu_seqlens_k if cu_seqlens_k.dtype == torch.int32 else cu_seqlens_k.to(torch.int32)
+    offs = torch.empty((3, bsz + 1), dtype=torch.int32, device=dev)  # cu_qs, cu_ks, cu_vt
+    cu_qs, cu_ks, cu_vt = offs[0], offs[1], offs[2]
+    _lib.check(L.qattn_varlen_offsets(_lib.ptr(cq), _lib.ptr(ck), bsz, _lib.ptr(cu_qs), _lib.ptr(cu_ks),
+                                      _lib.ptr(cu_vt), st))
+    # block counts are bounded by ceil(total / block) + batch_size, whatever the split into sequences
+    nqblk = -(-q.shape[0] // BLKQ) + bsz
+    nkblk = -(-k.shape[0] // BLKK) + bsz
+    q4, k4, v4 = q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0)  # [1, total, H, D] views
     km = k_mean(k4, "NHD") if smooth_k else None  # mean over every packed key, as k.mean(dim=0)
-    v16 = v if v.dtype == torch.float16 else v.to(torch.float16)  # the reference runs P.V in fp16
-    out = torch.zeros((q.shape[0], hq, q.shape[2]), dtype=dtype, device=q.device)
-    for b in range(len(cq) - 1):
-        lq, lk = cq[b + 1] - cq[b], ck[b + 1] - ck[b]
-        if lq == 0 or lk == 0:
-            continue  # no queries, or no keys: the rows stay zero
-        qb = q4[:, cq[b]:cq[b + 1]]
-        kb = k4[:, ck[b]:ck[b + 1]]
-        q8, qsc = quant_per_block_int8(qb, BLKQ, sm_scale=sm_scale * LOG2E, tensor_layout="NHD", variant="triton")
-        k8, ksc = quant_per_block_int8(kb, BLKK, mean=km, tensor_layout="NHD", variant="triton")
-        vt = v_tile_half(v16[ck[b]:ck[b + 1]].unsqueeze(0), tensor_layout="NHD")
-        qattn_fwd(q8, qsc, k8, ksc, vt, None, tensor_layout="NHD", out_dtype=dtype, is_causal=is_causal,
-                  out=out[cq[b]:cq[b + 1]].unsqueeze(0))
+    q8 = torch.empty((1,) + tuple(q.shape), dtype=torch.int8, device=dev)
+    k8 = torch.empty((1,) + tuple(k.shape), dtype=torch.int8, device=dev)
+    qsc = torch.empty((nqblk, hq), dtype=torch.float32, device=dev)
+    ksc = torch.empty((nkblk, hkv), dtype=torch.float32, device=dev)
+    _lib.check(L.qattn_quant_qk_varlen_int8(
+        _lib.seq(q4, "NHD"), _lib.seq(k4, "NHD"), _lib.dtype_code(dtype), bsz, max_seqlen_q, max_seqlen_k, hq, hkv,
+        d, _lib.ptr(km) if km is not None else None, _lib.ptr(cq), _lib.ptr(ck), _lib.ptr(cu_qs), _lib.ptr(cu_ks),
+        _lib.seq(q8, "NHD"), _lib.seq(k8, "NHD"), _lib.ptr(qsc), _lib.ptr(ksc), sm_scale * LOG2E,
+        _lib.QATTN_QUANT_TRITON, st))
+    v16 = v4 if v4.dtype == torch.float16 else v4.to(torch.float16)  # the reference runs P.V in fp16
+    lpad = nkblk * BLKK
+    vt = torch.empty((1, hkv, d, lpad), dtype=torch.float16, device=dev)
+    _lib.check(L.qattn_v_tile_half_varlen(_lib.seq(v16, "NHD"), _lib.QATTN_FP16, bsz, max_seqlen_k, hkv, d,
+                                          _lib.ptr(ck), _lib.ptr(cu_vt), _lib.ptr(vt), lpad, st))
+    o4 = out.unsqueeze(0)
+    _lib.check(L.qattn_fwd_varlen(
+        _lib.seq(q8, "NHD"), _lib.ptr(qsc), _lib.seq(k8, "NHD"), _lib.ptr(ksc), _lib.ptr(vt), lpad,
+        _lib.seq(o4, "NHD"), _lib.dtype_code(dtype), bsz, max_seqlen_q, max_seqlen_k, hq, hkv, d, 1.0,
+        1 if is_causal else 0, _lib.ptr(cq), _lib.ptr(ck), _lib.ptr(cu_qs), _lib.ptr(cu_ks), _lib.ptr(cu_vt), st))
     return out[..., :head_dim_og]
 
 

@@ -268,27 +268,30 @@ def test_quant_granularities(oracle, gran, case):
 
 @pytest.mark.parametrize("causal", [False, True])
 def test_sageattn_varlen(oracle, causal):
-    """Packed variable-length batch (sageattn2.py:772-927): every sequence against the oracle (Triton
-    quantizer, fp16 P.V, the kernel's schedule) and float64 truth; empty sequences stay zero."""
+    """Packed variable-length batch (sageattn2.py:772-927) in one device-side launch per stage: every
+    sequence against the oracle (Triton quantizer, fp16 P.V, the kernel's schedule, no KV split) and
+    float64 truth; sequences without queries or keys stay zero, and the host never reads cu_seqlens."""
     dev = require_gpu()
     from telefuser_amd import _lib
     from telefuser_amd import sageattn2 as sa
 
-    lq = [100, 257, 0, 64] if not causal else [130, 257, 64]
-    lk = [130, 300, 50, 64] if not causal else [130, 257, 64]
-    H, D = 2, 128
+    lq = [100, 257, 0, 64, 70, 1] if not causal else [130, 257, 64, 300]
+    lk = [130, 1100, 50, 64, 0, 700] if not causal else [130, 257, 64, 300]
+    Hq, Hkv, D = 4, 2, 128
     cq, ck = np.concatenate([[0], np.cumsum(lq)]), np.concatenate([[0], np.cumsum(lk)])
     g = torch.Generator().manual_seed(41 + causal)
-    q = torch.randn((int(cq[-1]), H, D), generator=g).to(torch.bfloat16)
-    k = (torch.randn((int(ck[-1]), H, D), generator=g) + 0.5).to(torch.bfloat16)
-    v = torch.randn((int(ck[-1]), H, D), generator=g).to(torch.bfloat16)
+    q = torch.randn((int(cq[-1]), Hq, D), generator=g).to(torch.bfloat16)
+    k = (torch.randn((int(ck[-1]), Hkv, D), generator=g) + 0.5).to(torch.bfloat16)
+    v = torch.randn((int(ck[-1]), Hkv, D), generator=g).to(torch.bfloat16)
     log(f"varlen causal={causal} lq={lq} lk={lk}")
+    L = _lib.load()
+    L.qattn_set_kernel(_lib.QATTN_KERNEL_AUTO)
     o = sa.sageattn_varlen(q.to(dev), k.to(dev), v.to(dev), torch.tensor(cq, dtype=torch.int32, device=dev),
                            torch.tensor(ck, dtype=torch.int32, device=dev), max(lq), max(lk), is_causal=causal)
     torch.cuda.synchronize()
+    assert L.qattn_last_kernel() == _lib.QATTN_KERNEL_ONE_BLOCK
     og = o.float().cpu().numpy()
-    km = sa.k_mean(k.to(dev).unsqueeze(0), "NHD").cpu()  # [1, H, D], the kernel's smoothing vector
-    L = _lib.load()
+    km = sa.k_mean(k.to(dev).unsqueeze(0), "NHD").cpu()  # [1, Hkv, D], the kernel's smoothing vector
     sm = D ** -0.5
     for b in range(len(lq)):
         rows = slice(int(cq[b]), int(cq[b + 1]))
@@ -301,15 +304,25 @@ def test_sageattn_varlen(oracle, causal):
         q8, qs = oracle.quant_per_block_int8(bf16_bits(qb), sm_scale=sm * LOG2E, blk=128, variant="triton")
         k8, ks = oracle.quant_per_block_int8(bf16_bits(kb), km_bits=bf16_bits(km), blk=64, variant="triton")
         vh = vb.to(torch.float16).contiguous().view(torch.int16).numpy().view(np.uint16)
-        nkb = (lk[b] + 63) // 64
-        ns = min(L.qattn_fwd_ex_num_splits(1, lq[b], lk[b], H, 2, 1), nkb)
-        tps = (nkb + ns - 1) // ns if ns > 1 else 0
         ref = oracle.qattn_fwd(q8, qs, k8, ks, vh_bits=vh, pv_mode=1, is_fp16=True, causal=causal,
-                               tiles_per_split=tps, lazy_tau=KERNEL_LAZY_TAU)
+                               tiles_per_split=0, lazy_tau=KERNEL_LAZY_TAU)
         truth = oracle.attn_fp64(bf16_bits(qb), bf16_bits(kb), bf16_bits(vb), sm, causal=causal)
         got = og[rows][None]
+        # the same kernel on this sequence alone, as a dense batch of one: bit-identical
+        q8d, qsd = sa.quant_per_block_int8(qb.to(dev), 128, sm_scale=sm * LOG2E, tensor_layout="NHD",
+                                           variant="triton")
+        k8d, ksd = sa.quant_per_block_int8(kb.to(dev), 64, mean=km.to(dev), tensor_layout="NHD", variant="triton")
+        vtd = sa.v_tile_half(vb.to(dev).to(torch.float16), "NHD")
+        L.qattn_set_kernel(_lib.QATTN_KERNEL_ONE_BLOCK)
+        try:
+            od = sa.qattn_fwd(q8d, qsd, k8d, ksd, vtd, None, tensor_layout="NHD", out_dtype=torch.bfloat16,
+                              is_causal=causal, num_splits=1)
+        finally:
+            L.qattn_set_kernel(_lib.QATTN_KERNEL_AUTO)
+        assert torch.equal(od[0].cpu(), o[rows].cpu()), f"seq {b}: varlen launch differs from the dense launch"
         c, ct = cosine(got, ref), cosine(got, truth)
-        log(f"  seq {b}: lq={lq[b]} lk={lk[b]} cos_oracle={c:.6f} cos_truth={ct:.6f}")
+        err = float(np.abs(got - ref).max())
+        log(f"  seq {b}: lq={lq[b]} lk={lk[b]} cos_oracle={c:.6f} cos_truth={ct:.6f} max|d|={err:.3g}")
         assert c >= COS_KERNEL
         assert ct >= COS_E2E
 
