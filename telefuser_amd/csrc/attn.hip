@@ -102,6 +102,10 @@ struct AttnParams {
   const int32_t* cu_qs;
   const int32_t* cu_ks;
   const int32_t* cu_vt;
+  // resident-K/V launches: each workgroup takes wb_per_wg consecutive 32-row wave blocks of one head,
+  // n_chunk workgroups per (batch, head)
+  int64_t wb_per_wg;
+  int64_t n_chunk;
 };
 
 __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t n) {
@@ -153,6 +157,14 @@ __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
     __builtin_memcpy(&r, &v, 4);
   }
   return r;
+}
+
+// One output value: O / l * v_scale (+ v_mean for smoothed V), rounded after every operation (no fused
+// multiply-add), so that every kernel and the split combine produce the same bits.
+__device__ __forceinline__ float epilogue_value(float o, float inv_l, float sc, float vm, bool add_mean) {
+#pragma clang fp contract(off)
+  const float x = o * inv_l * sc;
+  return add_mean ? x + vm : x;
 }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -465,13 +477,10 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
           const int d = dblk * 32 + g * 8 + hf * 4;
           const v4f sc = PV == PV_FP8 ? *reinterpret_cast<const v4f*>(&lds_vs[d]) : v4f{1.f, 1.f, 1.f, 1.f};
           float f[4];
+          const v4f vm = PV == PV_FP8 ? *reinterpret_cast<const v4f*>(&lds_vm[d]) : v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int e = 0; e < 4; e++) f[e] = o[dblk][g * 4 + e] * inv_l * sc[e];
-          if (PV == PV_FP8 && p.v_mean) {
-            const v4f vm = *reinterpret_cast<const v4f*>(&lds_vm[d]);
-#pragma unroll
-            for (int e = 0; e < 4; e++) f[e] += vm[e];
-          }
+          for (int e = 0; e < 4; e++)
+            f[e] = epilogue_value(o[dblk][g * 4 + e], inv_l, sc[e], vm[e], PV == PV_FP8 && p.v_mean);
           const v2u packed{pack_half2<IS_FP16_OUT>(f[0], f[1]), pack_half2<IS_FP16_OUT>(f[2], f[3])};
           const int c = db * 4 + g;  // 16-byte chunk of the staged 128-byte row (8 channels)
           *reinterpret_cast<v2u*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4) + hf * 8) = packed;
@@ -1036,13 +1045,9 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
         const int d = dblk * 32 + g * 8 + hf * 4;
         const v4f sc = *reinterpret_cast<const v4f*>(&lds_vs[d]);
         float f[4];
+        const v4f vm = *reinterpret_cast<const v4f*>(&lds_vm[d]);
 #pragma unroll
-        for (int e = 0; e < 4; e++) f[e] = o[dblk][g * 4 + e] * inv_l * sc[e];
-        if (p.v_mean) {
-          const v4f vm = *reinterpret_cast<const v4f*>(&lds_vm[d]);
-#pragma unroll
-          for (int e = 0; e < 4; e++) f[e] += vm[e];
-        }
+        for (int e = 0; e < 4; e++) f[e] = epilogue_value(o[dblk][g * 4 + e], inv_l, sc[e], vm[e], p.v_mean != nullptr);
         const v2u packed{pack_half2<IS_FP16_OUT>(f[0], f[1]), pack_half2<IS_FP16_OUT>(f[2], f[3])};
         const int c = db * 4 + g;
         *reinterpret_cast<v2u*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4) + hf * 8) = packed;
@@ -1065,6 +1070,242 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
 template <bool IS_FP16_OUT, bool KT>
 __global__ __launch_bounds__(kPPThreads) void qattn_fwd_pp_kernel(AttnParams p) {
   qattn_fwd_pp<IS_FP16_OUT, KT>(p);
+}
+
+// ---- resident K/V: short key ranges (at most kResMaxTiles tiles, e.g. text cross-attention) ----
+//
+// The whole key range of a head (K int8 and e4m3 V, fragment-major as in the streaming kernels) is
+// loaded into LDS once per workgroup; then each of the 8 waves walks its own 32-row query blocks over
+// the resident tiles with no workgroup barrier at all: Q fragments come straight from global memory
+// (the next block's are in flight while the current one computes), the two waves of a SIMD drift apart
+// freely so that one's softmax overlaps the other's MFMAs, and O leaves through a 2 KiB wave-private
+// LDS stage as whole 64-byte row segments.  Per element the arithmetic is that of qattn_fwd_kernel
+// (same MFMA chains, masking, lazy running max, FP8 offset, row sums on the matrix pipe), so the
+// results are identical to it.
+constexpr int kResMaxTiles = 8;
+constexpr int kResThreads = 512;
+
+template <bool IS_FP16_OUT, bool KT>
+__global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p) {
+  constexpr int KS = ks_per_tile(KT);
+  constexpr int NW = kResThreads / 64;
+  __shared__ __align__(16) uint8_t lds_k[kResMaxTiles][kBK * kD];
+  __shared__ __align__(16) uint8_t lds_v[kResMaxTiles][kD * kBK];
+  __shared__ __align__(16) uint8_t lds_o[NW][32 * 64];
+  __shared__ float lds_ks[kResMaxTiles * 4];
+  __shared__ __align__(16) float lds_vs[kD];
+  __shared__ __align__(16) float lds_vm[kD];
+
+  const int64_t wg = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t chunk = wg % p.n_chunk;
+  const int64_t h = (wg / p.n_chunk) % p.Hq;
+  const int64_t b = wg / (p.n_chunk * p.Hq);
+  const int64_t hk = h / p.group;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31, hf = lane >> 5;
+
+  int64_t kv_end = p.Lk;
+  if (p.kv_valid) kv_end = min(kv_end, (int64_t)p.kv_valid[b]);
+  const int n_tiles = kv_end > 0 ? (int)((kv_end + kBK - 1) / kBK) : 0;
+
+  // ---- the key range into LDS: tile t of K / V in lds_k[t] / lds_v[t], fragment-major ----
+  {
+    const int8_t* kbase = p.k8 + b * p.ksb + hk * p.ksh;
+    const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad;
+    const int64_t kbytes = (p.Lk - 1) * p.ksl + kD;
+    const v4u vrsrc = make_rsrc(vbase, (uint32_t)((int64_t)kD * p.Lpad));
+    // DMA instruction i of wave w fills 1 KiB block f = 8 i' + w of a tile, i' = 0 (K) or V; 8 waves
+    // cover the 8 blocks of K and the 8 blocks of V of a tile in one instruction each
+    const int j = w;
+    const uint32_t koff = (uint32_t)(((j & 1) * 32 + lq) * p.ksl + (2 * (j >> 1) + hf) * 16);
+    const uint32_t voff = (uint32_t)(((j >> 1) * 32 + lq) * p.Lpad + (2 * hf + (j & 1)) * 16);
+    const uint32_t lk0 = lds_addr(&lds_k[0][0]) + w * 1024, lv0 = lds_addr(&lds_v[0][0]) + w * 1024;
+    for (int t = 0; t < n_tiles; t++) {
+      const int64_t kso = (int64_t)t * kBK * p.ksl;
+      const v4u krsrc = make_rsrc(kbase + kso, (uint32_t)(kbytes - kso));
+      lds_dma16(koff, krsrc, 0, lk0 + t * (kBK * kD));
+      lds_dma16(voff, vrsrc, (uint32_t)t * kBK, lv0 + t * (kD * kBK));
+    }
+    const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
+    if (tid < n_tiles * KS) lds_ks[tid] = ks_ptr[tid];
+    if (tid < kD) {
+      lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * kD + tid];
+      lds_vm[tid] = p.v_mean ? p.v_mean[(b * p.Hkv + hk) * kD + tid] : 0.f;
+    }
+  }
+
+  // this wave's 32-row blocks: wb = wb0 + w, wb0 + w + 8, ... below wb_end
+  const int64_t n_wb = (p.Lq + 31) / 32;
+  const int64_t wb0 = chunk * p.wb_per_wg;
+  const int64_t wb_end = min(n_wb, wb0 + p.wb_per_wg);
+  const int8_t* qhead = p.q8 + b * p.qsb + h * p.qsh;
+  const float* qs_tab = p.q_scale + (b * p.Hq + h) * p.nQS;
+  // lane (lq, hf) holds bytes 32 m + 16 hf .. + 16 of query row lq (the MFMA B operand)
+  auto load_q = [&](int64_t wb, v4i (&qf)[4]) {
+    const int64_t row = wb * 32 + lq;
+#pragma unroll
+    for (int m = 0; m < 4; m++)
+      qf[m] = row < p.Lq ? *reinterpret_cast<const v4i*>(qhead + row * p.qsl + m * 32 + hf * 16) : v4i{0, 0, 0, 0};
+  };
+  v4i qf[4], qn[4];
+  int64_t wb = wb0 + w;
+  if (wb < wb_end) load_q(wb, qn);
+  v16i kbias;
+#pragma unroll
+  for (int r = 0; r < 16; r++) kbias[r] = kAccBiasBits;
+  uint8_t* stage = &lds_o[w][0];
+  uint16_t* obase = static_cast<uint16_t*>(p.o) + b * p.osb + h * p.osh;
+
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();  // every wave's share of the key range has landed
+
+  for (; wb < wb_end; wb += NW) {
+#pragma unroll
+    for (int m = 0; m < 4; m++) qf[m] = qn[m];
+    if (wb + NW < wb_end) load_q(wb + NW, qn);
+    const int64_t wrow0 = wb * 32, qrow = wrow0 + lq;
+    const int64_t qsi = p.qgran == QATTN_GRAN_THREAD ? wb * 8 + (lq & 7) : p.qgran == QATTN_GRAN_WARP ? wb : wb / 4;
+    const float qs = qs_tab[qsi] * p.qk_mult;
+
+    v16f o[4], lacc;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) o[i][r] = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; r++) lacc[r] = 0.f;
+    float m_run = kMInit;
+
+    for (int t = 0; t < n_tiles; t++) {
+      float cs_a, cs_b;
+      if constexpr (KT) {
+        cs_a = qs * lds_ks[t * 4 + 2 * hf];
+        cs_b = qs * lds_ks[t * 4 + 2 * hf + 1];
+      } else {
+        cs_a = cs_b = qs * lds_ks[t];
+      }
+      v16i s[2];
+      {
+        v4i kf[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) kf[j] = *reinterpret_cast<const v4i*>(&lds_k[t][j * 1024 + lane * 16]);
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const int m = j >> 1, kb = j & 1;
+          s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j], qf[m], m == 0 ? kbias : s[kb], 0, 0, 0);
+        }
+        __builtin_amdgcn_s_setprio(0);
+      }
+      const int64_t k0 = (int64_t)t * kBK;
+      const bool masked = k0 + kBK > kv_end;
+      if (masked) {
+        const int lim = (int)min(kv_end - k0, (int64_t)kBK) - hf * 4;
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+          for (int r = 0; r < 16; r++)
+            if (kb * 32 + (r >> 2) * 8 + (r & 3) >= lim) s[kb][r] = INT32_MIN;
+      }
+      float m_tile;
+      if constexpr (!KT) {
+        int mx = max(s[0][0], s[0][1]);
+#pragma unroll
+        for (int r = 2; r < 16; r++) mx = max(mx, s[0][r]);
+#pragma unroll
+        for (int r = 0; r < 16; r++) mx = max(mx, s[1][r]);
+        const auto sw = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);
+        mx = max((int)sw[0], (int)sw[1]);
+        m_tile = mx == INT32_MIN ? kMInit : fmaf(__int_as_float(mx), cs_a, -fmaf(kAccBias, cs_a, kFp8Offset - kLazyTau));
+      } else {
+        int ma = INT32_MIN, mb = INT32_MIN;
+#pragma unroll
+        for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            if ((r & 3) < 2) ma = max(ma, s[kb][r]);
+            else mb = max(mb, s[kb][r]);
+          }
+        const float fa = ma == INT32_MIN ? kMInit : fmaf(__int_as_float(ma), cs_a, -fmaf(kAccBias, cs_a, kFp8Offset - kLazyTau));
+        const float fb = mb == INT32_MIN ? kMInit : fmaf(__int_as_float(mb), cs_b, -fmaf(kAccBias, cs_b, kFp8Offset - kLazyTau));
+        const float mt = fmaxf(fa, fb);
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+        m_tile = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+      }
+      const bool grow = m_tile > m_run + kLazyTau;
+      if (__any(grow)) {
+        const float m_new = grow ? m_tile : m_run;
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) o[i][r] *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; r++) lacc[r] *= alpha;
+        m_run = m_new;
+      }
+      const float nc_a = -fmaf(kAccBias, cs_a, m_run), nc_b = -fmaf(kAccBias, cs_b, m_run);
+      v8i pf;
+      auto body = [&](auto mk) {
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          const int kb = j >> 2, r0 = (j & 3) * 4;
+          float pv[4];
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const int sv = s[kb][r0 + e];
+            pv[e] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(sv), e < 2 ? cs_a : cs_b, e < 2 ? nc_a : nc_b));
+            if constexpr (decltype(mk)::value) pv[e] = sv == INT32_MIN ? 0.f : pv[e];
+          }
+          const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], __builtin_nondeterministic_value(0), false);
+          pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
+        }
+      };
+      if (masked) body(std::true_type{});
+      else body(std::false_type{});
+      v8i vf[4];
+#pragma unroll
+      for (int dblk = 0; dblk < 4; dblk++) {
+        const v4i a0 = *reinterpret_cast<const v4i*>(&lds_v[t][(2 * dblk) * 1024 + lane * 16]);
+        const v4i a1 = *reinterpret_cast<const v4i*>(&lds_v[t][(2 * dblk + 1) * 1024 + lane * 16]);
+        vf[dblk] = v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+      }
+#pragma unroll
+      for (int dblk = 0; dblk < 4; dblk++)
+        o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, o[dblk], 0, 0, 0, 0, 0, 0);
+      lacc = row_sum_mfma(lacc, pf);
+    }
+
+    // ---- epilogue: O / l * v_scale (+ v_mean), 32 channels per pass through the 2 KiB stage ----
+    const float l_tot = lacc[0];
+    const float inv_l = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+#pragma unroll
+    for (int dblk = 0; dblk < 4; dblk++) {
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int d = dblk * 32 + g * 8 + hf * 4;
+        const v4f sc = *reinterpret_cast<const v4f*>(&lds_vs[d]);
+        const v4f vm = *reinterpret_cast<const v4f*>(&lds_vm[d]);
+        float f[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) f[e] = epilogue_value(o[dblk][g * 4 + e], inv_l, sc[e], vm[e], p.v_mean != nullptr);
+        const v2u packed{pack_half2<IS_FP16_OUT>(f[0], f[1]), pack_half2<IS_FP16_OUT>(f[2], f[3])};
+        // stage row lq: 4 chunks of 16 B (8 channels), chunk g stored at g ^ (lq & 3)
+        *reinterpret_cast<v2u*>(stage + lq * 64 + ((g ^ (lq & 3)) << 4) + hf * 8) = packed;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+      for (int i = 0; i < 2; i++) {
+        const int id = i * 64 + lane, r = id >> 2, c = id & 3;
+        const v4u val = *reinterpret_cast<const v4u*>(stage + r * 64 + ((c ^ (r & 3)) << 4));
+        const int64_t row = wrow0 + r;
+        if (row < p.Lq) *reinterpret_cast<v4u*>(obase + row * p.osl + dblk * 32 + c * 8) = val;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    }
+    if (p.lse && hf == 0 && qrow < p.Lq)
+      p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
+  }
 }
 
 // Merge the KV-split partials: one wave per query row, 2 channels per lane.
@@ -1093,12 +1334,9 @@ __global__ __launch_bounds__(256) void qattn_combine_kernel(AttnParams p) {
   const float inv = L > 0.f ? 1.0f / L : 0.f;
   const float* vs = p.v_scale ? p.v_scale + (b * p.Hkv + hk) * kD + lane * 2 : nullptr;
   uint16_t* orow = static_cast<uint16_t*>(p.o) + b * p.osb + qrow * p.osl + h * p.osh + lane * 2;
-  float r0 = a0 * inv * (vs ? vs[0] : 1.f), r1 = a1 * inv * (vs ? vs[1] : 1.f);
-  if (p.v_mean) {
-    const float* vm = p.v_mean + (b * p.Hkv + hk) * kD + lane * 2;
-    r0 += vm[0];
-    r1 += vm[1];
-  }
+  const float* vm = p.v_mean ? p.v_mean + (b * p.Hkv + hk) * kD + lane * 2 : nullptr;
+  const float r0 = epilogue_value(a0, inv, vs ? vs[0] : 1.f, vm ? vm[0] : 0.f, vm != nullptr);
+  const float r1 = epilogue_value(a1, inv, vs ? vs[1] : 1.f, vm ? vm[1] : 0.f, vm != nullptr);
   orow[0] = f32_to_half<IS_FP16_OUT>(r0);
   orow[1] = f32_to_half<IS_FP16_OUT>(r1);
   if (p.lse && lane == 0) p.lse[(b * p.Hq + h) * p.Lq + qrow] = L > 0.f ? __builtin_log2f(L) + M : -INFINITY;
@@ -1162,21 +1400,44 @@ static thread_local int t_last_kernel = QATTN_KERNEL_AUTO;
 
 extern "C" int qattn_set_kernel(int kernel) {
   const int prev = t_kernel_override;
-  if (kernel >= QATTN_KERNEL_AUTO && kernel <= QATTN_KERNEL_PINGPONG) t_kernel_override = kernel;
+  if (kernel >= QATTN_KERNEL_AUTO && kernel <= QATTN_KERNEL_RESIDENT) t_kernel_override = kernel;
   return prev;
 }
 
 extern "C" int qattn_last_kernel(void) { return t_last_kernel; }
 
-// the kernel a launch runs, given its split count and whether the multi-block layout applies
+// the kernel a launch runs, given its split count and whether the multi-block / resident layouts apply
 static int pick_kernel(int pv, bool sparse, int ns, int causal, int64_t B, int64_t Hq, int64_t nQB, int qpw_auto,
-                       bool mq_ok) {
+                       bool mq_ok, bool res_ok) {
   if (pv != PV_FP8 || sparse || ns > 1) return QATTN_KERNEL_ONE_BLOCK;
   const int ov = t_kernel_override;
   if (ov == QATTN_KERNEL_PINGPONG || ov == QATTN_KERNEL_ONE_BLOCK) return ov;
   if (ov == QATTN_KERNEL_MULTI_BLOCK && mq_ok && !causal) return QATTN_KERNEL_MULTI_BLOCK;
+  if (ov == QATTN_KERNEL_RESIDENT && res_ok) return QATTN_KERNEL_RESIDENT;
+  if (res_ok) return QATTN_KERNEL_RESIDENT;
   if (qpw_auto > 1) return QATTN_KERNEL_MULTI_BLOCK;
   return B * Hq * ((nQB + 1) / 2) >= 256 ? QATTN_KERNEL_PINGPONG : QATTN_KERNEL_ONE_BLOCK;
+}
+
+// Resident-K/V launches: the 32-row wave blocks of each (batch, head) are cut into n_chunk workgroups
+// of wb_per_wg blocks.  One workgroup runs per CU (its LDS holds the key range), 8 waves each taking
+// every 8th block; the cut minimises full rounds of 256 workgroups x (wave rounds per workgroup + one
+// round of start-up for the key-range load).
+static void resident_layout(int64_t bh, int64_t n_wb, int64_t& wb_per_wg, int64_t& n_chunk) {
+  double best = 1e300;
+  wb_per_wg = n_wb;
+  n_chunk = 1;
+  for (int64_t c = 1; c <= std::max<int64_t>(1, (n_wb + 7) / 8); c++) {
+    const int64_t per = (n_wb + c - 1) / c;
+    const int64_t chunks = (n_wb + per - 1) / per;
+    const int64_t rounds = (bh * chunks + 255) / 256;
+    const double cost = (double)rounds * (double)((per + 7) / 8 + 1);
+    if (cost < best) {
+      best = cost;
+      wb_per_wg = per;
+      n_chunk = chunks;
+    }
+  }
 }
 
 template <int PV, bool KT, bool SP = false>
@@ -1192,6 +1453,16 @@ static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, siz
       QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
       if (out_dtype == QATTN_BF16) qattn_fwd_kernel<false, false, PV, KT, false, true><<<g, kThreads, 0, st>>>(p);
       else qattn_fwd_kernel<true, false, PV, KT, false, true><<<g, kThreads, 0, st>>>(p);
+      return check_launch("qattn_fwd");
+    }
+    if (kernel == QATTN_KERNEL_RESIDENT) {
+      p.nsplit = 1;
+      p.tiles_per_split = (int)p.nKB;
+      resident_layout(p.B * p.Hq, (p.Lq + 31) / 32, p.wb_per_wg, p.n_chunk);
+      const int64_t g = p.B * p.Hq * p.n_chunk;
+      QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
+      if (out_dtype == QATTN_BF16) qattn_fwd_res_kernel<false, KT><<<g, kResThreads, 0, st>>>(p);
+      else qattn_fwd_res_kernel<true, KT><<<g, kResThreads, 0, st>>>(p);
       return check_launch("qattn_fwd");
     }
     if (kernel == QATTN_KERNEL_PINGPONG) {
@@ -1257,8 +1528,9 @@ static void plan_fwd(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int pv, int 
   // a workgroup stages the k_scales of at most max_tiles key tiles
   ns = (int)std::max<int64_t>(ns, (nKB + max_tiles - 1) / max_tiles);
   const bool mq_ok = ns == 1 && !sparse && !causal && pv == PV_FP8 && nKB <= kMqMaxTiles;
+  const bool res_ok = ns == 1 && !sparse && !causal && pv == PV_FP8 && nKB <= kResMaxTiles;
   const int qpw_auto = mq_ok ? blocks_per_workgroup(B * Hq, nQB, nKB) : 1;
-  kernel = pick_kernel(pv, sparse, ns, causal, B, Hq, nQB, qpw_auto, mq_ok);
+  kernel = pick_kernel(pv, sparse, ns, causal, B, Hq, nQB, qpw_auto, mq_ok, res_ok);
   qpw = kernel == QATTN_KERNEL_MULTI_BLOCK ? qpw_auto : 1;
 }
 

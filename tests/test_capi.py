@@ -95,10 +95,13 @@ def test_fwd_ex_granularity_validation_and_splits(lib):
 
 def test_kernel_selection_rule(lib):
     """qattn_fwd_ex_kernel reports the automatic choice; qattn_set_kernel overrides it per thread."""
-    one, multi, pp = 1, 2, 3
+    one, multi, pp, res = 1, 2, 3, 4
     assert lib.qattn_fwd_ex_kernel(1, 32760, 32760, 12, 0, 1, 0, 0) == pp      # C2: 1536 ping-pong workgroups
     assert lib.qattn_fwd_ex_kernel(1, 32760, 32760, 12, 0, 3, 0, 0) == pp      # per-thread scales, same rule
-    assert lib.qattn_fwd_ex_kernel(1, 75600, 512, 40, 0, 1, 0, 0) == multi     # C4: short key range
+    assert lib.qattn_fwd_ex_kernel(1, 75600, 512, 40, 0, 1, 0, 0) == res       # C4: key range fits in LDS
+    assert lib.qattn_fwd_ex_kernel(1, 75600, 513, 40, 0, 1, 0, 0) == multi     # 9 tiles: streamed
+    assert lib.qattn_fwd_ex_kernel(1, 75600, 512, 40, 0, 1, 1, 0) != res       # causal: resident does not apply
+    assert lib.qattn_fwd_ex_kernel(1, 75600, 512, 40, 1, 1, 0, 0) == one       # half P.V
     assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 12, 0, 1, 0, 0) == one      # C5: KV split
     assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 0) == one        # C1: grid too small
     assert lib.qattn_fwd_ex_kernel(1, 32760, 32760, 12, 1, 1, 0, 0) == one     # half P.V
@@ -109,6 +112,11 @@ def test_kernel_selection_rule(lib):
         lib.qattn_set_kernel(multi)
         assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 1, 1) == one    # causal: multi-block does not apply
         assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 1) == multi
+        lib.qattn_set_kernel(res)
+        assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 1) == one    # 16 tiles: resident does not apply
+        assert lib.qattn_fwd_ex_kernel(1, 1024, 300, 2, 0, 1, 0, 1) == res
+        lib.qattn_set_kernel(one)
+        assert lib.qattn_fwd_ex_kernel(1, 75600, 512, 40, 0, 1, 0, 0) == one
     finally:
         lib.qattn_set_kernel(prev)
     assert lib.qattn_set_kernel(0) == 0

@@ -23,7 +23,7 @@ LSE_ROUNDED_SUM_BOUND = 0.0931  # log2(16/15): bound of the rounded-vs-unrounded
 
 
 GRAN_CODE = {"per_block": 1, "per_warp": 2, "per_thread": 3}
-KERNEL_ONE_BLOCK, KERNEL_MULTI_BLOCK, KERNEL_PINGPONG = 1, 2, 3  # enum qattn_kernel
+KERNEL_ONE_BLOCK, KERNEL_MULTI_BLOCK, KERNEL_PINGPONG, KERNEL_RESIDENT = 1, 2, 3, 4  # enum qattn_kernel
 
 
 def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None, num_splits=0, q_offset=0,
@@ -398,7 +398,7 @@ def test_multi_block_workgroups(oracle, case):
 
     gran, layout, dt = ("per_block", "NHD", torch.bfloat16) if case == "block_nhd_bf16" else \
         ("per_thread", "HND", torch.float16)
-    B, Lq, Lk, H, D = 2, 16300, 500, 20, 128
+    B, Lq, Lk, H, D = 2, 16300, 600, 20, 128  # 10 key tiles: past the resident kernel
     kv_valid = [300, 0]
     L = _lib.load()
     qpw = L.qattn_fwd_ex_blocks_per_workgroup(B, Lq, Lk, H, 0, GRAN_CODE[gran], 0)
@@ -449,6 +449,77 @@ def test_multi_block_workgroups(oracle, case):
     log(f"  head 7 vs quantized oracle: cosine={c:.6f} max_abs={float(np.abs(og - ref).max()):.4g}")
     assert c >= COS_KERNEL
     assert float(np.max(np.abs(lse[:1, 7:8].cpu().numpy() - ref_lse))) < 2e-2
+
+
+@pytest.mark.parametrize("case", ["padding", "ragged", "empty_batch", "gqa_hnd_thread", "fp16_warp_gqa", "one_tile",
+                                  "tiny", "smooth_v", "many_blocks"])
+def test_resident_kernel_matches(oracle, case):
+    """The resident-K/V kernel (whole key range in LDS, 8 barrier-free waves per workgroup, each on its own
+    32-row query blocks) runs the per-element arithmetic of qattn_fwd_kernel, so output and LSE must be
+    identical, bit for bit, on the same operands.  Checked with key padding (a tail tile of 44 keys), one
+    batch without any valid key, ragged lengths whose last wave block is partial, GQA + HND + per-thread
+    scales, GQA + per-warp scales + fp16 output, a single tile, fewer queries than one wave block,
+    smoothed V (v_mean epilogue), and enough query blocks that every wave walks many of them; the
+    automatic rule must pick the kernel for these non-causal FP8 launches with Lk <= 512, and the
+    padding case is also checked against the oracle."""
+    dev = require_gpu()
+    from telefuser_amd import _lib
+    from telefuser_amd import sageattn2 as sa
+
+    B, Lq, Lk, Hq, Hkv, layout, kv_valid, gran = {
+        "padding": (1, 1500, 512, 4, 4, "NHD", [300], "per_block"),
+        "ragged": (2, 1001, 333, 3, 3, "NHD", None, "per_block"),
+        "empty_batch": (2, 700, 450, 2, 2, "NHD", [450, 0], "per_block"),
+        "gqa_hnd_thread": (1, 2000, 500, 4, 2, "HND", None, "per_thread"),
+        "fp16_warp_gqa": (1, 900, 260, 6, 2, "NHD", None, "per_warp"),
+        "one_tile": (1, 640, 64, 2, 2, "NHD", None, "per_block"),
+        "tiny": (1, 31, 7, 1, 1, "NHD", None, "per_block"),
+        "smooth_v": (1, 1200, 400, 2, 2, "NHD", [390], "per_block"),
+        "many_blocks": (1, 40000, 300, 2, 2, "NHD", None, "per_block"),
+    }[case]
+    log(f"resident vs one-block: {case} B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} layout={layout} "
+        f"kv_valid={kv_valid} gran={gran}")
+    q, k, v = qkv(B, Lq, Lk, Hq, Hkv, seed=4343, k_offset_std=0.5)
+    qd, kd, vd = (t.to(dev) for t in (q, k, v))
+    if layout == "HND":
+        qd, kd, vd = (t.transpose(1, 2).contiguous() for t in (qd, kd, vd))
+    km = sa.k_mean(kd, layout)
+    qk_mult = 1.0
+    if gran == "per_block":
+        q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=128 ** -0.5, tensor_layout=layout)
+    else:
+        quant = sa.per_thread_int8 if gran == "per_thread" else sa.per_warp_int8
+        q8, qs, k8, ks = quant(qd, kd, km, tensor_layout=layout)
+        qk_mult = 128 ** -0.5 * LOG2E
+    v8, vs, vm = sa.per_channel_fp8(vd, tensor_layout=layout, smooth_v=case == "smooth_v")
+    out_dtype = torch.float16 if case == "fp16_warp_gqa" else torch.bfloat16
+    kw = dict(tensor_layout=layout, out_dtype=out_dtype, is_causal=False, kv_valid_len=kv_valid,
+              return_lse=True, qk_mult=qk_mult, qk_quant_gran=gran, num_splits=1, v_mean=vm)
+    L = _lib.load()
+    assert L.qattn_fwd_ex_kernel(B, Lq, Lk, Hq, 0, _lib.QATTN_GRAN_BLOCK, 0, 0) == KERNEL_RESIDENT
+    prev = L.qattn_set_kernel(KERNEL_ONE_BLOCK)
+    try:
+        o0, l0 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
+        assert L.qattn_last_kernel() == KERNEL_ONE_BLOCK
+        L.qattn_set_kernel(_lib.QATTN_KERNEL_AUTO)
+        o1, l1 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
+        assert L.qattn_last_kernel() == KERNEL_RESIDENT
+        o2, l2 = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, **kw)
+    finally:
+        L.qattn_set_kernel(prev)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(l1, l2), "resident kernel is not deterministic"
+    assert torch.equal(o0, o1), f"resident kernel differs: max {float((o0.float() - o1.float()).abs().max()):.4g}"
+    assert torch.equal(l0, l1)
+    if case == "empty_batch":  # no valid key: zero output, LSE -inf
+        assert bool((o1[1] == 0).all()) and bool(torch.isneginf(l1[1]).all())
+    if case == "padding":
+        ref = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
+                               ks.cpu().numpy(), v8=untile_v(v8), v_scale=vs.cpu().numpy(), kv_valid=kv_valid,
+                               lazy_tau=KERNEL_LAZY_TAU)
+        c = cosine(o1.float().cpu().numpy(), ref)
+        log(f"  resident padding cos_oracle={c:.6f}")
+        assert c >= COS_KERNEL
 
 
 @pytest.mark.parametrize("case", ["ragged", "padding", "empty_batch", "causal", "causal_odd", "gqa_hnd_thread",
