@@ -161,10 +161,12 @@ __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
 
 // One output value: O / l * v_scale (+ v_mean for smoothed V), rounded after every operation (no fused
 // multiply-add), so that every kernel and the split combine produce the same bits.
-__device__ __forceinline__ float epilogue_value(float o, float inv_l, float sc, float vm, bool add_mean) {
+template <bool ADD_MEAN>
+__device__ __forceinline__ float epilogue_value(float o, float inv_l, float sc, float vm) {
 #pragma clang fp contract(off)
   const float x = o * inv_l * sc;
-  return add_mean ? x + vm : x;
+  if constexpr (ADD_MEAN) return x + vm;
+  else return x;
 }
 
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -467,6 +469,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
     // barrier; multi-block launches use their own region), 64 channels per pass, so that every row is
     // stored as whole 128-byte lines
     uint16_t* obase = ob + h * p.osh;
+    auto store = [&](auto mean_t) {
+    constexpr bool kMean = decltype(mean_t)::value;
 #pragma unroll
     for (int pass = 0; pass < 2; pass++) {
 #pragma unroll
@@ -477,10 +481,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
           const int d = dblk * 32 + g * 8 + hf * 4;
           const v4f sc = PV == PV_FP8 ? *reinterpret_cast<const v4f*>(&lds_vs[d]) : v4f{1.f, 1.f, 1.f, 1.f};
           float f[4];
-          const v4f vm = PV == PV_FP8 ? *reinterpret_cast<const v4f*>(&lds_vm[d]) : v4f{0.f, 0.f, 0.f, 0.f};
+          const v4f vm = kMean ? *reinterpret_cast<const v4f*>(&lds_vm[d]) : v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int e = 0; e < 4; e++)
-            f[e] = epilogue_value(o[dblk][g * 4 + e], inv_l, sc[e], vm[e], PV == PV_FP8 && p.v_mean);
+          for (int e = 0; e < 4; e++) f[e] = epilogue_value<kMean>(o[dblk][g * 4 + e], inv_l, sc[e], vm[e]);
           const v2u packed{pack_half2<IS_FP16_OUT>(f[0], f[1]), pack_half2<IS_FP16_OUT>(f[2], f[3])};
           const int c = db * 4 + g;  // 16-byte chunk of the staged 128-byte row (8 channels)
           *reinterpret_cast<v2u*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4) + hf * 8) = packed;
@@ -496,6 +499,9 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
+    };
+    if (PV == PV_FP8 && p.v_mean) store(std::true_type{});
+    else store(std::false_type{});
     if (p.lse && hf == 0 && qrow < Lq)
       p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
   };
@@ -1035,6 +1041,8 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   const float l_tot = lacc[0];
   const float inv_l = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   uint16_t* obase = static_cast<uint16_t*>(p.o) + b * p.osb + h * p.osh;
+  auto store = [&](auto mean_t) {
+  constexpr bool kMean = decltype(mean_t)::value;
 #pragma unroll
   for (int pass = 0; pass < 2; pass++) {
 #pragma unroll
@@ -1045,9 +1053,9 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
         const int d = dblk * 32 + g * 8 + hf * 4;
         const v4f sc = *reinterpret_cast<const v4f*>(&lds_vs[d]);
         float f[4];
-        const v4f vm = *reinterpret_cast<const v4f*>(&lds_vm[d]);
+        const v4f vm = kMean ? *reinterpret_cast<const v4f*>(&lds_vm[d]) : v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int e = 0; e < 4; e++) f[e] = epilogue_value(o[dblk][g * 4 + e], inv_l, sc[e], vm[e], p.v_mean != nullptr);
+        for (int e = 0; e < 4; e++) f[e] = epilogue_value<kMean>(o[dblk][g * 4 + e], inv_l, sc[e], vm[e]);
         const v2u packed{pack_half2<IS_FP16_OUT>(f[0], f[1]), pack_half2<IS_FP16_OUT>(f[2], f[3])};
         const int c = db * 4 + g;
         *reinterpret_cast<v2u*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4) + hf * 8) = packed;
@@ -1063,6 +1071,9 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     }
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   }
+  };
+  if (p.v_mean) store(std::true_type{});
+  else store(std::false_type{});
   if (p.lse && hf == 0 && qrow < p.Lq)
     p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
 }
@@ -1168,15 +1179,13 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
     const float qs = qs_tab[qsi] * p.qk_mult;
 
     v16f o[4], lacc;
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) o[i][r] = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; r++) lacc[r] = 0.f;
     float m_run = kMInit;
-
-    for (int t = 0; t < n_tiles; t++) {
+    // One key tile.  The first tile of a block is peeled: its running max is the tile max and its P.V
+    // starts from zero accumulators, which is what the general step computes there (the rescale factor
+    // exp2(kMInit - m) is 0 while O and l are still 0, and a first tile always holds a valid key),
+    // without zeroing O and l and without the O rescale.
+    auto tile = [&](int t, auto first_t) {
+      constexpr bool kFirst = decltype(first_t)::value;
       float cs_a, cs_b;
       if constexpr (KT) {
         cs_a = qs * lds_ks[t * 4 + 2 * hf];
@@ -1232,17 +1241,21 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
         m_tile = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
       }
-      const bool grow = m_tile > m_run + kLazyTau;
-      if (__any(grow)) {
-        const float m_new = grow ? m_tile : m_run;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      if constexpr (kFirst) {
+        m_run = m_tile;
+      } else {
+        const bool grow = m_tile > m_run + kLazyTau;
+        if (__any(grow)) {
+          const float m_new = grow ? m_tile : m_run;
+          const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+          for (int i = 0; i < 4; i++)
 #pragma unroll
-          for (int r = 0; r < 16; r++) o[i][r] *= alpha;
+            for (int r = 0; r < 16; r++) o[i][r] *= alpha;
 #pragma unroll
-        for (int r = 0; r < 16; r++) lacc[r] *= alpha;
-        m_run = m_new;
+          for (int r = 0; r < 16; r++) lacc[r] *= alpha;
+          m_run = m_new;
+        }
       }
       const float nc_a = -fmaf(kAccBias, cs_a, m_run), nc_b = -fmaf(kAccBias, cs_b, m_run);
       v8i pf;
@@ -1270,25 +1283,39 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
         const v4i a1 = *reinterpret_cast<const v4i*>(&lds_v[t][(2 * dblk + 1) * 1024 + lane * 16]);
         vf[dblk] = v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
       }
+      const v16f zero = {};
 #pragma unroll
       for (int dblk = 0; dblk < 4; dblk++)
-        o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, o[dblk], 0, 0, 0, 0, 0, 0);
-      lacc = row_sum_mfma(lacc, pf);
+        o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, kFirst ? zero : o[dblk], 0, 0, 0, 0, 0, 0);
+      lacc = row_sum_mfma(kFirst ? zero : lacc, pf);
+    };
+    if (n_tiles > 0) {
+      tile(0, std::true_type{});
+      for (int t = 1; t < n_tiles; t++) tile(t, std::false_type{});
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) o[i][r] = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; r++) lacc[r] = 0.f;
     }
 
     // ---- epilogue: O / l * v_scale (+ v_mean), 32 channels per pass through the 2 KiB stage ----
     const float l_tot = lacc[0];
     const float inv_l = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+    auto store = [&](auto mean_t) {
+    constexpr bool kMean = decltype(mean_t)::value;
 #pragma unroll
     for (int dblk = 0; dblk < 4; dblk++) {
 #pragma unroll
       for (int g = 0; g < 4; g++) {
         const int d = dblk * 32 + g * 8 + hf * 4;
         const v4f sc = *reinterpret_cast<const v4f*>(&lds_vs[d]);
-        const v4f vm = *reinterpret_cast<const v4f*>(&lds_vm[d]);
+        const v4f vm = kMean ? *reinterpret_cast<const v4f*>(&lds_vm[d]) : v4f{0.f, 0.f, 0.f, 0.f};
         float f[4];
 #pragma unroll
-        for (int e = 0; e < 4; e++) f[e] = epilogue_value(o[dblk][g * 4 + e], inv_l, sc[e], vm[e], p.v_mean != nullptr);
+        for (int e = 0; e < 4; e++) f[e] = epilogue_value<kMean>(o[dblk][g * 4 + e], inv_l, sc[e], vm[e]);
         const v2u packed{pack_half2<IS_FP16_OUT>(f[0], f[1]), pack_half2<IS_FP16_OUT>(f[2], f[3])};
         // stage row lq: 4 chunks of 16 B (8 channels), chunk g stored at g ^ (lq & 3)
         *reinterpret_cast<v2u*>(stage + lq * 64 + ((g ^ (lq & 3)) << 4) + hf * 8) = packed;
@@ -1303,6 +1330,9 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
+    };
+    if (p.v_mean) store(std::true_type{});
+    else store(std::false_type{});
     if (p.lse && hf == 0 && qrow < p.Lq)
       p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
   }
@@ -1335,8 +1365,8 @@ __global__ __launch_bounds__(256) void qattn_combine_kernel(AttnParams p) {
   const float* vs = p.v_scale ? p.v_scale + (b * p.Hkv + hk) * kD + lane * 2 : nullptr;
   uint16_t* orow = static_cast<uint16_t*>(p.o) + b * p.osb + qrow * p.osl + h * p.osh + lane * 2;
   const float* vm = p.v_mean ? p.v_mean + (b * p.Hkv + hk) * kD + lane * 2 : nullptr;
-  const float r0 = epilogue_value(a0, inv, vs ? vs[0] : 1.f, vm ? vm[0] : 0.f, vm != nullptr);
-  const float r1 = epilogue_value(a1, inv, vs ? vs[1] : 1.f, vm ? vm[1] : 0.f, vm != nullptr);
+  const float r0 = vm ? epilogue_value<true>(a0, inv, vs ? vs[0] : 1.f, vm[0]) : epilogue_value<false>(a0, inv, vs ? vs[0] : 1.f, 0.f);
+  const float r1 = vm ? epilogue_value<true>(a1, inv, vs ? vs[1] : 1.f, vm[1]) : epilogue_value<false>(a1, inv, vs ? vs[1] : 1.f, 0.f);
   orow[0] = f32_to_half<IS_FP16_OUT>(r0);
   orow[1] = f32_to_half<IS_FP16_OUT>(r1);
   if (p.lse && lane == 0) p.lse[(b * p.Hq + h) * p.Lq + qrow] = L > 0.f ? __builtin_log2f(L) + M : -INFINITY;
