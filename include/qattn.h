@@ -180,6 +180,23 @@ int qattn_v_tile_half(qattn_seq v, int dtype, int64_t B, int64_t L, int64_t H, i
                       int64_t Lpad, qattn_stream_t stream);
 
 /*
+ * The prologue of the INT8-QK / FP8-PV path in four launches: one pass over K and V for their column
+ * statistics (K sum when smooth_k; V max |v|, or sum / max / min when smooth_v), one finalize (k_mean
+ * [B, Hkv, D] in the input dtype, v_scale, v_mean), V to FP8 tiles (as qattn_per_channel_fp8_ex), and K then
+ * Q to INT8 in one launch (qk_quant_gran 1: per block, Q times q_sm_scale = sm_scale * log2(e), CUDA
+ * rounding; 2: per warp; 3: per thread, as qattn_quant_qk_per_warp_int8 / _per_thread_int8).  Outputs are
+ * bit-identical to qattn_seq_mean + the quantizer + qattn_per_channel_fp8_ex.  Replaces the quantization
+ * block of sageattn_qk_int8_pv_fp8_cuda (tf-kernel/tf_kernel/sageattn2.py:1334-1383), which the reference
+ * runs as separate kernels.  workspace: qattn_sage_quant_workspace_size bytes.
+ */
+size_t qattn_sage_quant_workspace_size(int64_t B, int64_t Lk, int64_t Hkv, int64_t D);
+int qattn_sage_quant(qattn_seq q, qattn_seq k, qattn_seq v, int dtype, int64_t B, int64_t Lq, int64_t Lk, int64_t Hq,
+                     int64_t Hkv, int64_t D, int qk_quant_gran, float q_sm_scale, int smooth_k, float scale_max,
+                     int smooth_v, qattn_seq q_out, float* q_scale, qattn_seq k_out, float* k_scale, void* k_mean,
+                     uint8_t* v8, int64_t Lpad, float* v_scale, float* v_mean, void* workspace,
+                     size_t workspace_bytes, qattn_stream_t stream);
+
+/*
  * Packed variable-length batches: sequence b spans rows cu_seqlens[b] .. cu_seqlens[b + 1] of a packed
  * [total, H, D] tensor (int32 device tables of B + 1 entries, read only on the device).
  *

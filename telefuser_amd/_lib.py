@@ -44,6 +44,8 @@ EXPORTED = (
     "qattn_fwd",
     "qattn_v_tile_half",
     "qattn_fwd_pv16",
+    "qattn_sage_quant_workspace_size",
+    "qattn_sage_quant",
     "qattn_varlen_offsets",
     "qattn_quant_qk_varlen_int8",
     "qattn_v_tile_half_varlen",
@@ -133,6 +135,11 @@ def load() -> ctypes.CDLL:
     L.qattn_norm_rope_seq_mean.argtypes = [S, i32, i64, i64, i64, i64, vp, vp, vp, vp, i64, vp, vp, sz, vp]
     L.qattn_norm_rope_quant_qk.argtypes = [S, S, i32, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp, i64, vp, S, S, vp,
                                            vp, f32, i32, vp]
+    L.qattn_sage_quant_workspace_size.argtypes = [i64, i64, i64, i64]
+    L.qattn_sage_quant_workspace_size.restype = sz
+    L.qattn_sage_quant.argtypes = [S, S, S, i32, i64, i64, i64, i64, i64, i64, i32, f32, i32, f32, i32, S, vp, S, vp,
+                                   vp, vp, i64, vp, vp, vp, sz, vp]
+    L.qattn_sage_quant.restype = i32
     L.qattn_varlen_offsets.argtypes = [vp, vp, i64, vp, vp, vp, vp]
     L.qattn_quant_qk_varlen_int8.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, vp, vp, vp, vp, S, S, vp,
                                              vp, f32, i32, vp]

@@ -250,12 +250,12 @@ constexpr int kColChunk = 256;  // sequence rows per workgroup
 
 // MODE 0: sum; 1: max |x|; 2: sum, max and min (V smoothing), stored as three D-vectors per chunk
 template <bool IS_FP16, int MODE, int D>
-__global__ __launch_bounds__(256) void col_partial_kernel(NormRope nr, const uint16_t* in, int64_t sb, int64_t sl, int64_t sh,
-                                                          int64_t L, int64_t H, int64_t nchunk, float* part) {
+__device__ __forceinline__ void col_partial_body(const NormRope& nr, const uint16_t* in, int64_t sb, int64_t sl,
+                                                 int64_t sh, int64_t L, int64_t H, int64_t nchunk, float* part,
+                                                 int64_t c, int64_t h, int64_t b) {
   constexpr int TPR = D / 8;
   constexpr int RPP = 256 / TPR;  // rows per pass
   __shared__ float red[RPP][D + 1];
-  const int64_t c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, r0 = tid / TPR, dc = tid % TPR;
   float acc[8], amx[8], amn[8];
 #pragma unroll
@@ -316,6 +316,24 @@ __global__ __launch_bounds__(256) void col_partial_kernel(NormRope nr, const uin
   }
 }
 
+template <bool IS_FP16, int MODE, int D>
+__global__ __launch_bounds__(256) void col_partial_kernel(NormRope nr, const uint16_t* in, int64_t sb, int64_t sl, int64_t sh,
+                                                          int64_t L, int64_t H, int64_t nchunk, float* part) {
+  col_partial_body<IS_FP16, MODE, D>(nr, in, sb, sl, sh, L, H, nchunk, part, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// The column passes of the SAGE prologue in one launch: z < B sums K (the smoothing mean), z >= B reduces
+// V (max |v|, or sum / max / min when V is smoothed).  Same per-chunk work and order as col_partial_kernel.
+template <bool IS_FP16, int VMODE, int D>
+__global__ __launch_bounds__(256) void prep_col_kernel(const uint16_t* k, int64_t ksb, int64_t ksl, int64_t ksh,
+                                                       const uint16_t* v, int64_t vsb, int64_t vsl, int64_t vsh,
+                                                       int64_t L, int64_t H, int64_t B, int64_t nchunk, float* kpart,
+                                                       float* vpart, int64_t zoff) {
+  const int64_t z = blockIdx.z + zoff;  // zoff = B: no K mean, V only
+  if (z >= B) col_partial_body<IS_FP16, VMODE, D>(NormRope{}, v, vsb, vsl, vsh, L, H, nchunk, vpart, blockIdx.x, blockIdx.y, z - B);
+  else col_partial_body<IS_FP16, 0, D>(NormRope{}, k, ksb, ksl, ksh, L, H, nchunk, kpart, blockIdx.x, blockIdx.y, z);
+}
+
 // Chunk partials -> one value per (b, h, d).  One workgroup per (b, h), one thread per channel; the
 // loop over chunks keeps 4 independent loads in flight (it is latency-bound, not bandwidth-bound).
 // MODE 0: sum, 1: max, 2: min.  Chunk c's vector is at part + ((bh * nchunk + c) * NV + k) * D.
@@ -368,6 +386,41 @@ __global__ void vsmooth_finalize_kernel(const float* part, int64_t nchunk, int64
   v_mean[bh * D + d] = mean;
   v_scale[bh * D + d] = a / scale_max;
   recp[bh * D + d] = scale_max / a;
+}
+
+// The finalize steps of the SAGE prologue in one launch: blocks [0, BH) write the K mean (when kpart is
+// given), blocks [BH, 2 BH) the V scales (and mean, when V is smoothed); same arithmetic as
+// mean_finalize_kernel, vscale_finalize_kernel and vsmooth_finalize_kernel.
+template <bool IS_FP16, bool SMOOTH_V, int D>
+__global__ void prep_finalize_kernel(const float* kpart, const float* vpart, int64_t nchunk, int64_t L, int64_t BH,
+                                     uint16_t* kmean, float scale_max, float* v_scale, float* recp, float* v_mean,
+                                     int64_t boff) {
+  const int64_t blk = blockIdx.x + boff;  // boff = BH: no K mean, V only
+  const int64_t bh = blk % BH;
+  const int d = threadIdx.x;
+  if (blk < BH) {
+    kmean[bh * D + d] = f32_to_half<IS_FP16>(reduce_chunks<0, D>(kpart, bh, nchunk, d) / (float)L);
+    return;
+  }
+  if constexpr (SMOOTH_V) {
+    const float sum = reduce_chunks<0, D, 3>(vpart, bh, nchunk, d, 0);
+    float mx = reduce_chunks<1, D, 3>(vpart, bh, nchunk, d, 1);
+    float mn = reduce_chunks<2, D, 3>(vpart, bh, nchunk, d, 2);
+    const int64_t l16 = (L + 15) / 16 * 16;
+    if (l16 != L) {
+      mx = fmaxf(mx, 0.f);
+      mn = fminf(mn, 0.f);
+    }
+    const float mean = sum / (float)l16;
+    const float a = fmaxf(fabsf(mx - mean), fabsf(mn - mean));
+    v_mean[bh * D + d] = mean;
+    v_scale[bh * D + d] = a / scale_max;
+    recp[bh * D + d] = scale_max / a;
+  } else {
+    const float a = reduce_chunks<1, D>(vpart, bh, nchunk, d);
+    v_scale[bh * D + d] = a / scale_max;
+    recp[bh * D + d] = scale_max / a;
+  }
 }
 
 template <int D>
@@ -1042,4 +1095,114 @@ extern "C" int qattn_v_tile_half_varlen(qattn_seq v, int dtype, int64_t B, int64
   if (D == 128) v_tile_half_kernel<128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, max_lk, H, v16, Lpad, cu_seqlens_k, cu_vt);
   else v_tile_half_kernel<64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, max_lk, H, v16, Lpad, cu_seqlens_k, cu_vt);
   return check_launch("v_tile_half_varlen");
+}
+
+// ------------------------------------------------------------------------------------------------
+// the whole SAGE prologue: K mean, Q/K INT8, V FP8 in four launches
+// ------------------------------------------------------------------------------------------------
+
+extern "C" size_t qattn_sage_quant_workspace_size(int64_t B, int64_t Lk, int64_t Hkv, int64_t D) {
+  const int64_t n = B * Hkv * col_chunks(Lk) * D;
+  return (size_t)(n + 3 * n + B * Hkv * D) * sizeof(float);
+}
+
+extern "C" int qattn_sage_quant(qattn_seq q, qattn_seq k, qattn_seq v, int dtype, int64_t B, int64_t Lq, int64_t Lk,
+                                int64_t Hq, int64_t Hkv, int64_t D, int qk_quant_gran, float q_sm_scale, int smooth_k,
+                                float scale_max, int smooth_v, qattn_seq q_out, float* q_scale, qattn_seq k_out,
+                                float* k_scale, void* k_mean, uint8_t* v8, int64_t Lpad, float* v_scale,
+                                float* v_mean, void* workspace, size_t workspace_bytes, qattn_stream_t stream) {
+  int rc;
+  if ((rc = check_common(dtype, D, QATTN_QUANT_CUDA, 64))) return rc;
+  QATTN_REQUIRE(qk_quant_gran == 1 || qk_quant_gran == 2 || qk_quant_gran == 3, QATTN_ERR_ARG,
+                "qk_quant_gran must be 1 (per block), 2 (per warp) or 3 (per thread), got %d", qk_quant_gran);
+  QATTN_REQUIRE(B > 0 && Lq > 0 && Lk > 0 && Hq > 0 && Hkv > 0, QATTN_ERR_SHAPE, "sage_quant needs non-empty input");
+  if ((rc = check_seq("q", q, 2)) || (rc = check_seq("k", k, 2)) || (rc = check_seq("v", v, 2)) ||
+      (rc = check_seq("q_out", q_out, 1)) || (rc = check_seq("k_out", k_out, 1)))
+    return rc;
+  QATTN_REQUIRE(q_scale && k_scale && v_scale && v8 && aligned16(v8), QATTN_ERR_ARG, "null or misaligned output");
+  QATTN_REQUIRE(!smooth_k || (k_mean && aligned16(k_mean)), QATTN_ERR_ALIGN, "smooth_k needs an aligned k_mean output");
+  QATTN_REQUIRE(!smooth_v || v_mean, QATTN_ERR_ARG, "smooth_v needs a v_mean output");
+  QATTN_REQUIRE(Lpad >= (Lk + 63) / 64 * 64 && Lpad % 64 == 0, QATTN_ERR_SHAPE,
+                "Lpad must be a multiple of 64 and >= Lk rounded up to 64");
+  QATTN_REQUIRE(workspace && workspace_bytes >= qattn_sage_quant_workspace_size(B, Lk, Hkv, D), QATTN_ERR_WORKSPACE,
+                "sage_quant workspace too small");
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t nchunk = col_chunks(Lk), BH = B * Hkv;
+  float* kpart = static_cast<float*>(workspace);
+  float* vpart = kpart + BH * nchunk * D;
+  float* recp = vpart + 3 * BH * nchunk * D;
+  const uint16_t* kp = static_cast<const uint16_t*>(k.data);
+  const uint16_t* vp = static_cast<const uint16_t*>(v.data);
+  uint16_t* km = static_cast<uint16_t*>(k_mean);
+
+  // 1. column partials of K (sum) and V (max |v|, or sum / max / min), one launch
+  {
+    const int64_t zoff = smooth_k ? 0 : B;
+    dim3 grid((unsigned)nchunk, (unsigned)Hkv, (unsigned)(2 * B - zoff));
+#define QATTN_PC(F16, VM, DD)                                                                                       \
+  prep_col_kernel<F16, VM, DD><<<grid, 256, 0, st>>>(kp, k.sb, k.sl, k.sh, vp, v.sb, v.sl, v.sh, Lk, Hkv, B, nchunk, \
+                                                     kpart, vpart, zoff)
+#define QATTN_PC2(F16, DD) \
+  if (smooth_v) QATTN_PC(F16, 2, DD); else QATTN_PC(F16, 1, DD)
+    if (dtype == QATTN_BF16) { if (D == 128) { QATTN_PC2(false, 128); } else { QATTN_PC2(false, 64); } }
+    else { if (D == 128) { QATTN_PC2(true, 128); } else { QATTN_PC2(true, 64); } }
+#undef QATTN_PC2
+#undef QATTN_PC
+  }
+  // 2. K mean and V scales, one launch
+  {
+    const int64_t boff = smooth_k ? 0 : BH;
+    const unsigned g = (unsigned)(2 * BH - boff);
+#define QATTN_PF(F16, SV, DD) \
+  prep_finalize_kernel<F16, SV, DD><<<g, DD, 0, st>>>(kpart, vpart, nchunk, Lk, BH, km, scale_max, v_scale, recp, v_mean, boff)
+#define QATTN_PF2(F16, DD) \
+  if (smooth_v) QATTN_PF(F16, true, DD); else QATTN_PF(F16, false, DD)
+    if (dtype == QATTN_BF16) { if (D == 128) { QATTN_PF2(false, 128); } else { QATTN_PF2(false, 64); } }
+    else { if (D == 128) { QATTN_PF2(true, 128); } else { QATTN_PF2(true, 64); } }
+#undef QATTN_PF2
+#undef QATTN_PF
+  }
+  // 3. V to FP8 tiles (V was read by step 1 just before: its second read finds much of it in cache)
+  {
+    dim3 grid((unsigned)(Lpad / 64), (unsigned)Hkv, (unsigned)B);
+    const VTileFilter nof{nullptr, {0, 0, 0, 0}};
+    const float* mean = smooth_v ? v_mean : nullptr;
+    if (dtype == QATTN_BF16) {
+      if (D == 128) v_fp8_kernel<false, 128><<<grid, 256, 0, st>>>(vp, v.sb, v.sl, v.sh, Lk, Hkv, recp, v8, Lpad, nof, mean);
+      else v_fp8_kernel<false, 64><<<grid, 256, 0, st>>>(vp, v.sb, v.sl, v.sh, Lk, Hkv, recp, v8, Lpad, nof, mean);
+    } else {
+      if (D == 128) v_fp8_kernel<true, 128><<<grid, 256, 0, st>>>(vp, v.sb, v.sl, v.sh, Lk, Hkv, recp, v8, Lpad, nof, mean);
+      else v_fp8_kernel<true, 64><<<grid, 256, 0, st>>>(vp, v.sb, v.sl, v.sh, Lk, Hkv, recp, v8, Lpad, nof, mean);
+    }
+  }
+  // 4. K then Q to INT8 in one launch (K first: its rows were read by step 1 as well)
+  QuantArgs a{};
+  a.njobs = 0;
+  int variant = QATTN_QUANT_CUDA;
+  const void* kmean_in = smooth_k ? k_mean : nullptr;
+  {
+    QuantJob& J = a.job[a.njobs++];
+    fill_job(J, k, k_out, B, Lk, Hkv, kmean_in, k_scale, 1.0f, 0, 64);
+    if (qk_quant_gran == 3) {
+      J.ncls = 4;
+      J.cls_shift = 1;
+    }
+  }
+  {
+    QuantJob& J = a.job[a.njobs++];
+    if (qk_quant_gran == 1) {
+      fill_job(J, q, q_out, B, Lq, Hq, nullptr, q_scale, q_sm_scale, 1, 128);
+    } else {
+      fill_job(J, q, q_out, B, Lq, Hq, nullptr, q_scale, 1.0f, 0, 32);
+      J.nblk = (Lq + 127) / 128 * 4;  // warp blocks of the 128-row CTA grid, trailing ones empty
+      J.nwg = B * Hq * J.nblk;
+      if (qk_quant_gran == 3) {
+        J.ncls = 8;
+        J.cls_shift = 0;
+        variant = QATTN_QUANT_TRITON_THREAD;
+      }
+    }
+  }
+  if ((rc = check_launch("sage_quant"))) return rc;
+  return run_quant(a, dtype, D, variant, st);
 }

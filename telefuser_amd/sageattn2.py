@@ -168,6 +168,45 @@ def per_channel_fp8(v: torch.Tensor, tensor_layout: str = "HND", scale_max: floa
     return v_fp8, v_scale, vm
 
 
+def sage_quant(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str = "HND",
+               qk_quant_gran: str = "per_block", sm_scale: Optional[float] = None, smooth_k: bool = True,
+               scale_max: float = 448.0, smooth_v: bool = False):
+    """The whole prologue of the INT8-QK / FP8-PV path in four launches (column passes of K and V,
+    their finalize, V to FP8, K and Q to INT8): the same outputs, bit for bit, as k_mean + the
+    per_block / per_warp / per_thread quantizer + per_channel_fp8 (CUDA quantizer variant).
+    Returns (q_int8, q_scale, k_int8, k_scale, km or None, v_fp8, v_scale, vm or None)."""
+    L = _lib.load()
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k and v must have the same dtype")
+    gran = {"per_block": 1, "per_warp": 2, "per_thread": 3}.get(qk_quant_gran)
+    if gran is None:
+        raise ValueError(f"unknown qk_quant_gran {qk_quant_gran!r}")
+    b, lq, hq, d = _dims(q, tensor_layout)
+    _, lk, hkv, _ = _dims(k, tensor_layout)
+    dev = q.device
+    nqb, nkb = (lq + 127) // 128, (lk + 63) // 64
+    q_int8 = torch.empty(q.shape, dtype=torch.int8, device=dev)
+    k_int8 = torch.empty(k.shape, dtype=torch.int8, device=dev)
+    q_per = {1: 1, 2: 4, 3: 32}[gran]
+    q_scale = torch.empty((b, hq, nqb * q_per), dtype=torch.float32, device=dev)
+    k_scale = torch.empty((b, hkv, nkb * (4 if gran == 3 else 1)), dtype=torch.float32, device=dev)
+    km = torch.empty((b, hkv, d), dtype=k.dtype, device=dev) if smooth_k else None
+    lpad = nkb * 64
+    v_fp8 = torch.empty((b, hkv, d, lpad), dtype=torch.float8_e4m3fn, device=dev)
+    v_scale = torch.empty((b, hkv, d), dtype=torch.float32, device=dev)
+    vm = torch.empty((b, hkv, d), dtype=torch.float32, device=dev) if smooth_v else None
+    ws = torch.empty(L.qattn_sage_quant_workspace_size(b, lk, hkv, d), dtype=torch.uint8, device=dev)
+    if sm_scale is None:
+        sm_scale = d ** -0.5
+    _lib.check(L.qattn_sage_quant(
+        _lib.seq(q, tensor_layout), _lib.seq(k, tensor_layout), _lib.seq(v, tensor_layout), _lib.dtype_code(q.dtype),
+        b, lq, lk, hq, hkv, d, gran, float(sm_scale * LOG2E), int(bool(smooth_k)), float(scale_max),
+        int(bool(smooth_v)), _lib.seq(q_int8, tensor_layout), _lib.ptr(q_scale), _lib.seq(k_int8, tensor_layout),
+        _lib.ptr(k_scale), _lib.ptr(km), _lib.ptr(v_fp8), lpad, _lib.ptr(v_scale), _lib.ptr(vm), _lib.ptr(ws),
+        ws.numel(), _lib.stream_of(q)))
+    return q_int8, q_scale, k_int8, k_scale, km, v_fp8, v_scale, vm
+
+
 def v_tile_half(v: torch.Tensor, tensor_layout: str = "HND") -> torch.Tensor:
     """V in the kernels' transposed tile layout, in its own dtype: [B, H, D, Lpad] (bf16/fp16 P.V path)."""
     L = _lib.load()
@@ -299,15 +338,7 @@ def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv
     if hq % hkv != 0:
         raise ValueError(f"num_qo_heads ({hq}) must be divisible by num_kv_heads ({hkv})")
 
-    km = k_mean(k, tensor_layout) if smooth_k else None
-    qk_mult = 1.0
-    if qk_quant_gran == "per_block":
-        q_int8, q_scale, k_int8, k_scale = per_block_int8(q, k, km, BLKQ, BLKK, sm_scale=sm_scale,
-                                                          tensor_layout=tensor_layout, variant=quant_variant)
-    else:  # sm_scale stays out of Q and is applied by the attention kernel (sm89 kernel :136,318-323)
-        quant = per_thread_int8 if qk_quant_gran == "per_thread" else per_warp_int8
-        q_int8, q_scale, k_int8, k_scale = quant(q, k, km, tensor_layout=tensor_layout)
-        qk_mult = sm_scale * LOG2E
+    qk_mult = 1.0 if qk_quant_gran == "per_block" else sm_scale * LOG2E
     vm = None
     if pv == "fp8":
         # sageattn2.py:1368-1383: smooth_v only with "fp32" accumulation; "fp32+fp16" quantizes V to
@@ -318,11 +349,26 @@ def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv
             warnings.warn(f"pv_accum_dtype is '{pv_accum_dtype}', smooth_v will be ignored.")
             smooth_v = False
         scale_max = 2.25 if pv_accum_dtype == "fp32+fp16" else 448.0
-        v_fp8, v_scale, vm = per_channel_fp8(v, tensor_layout=tensor_layout, scale_max=scale_max, smooth_v=smooth_v)
+    if pv == "fp8" and quant_variant == "cuda":
+        # K mean, Q/K INT8 and V FP8 in one fused prologue (four launches)
+        q_int8, q_scale, k_int8, k_scale, km, v_fp8, v_scale, vm = sage_quant(
+            q, k, v, tensor_layout=tensor_layout, qk_quant_gran=qk_quant_gran, sm_scale=sm_scale, smooth_k=smooth_k,
+            scale_max=scale_max, smooth_v=smooth_v)
     else:
-        if smooth_v:
-            warnings.warn(f"pv_accum_dtype is '{pv_accum_dtype}', smooth_v will be ignored.")
-        v_fp8, v_scale = v_tile_half(v, tensor_layout), None
+        km = k_mean(k, tensor_layout) if smooth_k else None
+        if qk_quant_gran == "per_block":
+            q_int8, q_scale, k_int8, k_scale = per_block_int8(q, k, km, BLKQ, BLKK, sm_scale=sm_scale,
+                                                              tensor_layout=tensor_layout, variant=quant_variant)
+        else:  # sm_scale stays out of Q and is applied by the attention kernel (sm89 kernel :136,318-323)
+            quant = per_thread_int8 if qk_quant_gran == "per_thread" else per_warp_int8
+            q_int8, q_scale, k_int8, k_scale = quant(q, k, km, tensor_layout=tensor_layout)
+        if pv == "fp8":
+            v_fp8, v_scale, vm = per_channel_fp8(v, tensor_layout=tensor_layout, scale_max=scale_max,
+                                                 smooth_v=smooth_v)
+        else:
+            if smooth_v:
+                warnings.warn(f"pv_accum_dtype is '{pv_accum_dtype}', smooth_v will be ignored.")
+            v_fp8, v_scale = v_tile_half(v, tensor_layout), None
     res = qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, tensor_layout=tensor_layout, out_dtype=dtype,
                     qk_mult=qk_mult, is_causal=is_causal, q_offset=q_offset, kv_valid_len=kv_valid_len,
                     return_lse=return_lse, qk_quant_gran=qk_quant_gran, v_mean=vm)
@@ -480,6 +526,7 @@ __all__ = [
     "per_thread_int8",
     "quant_per_block_int8",
     "per_channel_fp8",
+    "sage_quant",
     "k_mean",
     "qattn_fwd",
     "sageattn",

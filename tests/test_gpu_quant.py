@@ -167,3 +167,50 @@ def test_v_fp8_smooth_bit_exact(oracle, B, L, H, layout, dtype, scale_max):
                                          scale_max=scale_max, mean_in=gvm)
     assert np.array_equal(vs.cpu().numpy(), ovs)
     assert np.array_equal(untile_v(v8), ov8)
+
+
+@pytest.mark.parametrize("gran,smooth_k,smooth_v,scale_max,layout,dtype,shape", [
+    ("per_block", True, False, 448.0, "NHD", torch.bfloat16, (1, 1024, 1024, 2, 2)),
+    ("per_block", True, True, 448.0, "NHD", torch.bfloat16, (2, 1000, 777, 4, 2)),
+    ("per_block", False, False, 2.25, "HND", torch.float16, (1, 300, 130, 3, 3)),
+    ("per_warp", True, False, 448.0, "NHD", torch.bfloat16, (1, 517, 333, 2, 1)),
+    ("per_thread", True, False, 448.0, "HND", torch.bfloat16, (2, 700, 515, 2, 2)),
+    ("per_thread", False, True, 2.25, "NHD", torch.float16, (1, 129, 65, 2, 2)),
+])
+def test_sage_quant_matches_separate_calls(gran, smooth_k, smooth_v, scale_max, layout, dtype, shape):
+    """The fused prologue (column passes of K and V in one launch, one finalize, V FP8, K then Q INT8 in one
+    launch) must give exactly what the separate entry points give: k_mean, the per_block / per_warp /
+    per_thread quantizer and per_channel_fp8, with and without K / V smoothing, both V ranges."""
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    B, Lq, Lk, Hq, Hkv = shape
+    log(f"sage_quant {gran} smooth_k={smooth_k} smooth_v={smooth_v} scale_max={scale_max} {layout} {dtype} {shape}")
+    q, k, v = qkv(B, Lq, Lk, Hq, Hkv, seed=777, k_offset_std=0.5)
+    qd, kd, vd = (t.to(dev).to(dtype) for t in (q, k, v))
+    if layout == "HND":
+        qd, kd, vd = (t.transpose(1, 2).contiguous() for t in (qd, kd, vd))
+    sm = 128 ** -0.5
+    got = sa.sage_quant(qd, kd, vd, tensor_layout=layout, qk_quant_gran=gran, sm_scale=sm, smooth_k=smooth_k,
+                        scale_max=scale_max, smooth_v=smooth_v)
+    km = sa.k_mean(kd, layout) if smooth_k else None
+    if gran == "per_block":
+        ref_qk = sa.per_block_int8(qd, kd, km, sm_scale=sm, tensor_layout=layout)
+    elif gran == "per_warp":
+        ref_qk = sa.per_warp_int8(qd, kd, km, tensor_layout=layout)
+    else:
+        ref_qk = sa.per_thread_int8(qd, kd, km, tensor_layout=layout)
+    v8, vs, vm = sa.per_channel_fp8(vd, tensor_layout=layout, scale_max=scale_max, smooth_v=smooth_v)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("q_int8", "q_scale", "k_int8", "k_scale"), got[:4], ref_qk):
+        assert torch.equal(a, b), f"{name} differs"
+    if smooth_k:
+        assert torch.equal(got[4], km)
+    else:
+        assert got[4] is None
+    assert torch.equal(got[5].view(torch.uint8), v8.view(torch.uint8))
+    assert torch.equal(got[6], vs)
+    if smooth_v:
+        assert torch.equal(got[7], vm)
+    else:
+        assert got[7] is None
