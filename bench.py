@@ -191,8 +191,8 @@ def _prologue_bench(reps: int = 10) -> dict:
 
 
 def _config_bench(name: str, calls: int = 5, warmup: int = 2) -> dict:
-    """One BASELINE config through the same drop-in sequence as the headline step (K mean, per-block Q/K
-    quantizer, V fp8, attention), inputs resident in HBM: ms per call, the attention launch alone (HIP
+    """One BASELINE config through the same drop-in sequence as the headline step (the fused prologue:
+    K mean, per-block Q/K quantizer, V fp8; then the attention), inputs resident in HBM: ms per call, the attention launch alone (HIP
     events on the launch stream) and its roofline fraction.  C4's attention launch is bounded by HBM
     (int8 Q + K + e4m3 V read once, bf16 O written), the others by the dense INT8/FP8 MFMA peak."""
     import torch
@@ -209,9 +209,7 @@ def _config_bench(name: str, calls: int = 5, warmup: int = 2) -> dict:
     t_attn = []
 
     def call(record):
-        km = sa.k_mean(k, "NHD")
-        q8, qs, k8, ks = sa.per_block_int8(q, k, km, sm_scale=sm, tensor_layout="NHD")
-        v8, vs, _ = sa.per_channel_fp8(v, tensor_layout="NHD", smooth_v=False)
+        q8, qs, k8, ks, _, v8, vs, _ = sa.sage_quant(q, k, v, tensor_layout="NHD", sm_scale=sm)
         s = torch.cuda.current_stream()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(s)

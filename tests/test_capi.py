@@ -37,7 +37,8 @@ def test_workspace_queries(lib):
     assert lib.qattn_fwd_workspace_size(1, 4680, 12, 128, 4) == 4 * 12 * 4680 * 130 * 4
     assert lib.qattn_seq_mean_workspace_size(1, 32760, 12, 128) == 12 * 128 * 128 * 4
     # the C5 shape (444 query blocks) is split, the C2 shape (3072) is not
-    assert lib.qattn_fwd_num_splits(1, 4680, 32760, 12) > 1
+    assert lib.qattn_fwd_num_splits(1, 4680, 32760, 12) == 1    # C5: 444 workgroups, splitting costs more
+    assert lib.qattn_fwd_num_splits(1, 1024, 32760, 2) > 1      # 16 workgroups: split
     assert lib.qattn_fwd_num_splits(1, 32760, 32760, 12) == 1
 
 
@@ -102,13 +103,14 @@ def test_kernel_selection_rule(lib):
     assert lib.qattn_fwd_ex_kernel(1, 75600, 513, 40, 0, 1, 0, 0) == multi     # 9 tiles: streamed
     assert lib.qattn_fwd_ex_kernel(1, 75600, 512, 40, 0, 1, 1, 0) != res       # causal: resident does not apply
     assert lib.qattn_fwd_ex_kernel(1, 75600, 512, 40, 1, 1, 0, 0) == one       # half P.V
-    assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 12, 0, 1, 0, 0) == one      # C5: KV split
+    assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 12, 0, 1, 0, 0) == one      # C5: 228 ping-pong workgroups
+    assert lib.qattn_fwd_ex_kernel(1, 1024, 32760, 2, 0, 1, 0, 0) == one       # KV split
     assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 0) == one        # C1: grid too small
     assert lib.qattn_fwd_ex_kernel(1, 32760, 32760, 12, 1, 1, 0, 0) == one     # half P.V
     prev = lib.qattn_set_kernel(pp)
     try:
         assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 1) == pp
-        assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 12, 0, 1, 0, 0) == one  # a split launch cannot
+        assert lib.qattn_fwd_ex_kernel(1, 1024, 32760, 2, 0, 1, 0, 0) == one   # a split launch cannot
         lib.qattn_set_kernel(multi)
         assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 1, 1) == one    # causal: multi-block does not apply
         assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 1) == multi

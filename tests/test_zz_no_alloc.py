@@ -49,8 +49,8 @@ def test_noalloc_matches_workspace_entry_twice():
     from telefuser_amd import _lib
 
     L = _lib.load()
-    cases = [  # (B, Lq, Lk, H, splits, kv_valid): the C5 shape with its automatic split, then a smaller one
-        (1, 4680, 32760, 12, 0, None),
+    cases = [  # (B, Lq, Lk, H, splits, kv_valid): a C5-length chunk on 2 heads with its automatic split
+        (1, 4680, 32760, 2, 0, None),  # (74 workgroups: 14 splits), then a smaller launch
         (2, 700, 9000, 3, 5, [9000, 4100]),
     ]
     for i, (B, Lq, Lk, H, splits, kvv) in enumerate(cases):
