@@ -198,11 +198,16 @@ int qattn_sage_quant(qattn_seq q, qattn_seq k, qattn_seq v, int dtype, int64_t B
 
 /*
  * Packed variable-length batches: sequence b spans rows cu_seqlens[b] .. cu_seqlens[b + 1] of a packed
- * [total, H, D] tensor (int32 device tables of B + 1 entries, read only on the device).
+ * [total, H, D] tensor (int32 device tables of B + 1 entries, read only on the device).  Every kernel
+ * clamps a sequence to rows [0, total) of its tensor and to max_seqlen rows, so a malformed table cannot
+ * make it address memory outside the packed tensors (the reference leaves such tables undefined).
  *
- * qattn_varlen_offsets: the per-sequence block offsets cu_qs[b] = sum over earlier sequences of
- * ceil(len_q / 128), cu_ks[b] = cu_vt[b] = the same of ceil(len_k / 64) (each B + 1 entries); replaces the
- * cumsum of quant_per_block_varlen.py:92-107 (tf-kernel/tf_kernel/).
+ * qattn_varlen_offsets: seq_q / seq_k = the sequence tables made non-decreasing and clamped to [0, total]
+ * (so that sequences are disjoint row ranges of the packed tensors whatever the input), and the block
+ * offsets cu_qs[b] = sum over earlier sequences of ceil(len_q / 128), cu_ks[b] = cu_vt[b] = the same of
+ * ceil(len_k / 64), with len = min(rows, max_seqlen) (all B + 1 entries); replaces the cumsum of
+ * quant_per_block_varlen.py:92-107 (tf-kernel/tf_kernel/).  The three kernels below take seq_q / seq_k
+ * as their cu_seqlens_q / cu_seqlens_k.
  *
  * qattn_quant_qk_varlen_int8: per-sequence INT8 blocks of 128 Q rows and 64 K rows, with the Triton rounding
  * of variant; q_scale [cu_qs[B], Hq] and k_scale [cu_ks[B], Hkv] (block-major, the reference's layout);
@@ -218,21 +223,22 @@ int qattn_sage_quant(qattn_seq q, qattn_seq k, qattn_seq v, int dtype, int64_t B
  * qattn_v_tile_half_varlen.  Rows of sequences with no keys are left untouched.  Replaces
  * attn_qk_int8_block_varlen.forward (attn_qk_int8_block_varlen.py:157-200).
  */
-int qattn_varlen_offsets(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t B, int32_t* cu_qs,
-                         int32_t* cu_ks, int32_t* cu_vt, qattn_stream_t stream);
-int qattn_quant_qk_varlen_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t max_lq, int64_t max_lk,
-                               int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean, const int32_t* cu_seqlens_q,
-                               const int32_t* cu_seqlens_k, const int32_t* cu_qs, const int32_t* cu_ks,
-                               qattn_seq q_out, qattn_seq k_out, float* q_scale, float* k_scale, float sm_scale,
-                               int variant, qattn_stream_t stream);
-int qattn_v_tile_half_varlen(qattn_seq v, int dtype, int64_t B, int64_t max_lk, int64_t H, int64_t D,
+int qattn_varlen_offsets(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t B, int64_t total_q,
+                         int64_t total_k, int64_t max_lq, int64_t max_lk, int32_t* seq_q, int32_t* seq_k,
+                         int32_t* cu_qs, int32_t* cu_ks, int32_t* cu_vt, qattn_stream_t stream);
+int qattn_quant_qk_varlen_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t total_q, int64_t total_k,
+                               int64_t max_lq, int64_t max_lk, int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean,
+                               const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, const int32_t* cu_qs,
+                               const int32_t* cu_ks, qattn_seq q_out, qattn_seq k_out, float* q_scale, float* k_scale,
+                               float sm_scale, int variant, qattn_stream_t stream);
+int qattn_v_tile_half_varlen(qattn_seq v, int dtype, int64_t B, int64_t total_k, int64_t max_lk, int64_t H, int64_t D,
                              const int32_t* cu_seqlens_k, const int32_t* cu_vt, uint16_t* v16, int64_t Lpad,
                              qattn_stream_t stream);
 int qattn_fwd_varlen(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const uint16_t* v16,
-                     int64_t Lpad, qattn_seq o, int out_dtype, int64_t B, int64_t max_lq, int64_t max_lk, int64_t Hq,
-                     int64_t Hkv, int64_t D, float qk_mult, int causal, const int32_t* cu_seqlens_q,
-                     const int32_t* cu_seqlens_k, const int32_t* cu_qs, const int32_t* cu_ks, const int32_t* cu_vt,
-                     qattn_stream_t stream);
+                     int64_t Lpad, qattn_seq o, int out_dtype, int64_t B, int64_t total_q, int64_t total_k,
+                     int64_t max_lq, int64_t max_lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int causal,
+                     const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, const int32_t* cu_qs,
+                     const int32_t* cu_ks, const int32_t* cu_vt, qattn_stream_t stream);
 
 /*
  * Quantized attention with INT8 Q.K^T and P.V in the half dtype of V (P rounded to that dtype,

@@ -140,12 +140,12 @@ def load() -> ctypes.CDLL:
     L.qattn_sage_quant.argtypes = [S, S, S, i32, i64, i64, i64, i64, i64, i64, i32, f32, i32, f32, i32, S, vp, S, vp,
                                    vp, vp, i64, vp, vp, vp, sz, vp]
     L.qattn_sage_quant.restype = i32
-    L.qattn_varlen_offsets.argtypes = [vp, vp, i64, vp, vp, vp, vp]
-    L.qattn_quant_qk_varlen_int8.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, vp, vp, vp, vp, S, S, vp,
-                                             vp, f32, i32, vp]
-    L.qattn_v_tile_half_varlen.argtypes = [S, i32, i64, i64, i64, i64, vp, vp, vp, i64, vp]
-    L.qattn_fwd_varlen.argtypes = [S, vp, S, vp, vp, i64, S, i32, i64, i64, i64, i64, i64, i64, f32, i32, vp, vp, vp,
-                                   vp, vp, vp]
+    L.qattn_varlen_offsets.argtypes = [vp, vp, i64, i64, i64, i64, i64, vp, vp, vp, vp, vp, vp]
+    L.qattn_quant_qk_varlen_int8.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, i64, i64, vp, vp, vp, vp, vp, S,
+                                             S, vp, vp, f32, i32, vp]
+    L.qattn_v_tile_half_varlen.argtypes = [S, i32, i64, i64, i64, i64, i64, vp, vp, vp, i64, vp]
+    L.qattn_fwd_varlen.argtypes = [S, vp, S, vp, vp, i64, S, i32, i64, i64, i64, i64, i64, i64, i64, i64, f32, i32, vp,
+                                   vp, vp, vp, vp, vp]
     for name in ("qattn_varlen_offsets", "qattn_quant_qk_varlen_int8", "qattn_v_tile_half_varlen",
                  "qattn_fwd_varlen"):
         getattr(L, name).restype = i32

@@ -102,6 +102,7 @@ struct AttnParams {
   const int32_t* cu_qs;
   const int32_t* cu_ks;
   const int32_t* cu_vt;
+  int64_t var_tq, var_tk;  // rows of the packed Q / K tensors
   // resident-K/V launches: each workgroup takes wb_per_wg consecutive 32-row wave blocks of one head,
   // n_chunk workgroups per (batch, head)
   int64_t wb_per_wg;
@@ -238,10 +239,11 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   int64_t qs_stride = 1, ks_stride = 1;
   uint16_t* ob = static_cast<uint16_t*>(p.o) + b * p.osb;
   if (p.cu_q) {
-    const int64_t q0 = p.cu_q[b], k0s = p.cu_k[b];
-    Lq = p.cu_q[b + 1] - q0;
-    Lk = p.cu_k[b + 1] - k0s;
-    if (qb * kBQ >= Lq || Lk <= 0) return;  // uniform over the workgroup: no query row of this sequence here
+    int64_t q0, k0s;
+    varlen_range(p.cu_q, b, p.var_tq, p.Lq, q0, Lq);
+    varlen_range(p.cu_k, b, p.var_tk, p.Lk, k0s, Lk);
+    // (a V tile range past Lpad, from a too small Lpad, leaves the sequence's rows untouched)
+    if (qb * kBQ >= Lq || Lk <= 0 || ((int64_t)p.cu_vt[b] + (Lk + kBK - 1) / kBK) * kBK > p.Lpad) return;
     q8b = p.q8 + q0 * p.qsl;
     k8b = p.k8 + k0s * p.ksl;
     vcol0 = (int64_t)p.cu_vt[b] * kBK;
@@ -1681,11 +1683,13 @@ extern "C" int qattn_fwd_ex2(qattn_seq q8, const float* q_scale, qattn_seq k8, c
 // offsets and V tile column from the device tables, so the host never reads cu_seqlens.
 extern "C" int qattn_fwd_varlen(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale,
                                 const uint16_t* v16, int64_t Lpad, qattn_seq o, int out_dtype, int64_t B,
-                                int64_t max_lq, int64_t max_lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult,
+                                int64_t total_q, int64_t total_k, int64_t max_lq, int64_t max_lk, int64_t Hq,
+                                int64_t Hkv, int64_t D, float qk_mult,
                                 int causal, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
                                 const int32_t* cu_qs, const int32_t* cu_ks, const int32_t* cu_vt,
                                 qattn_stream_t stream) {
   QATTN_REQUIRE(cu_seqlens_q && cu_seqlens_k && cu_qs && cu_ks && cu_vt, QATTN_ERR_ARG, "null sequence table");
+  QATTN_REQUIRE(total_q >= 0 && total_k >= 0, QATTN_ERR_SHAPE, "negative packed size");
   AttnParams p;
   int ns = 1, kernel = QATTN_KERNEL_AUTO;
   const int rc = setup_fwd(p, ns, q8, q_scale, k8, k_scale, v16, Lpad, o, out_dtype, B, max_lq, max_lk, Hq, Hkv, D,
@@ -1697,6 +1701,8 @@ extern "C" int qattn_fwd_varlen(qattn_seq q8, const float* q_scale, qattn_seq k8
   p.cu_qs = cu_qs;
   p.cu_ks = cu_ks;
   p.cu_vt = cu_vt;
+  p.var_tq = total_q;
+  p.var_tk = total_k;
   p.v_scale = nullptr;
   p.qpw = 1;
   return launch_fwd<PV_FP16, false>(p, out_dtype, 1, nullptr, 0, (hipStream_t)stream, D, QATTN_KERNEL_ONE_BLOCK);

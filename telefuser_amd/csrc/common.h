@@ -71,6 +71,17 @@ __device__ __forceinline__ uint16_t f32_to_half(float f) {
   else return f32_to_bf16(f);
 }
 
+// Rows [start, start + len) of sequence b of a packed variable-length batch: cu[b] .. cu[b + 1] clamped to
+// the packed tensor's `total` rows and to `maxlen`, so that a malformed sequence table cannot address
+// memory outside the packed tensors (every varlen kernel and the block-offset kernel use this).
+__device__ __forceinline__ void varlen_range(const int32_t* cu, int64_t b, int64_t total, int64_t maxlen,
+                                             int64_t& start, int64_t& len) {
+  const int64_t s0 = min(max((int64_t)cu[b], (int64_t)0), total);
+  const int64_t s1 = min(max((int64_t)cu[b + 1], s0), total);
+  start = s0;
+  len = min(s1 - s0, maxlen);
+}
+
 // wave64 reductions (DPP / permute through the compiler's shuffle lowering)
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll

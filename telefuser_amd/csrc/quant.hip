@@ -73,6 +73,7 @@ struct QuantJob {
   // block n's scale goes to scale[(cu_blk[b] + n) * H + h] (quant_per_block_varlen.py:22-70)
   const int32_t* cu_seq;
   const int32_t* cu_blk;
+  int64_t total;  // rows of the packed tensor
 };
 
 struct QuantArgs {
@@ -137,8 +138,8 @@ __global__ __launch_bounds__(quant_threads<VARIANT>()) void quant_per_block_kern
   int64_t mb = b;  // batch entry of the mean (packed sequences share entry 0)
   if (J.cu_seq) {
     mb = 0;
-    const int64_t r0 = J.cu_seq[b];
-    Lb = J.cu_seq[b + 1] - r0;
+    int64_t r0;
+    varlen_range(J.cu_seq, b, J.total, J.L, r0, Lb);
     if (n * J.blk >= Lb) return;  // uniform over the workgroup
     in_b = J.in + r0 * J.sl;
     out_b = J.out + r0 * J.ol;
@@ -537,18 +538,19 @@ __global__ __launch_bounds__(256) void v_fp8_kernel(const uint16_t* in, int64_t 
 template <int D>
 __global__ __launch_bounds__(256) void v_tile_half_kernel(const uint16_t* in, int64_t sb, int64_t sl, int64_t sh,
                                                           int64_t L, int64_t H, uint16_t* v16, int64_t Lpad,
-                                                          const int32_t* cu_k = nullptr, const int32_t* cu_vt = nullptr) {
+                                                          const int32_t* cu_k = nullptr, const int32_t* cu_vt = nullptr,
+                                                          int64_t total_k = 0) {
   constexpr int TPR = D / 8;
   __shared__ __align__(16) uint16_t tile[D][64];
   int64_t t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
   int64_t tcol = t;  // tile column in v16
   if (cu_k) {  // packed variable-length keys: sequence b's tile t goes to tile column cu_vt[b] + t of entry 0
-    const int64_t k0 = cu_k[b];
-    L = cu_k[b + 1] - k0;
-    if (t * 64 >= L) return;
+    int64_t k0;
+    varlen_range(cu_k, b, total_k, L, k0, L);
+    tcol = (int64_t)cu_vt[b] + t;
+    if (t * 64 >= L || (tcol + 1) * 64 > Lpad) return;  // (a too small Lpad drops tiles, never overruns)
     in += k0 * sl;
-    tcol = cu_vt[b] + t;
     b = 0;
   }
 #pragma unroll
@@ -635,6 +637,7 @@ static bool fill_job(QuantJob& J, const qattn_seq& in, const qattn_seq& out, int
   J.cls_shift = 3;
   J.nr = NormRope{};
   J.cu_seq = J.cu_blk = nullptr;
+  J.total = 0;
   return true;
 }
 
@@ -1021,42 +1024,64 @@ extern "C" int qattn_norm_rope_quant_qk(qattn_seq xq, qattn_seq xk, int dtype, i
 // ------------------------------------------------------------------------------------------------
 
 namespace qattn {
-// Block offsets of every sequence: cu_qs[b] = sum of ceil(len_q / 128), cu_ks[b] = cu_vt[b] = sum of
-// ceil(len_k / 64) over the sequences before b (the cumsum of quant_per_block_varlen.py:92-107).  One
-// thread: B is small and the loop reads B + 1 entries.
-__global__ void varlen_offsets_kernel(const int32_t* cu_q, const int32_t* cu_k, int64_t B, int32_t* cu_qs,
-                                      int32_t* cu_ks, int32_t* cu_vt) {
+// Sanitised sequence tables and block offsets of a packed batch, by one thread (B is small).  The
+// sanitised tables are the caller's cu_seqlens made non-decreasing and clamped to [0, total], so that the
+// sequences are disjoint row ranges of the packed tensors whatever the input; the other varlen kernels read
+// only these.  cu_qs[b] = sum of ceil(len_q / 128), cu_ks[b] = cu_vt[b] = sum of ceil(len_k / 64) over the
+// sequences before b, with len = min(rows of the sequence, max_seqlen) (the cumsum of
+// quant_per_block_varlen.py:92-107).
+__global__ void varlen_offsets_kernel(const int32_t* cu_q, const int32_t* cu_k, int64_t B, int64_t total_q,
+                                      int64_t total_k, int64_t max_lq, int64_t max_lk, int32_t* sq, int32_t* sk,
+                                      int32_t* cu_qs, int32_t* cu_ks, int32_t* cu_vt) {
   if (threadIdx.x != 0) return;
+  int64_t pq = 0, pk = 0;
+  for (int64_t b = 0; b <= B; b++) {
+    pq = min(max((int64_t)cu_q[b], pq), total_q);
+    pk = min(max((int64_t)cu_k[b], pk), total_k);
+    sq[b] = (int32_t)pq;
+    sk[b] = (int32_t)pk;
+  }
   int32_t aq = 0, ak = 0;
   for (int64_t b = 0; b <= B; b++) {
     cu_qs[b] = aq;
     cu_ks[b] = ak;
     cu_vt[b] = ak;
     if (b < B) {
-      aq += (cu_q[b + 1] - cu_q[b] + 127) / 128;
-      ak += (cu_k[b + 1] - cu_k[b] + 63) / 64;
+      int64_t s, lq, lk;
+      varlen_range(sq, b, total_q, max_lq, s, lq);
+      varlen_range(sk, b, total_k, max_lk, s, lk);
+      aq += (int32_t)((lq + 127) / 128);
+      ak += (int32_t)((lk + 63) / 64);
     }
   }
 }
 }  // namespace qattn
 
 extern "C" int qattn_varlen_offsets(const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, int64_t B,
-                                    int32_t* cu_qs, int32_t* cu_ks, int32_t* cu_vt, qattn_stream_t stream) {
-  QATTN_REQUIRE(B > 0, QATTN_ERR_SHAPE, "varlen batch must hold at least one sequence");
-  QATTN_REQUIRE(cu_seqlens_q && cu_seqlens_k && cu_qs && cu_ks && cu_vt, QATTN_ERR_ARG, "null pointer");
-  varlen_offsets_kernel<<<1, 64, 0, (hipStream_t)stream>>>(cu_seqlens_q, cu_seqlens_k, B, cu_qs, cu_ks, cu_vt);
+                                    int64_t total_q, int64_t total_k, int64_t max_lq, int64_t max_lk,
+                                    int32_t* seq_q, int32_t* seq_k, int32_t* cu_qs, int32_t* cu_ks, int32_t* cu_vt,
+                                    qattn_stream_t stream) {
+  QATTN_REQUIRE(B > 0 && total_q >= 0 && total_k >= 0 && max_lq >= 0 && max_lk >= 0, QATTN_ERR_SHAPE,
+                "varlen batch must hold at least one sequence; sizes must be non-negative");
+  QATTN_REQUIRE(total_q < (1ll << 31) && total_k < (1ll << 31), QATTN_ERR_SHAPE, "packed tensors too long");
+  QATTN_REQUIRE(cu_seqlens_q && cu_seqlens_k && seq_q && seq_k && cu_qs && cu_ks && cu_vt, QATTN_ERR_ARG,
+                "null pointer");
+  varlen_offsets_kernel<<<1, 64, 0, (hipStream_t)stream>>>(cu_seqlens_q, cu_seqlens_k, B, total_q, total_k, max_lq,
+                                                           max_lk, seq_q, seq_k, cu_qs, cu_ks, cu_vt);
   return check_launch("varlen_offsets");
 }
 
-extern "C" int qattn_quant_qk_varlen_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t max_lq,
-                                          int64_t max_lk, int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean,
+extern "C" int qattn_quant_qk_varlen_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t total_q,
+                                          int64_t total_k, int64_t max_lq, int64_t max_lk, int64_t Hq, int64_t Hkv,
+                                          int64_t D, const void* k_mean,
                                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
                                           const int32_t* cu_qs, const int32_t* cu_ks, qattn_seq q_out,
                                           qattn_seq k_out, float* q_scale, float* k_scale, float sm_scale,
                                           int variant, qattn_stream_t stream) {
   int rc;
   if ((rc = check_common(dtype, D, variant, 128))) return rc;
-  QATTN_REQUIRE(B > 0 && max_lq >= 0 && max_lk >= 0 && Hq > 0 && Hkv > 0, QATTN_ERR_SHAPE, "bad sizes");
+  QATTN_REQUIRE(B > 0 && total_q >= 0 && total_k >= 0 && max_lq >= 0 && max_lk >= 0 && Hq > 0 && Hkv > 0,
+                QATTN_ERR_SHAPE, "bad sizes");
   QATTN_REQUIRE(cu_seqlens_q && cu_seqlens_k && cu_qs && cu_ks && q_scale && k_scale, QATTN_ERR_ARG, "null pointer");
   if ((rc = check_seq("q", q, 2)) || (rc = check_seq("q_out", q_out, 1)) || (rc = check_seq("k", k, 2)) ||
       (rc = check_seq("k_out", k_out, 1)))
@@ -1069,31 +1094,35 @@ extern "C" int qattn_quant_qk_varlen_int8(qattn_seq q, qattn_seq k, int dtype, i
     fill_job(J, q, q_out, B, max_lq, Hq, nullptr, q_scale, sm_scale, 1, 128);
     J.cu_seq = cu_seqlens_q;
     J.cu_blk = cu_qs;
+    J.total = total_q;
   }
   if (max_lk > 0) {
     QuantJob& J = a.job[a.njobs++];
     fill_job(J, k, k_out, B, max_lk, Hkv, k_mean, k_scale, 1.0f, 0, 64);
     J.cu_seq = cu_seqlens_k;
     J.cu_blk = cu_ks;
+    J.total = total_k;
   }
   if (a.njobs == 0) return QATTN_OK;
   return run_quant(a, dtype, D, variant, (hipStream_t)stream);
 }
 
-extern "C" int qattn_v_tile_half_varlen(qattn_seq v, int dtype, int64_t B, int64_t max_lk, int64_t H, int64_t D,
+extern "C" int qattn_v_tile_half_varlen(qattn_seq v, int dtype, int64_t B, int64_t total_k, int64_t max_lk, int64_t H,
+                                        int64_t D,
                                         const int32_t* cu_seqlens_k, const int32_t* cu_vt, uint16_t* v16,
                                         int64_t Lpad, qattn_stream_t stream) {
   int rc;
   if ((rc = check_common(dtype, D, QATTN_QUANT_CUDA, 64))) return rc;
-  QATTN_REQUIRE(B > 0 && max_lk > 0 && H > 0, QATTN_ERR_SHAPE, "v_tile_half_varlen needs non-empty input");
+  QATTN_REQUIRE(B > 0 && total_k >= 0 && max_lk > 0 && H > 0, QATTN_ERR_SHAPE, "v_tile_half_varlen needs non-empty input");
   if ((rc = check_seq("v", v, 2))) return rc;
   QATTN_REQUIRE(Lpad % 64 == 0, QATTN_ERR_SHAPE, "Lpad must be a multiple of 64");
   QATTN_REQUIRE(v16 && aligned16(v16) && cu_seqlens_k && cu_vt, QATTN_ERR_ARG, "null or misaligned pointer");
   hipStream_t st = (hipStream_t)stream;
   dim3 grid((unsigned)((max_lk + 63) / 64), (unsigned)H, (unsigned)B);
   const uint16_t* p = static_cast<const uint16_t*>(v.data);
-  if (D == 128) v_tile_half_kernel<128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, max_lk, H, v16, Lpad, cu_seqlens_k, cu_vt);
-  else v_tile_half_kernel<64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, max_lk, H, v16, Lpad, cu_seqlens_k, cu_vt);
+  if (D == 128) v_tile_half_kernel<128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, max_lk, H, v16, Lpad, cu_seqlens_k, cu_vt, total_k);
+  else v_tile_half_kernel<64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, max_lk, H, v16, Lpad, cu_seqlens_k, cu_vt,
+                                                    total_k);
   return check_launch("v_tile_half_varlen");
 }
 

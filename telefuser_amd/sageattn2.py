@@ -438,9 +438,11 @@ def sageattn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlen
     (attn_qk_int8_block_varlen.py:42-65; P.V accumulates in fp32 here).  ``is_causal`` masks per
     sequence, top-left aligned.  The whole batch is four launches (block offsets, Q/K quantizer, V tiles,
     attention) whose workgroups read the sequence tables on the device: the host never reads cu_seqlens,
-    and sizes its buffers from the packed lengths and max_seqlen_q / max_seqlen_k alone.  As in the
-    reference, the tables must be valid (start at 0, non-decreasing, within the packed tensors, every
-    length at most its max_seqlen); rows of sequences without keys are zero.
+    and sizes its buffers from the packed lengths and max_seqlen_q / max_seqlen_k alone.  The tables are
+    expected to be valid as in the reference (start at 0, non-decreasing, within the packed tensors, every
+    length at most its max_seqlen); the kernels clamp each sequence to the packed tensors and to
+    max_seqlen, so a malformed table gives wrong rows but never an out-of-bounds access.  Rows of
+    sequences without keys are zero.
     """
     dtype = q.dtype
     if not q.is_cuda:
@@ -478,10 +480,13 @@ def sageattn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlen
         return out[..., :head_dim_og]
     cq = cu_seqlens_q if cu_seqlens_q.dtype == torch.int32 else cu_seqlens_q.to(torch.int32)
     ck = cu_seqlens_k if cu_seqlens_k.dtype == torch.int32 else cu_seqlens_k.to(torch.int32)
-    offs = torch.empty((3, bsz + 1), dtype=torch.int32, device=dev)  # cu_qs, cu_ks, cu_vt
-    cu_qs, cu_ks, cu_vt = offs[0], offs[1], offs[2]
-    _lib.check(L.qattn_varlen_offsets(_lib.ptr(cq), _lib.ptr(ck), bsz, _lib.ptr(cu_qs), _lib.ptr(cu_ks),
+    offs = torch.empty((5, bsz + 1), dtype=torch.int32, device=dev)  # sanitised tables, block offsets
+    seq_q, seq_k, cu_qs, cu_ks, cu_vt = offs[0], offs[1], offs[2], offs[3], offs[4]
+    tq, tk = q.shape[0], k.shape[0]
+    _lib.check(L.qattn_varlen_offsets(_lib.ptr(cq), _lib.ptr(ck), bsz, tq, tk, max_seqlen_q, max_seqlen_k,
+                                      _lib.ptr(seq_q), _lib.ptr(seq_k), _lib.ptr(cu_qs), _lib.ptr(cu_ks),
                                       _lib.ptr(cu_vt), st))
+    cq, ck = seq_q, seq_k  # the kernels read the sanitised tables only
     # block counts are bounded by ceil(total / block) + batch_size, whatever the split into sequences
     nqblk = -(-q.shape[0] // BLKQ) + bsz
     nkblk = -(-k.shape[0] // BLKK) + bsz
@@ -492,19 +497,19 @@ def sageattn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlen
     qsc = torch.empty((nqblk, hq), dtype=torch.float32, device=dev)
     ksc = torch.empty((nkblk, hkv), dtype=torch.float32, device=dev)
     _lib.check(L.qattn_quant_qk_varlen_int8(
-        _lib.seq(q4, "NHD"), _lib.seq(k4, "NHD"), _lib.dtype_code(dtype), bsz, max_seqlen_q, max_seqlen_k, hq, hkv,
+        _lib.seq(q4, "NHD"), _lib.seq(k4, "NHD"), _lib.dtype_code(dtype), bsz, tq, tk, max_seqlen_q, max_seqlen_k, hq, hkv,
         d, _lib.ptr(km) if km is not None else None, _lib.ptr(cq), _lib.ptr(ck), _lib.ptr(cu_qs), _lib.ptr(cu_ks),
         _lib.seq(q8, "NHD"), _lib.seq(k8, "NHD"), _lib.ptr(qsc), _lib.ptr(ksc), sm_scale * LOG2E,
         _lib.QATTN_QUANT_TRITON, st))
     v16 = v4 if v4.dtype == torch.float16 else v4.to(torch.float16)  # the reference runs P.V in fp16
     lpad = nkblk * BLKK
     vt = torch.empty((1, hkv, d, lpad), dtype=torch.float16, device=dev)
-    _lib.check(L.qattn_v_tile_half_varlen(_lib.seq(v16, "NHD"), _lib.QATTN_FP16, bsz, max_seqlen_k, hkv, d,
+    _lib.check(L.qattn_v_tile_half_varlen(_lib.seq(v16, "NHD"), _lib.QATTN_FP16, bsz, tk, max_seqlen_k, hkv, d,
                                           _lib.ptr(ck), _lib.ptr(cu_vt), _lib.ptr(vt), lpad, st))
     o4 = out.unsqueeze(0)
     _lib.check(L.qattn_fwd_varlen(
         _lib.seq(q8, "NHD"), _lib.ptr(qsc), _lib.seq(k8, "NHD"), _lib.ptr(ksc), _lib.ptr(vt), lpad,
-        _lib.seq(o4, "NHD"), _lib.dtype_code(dtype), bsz, max_seqlen_q, max_seqlen_k, hq, hkv, d, 1.0,
+        _lib.seq(o4, "NHD"), _lib.dtype_code(dtype), bsz, tq, tk, max_seqlen_q, max_seqlen_k, hq, hkv, d, 1.0,
         1 if is_causal else 0, _lib.ptr(cq), _lib.ptr(ck), _lib.ptr(cu_qs), _lib.ptr(cu_ks), _lib.ptr(cu_vt), st))
     return out[..., :head_dim_og]
 

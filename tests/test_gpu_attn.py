@@ -327,6 +327,42 @@ def test_sageattn_varlen(oracle, causal):
         assert ct >= COS_E2E
 
 
+def test_sageattn_varlen_malformed_tables():
+    """Sequence tables that break the contract (decreasing entries, entries past the packed tensors, a
+    sequence longer than max_seqlen) are clamped on the device to disjoint row ranges of the packed
+    tensors: the output equals the one computed from the clamped table written out by hand, and no
+    access leaves the tensors."""
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    H, D, tq, tk = 2, 128, 700, 900
+    g = torch.Generator().manual_seed(77)
+    q = torch.randn((tq, H, D), generator=g).to(torch.bfloat16).to(dev)
+    k = (torch.randn((tk, H, D), generator=g) + 0.5).to(torch.bfloat16).to(dev)
+    v = torch.randn((tk, H, D), generator=g).to(torch.bfloat16).to(dev)
+    # raw tables -> what the device makes of them (non-decreasing, clamped to [0, total])
+    cases = [
+        ([0, 300, 200, 700], [0, 400, 100, 900], [0, 300, 300, 700], [0, 400, 400, 900]),  # decreasing
+        ([0, 100, 5000], [0, 300, 99999], [0, 100, 700], [0, 300, 900]),                  # past the end
+        ([-50, 250, 700], [0, 450, 900], [0, 250, 700], [0, 450, 900]),                    # negative start
+    ]
+    for raw_q, raw_k, fix_q, fix_k in cases:
+        mq = max(b - a for a, b in zip(fix_q, fix_q[1:]))
+        mk = max(b - a for a, b in zip(fix_k, fix_k[1:]))
+        t = lambda x: torch.tensor(x, dtype=torch.int32, device=dev)
+        log(f"varlen malformed: q {raw_q} -> {fix_q}, k {raw_k} -> {fix_k}")
+        o_raw = sa.sageattn_varlen(q, k, v, t(raw_q), t(raw_k), mq, mk)
+        o_fix = sa.sageattn_varlen(q, k, v, t(fix_q), t(fix_k), mq, mk)
+        torch.cuda.synchronize()
+        assert torch.equal(o_raw, o_fix)
+    # a sequence longer than max_seqlen_q: only its first max_seqlen_q rows are computed
+    o_cut = sa.sageattn_varlen(q, k, v, t([0, 500, 700]), t([0, 450, 900]), 200, 450)
+    o_ref = sa.sageattn_varlen(q, k, v, t([0, 200, 500, 700]), t([0, 450, 450, 900]), 200, 450)
+    torch.cuda.synchronize()
+    assert torch.equal(o_cut[:200], o_ref[:200]) and torch.equal(o_cut[500:700], o_ref[500:700])
+    assert not o_cut[200:500].float().any()
+
+
 @pytest.mark.parametrize("case", ["nhd", "hnd_gqa_causal", "split"])
 def test_block_sparse(oracle, case):
     """sparse_sageattn (sparse_sage.py:25-80, sparse_int8_attn.py k_block_id skip) against the oracle with
