@@ -12,8 +12,9 @@ Differences from the reference, all deliberate:
     quant_per_thread.py), "per_warp" (CUDA quant_per_warp_int8) or the extra "per_block" (CUDA
     QuantInt8Kernel with sm_scale*log2e folded into Q).  Per-warp Q blocks are always 32 rows (the
     reference uses 16 for head_dim 128 with "fp16+fp32" accumulation).
-  * ``pv_accum_dtype`` variants all accumulate P.V in full fp32 (MFMA accumulators are fp32), so
-    "fp32", "fp32+fp32" and "fp32+fp16" give the same result; V uses scale_max 448.
+  * ``pv_accum_dtype`` variants all accumulate P.V in full fp32 (MFMA accumulators are fp32); they keep
+    the reference's other semantics: "fp32" honours ``smooth_v``, "fp32+fp32" and "fp32+fp16" ignore it
+    with the reference's warning, and "fp32+fp16" quantizes V with scale_max 2.25 (448 otherwise).
   * ``kv_valid_len`` (per-batch number of valid keys) is honoured; ``attn_mask`` is ignored exactly as
     the reference CUDA functions ignore it (it is swallowed by ``**kwargs``).
   * ``per_channel_fp8`` returns V in this library's tile layout [B, H, D, Lpad] for both tensor
