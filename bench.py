@@ -86,6 +86,20 @@ def _cpu_baseline(cfg, budget_s: float = 12.0) -> dict:
         dt = whole(rows)
     pairs = rows * cfg.Lk
     ops = 4.0 * pairs * cfg.D
+
+    # the reference's own CPU-runnable case (config 1: B=1, H=2, L=1024) timed in full on all threads
+    from telefuser_amd.workloads import CONFIGS
+    c1 = CONFIGS["c1"]
+    q1, k1, v1, _ = make_inputs(c1, "cpu", call=0)
+    bits = lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)
+    q1b, k1b, v1b = bits(q1), bits(k1), bits(v1)
+    t0 = time.perf_counter()
+    km1 = oracle.k_mean_bits(k1b)
+    q18, q1s = oracle.quant_per_block_int8(q1b, sm_scale=c1.D ** -0.5 * oracle.LOG2E, blk=128)
+    k18, k1s = oracle.quant_per_block_int8(k1b, km_bits=km1, blk=64)
+    v18, v1s = oracle.per_channel_fp8(v1b)
+    oracle.qattn_fwd(q18, q1s, k18, k1s, v18, v1s)
+    dt_c1 = time.perf_counter() - t0
     return {
         "value": round(ops / dt / 1e12, 6),
         "unit": "TOPS",
@@ -97,6 +111,8 @@ def _cpu_baseline(cfg, budget_s: float = 12.0) -> dict:
         "single_thread": {"sample": f"attention only, 128 queries x {cfg.Lk} keys", "s": round(dt1, 3),
                           "ns_per_query_key_pair": round(ns_pair_1t, 2), "threads_observed": one},
         "host": dict(_cpu_info(), omp_max_threads=threads_all, omp_threads_observed=observed),
+        "c1_full": {"workload": c1.name, "s": round(dt_c1, 4), "TOPS": round(c1.ops() / dt_c1 / 1e12, 6),
+                    "threads": observed},
     }
 
 

@@ -1117,9 +1117,11 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31, hf = lane >> 5;
 
-  int64_t kv_end = p.Lk;
-  if (p.kv_valid) kv_end = min(kv_end, (int64_t)p.kv_valid[b]);
-  const int n_tiles = kv_end > 0 ? (int)((kv_end + kBK - 1) / kBK) : 0;
+  // key range (wave-uniform, in scalar registers: kv_valid comes through a vector load)
+  int64_t kv_lim = p.Lk;
+  if (p.kv_valid) kv_lim = min(kv_lim, (int64_t)p.kv_valid[b]);
+  const int64_t kv_end = __builtin_amdgcn_readfirstlane((int)max(kv_lim, (int64_t)0));
+  const int n_tiles = (int)((kv_end + kBK - 1) / kBK);
 
   // ---- the key range into LDS: tile t of K / V in lds_k[t] / lds_v[t], fragment-major ----
   {
@@ -1127,8 +1129,8 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
     const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad;
     const int64_t kbytes = (p.Lk - 1) * p.ksl + kD;
     const v4u vrsrc = make_rsrc(vbase, (uint32_t)((int64_t)kD * p.Lpad));
-    // DMA instruction i of wave w fills 1 KiB block f = 8 i' + w of a tile, i' = 0 (K) or V; 8 waves
-    // cover the 8 blocks of K and the 8 blocks of V of a tile in one instruction each
+    // per tile, wave w fills 1 KiB block w of the K tile and block w of the V tile (one DMA instruction
+    // each), so the 8 waves cover both tiles
     const int j = w;
     const uint32_t koff = (uint32_t)(((j & 1) * 32 + lq) * p.ksl + (2 * (j >> 1) + hf) * 16);
     const uint32_t voff = (uint32_t)(((j >> 1) * 32 + lq) * p.Lpad + (2 * hf + (j & 1)) * 16);
