@@ -104,6 +104,18 @@ __device__ __forceinline__ int8_t s8_rne_sat(float t) {
   return (int8_t)(int)r;
 }
 
+// fp32 -> half dtype -> fp32, round to nearest even (bf16 through v_cvt_pk_bf16_f32: one instruction
+// instead of the integer sequence; the two differ only in the payload of a NaN, which quantizes to 0)
+template <bool IS_FP16>
+__device__ __forceinline__ float round_to_half(float v) {
+  if constexpr (IS_FP16) {
+    return f16_to_f32(f32_to_f16(v));
+  } else {
+    const __bf16 h = (__bf16)v;
+    return (float)h;
+  }
+}
+
 template <bool IS_FP16, int VARIANT, int D>
 __global__ __launch_bounds__(quant_threads<VARIANT>()) void quant_per_block_kernel(QuantArgs args) {
   constexpr int kQuantThreads = quant_threads<VARIANT>();
@@ -179,7 +191,7 @@ __global__ __launch_bounds__(quant_threads<VARIANT>()) void quant_per_block_kern
         if (J.mean) {
           v = v - mv[e];
           // Triton paths: k - km is a torch op on half tensors, rounded back to the half type
-          if constexpr (VARIANT != QATTN_QUANT_CUDA) v = half_to_f32<IS_FP16>(f32_to_half<IS_FP16>(v));
+          if constexpr (VARIANT != QATTN_QUANT_CUDA) v = round_to_half<IS_FP16>(v);
         }
         if (J.has_sm_scale) v = v * J.sm_scale;
         x[i][e] = v;
