@@ -54,19 +54,24 @@ __device__ __forceinline__ void norm_rope8(const NormRope& nr, int64_t b, int64_
   }
 }
 
+// One quantizer job (Q or K).  A workgroup covers blk rows of one (batch entry, head): one scale block of
+// the quantizer's block size (128, 64 or 32 rows), or, with nsub = 4, 128 rows that are four 32-row scale
+// blocks (the warp blocks of the per-warp / per-thread Q layouts).
 struct QuantJob {
   const uint16_t* in;
   int64_t sb, sl, sh;
   int8_t* out;
   int64_t ob, ol, oh;
-  float* scale;  // [B, H, nblk]
+  float* scale;  // [B, H, scale_blocks, ncls]
   const uint16_t* mean;  // [B, H, D] or null
-  int64_t L, H, nblk;
-  int blk;
+  int64_t L, H;
+  int64_t nblk;          // workgroup blocks per (batch entry, head)
+  int64_t scale_blocks;  // scale blocks per (batch entry, head) in the scale tensor
+  int blk, nsub;
   int has_sm_scale;
   float sm_scale;
   int64_t nwg;  // B * H * nblk
-  int ncls;     // scale classes per block: 1 (per block), 8 (per-thread Q), 4 (per-thread K)
+  int ncls;     // scale classes per scale block: 1 (per block), 8 (per-thread Q), 4 (per-thread K)
   int cls_shift;  // class of row r = (r % 8) >> cls_shift  (3, 0, 1 for the cases above)
   NormRope nr;    // optional RMSNorm + RoPE prologue on the loaded chunks
   // packed variable-length input (null otherwise): entry b is rows cu_seq[b] .. cu_seq[b + 1] of batch 0, its
@@ -84,25 +89,8 @@ struct QuantArgs {
 // Rounding of the Triton per-thread quantizer (quant_per_thread.py:63-70): scale = amax/127 + 1e-7,
 // half-rounded K - km, round half away.  Used with per-thread scale classes only.
 constexpr int QATTN_QUANT_TRITON_THREAD = 2;
-// threads per quantizer workgroup: 512 (4 chunks of 16 bytes per thread at 128 rows; measured faster than
-// 256 and 1024) for one scale per block, 256 for the per-thread scale classes (their class maxima loop
-// over the rows of a pass, twice as many at 512)
-template <int VARIANT> constexpr int quant_threads() { return VARIANT == QATTN_QUANT_TRITON_THREAD ? 256 : 512; }
-
-// Round-half-away-from-zero of the Triton kernel: t + 0.5*sign, truncate; NaN -> 0.
-__device__ __forceinline__ int8_t s8_half_away(float t) {
-  if (t != t) return 0;
-  float r = truncf(t + (t >= 0.f ? 0.5f : -0.5f));
-  r = fminf(fmaxf(r, -128.f), 127.f);
-  return (int8_t)(int)r;
-}
-
-// cvt.rni.sat.s8.f32: round to nearest even, then saturate
-__device__ __forceinline__ int8_t s8_rne_sat(float t) {
-  float r = __builtin_rintf(t);
-  r = fminf(fmaxf(r, -128.f), 127.f);
-  return (int8_t)(int)r;
-}
+// threads per quantizer workgroup: 512 (4 chunks of 16 bytes per thread at 128 rows and D = 128)
+template <int VARIANT> constexpr int quant_threads() { return 512; }
 
 // fp32 -> half dtype -> fp32, round to nearest even (bf16 through v_cvt_pk_bf16_f32: one instruction
 // instead of the integer sequence; the two differ only in the payload of a NaN, which quantizes to 0)
@@ -116,64 +104,105 @@ __device__ __forceinline__ float round_to_half(float v) {
   }
 }
 
-template <bool IS_FP16, int VARIANT, int D>
-__global__ __launch_bounds__(quant_threads<VARIANT>()) void quant_per_block_kernel(QuantArgs args) {
+// v_cvt_i32_f32: truncate toward zero, saturate to the int32 range, NaN -> 0 (the hardware conversion; a C
+// cast leaves NaN and out-of-range values undefined)
+__device__ __forceinline__ int cvt_i32_trunc_sat(float t) {
+  int r;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(t));
+  return r;
+}
+
+// a / b, correctly rounded, from y1 = refined_rcp(b): the fma corrections of the IEEE division sequence
+// without its range scaling (div_scale / div_fixup).  Exact wherever the residuals do not underflow: the
+// quantizers divide |a| <= 127 b with b >= 1e-7, where only quotients below 2^-80 (which quantize to 0
+// either way) can differ.
+__device__ __forceinline__ float refined_rcp(float b) {
+  const float y0 = __builtin_amdgcn_rcpf(b);
+  return fmaf(fmaf(-b, y0, 1.0f), y0, y0);
+}
+__device__ __forceinline__ float div_by(float a, float b, float y1) {
+  const float q0 = a * y1;
+  const float q1 = fmaf(fmaf(-b, q0, a), y1, q0);
+  return fmaf(fmaf(-b, q1, a), y1, q1);
+}
+
+// One workgroup per block of one (batch entry, head) of a job; a launch covers up to two jobs (Q and K)
+// of equal nsub: workgroups [0, job[0].nwg) take job 0, the rest job 1.  Two passes over registers: |x|
+// maxima, then the scales and the quantized bytes.  GROUPED (nsub = 4): the block's 128 rows are four
+// 32-row scale blocks; a wave's rows of one pass lie in one of them.
+// The plain kernel is held to 64 VGPRs: 4 workgroups (8 waves per SIMD) per CU instead of 3, worth more than
+// the two registers it spills.
+template <bool IS_FP16, int VARIANT, int D, bool GROUPED>
+__global__ __launch_bounds__(quant_threads<VARIANT>()) __attribute__((amdgpu_waves_per_eu(GROUPED ? 7 : 8)))
+void quant_per_block_kernel(QuantArgs args) {
   constexpr int kQuantThreads = quant_threads<VARIANT>();
   constexpr int TPR = D / 8;                       // threads (16-byte chunks) per row
-  constexpr int MAXC = 128 * TPR / kQuantThreads;  // chunks per thread at blk = 128
+  constexpr int MAXC = 128 * TPR / kQuantThreads;  // chunks per thread at 128 rows
+  constexpr int RPP = kQuantThreads / TPR;         // rows per pass: chunk i of a thread is row RPP i + tid / TPR
+  constexpr int RPW = 64 / TPR;                    // rows per wave and pass
+  constexpr int NW = kQuantThreads / 64;
+  constexpr int NA = GROUPED ? MAXC : 1;           // |x| maxima kept per thread
+  static_assert(RPP % 32 == 0 && 32 % RPW == 0 && MAXC * RPP == 128, "row cells");
 
-  int64_t wg = blockIdx.x;
+  // index math in 32 bits (the grid is below 2^31 workgroups)
+  uint32_t wg = blockIdx.x;
   int j = 0;
-  if (args.njobs > 1 && wg >= args.job[0].nwg) {
-    wg -= args.job[0].nwg;
+  if (args.njobs > 1 && wg >= (uint32_t)args.job[0].nwg) {
+    wg -= (uint32_t)args.job[0].nwg;
     j = 1;
   }
   const QuantJob& J = args.job[j];
+  const uint32_t H = (uint32_t)J.H, NB = (uint32_t)J.nblk;
   // Heads interleaved inside a row (sequence-major layouts): the heads of one row block run next to
   // each other, so concurrent workgroups read contiguous row segments; head-major layouts walk blocks.
-  int64_t n, h;
+  uint32_t n, h, b;
   if (J.sh < J.sl) {
-    h = wg % J.H;
-    n = (wg / J.H) % J.nblk;
+    const uint32_t q = wg / H;
+    h = wg - q * H;
+    b = q / NB;
+    n = q - b * NB;
   } else {
-    n = wg % J.nblk;
-    h = (wg / J.nblk) % J.H;
+    const uint32_t bh = wg / NB;
+    n = wg - bh * NB;
+    b = bh / H;
+    h = bh - b * H;
   }
-  const int64_t b = wg / (J.nblk * J.H);
   const int tid = threadIdx.x;
-  const int nchunks = J.blk * TPR;
+  const int blk = GROUPED ? 128 : J.blk;
   // this entry's rows: in_b[l * sl], l < Lb (a dense batch entry, or one packed sequence)
-  const uint16_t* in_b = J.in + b * J.sb;
-  int8_t* out_b = J.out + b * J.ob;
+  const uint16_t* in_b = J.in + (int64_t)b * J.sb;
+  int8_t* out_b = J.out + (int64_t)b * J.ob;
   int64_t Lb = J.L;
-  float* scale_at = J.scale + ((b * J.H + h) * J.nblk + n) * J.ncls;
+  float* scale_at = J.scale + (((int64_t)b * J.H + h) * J.scale_blocks + (int64_t)n * J.nsub) * J.ncls;
   int64_t mb = b;  // batch entry of the mean (packed sequences share entry 0)
   if (J.cu_seq) {
     mb = 0;
     int64_t r0;
     varlen_range(J.cu_seq, b, J.total, J.L, r0, Lb);
-    if (n * J.blk >= Lb) return;  // uniform over the workgroup
+    if ((int64_t)n * blk >= Lb) return;  // uniform over the workgroup
     in_b = J.in + r0 * J.sl;
     out_b = J.out + r0 * J.ol;
     scale_at = J.scale + ((int64_t)J.cu_blk[b] + n) * J.H + h;
   }
 
   // the scale class of a row: rows r with equal (r % 8) / (8 / ncls) share a scale.  Every thread
-  // touches rows of a single class (rows per pass, 256 / TPR, is a multiple of 8).
-  constexpr int RPP = kQuantThreads / TPR;
+  // touches rows of a single class (RPP is a multiple of 8).
   const int cls = ((tid / TPR) & 7) >> J.cls_shift;
+  const int row0 = tid / TPR, dc = tid % TPR;
 
   float x[MAXC][8];
-  float amax = VARIANT == QATTN_QUANT_CUDA ? 0.0000001f : 0.f;
+  const float amax0 = VARIANT == QATTN_QUANT_CUDA ? 0.0000001f : 0.f;
+  float am[NA];  // |x| maximum of each chunk (GROUPED), or of all of them
+#pragma unroll
+  for (int i = 0; i < NA; i++) am[i] = amax0;
 #pragma unroll
   for (int i = 0; i < MAXC; i++) {
-    const int c = tid + i * kQuantThreads;
-    const int row = c / TPR, dc = c % TPR;
-    const int64_t l = n * J.blk + row;
+    const int r = row0 + RPP * i;
+    const int64_t l = (int64_t)n * blk + r;
 #pragma unroll
     for (int e = 0; e < 8; e++) x[i][e] = 0.f;
-    if (c < nchunks && l < Lb) {
-      v4u raw = *reinterpret_cast<const v4u*>(in_b + l * J.sl + h * J.sh + dc * 8);
+    if (r < blk && l < Lb) {
+      v4u raw = *reinterpret_cast<const v4u*>(in_b + l * J.sl + (int64_t)h * J.sh + dc * 8);
       uint16_t hv[8];
       __builtin_memcpy(hv, &raw, 16);
       if (J.nr.rstd) norm_rope8<IS_FP16>(J.nr, b, J.L, l, h, D, dc, hv);
@@ -195,32 +224,9 @@ __global__ __launch_bounds__(quant_threads<VARIANT>()) void quant_per_block_kern
         }
         if (J.has_sm_scale) v = v * J.sm_scale;
         x[i][e] = v;
-        amax = fmaxf(amax, fabsf(v));
+        am[GROUPED ? i : 0] = fmaxf(am[GROUPED ? i : 0], fabsf(v));
       }
     }
-  }
-  __shared__ float row_max[RPP];
-  auto class_max = [&](int k) {
-    float a = 0.f;
-#pragma unroll
-    for (int r = 0; r < RPP; r++)
-      if (((r & 7) >> J.cls_shift) == k) a = fmaxf(a, row_max[r]);
-    return a;
-  };
-  if constexpr (VARIANT == QATTN_QUANT_TRITON_THREAD) {
-    // per-thread scale classes: max over the TPR lanes of a row, then over the rows of each class
-#pragma unroll
-    for (int o = 1; o < TPR; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-    if (tid % TPR == 0) row_max[tid / TPR] = amax;
-    __syncthreads();
-    amax = class_max(cls);
-  } else {  // one scale per block: wave max, then across the waves
-    amax = wave_max(amax);
-    if ((tid & 63) == 0) row_max[tid >> 6] = amax;
-    __syncthreads();
-    amax = row_max[0];
-#pragma unroll
-    for (int w = 1; w < kQuantThreads / 64; w++) amax = fmaxf(amax, row_max[w]);
   }
 
   // IEEE division (hipcc default: correctly rounded)
@@ -228,29 +234,92 @@ __global__ __launch_bounds__(quant_threads<VARIANT>()) void quant_per_block_kern
     if constexpr (VARIANT == QATTN_QUANT_TRITON_THREAD) return a / 127.0f + 0.0000001f;
     else return a / 127.0f;
   };
-  const float scale = scale_of(amax);
+  // per chunk (GROUPED) or per thread: the scale (Triton rounding) or 127 / amax (CUDA rounding)
+  float sc[NA];
   if constexpr (VARIANT == QATTN_QUANT_TRITON_THREAD) {
-    if (tid < J.ncls) scale_at[tid] = scale_of(class_max(tid));
-  } else if (tid == 0) {
-    *scale_at = scale;
+    // per-thread scale classes: each row's maximum (over its TPR lanes) into LDS, then the maximum over
+    // the rows of a class in the row's scale block (ungrouped: rows r, r + RPP, ... already share theirs)
+    __shared__ float row_max[GROUPED ? 128 : RPP];
+#pragma unroll
+    for (int i = 0; i < NA; i++) {
+      float a = am[i];
+#pragma unroll
+      for (int o = 1; o < TPR; o <<= 1) a = fmaxf(a, __shfl_xor(a, o, 64));
+      if (dc == 0) row_max[RPP * i + row0] = a;
+    }
+    __syncthreads();
+    // rows r of class k in scale block g: (r % 8) in [k * cw, (k + 1) * cw), cw = 8 / ncls (a loop over
+    // those rows only)
+    const int cw = 1 << J.cls_shift;
+    auto class_max = [&](int g, int k) {
+      float a = 0.f;
+      const int r0 = GROUPED ? 32 * g : 0, r1 = GROUPED ? r0 + 32 : RPP;
+      for (int o = r0; o < r1; o += 8)
+        for (int m = 0; m < cw; m++) a = fmaxf(a, row_max[o + k * cw + m]);
+      return a;
+    };
+#pragma unroll
+    for (int i = 0; i < NA; i++) sc[i] = scale_of(class_max(GROUPED ? (RPP * i + row0) / 32 : 0, cls));
+    if (tid < J.nsub * J.ncls) scale_at[tid] = scale_of(class_max(tid / J.ncls, tid % J.ncls));
+  } else {  // one scale per scale block: wave maxima, then over the waves (of each 32-row cell)
+    __shared__ float wave_maxes[NA][NW];
+#pragma unroll
+    for (int i = 0; i < NA; i++) {
+      const float a = wave_max(am[i]);
+      if ((tid & 63) == 0) wave_maxes[i][tid >> 6] = a;
+    }
+    __syncthreads();
+    float cell[GROUPED ? 4 : 1];  // cell c: rows [32 c, 32 c + 32) = the waves w of chunk i with (RPP i + RPW w) / 32 == c
+#pragma unroll
+    for (int c = 0; c < (GROUPED ? 4 : 1); c++) {
+      cell[c] = amax0;
+#pragma unroll
+      for (int i = 0; i < NA; i++)
+#pragma unroll
+        for (int ww = 0; ww < NW; ww++)
+          if (!GROUPED || (RPP * i + RPW * ww) / 32 == c) cell[c] = fmaxf(cell[c], wave_maxes[i][ww]);
+    }
+#pragma unroll
+    for (int i = 0; i < NA; i++) {
+      float a = cell[0];
+      if constexpr (GROUPED) {
+        // this thread's cell of chunk i: (RPP i + row0) / 32, row0 / 32 = RPW (tid / 64) / 32
+        a = cell[(RPP * i) / 32];
+        if constexpr (RPP > 32) {
+          if ((RPW * (tid >> 6)) / 32 == 1) a = cell[(RPP * i) / 32 + 1];
+        }
+      }
+      sc[i] = VARIANT == QATTN_QUANT_CUDA ? 127.0f / a : scale_of(a);
+    }
+#pragma unroll
+    for (int c = 0; c < (GROUPED ? 4 : 1); c++)
+      if (tid == c) scale_at[c] = scale_of(cell[c]);
   }
-  const float inv = 127.0f / amax;
 
 #pragma unroll
   for (int i = 0; i < MAXC; i++) {
-    const int c = tid + i * kQuantThreads;
-    const int row = c / TPR, dc = c % TPR;
-    const int64_t l = n * J.blk + row;
-    if (c < nchunks && l < Lb) {
+    const int r = row0 + RPP * i;
+    const int64_t l = (int64_t)n * blk + r;
+    if (r < blk && l < Lb) {
+      const float s = sc[GROUPED ? i : 0];
+      const float iv = VARIANT == QATTN_QUANT_CUDA ? s : refined_rcp(s);
       int8_t qv[8];
 #pragma unroll
       for (int e = 0; e < 8; e++) {
-        if constexpr (VARIANT == QATTN_QUANT_CUDA) qv[e] = s8_rne_sat(x[i][e] * inv);
-        else qv[e] = s8_half_away(x[i][e] / scale);
+        // |x| <= amax, so the quotients stay within [-127, 127] before rounding (no saturation step);
+        // NaN converts to 0
+        if constexpr (VARIANT == QATTN_QUANT_CUDA) {
+          // cvt.rni.sat.s8.f32: round to nearest even
+          qv[e] = (int8_t)cvt_i32_trunc_sat(__builtin_rintf(x[i][e] * iv));
+        } else {
+          // Triton: t + 0.5 * sign(t) in fp32, truncate toward zero
+          const float t = div_by(x[i][e], s, iv);
+          qv[e] = (int8_t)cvt_i32_trunc_sat(t + __builtin_copysignf(0.5f, t));
+        }
       }
       v2u packed;
       __builtin_memcpy(&packed, qv, 8);
-      *reinterpret_cast<v2u*>(out_b + l * J.ol + h * J.oh + dc * 8) = packed;
+      *reinterpret_cast<v2u*>(out_b + l * J.ol + (int64_t)h * J.oh + dc * 8) = packed;
     }
   }
 }
@@ -640,8 +709,11 @@ static bool fill_job(QuantJob& J, const qattn_seq& in, const qattn_seq& out, int
   J.ob = out.sb; J.ol = out.sl; J.oh = out.sh;
   J.scale = scale;
   J.mean = static_cast<const uint16_t*>(mean);
-  J.L = L; J.H = H; J.blk = blk;
+  J.L = L; J.H = H;
+  J.blk = blk;
+  J.nsub = 1;
   J.nblk = (L + blk - 1) / blk;
+  J.scale_blocks = J.nblk;
   J.has_sm_scale = has_sm;
   J.sm_scale = sm_scale;
   J.nwg = B * H * J.nblk;
@@ -653,10 +725,21 @@ static bool fill_job(QuantJob& J, const qattn_seq& in, const qattn_seq& out, int
   return true;
 }
 
-template <int D>
+// Q in the per-warp / per-thread layouts: the reference grid's 128-row CTA blocks, each four 32-row warp
+// blocks with scales of their own (trailing warp blocks past L get the scale of an empty block).  One
+// workgroup covers a CTA block.
+static void warp_block_job(QuantJob& J, int64_t B) {
+  J.blk = 128;
+  J.nsub = 4;
+  J.nblk = (J.L + 127) / 128;
+  J.scale_blocks = J.nblk * 4;
+  J.nwg = B * J.H * J.nblk;
+}
+
+template <int D, bool GROUPED>
 static void launch_quant(const QuantArgs& a, int dtype, int variant, int64_t nwg, hipStream_t st) {
   dim3 grid((unsigned)nwg);
-#define QATTN_QK(F16, V) quant_per_block_kernel<F16, V, D><<<grid, quant_threads<V>(), 0, st>>>(a)
+#define QATTN_QK(F16, V) quant_per_block_kernel<F16, V, D, GROUPED><<<grid, quant_threads<V>(), 0, st>>>(a)
   if (dtype == QATTN_BF16) {
     if (variant == QATTN_QUANT_CUDA) QATTN_QK(false, QATTN_QUANT_CUDA);
     else if (variant == QATTN_QUANT_TRITON) QATTN_QK(false, QATTN_QUANT_TRITON);
@@ -669,13 +752,28 @@ static void launch_quant(const QuantArgs& a, int dtype, int variant, int64_t nwg
 #undef QATTN_QK
 }
 
+// One launch per scale-block layout among the jobs (Q in warp blocks next to K in plain blocks takes two:
+// each kernel keeps the register budget of its own layout).
 static int run_quant(QuantArgs& a, int dtype, int64_t D, int variant, hipStream_t st) {
-  int64_t nwg = 0;
-  for (int j = 0; j < a.njobs; j++) nwg += a.job[j].nwg;
-  if (nwg == 0) return QATTN_OK;
-  QATTN_REQUIRE(nwg < (1ll << 31), QATTN_ERR_SHAPE, "quantizer grid too large");
-  if (D == 128) launch_quant<128>(a, dtype, variant, nwg, st);
-  else launch_quant<64>(a, dtype, variant, nwg, st);
+  for (int nsub : {1, 4}) {
+    QuantArgs s{};
+    s.njobs = 0;
+    int64_t nwg = 0;
+    for (int j = 0; j < a.njobs; j++)
+      if (a.job[j].nsub == nsub && a.job[j].nwg > 0) {
+        s.job[s.njobs++] = a.job[j];
+        nwg += a.job[j].nwg;
+      }
+    if (nwg == 0) continue;
+    QATTN_REQUIRE(nwg < (1ll << 31), QATTN_ERR_SHAPE, "quantizer grid too large");
+    if (nsub == 4) {
+      if (D == 128) launch_quant<128, true>(s, dtype, variant, nwg, st);
+      else launch_quant<64, true>(s, dtype, variant, nwg, st);
+    } else {
+      if (D == 128) launch_quant<128, false>(s, dtype, variant, nwg, st);
+      else launch_quant<64, false>(s, dtype, variant, nwg, st);
+    }
+  }
   return check_launch("quant_per_block_int8");
 }
 
@@ -746,8 +844,7 @@ extern "C" int qattn_quant_qk_per_warp_int8(qattn_seq q, qattn_seq k, int dtype,
     if ((rc = check_seq("q", q, 2)) || (rc = check_seq("q_out", q_out, 1))) return rc;
     QuantJob& J = a.job[a.njobs++];
     fill_job(J, q, q_out, B, Lq, Hq, nullptr, q_scale, 1.0f, 0, 32);
-    J.nblk = (Lq + 127) / 128 * 4;  // the reference's grid: warp blocks of every 128-row CTA block
-    J.nwg = B * Hq * J.nblk;
+    warp_block_job(J, B);
   }
   if (B * Lk * Hkv > 0) {
     if ((rc = check_seq("k", k, 2)) || (rc = check_seq("k_out", k_out, 1))) return rc;
@@ -772,8 +869,7 @@ extern "C" int qattn_quant_qk_per_thread_int8(qattn_seq q, qattn_seq k, int dtyp
     if ((rc = check_seq("q", q, 2)) || (rc = check_seq("q_out", q_out, 1))) return rc;
     QuantJob& J = a.job[a.njobs++];
     fill_job(J, q, q_out, B, Lq, Hq, nullptr, q_scale, 1.0f, 0, 32);
-    J.nblk = (Lq + 127) / 128 * 4;  // warp blocks of the 128-row CTA grid, trailing ones empty
-    J.nwg = B * Hq * J.nblk;
+    warp_block_job(J, B);
     J.ncls = 8;
     J.cls_shift = 0;
   }
@@ -1235,8 +1331,7 @@ extern "C" int qattn_sage_quant(qattn_seq q, qattn_seq k, qattn_seq v, int dtype
       fill_job(J, q, q_out, B, Lq, Hq, nullptr, q_scale, q_sm_scale, 1, 128);
     } else {
       fill_job(J, q, q_out, B, Lq, Hq, nullptr, q_scale, 1.0f, 0, 32);
-      J.nblk = (Lq + 127) / 128 * 4;  // warp blocks of the 128-row CTA grid, trailing ones empty
-      J.nwg = B * Hq * J.nblk;
+      warp_block_job(J, B);
       if (qk_quant_gran == 3) {
         J.ncls = 8;
         J.cls_shift = 0;
