@@ -92,6 +92,46 @@ def test_per_thread_and_per_warp_quant_bit_exact(oracle, B, Lq, Lk, Hq, Hkv, lay
     assert np.array_equal(k8.cpu().numpy(), ok8)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_quant_nan_and_inf_inputs_match_oracle(oracle, dtype):
+    """NaN elements quantize to 0 and drop out of the block maximum (cvt.rni.sat.s8 and fmaxf semantics); an
+    infinite element makes its block's scale infinite and every code of the block 0."""
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    B, L, H = 1, 300, 2
+    log(f"quant nan/inf {dtype}")
+    q, k, _ = qkv(B, L, L, H, H, seed=103, k_offset_std=0.5, dtype=dtype)
+    q[0, 5, 0, 7] = float("nan")     # first 32-row warp block, first 64- and 128-row block
+    q[0, 70, 1, 0] = float("nan")
+    q[0, 200, 0, 3] = float("inf")   # a block of its own
+    k[0, 40, 1, 9] = float("nan")
+    k[0, 250, 0, 1] = float("-inf")
+    qd, kd = q.to(dev), k.to(dev)
+    km = torch.zeros((B, H, 128), dtype=dtype, device=dev)  # a finite mean: the inf stays in one block
+    f16 = dtype == torch.float16
+    kmb = _as_bits(km)
+    sm = 128 ** -0.5
+    for variant in ("cuda", "triton"):
+        q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=sm, tensor_layout="NHD", variant=variant)
+        oq8, oqs = oracle.quant_per_block_int8(_as_bits(q), sm_scale=sm * LOG2E, blk=128, layout="NHD",
+                                               is_fp16=f16, variant=variant)
+        ok8, oks = oracle.quant_per_block_int8(_as_bits(k), km_bits=kmb, blk=64, layout="NHD", is_fp16=f16,
+                                               variant=variant)
+        assert np.array_equal(q8.cpu().numpy(), oq8) and np.array_equal(k8.cpu().numpy(), ok8), variant
+        assert np.array_equal(qs.cpu().numpy(), oqs) and np.array_equal(ks.cpu().numpy(), oks), variant
+        assert q8.cpu()[0, 5, 0, 7].item() == 0 and k8.cpu()[0, 40, 1, 9].item() == 0
+    q8, qs, k8, ks = sa.per_thread_int8(qd, kd, km, tensor_layout="NHD")
+    oq8, oqs = oracle.quant_per_thread_int8(_as_bits(q), layout="NHD", is_fp16=f16)
+    ok8, oks = oracle.quant_per_thread_int8(_as_bits(k), km_bits=kmb, is_key=True, layout="NHD", is_fp16=f16)
+    assert np.array_equal(q8.cpu().numpy(), oq8) and np.array_equal(k8.cpu().numpy(), ok8)
+    assert np.array_equal(qs.cpu().numpy(), oqs) and np.array_equal(ks.cpu().numpy(), oks)
+    q8, qs, k8, ks = sa.per_warp_int8(qd, kd, km, tensor_layout="NHD")
+    oq8, oqs = oracle.quant_per_block_int8(_as_bits(q), blk=32, layout="NHD", is_fp16=f16)
+    assert np.array_equal(q8.cpu().numpy(), oq8)
+    assert np.array_equal(qs.cpu().numpy()[..., :oqs.shape[-1]], oqs)
+
+
 def test_quant_known_answers_on_gpu(oracle):
     """Closed-form cases (ties, all-zero block, tail rows) through the single-tensor entry."""
     dev = require_gpu()
