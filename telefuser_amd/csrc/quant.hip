@@ -558,62 +558,103 @@ struct VTileFilter {
   int64_t r[4];
 };
 
+// 64-key tiles per workgroup of v_fp8_kernel: the loads of all of them are issued before any is converted
+constexpr int kVTilesPerWG = 2;
+
 template <bool IS_FP16, int D>
 __global__ __launch_bounds__(256) void v_fp8_kernel(const uint16_t* in, int64_t sb, int64_t sl, int64_t sh,
                                                     int64_t L, int64_t H, const float* recp, uint8_t* v8,
-                                                    int64_t Lpad, VTileFilter filt, const float* vmean = nullptr) {
+                                                    int64_t Lpad, int64_t ntiles, VTileFilter filt,
+                                                    const float* vmean = nullptr) {
   constexpr int TPR = D / 8;
+  static_assert(16 * TPR <= 256, "one key quad x 8 channels per thread");
   // The tile as 4-byte words: word w of channel d holds the tile-permuted key slots 4w .. 4w + 3.  Its
   // 16-byte chunks (4 words) are XOR-swizzled by the channel group (d / 8) & 3, so that the word stores
   // of a wave (16 channel groups x 4 key quads) spread over the banks and each chunk is still read back
   // with one 16-byte load.
-  __shared__ __align__(16) uint32_t tile[D][16];
-  const int64_t t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  __shared__ __align__(16) uint32_t tile[kVTilesPerWG][D][16];
+  const int64_t h = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x;
-  if (filt.grown && !filt.grown[b * H + h]) {
-    const int64_t lo = t * 64, hi = lo + 64;
-    const bool hit = (filt.r[0] < hi && lo < filt.r[1]) || (filt.r[2] < hi && lo < filt.r[3]);
-    if (!hit) return;  // uniform over the workgroup
+  bool act[kVTilesPerWG];  // uniform over the workgroup
+#pragma unroll
+  for (int tt = 0; tt < kVTilesPerWG; tt++) {
+    const int64_t t = (int64_t)blockIdx.x * kVTilesPerWG + tt;
+    act[tt] = t < ntiles;
+    if (act[tt] && filt.grown && !filt.grown[b * H + h]) {
+      const int64_t lo = t * 64, hi = lo + 64;
+      act[tt] = (filt.r[0] < hi && lo < filt.r[1]) || (filt.r[2] < hi && lo < filt.r[3]);
+    }
   }
-  const float* rc = recp + (b * H + h) * D;
-  const float* mn = vmean ? vmean + (b * H + h) * D : nullptr;
-  // thread: key quad q (keys 4q .. 4q + 3 of the tile, which occupy consecutive slots) x 8 channels
-  for (int c = tid; c < 16 * TPR; c += 256) {
-    const int q = c / TPR, dc = c % TPR;
-    uint16_t hv[4][8];
+  // thread: key quad q (keys 4q .. 4q + 3 of a tile, which occupy consecutive slots) x 8 channels
+  const int q = tid / TPR, dc = tid % TPR;
+  const bool lane = tid < 16 * TPR;
+  uint16_t hv[kVTilesPerWG][4][8];
+#pragma unroll
+  for (int tt = 0; tt < kVTilesPerWG; tt++) {
+    const int64_t t = (int64_t)blockIdx.x * kVTilesPerWG + tt;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int64_t l = t * 64 + 4 * q + r;
       v4u raw = {0u, 0u, 0u, 0u};
-      if (l < L) raw = *reinterpret_cast<const v4u*>(in + b * sb + l * sl + h * sh + dc * 8);
-      __builtin_memcpy(hv[r], &raw, 16);
+      if (act[tt] && lane && l < L) raw = *reinterpret_cast<const v4u*>(in + b * sb + l * sl + h * sh + dc * 8);
+      __builtin_memcpy(hv[tt][r], &raw, 16);
     }
-    const int wi = vtile_pos(4 * q) >> 2;
-    const int sw = (dc & 3) << 2;
+  }
+  const float* rc = recp + (b * H + h) * D;
+  const float* mn = vmean ? vmean + (b * H + h) * D : nullptr;
+  const int wi = vtile_pos(4 * q) >> 2;
+  const int sw = (dc & 3) << 2;
+  if (lane) {
 #pragma unroll
     for (int e = 0; e < 8; e++) {
       const int d = dc * 8 + e;
       const float s = rc[d];
       const float m = mn ? mn[d] : 0.f;
-      uint32_t word = 0;
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        // x * recp or (x - mean) * recp as MeanScaleKernel computes it; key slots past L are zero (they
-        // are masked, and a zero byte keeps P.V finite there even for an all-zero channel's recp = inf)
-        const float x = half_to_f32<IS_FP16>(hv[r][e]);
-        const float y = t * 64 + 4 * q + r < L ? (mn ? (x - m) * s : x * s) : 0.f;
-        word |= (uint32_t)f32_to_e4m3_sat(y) << (8 * r);
+      for (int tt = 0; tt < kVTilesPerWG; tt++) {
+        const int64_t t = (int64_t)blockIdx.x * kVTilesPerWG + tt;
+        uint32_t word = 0;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          // x * recp or (x - mean) * recp as MeanScaleKernel computes it; key slots past L are zero (they
+          // are masked, and a zero byte keeps P.V finite there even for an all-zero channel's recp = inf)
+          const float x = half_to_f32<IS_FP16>(hv[tt][r][e]);
+          const float y = t * 64 + 4 * q + r < L ? (mn ? (x - m) * s : x * s) : 0.f;
+          word |= (uint32_t)f32_to_e4m3_sat(y) << (8 * r);
+        }
+        tile[tt][d][wi ^ sw] = word;
       }
-      tile[d][wi ^ sw] = word;
     }
   }
   __syncthreads();
-  for (int c = tid; c < D * 4; c += 256) {
-    const int d = c / 4, cc = c % 4;
-    const int sc = cc ^ ((d >> 3) & 3);
-    *reinterpret_cast<v4u*>(v8 + ((b * H + h) * D + d) * Lpad + t * 64 + cc * 16) =
-        *reinterpret_cast<const v4u*>(&tile[d][sc * 4]);
+#pragma unroll
+  for (int tt = 0; tt < kVTilesPerWG; tt++) {
+    if (!act[tt]) continue;
+    const int64_t t = (int64_t)blockIdx.x * kVTilesPerWG + tt;
+    for (int c = tid; c < D * 4; c += 256) {
+      const int d = c / 4, cc = c % 4;
+      const int sc = cc ^ ((d >> 3) & 3);
+      *reinterpret_cast<v4u*>(v8 + ((b * H + h) * D + d) * Lpad + t * 64 + cc * 16) =
+          *reinterpret_cast<const v4u*>(&tile[tt][d][sc * 4]);
+    }
   }
+}
+
+// V to FP8 tiles: tiles [0, ntiles) of every (batch entry, head)
+static void launch_v_fp8(int dtype, int64_t D, const uint16_t* p, const qattn_seq& v, int64_t L, int64_t B, int64_t H,
+                         const float* recp, uint8_t* v8, int64_t Lpad, int64_t ntiles, const VTileFilter& filt,
+                         const float* mean, hipStream_t st) {
+  dim3 grid((unsigned)((ntiles + kVTilesPerWG - 1) / kVTilesPerWG), (unsigned)H, (unsigned)B);
+#define QATTN_VF(F16, DD) \
+  v_fp8_kernel<F16, DD><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, ntiles, filt, mean)
+  if (dtype == QATTN_BF16) {
+    if (D == 128) QATTN_VF(false, 128);
+    else QATTN_VF(false, 64);
+  } else {
+    if (D == 128) QATTN_VF(true, 128);
+    else QATTN_VF(true, 64);
+  }
+#undef QATTN_VF
 }
 
 template <int D>
@@ -966,16 +1007,8 @@ extern "C" int qattn_per_channel_fp8_ex(qattn_seq v, int dtype, int64_t B, int64
     if (D == 128) vscale_finalize_kernel<128><<<B * H, 128, 0, st>>>(part, nchunk, scale_max, v_scale, recp);
     else vscale_finalize_kernel<64><<<B * H, 64, 0, st>>>(part, nchunk, scale_max, v_scale, recp);
   }
-  dim3 grid((unsigned)(Lpad / 64), (unsigned)H, (unsigned)B);
-  const uint16_t* p = static_cast<const uint16_t*>(v.data);
   const VTileFilter nof{nullptr, {0, 0, 0, 0}};
-  if (dtype == QATTN_BF16) {
-    if (D == 128) v_fp8_kernel<false, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof, mean);
-    else v_fp8_kernel<false, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof, mean);
-  } else {
-    if (D == 128) v_fp8_kernel<true, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof, mean);
-    else v_fp8_kernel<true, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, L, H, recp, v8, Lpad, nof, mean);
-  }
+  launch_v_fp8(dtype, D, static_cast<const uint16_t*>(v.data), v, L, B, H, recp, v8, Lpad, Lpad / 64, nof, mean, st);
   return check_launch("per_channel_fp8");
 }
 
@@ -1036,15 +1069,8 @@ extern "C" int qattn_v_fp8_cache_update(qattn_seq v, int dtype, int64_t B, int64
   else
     vcache_scale_kernel<64><<<B * H, 64, 0, st>>>(part0, c0, part1, c1, scale_max, amax, v_scale, recp, grown);
   const VTileFilter filt{grown, {begin0, end0, begin1, end1}};
-  dim3 grid((unsigned)((fill + 63) / 64), (unsigned)H, (unsigned)B);
-  const uint16_t* p = static_cast<const uint16_t*>(v.data);
-  if (dtype == QATTN_BF16) {
-    if (D == 128) v_fp8_kernel<false, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, fill, H, recp, v8, Lpad, filt);
-    else v_fp8_kernel<false, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, fill, H, recp, v8, Lpad, filt);
-  } else {
-    if (D == 128) v_fp8_kernel<true, 128><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, fill, H, recp, v8, Lpad, filt);
-    else v_fp8_kernel<true, 64><<<grid, 256, 0, st>>>(p, v.sb, v.sl, v.sh, fill, H, recp, v8, Lpad, filt);
-  }
+  launch_v_fp8(dtype, D, static_cast<const uint16_t*>(v.data), v, fill, B, H, recp, v8, Lpad, (fill + 63) / 64, filt,
+               nullptr, st);
   return check_launch("v_fp8_cache_update");
 }
 
@@ -1301,16 +1327,8 @@ extern "C" int qattn_sage_quant(qattn_seq q, qattn_seq k, qattn_seq v, int dtype
   }
   // 3. V to FP8 tiles (V was read by step 1 just before: its second read finds much of it in cache)
   {
-    dim3 grid((unsigned)(Lpad / 64), (unsigned)Hkv, (unsigned)B);
     const VTileFilter nof{nullptr, {0, 0, 0, 0}};
-    const float* mean = smooth_v ? v_mean : nullptr;
-    if (dtype == QATTN_BF16) {
-      if (D == 128) v_fp8_kernel<false, 128><<<grid, 256, 0, st>>>(vp, v.sb, v.sl, v.sh, Lk, Hkv, recp, v8, Lpad, nof, mean);
-      else v_fp8_kernel<false, 64><<<grid, 256, 0, st>>>(vp, v.sb, v.sl, v.sh, Lk, Hkv, recp, v8, Lpad, nof, mean);
-    } else {
-      if (D == 128) v_fp8_kernel<true, 128><<<grid, 256, 0, st>>>(vp, v.sb, v.sl, v.sh, Lk, Hkv, recp, v8, Lpad, nof, mean);
-      else v_fp8_kernel<true, 64><<<grid, 256, 0, st>>>(vp, v.sb, v.sl, v.sh, Lk, Hkv, recp, v8, Lpad, nof, mean);
-    }
+    launch_v_fp8(dtype, D, vp, v, Lk, B, Hkv, recp, v8, Lpad, Lpad / 64, nof, smooth_v ? v_mean : nullptr, st);
   }
   // 4. K then Q to INT8 in one launch (K first: its rows were read by step 1 as well)
   QuantArgs a{};
