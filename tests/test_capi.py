@@ -103,7 +103,8 @@ def test_kernel_selection_rule(lib):
     assert lib.qattn_fwd_ex_kernel(1, 75600, 513, 40, 0, 1, 0, 0) == multi     # 9 tiles: streamed
     assert lib.qattn_fwd_ex_kernel(1, 75600, 512, 40, 0, 1, 1, 0) != res       # causal: resident does not apply
     assert lib.qattn_fwd_ex_kernel(1, 75600, 512, 40, 1, 1, 0, 0) == one       # half P.V
-    assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 12, 0, 1, 0, 0) == one      # C5: 228 ping-pong workgroups
+    assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 12, 0, 1, 0, 0) == pp       # C5: 228 ping-pong workgroups (7/8 of the CUs)
+    assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 11, 0, 1, 0, 0) == one      # 209: below 7/8
     assert lib.qattn_fwd_ex_kernel(1, 1024, 32760, 2, 0, 1, 0, 0) == one       # KV split
     assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 0) == one        # C1: grid too small
     assert lib.qattn_fwd_ex_kernel(1, 32760, 32760, 12, 1, 1, 0, 0) == one     # half P.V
