@@ -1088,15 +1088,18 @@ __global__ __launch_bounds__(kPPThreads) void qattn_fwd_pp_kernel(AttnParams p) 
 // ---- resident K/V: short key ranges (at most kResMaxTiles tiles, e.g. text cross-attention) ----
 //
 // The whole key range of a head (K int8 and e4m3 V, fragment-major as in the streaming kernels) is
-// loaded into LDS once per workgroup; then each of the 8 waves walks its own 32-row query blocks over
-// the resident tiles with no workgroup barrier at all: Q fragments come straight from global memory
-// (the next block's are in flight while the current one computes), the two waves of a SIMD drift apart
-// freely so that one's softmax overlaps the other's MFMAs, and O leaves through a 2 KiB wave-private
-// LDS stage as whole 64-byte row segments.  Per element the arithmetic is that of qattn_fwd_kernel
+// loaded into LDS once per workgroup; then each of the 12 waves walks its own 32-row query blocks over
+// the resident tiles with no workgroup barrier at all: Q fragments come straight from global memory, the
+// three waves of a SIMD drift apart freely so that one's softmax and Q loads overlap the others' MFMAs,
+// and O leaves through a 2 KiB wave-private LDS stage as whole 64-byte row segments.  Twelve waves leave
+// each 168 VGPRs: K and V fragments are read from LDS next to their MFMAs, and the next block's Q is not
+// prefetched into registers (three waves per SIMD hide its latency better than two waves with prefetch:
+// C4 0.63 -> 0.615 ms).  Per element the arithmetic is that of qattn_fwd_kernel
 // (same MFMA chains, masking, lazy running max, FP8 offset, row sums on the matrix pipe), so the
 // results are identical to it.
 constexpr int kResMaxTiles = 8;
-constexpr int kResThreads = 512;
+constexpr int kResThreads = 768;
+constexpr int kResWaves = kResThreads / 64;
 
 template <bool IS_FP16_OUT, bool KT>
 __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p) {
@@ -1129,17 +1132,19 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
     const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad;
     const int64_t kbytes = (p.Lk - 1) * p.ksl + kD;
     const v4u vrsrc = make_rsrc(vbase, (uint32_t)((int64_t)kD * p.Lpad));
-    // per tile, wave w fills 1 KiB block w of the K tile and block w of the V tile (one DMA instruction
-    // each), so the 8 waves cover both tiles
+    // per tile, wave w < 8 fills 1 KiB block w of the K tile and block w of the V tile (one DMA
+    // instruction each), so waves 0-7 cover both tiles
     const int j = w;
     const uint32_t koff = (uint32_t)(((j & 1) * 32 + lq) * p.ksl + (2 * (j >> 1) + hf) * 16);
     const uint32_t voff = (uint32_t)(((j >> 1) * 32 + lq) * p.Lpad + (2 * hf + (j & 1)) * 16);
     const uint32_t lk0 = lds_addr(&lds_k[0][0]) + w * 1024, lv0 = lds_addr(&lds_v[0][0]) + w * 1024;
-    for (int t = 0; t < n_tiles; t++) {
-      const int64_t kso = (int64_t)t * kBK * p.ksl;
-      const v4u krsrc = make_rsrc(kbase + kso, (uint32_t)(kbytes - kso));
-      lds_dma16(koff, krsrc, 0, lk0 + t * (kBK * kD));
-      lds_dma16(voff, vrsrc, (uint32_t)t * kBK, lv0 + t * (kD * kBK));
+    if (w < 8) {
+      for (int t = 0; t < n_tiles; t++) {
+        const int64_t kso = (int64_t)t * kBK * p.ksl;
+        const v4u krsrc = make_rsrc(kbase + kso, (uint32_t)(kbytes - kso));
+        lds_dma16(koff, krsrc, 0, lk0 + t * (kBK * kD));
+        lds_dma16(voff, vrsrc, (uint32_t)t * kBK, lv0 + t * (kD * kBK));
+      }
     }
     const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
     if (tid < n_tiles * KS) lds_ks[tid] = ks_ptr[tid];
@@ -1149,7 +1154,7 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
     }
   }
 
-  // this wave's 32-row blocks: wb = wb0 + w, wb0 + w + 8, ... below wb_end
+  // this wave's 32-row blocks: wb = wb0 + w, wb0 + w + NW, ... below wb_end
   const int64_t n_wb = (p.Lq + 31) / 32;
   const int64_t wb0 = chunk * p.wb_per_wg;
   const int64_t wb_end = min(n_wb, wb0 + p.wb_per_wg);
@@ -1162,9 +1167,8 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
     for (int m = 0; m < 4; m++)
       qf[m] = row < p.Lq ? *reinterpret_cast<const v4i*>(qhead + row * p.qsl + m * 32 + hf * 16) : v4i{0, 0, 0, 0};
   };
-  v4i qf[4], qn[4];
+  v4i qf[4];
   int64_t wb = wb0 + w;
-  if (wb < wb_end) load_q(wb, qn);
   v16i kbias;
 #pragma unroll
   for (int r = 0; r < 16; r++) kbias[r] = kAccBiasBits;
@@ -1175,9 +1179,7 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
   __syncthreads();  // every wave's share of the key range has landed
 
   for (; wb < wb_end; wb += NW) {
-#pragma unroll
-    for (int m = 0; m < 4; m++) qf[m] = qn[m];
-    if (wb + NW < wb_end) load_q(wb + NW, qn);
+    load_q(wb, qf);
     const int64_t wrow0 = wb * 32, qrow = wrow0 + lq;
     const int64_t qsi = p.qgran == QATTN_GRAN_THREAD ? wb * 8 + (lq & 7) : p.qgran == QATTN_GRAN_WARP ? wb : wb / 4;
     const float qs = qs_tab[qsi] * p.qk_mult;
@@ -1199,14 +1201,12 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
       }
       v16i s[2];
       {
-        v4i kf[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) kf[j] = *reinterpret_cast<const v4i*>(&lds_k[t][j * 1024 + lane * 16]);
         __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int j = 0; j < 8; j++) {
           const int m = j >> 1, kb = j & 1;
-          s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j], qf[m], m == 0 ? kbias : s[kb], 0, 0, 0);
+          const v4i kf = *reinterpret_cast<const v4i*>(&lds_k[t][j * 1024 + lane * 16]);
+          s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, qf[m], m == 0 ? kbias : s[kb], 0, 0, 0);
         }
         __builtin_amdgcn_s_setprio(0);
       }
@@ -1280,17 +1280,14 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
       };
       if (masked) body(std::true_type{});
       else body(std::false_type{});
-      v8i vf[4];
+      const v16f zero = {};
 #pragma unroll
       for (int dblk = 0; dblk < 4; dblk++) {
         const v4i a0 = *reinterpret_cast<const v4i*>(&lds_v[t][(2 * dblk) * 1024 + lane * 16]);
         const v4i a1 = *reinterpret_cast<const v4i*>(&lds_v[t][(2 * dblk + 1) * 1024 + lane * 16]);
-        vf[dblk] = v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        const v8i vf = v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf, kFirst ? zero : o[dblk], 0, 0, 0, 0, 0, 0);
       }
-      const v16f zero = {};
-#pragma unroll
-      for (int dblk = 0; dblk < 4; dblk++)
-        o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, kFirst ? zero : o[dblk], 0, 0, 0, 0, 0, 0);
       lacc = row_sum_mfma(kFirst ? zero : lacc, pf);
     };
     if (n_tiles > 0) {
@@ -1458,18 +1455,18 @@ static int pick_kernel(int pv, bool sparse, int ns, int causal, int64_t B, int64
 }
 
 // Resident-K/V launches: the 32-row wave blocks of each (batch, head) are cut into n_chunk workgroups
-// of wb_per_wg blocks.  One workgroup runs per CU (its LDS holds the key range), 8 waves each taking
-// every 8th block; the cut minimises full rounds of 256 workgroups x (wave rounds per workgroup + one
-// round of start-up for the key-range load).
+// of wb_per_wg blocks.  One workgroup runs per CU (its LDS holds the key range), its kResWaves waves each
+// taking every kResWaves-th block; the cut minimises full rounds of 256 workgroups x (wave rounds per
+// workgroup + one round of start-up for the key-range load).
 static void resident_layout(int64_t bh, int64_t n_wb, int64_t& wb_per_wg, int64_t& n_chunk) {
   double best = 1e300;
   wb_per_wg = n_wb;
   n_chunk = 1;
-  for (int64_t c = 1; c <= std::max<int64_t>(1, (n_wb + 7) / 8); c++) {
+  for (int64_t c = 1; c <= std::max<int64_t>(1, (n_wb + kResWaves - 1) / kResWaves); c++) {
     const int64_t per = (n_wb + c - 1) / c;
     const int64_t chunks = (n_wb + per - 1) / per;
     const int64_t rounds = (bh * chunks + 255) / 256;
-    const double cost = (double)rounds * (double)((per + 7) / 8 + 1);
+    const double cost = (double)rounds * (double)((per + kResWaves - 1) / kResWaves + 1);
     if (cost < best) {
       best = cost;
       wb_per_wg = per;
