@@ -63,6 +63,8 @@ constexpr float kLazyTau = 1.0f;  // lazy-rescale threshold (log2 units), see th
 // without an int -> float conversion per element; the bias is folded into the exp2 offset.
 constexpr int kAccBiasBits = 0x4B400000;
 constexpr float kAccBias = 12582912.0f;
+// a masked logit as -inf: as int32 (-2^23) it lies below every biased logit, as fp32 its exp2 is 0
+constexpr int kMaskedLogitBits = (int)0xFF800000u;
 
 struct AttnParams {
   const int8_t* q8;
@@ -1212,14 +1214,22 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
       }
       const int64_t k0 = (int64_t)t * kBK;
       const bool masked = k0 + kBK > kv_end;
+      // Masked logits become -inf (as int32 below every biased logit, so the max skips them), whose
+      // exp2 is exactly 0: no per-logit select in the softmax.  A zero logit scale (an all-zero block
+      // under the Triton rounding) would turn -inf into NaN there, so a wave with one falls back to
+      // INT32_MIN and the select.
+      bool select_mask = false;
       if (masked) {
+        select_mask = !__all(cs_a > 0.f && cs_b > 0.f);
+        const int mval = select_mask ? INT32_MIN : kMaskedLogitBits;
         const int lim = (int)min(kv_end - k0, (int64_t)kBK) - hf * 4;
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
           for (int r = 0; r < 16; r++)
-            if (kb * 32 + (r >> 2) * 8 + (r & 3) >= lim) s[kb][r] = INT32_MIN;
+            if (kb * 32 + (r >> 2) * 8 + (r & 3) >= lim) s[kb][r] = mval;
       }
+      auto all_masked = [](int x) { return x == INT32_MIN || x == kMaskedLogitBits; };
       float m_tile;
       if constexpr (!KT) {
         int mx = max(s[0][0], s[0][1]);
@@ -1229,7 +1239,7 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
         for (int r = 0; r < 16; r++) mx = max(mx, s[1][r]);
         const auto sw = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);
         mx = max((int)sw[0], (int)sw[1]);
-        m_tile = mx == INT32_MIN ? kMInit : fmaf(__int_as_float(mx), cs_a, -fmaf(kAccBias, cs_a, kFp8Offset - kLazyTau));
+        m_tile = all_masked(mx) ? kMInit : fmaf(__int_as_float(mx), cs_a, -fmaf(kAccBias, cs_a, kFp8Offset - kLazyTau));
       } else {
         int ma = INT32_MIN, mb = INT32_MIN;
 #pragma unroll
@@ -1239,8 +1249,8 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
             if ((r & 3) < 2) ma = max(ma, s[kb][r]);
             else mb = max(mb, s[kb][r]);
           }
-        const float fa = ma == INT32_MIN ? kMInit : fmaf(__int_as_float(ma), cs_a, -fmaf(kAccBias, cs_a, kFp8Offset - kLazyTau));
-        const float fb = mb == INT32_MIN ? kMInit : fmaf(__int_as_float(mb), cs_b, -fmaf(kAccBias, cs_b, kFp8Offset - kLazyTau));
+        const float fa = all_masked(ma) ? kMInit : fmaf(__int_as_float(ma), cs_a, -fmaf(kAccBias, cs_a, kFp8Offset - kLazyTau));
+        const float fb = all_masked(mb) ? kMInit : fmaf(__int_as_float(mb), cs_b, -fmaf(kAccBias, cs_b, kFp8Offset - kLazyTau));
         const float mt = fmaxf(fa, fb);
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
         m_tile = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
@@ -1278,7 +1288,7 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
           pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
         }
       };
-      if (masked) body(std::true_type{});
+      if (select_mask) body(std::true_type{});
       else body(std::false_type{});
       const v16f zero = {};
 #pragma unroll

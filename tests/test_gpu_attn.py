@@ -488,16 +488,17 @@ def test_multi_block_workgroups(oracle, case):
 
 
 @pytest.mark.parametrize("case", ["padding", "ragged", "empty_batch", "gqa_hnd_thread", "fp16_warp_gqa", "one_tile",
-                                  "tiny", "smooth_v", "many_blocks"])
+                                  "tiny", "smooth_v", "many_blocks", "zero_scale_block"])
 def test_resident_kernel_matches(oracle, case):
-    """The resident-K/V kernel (whole key range in LDS, 8 barrier-free waves per workgroup, each on its own
+    """The resident-K/V kernel (whole key range in LDS, 12 barrier-free waves per workgroup, each on its own
     32-row query blocks) runs the per-element arithmetic of qattn_fwd_kernel, so output and LSE must be
     identical, bit for bit, on the same operands.  Checked with key padding (a tail tile of 44 keys), one
     batch without any valid key, ragged lengths whose last wave block is partial, GQA + HND + per-thread
     scales, GQA + per-warp scales + fp16 output, a single tile, fewer queries than one wave block,
-    smoothed V (v_mean epilogue), and enough query blocks that every wave walks many of them; the
-    automatic rule must pick the kernel for these non-causal FP8 launches with Lk <= 512, and the
-    padding case is also checked against the oracle."""
+    smoothed V (v_mean epilogue), enough query blocks that every wave walks many of them, and an
+    all-zero query block under the Triton rounding (q_scale 0: the masked tail tile takes the per-logit
+    select instead of -inf logits); the automatic rule must pick the kernel for these non-causal FP8
+    launches with Lk <= 512, and the padding case is also checked against the oracle."""
     dev = require_gpu()
     from telefuser_amd import _lib
     from telefuser_amd import sageattn2 as sa
@@ -512,17 +513,23 @@ def test_resident_kernel_matches(oracle, case):
         "tiny": (1, 31, 7, 1, 1, "NHD", None, "per_block"),
         "smooth_v": (1, 1200, 400, 2, 2, "NHD", [390], "per_block"),
         "many_blocks": (1, 40000, 300, 2, 2, "NHD", None, "per_block"),
+        "zero_scale_block": (1, 1000, 400, 2, 2, "NHD", [300], "per_block"),
     }[case]
     log(f"resident vs one-block: {case} B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} layout={layout} "
         f"kv_valid={kv_valid} gran={gran}")
     q, k, v = qkv(B, Lq, Lk, Hq, Hkv, seed=4343, k_offset_std=0.5)
+    if case == "zero_scale_block":
+        q[:, :128, 0] = 0  # first query block of head 0: amax 0, q_scale 0 under the Triton rounding
     qd, kd, vd = (t.to(dev) for t in (q, k, v))
     if layout == "HND":
         qd, kd, vd = (t.transpose(1, 2).contiguous() for t in (qd, kd, vd))
     km = sa.k_mean(kd, layout)
     qk_mult = 1.0
     if gran == "per_block":
-        q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=128 ** -0.5, tensor_layout=layout)
+        variant = "triton" if case == "zero_scale_block" else "cuda"
+        q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=128 ** -0.5, tensor_layout=layout, variant=variant)
+        if case == "zero_scale_block":
+            assert float(qs[0, 0, 0]) == 0.0
     else:
         quant = sa.per_thread_int8 if gran == "per_thread" else sa.per_warp_int8
         q8, qs, k8, ks = quant(qd, kd, km, tensor_layout=layout)
