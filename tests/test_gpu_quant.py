@@ -16,25 +16,27 @@ def _as_bits(t):
     return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("B,Lq,Lk,Hq,Hkv,layout,dtype,variant", [
-    (1, 1024, 1024, 2, 2, "NHD", torch.bfloat16, "cuda"),   # config 1
-    (2, 1000, 777, 4, 2, "NHD", torch.bfloat16, "cuda"),    # ragged tails, GQA
-    (1, 300, 130, 3, 3, "HND", torch.bfloat16, "cuda"),
-    (1, 517, 333, 2, 1, "NHD", torch.float16, "cuda"),
-    (1, 1000, 777, 2, 2, "NHD", torch.bfloat16, "triton"),
-    (1, 300, 200, 2, 2, "HND", torch.float16, "triton"),
+@pytest.mark.parametrize("B,Lq,Lk,Hq,Hkv,layout,dtype,variant,D", [
+    (1, 1024, 1024, 2, 2, "NHD", torch.bfloat16, "cuda", 128),   # config 1
+    (2, 1000, 777, 4, 2, "NHD", torch.bfloat16, "cuda", 128),    # ragged tails, GQA
+    (1, 300, 130, 3, 3, "HND", torch.bfloat16, "cuda", 128),
+    (1, 517, 333, 2, 1, "NHD", torch.float16, "cuda", 128),
+    (1, 1000, 777, 2, 2, "NHD", torch.bfloat16, "triton", 128),
+    (1, 300, 200, 2, 2, "HND", torch.float16, "triton", 128),
+    (2, 1000, 777, 4, 2, "NHD", torch.bfloat16, "cuda", 64),     # head_dim 64: two rows per wave pass
+    (1, 517, 333, 2, 1, "HND", torch.float16, "triton", 64),
 ])
-def test_qk_quant_bit_exact(oracle, B, Lq, Lk, Hq, Hkv, layout, dtype, variant):
+def test_qk_quant_bit_exact(oracle, B, Lq, Lk, Hq, Hkv, layout, dtype, variant, D):
     dev = require_gpu()
     from telefuser_amd import sageattn2 as sa
 
-    log(f"qk_quant B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} {layout} {dtype} {variant}")
-    q, k, _ = qkv(B, Lq, Lk, Hq, Hkv, seed=101, k_offset_std=0.5, dtype=dtype)
+    log(f"qk_quant B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} D={D} {layout} {dtype} {variant}")
+    q, k, _ = qkv(B, Lq, Lk, Hq, Hkv, D=D, seed=101, k_offset_std=0.5, dtype=dtype)
     if layout == "HND":
         q, k = q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
     qd, kd = q.to(dev), k.to(dev)
     km = sa.k_mean(kd, layout)
-    sm = 128 ** -0.5
+    sm = D ** -0.5
     q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=sm, tensor_layout=layout, variant=variant)
     torch.cuda.synchronize()
     f16 = dtype == torch.float16
@@ -49,19 +51,21 @@ def test_qk_quant_bit_exact(oracle, B, Lq, Lk, Hq, Hkv, layout, dtype, variant):
     assert np.array_equal(k8.cpu().numpy(), ok8)
 
 
-@pytest.mark.parametrize("B,Lq,Lk,Hq,Hkv,layout,dtype", [
-    (1, 1024, 1024, 2, 2, "NHD", torch.bfloat16),
-    (2, 1000, 777, 4, 2, "NHD", torch.bfloat16),   # ragged: empty trailing warp blocks, partial key blocks
-    (1, 300, 130, 3, 3, "HND", torch.bfloat16),
-    (1, 517, 333, 2, 1, "NHD", torch.float16),
+@pytest.mark.parametrize("B,Lq,Lk,Hq,Hkv,layout,dtype,D", [
+    (1, 1024, 1024, 2, 2, "NHD", torch.bfloat16, 128),
+    (2, 1000, 777, 4, 2, "NHD", torch.bfloat16, 128),   # ragged: empty trailing warp blocks, partial key blocks
+    (1, 300, 130, 3, 3, "HND", torch.bfloat16, 128),
+    (1, 517, 333, 2, 1, "NHD", torch.float16, 128),
+    (2, 1000, 777, 4, 2, "NHD", torch.bfloat16, 64),    # head_dim 64: a wave pass spans two warp blocks
+    (1, 300, 130, 3, 3, "HND", torch.float16, 64),
 ])
-def test_per_thread_and_per_warp_quant_bit_exact(oracle, B, Lq, Lk, Hq, Hkv, layout, dtype):
+def test_per_thread_and_per_warp_quant_bit_exact(oracle, B, Lq, Lk, Hq, Hkv, layout, dtype, D):
     """The reference's default quantizers: Triton per_thread_int8 and CUDA per_warp_int8."""
     dev = require_gpu()
     from telefuser_amd import sageattn2 as sa
 
-    log(f"per_thread/per_warp quant B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} {layout} {dtype}")
-    q, k, _ = qkv(B, Lq, Lk, Hq, Hkv, seed=102, k_offset_std=0.5, dtype=dtype)
+    log(f"per_thread/per_warp quant B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} D={D} {layout} {dtype}")
+    q, k, _ = qkv(B, Lq, Lk, Hq, Hkv, D=D, seed=102, k_offset_std=0.5, dtype=dtype)
     if layout == "HND":
         q, k = q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
     qd, kd = q.to(dev), k.to(dev)
