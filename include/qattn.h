@@ -305,10 +305,7 @@ int qattn_fwd_ex_blocks_per_workgroup(int64_t B, int64_t Lq, int64_t Lk, int64_t
  *   QATTN_KERNEL_RESIDENT:    the whole key range (at most 8 tiles of 64 keys) held in LDS, 12 waves per
  *                             workgroup each walking its own 32-row query blocks without barriers;
  *                             non-causal FP8 launches with Lk <= 512
- *   QATTN_KERNEL_STREAM:      12 waves per workgroup, one 32-row query block each, K/V tiles streamed
- *                             through an LDS ring ordered by counters instead of barriers; non-causal
- *                             FP8 launches
- * All five give identical results for a launch they can run.  qattn_fwd_ex_kernel returns the kernel the
+ * All four give identical results for a launch they can run.  qattn_fwd_ex_kernel returns the kernel the
  * automatic rule picks for these sizes; qattn_set_kernel(k) forces k for the calling thread's later
  * FP8, dense, unsplit launches (QATTN_KERNEL_AUTO restores the rule; MULTI_BLOCK and RESIDENT only where
  * they apply)
@@ -319,8 +316,7 @@ enum qattn_kernel {
   QATTN_KERNEL_ONE_BLOCK = 1,
   QATTN_KERNEL_MULTI_BLOCK = 2,
   QATTN_KERNEL_PINGPONG = 3,
-  QATTN_KERNEL_RESIDENT = 4,
-  QATTN_KERNEL_STREAM = 5
+  QATTN_KERNEL_RESIDENT = 4
 };
 int qattn_fwd_ex_kernel(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int v_kind, int qk_quant_gran, int causal,
                         int num_splits);

@@ -23,10 +23,8 @@ QATTN_GRAN_BLOCK, QATTN_GRAN_WARP, QATTN_GRAN_THREAD = 1, 2, 3
 QATTN_V_FP8, QATTN_V_BF16, QATTN_V_FP16 = 0, 1, 2
 QATTN_KERNEL_AUTO, QATTN_KERNEL_ONE_BLOCK, QATTN_KERNEL_MULTI_BLOCK, QATTN_KERNEL_PINGPONG = 0, 1, 2, 3
 QATTN_KERNEL_RESIDENT = 4
-QATTN_KERNEL_STREAM = 5
 KERNEL_NAMES = {QATTN_KERNEL_ONE_BLOCK: "qattn_fwd_kernel", QATTN_KERNEL_MULTI_BLOCK: "qattn_fwd_kernel (multi-block)",
-                QATTN_KERNEL_PINGPONG: "qattn_fwd_pp_kernel", QATTN_KERNEL_RESIDENT: "qattn_fwd_res_kernel",
-                QATTN_KERNEL_STREAM: "qattn_fwd_fr_kernel"}
+                QATTN_KERNEL_PINGPONG: "qattn_fwd_pp_kernel", QATTN_KERNEL_RESIDENT: "qattn_fwd_res_kernel"}
 
 EXPORTED = (
     "qattn_last_error",

@@ -935,10 +935,11 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
       s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j], qf[m], m == 0 ? kbias : s[kb], 0, 0, 0);
     }
   };
-  auto stage_m = [&](int t) {
-    if (t > 0) read_v(t - 1);
+  auto stage_m = [&](int t, auto first_t) {
+    constexpr bool kFirst = decltype(first_t)::value;
+    if (!kFirst) read_v(t - 1);
     read_k(t);
-    if (t > 0) pv();
+    if (!kFirst) pv();
     qk();
     // the logit scales of the tile, for the softmax of the next stage
     read_cs(t);
@@ -1016,14 +1017,13 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     else body(std::false_type{});
   };
 
-  if (grp == 1) pp_barrier();
-  for (int t = 0; t < n_tiles; t++) {
+  auto step = [&](int t, auto first_t) {
     const bool issue = t + 2 < n_tiles;
     if (issue) dma_tile(t + 2);
     // the matrix stage runs at raised wave priority: the vector-stage wave of the SIMD then cannot
     // delay the issue of its MFMAs (measured faster than equal priorities)
     __builtin_amdgcn_s_setprio(1);
-    stage_m(t);
+    stage_m(t, first_t);
     __builtin_amdgcn_s_setprio(0);
     // this wave's share of tile t + 1 has landed (tile t + 2 may stay in flight)
     if (issue) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
@@ -1031,7 +1031,11 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     pp_barrier();
     stage_v(t);
     pp_barrier();
-  }
+  };
+  if (grp == 1) pp_barrier();
+  // the first tile has no P.V of a previous one: peeled, so the loop body has no branch on it
+  if (n_tiles > 0) step(0, std::true_type{});
+  for (int t = 1; t < n_tiles; t++) step(t, std::false_type{});
   if (grp == 0) pp_barrier();
   if (n_tiles > 0) {
     read_v(n_tiles - 1);
@@ -1349,315 +1353,6 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
   }
 }
 
-// ---- free-running streaming kernel: long key ranges without workgroup barriers ----
-//
-// 12 waves per workgroup (three per SIMD, 168 VGPRs), each owning one 32-row query block of a head for
-// the whole key range, with the per-element arithmetic of qattn_fwd_kernel (same MFMA chains, masking,
-// lazy running max, FP8 offset, row sums on the matrix pipe), so the results are identical to it.  K/V
-// tiles stream through a ring of kFrSlots LDS slots without any barrier: waves 0-7 each DMA 1 KiB of K and
-// 1 KiB of V of tile t + kFrAhead while at tile t, after every active wave has finished the tile that held
-// the slot; a per-slot fill counter (added to by each loader once its DMA has landed) and a per-slot
-// consume counter (added to by each computing wave after its last read of the slot) order the slot's uses.
-// A wave can thus run up to kFrSlots - kFrAhead tiles ahead of the slowest one: the three waves of a SIMD
-// drift out of step and one's softmax overlaps the others' MFMAs, which a barrier per tile (or per four
-// tiles) prevents.  Every wait is bounded (kFrSpinLimit sleeps); a wait that runs out lets the wave go on,
-// which can only corrupt the output, never hang the GPU.
-constexpr int kFrWaves = 12;
-constexpr int kFrThreads = kFrWaves * 64;
-constexpr int kFrSlots = 6;
-constexpr int kFrAhead = 3;
-constexpr int kFrLoaders = 8;  // waves that DMA: 8 x 1 KiB of K and of V per tile
-constexpr int kFrSpinLimit = 1 << 20;
-
-__device__ __forceinline__ void fr_wait_ge(const uint32_t* counter, uint32_t target) {
-  for (int i = 0; i < kFrSpinLimit; i++) {
-    if (*reinterpret_cast<const volatile uint32_t*>(counter) >= target) break;
-    __builtin_amdgcn_s_sleep(1);
-  }
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-}
-
-template <bool IS_FP16_OUT, bool KT>
-__global__ __launch_bounds__(kFrThreads) void qattn_fwd_fr_kernel(AttnParams p) {
-  constexpr int KS = ks_per_tile(KT);
-  __shared__ __align__(16) uint8_t lds_k[kFrSlots][kBK * kD];
-  __shared__ __align__(16) uint8_t lds_v[kFrSlots][kD * kBK];
-  // each wave's Q fragments, fragment-major (fragment m of lane l at 1024 m + 16 l: every read is one
-  // contiguous, conflict-free KiB): the 168-register budget has no room for them next to O, S, the row
-  // sums and the logit bias; the epilogue reuses the space
-  __shared__ __align__(16) uint8_t lds_q[kFrWaves][32 * kD];
-  __shared__ __align__(16) float lds_vs[kD];
-  __shared__ __align__(16) float lds_vm[kD];
-  __shared__ uint32_t filled[kFrSlots], consumed[kFrSlots];
-
-  const int64_t n_wb = (p.Lq + 31) / 32;
-  const int64_t n_chunk = (n_wb + kFrWaves - 1) / kFrWaves;
-  const int64_t wg = xcd_remap(blockIdx.x, gridDim.x);
-  const int64_t chunk = wg % n_chunk;
-  const int64_t h = (wg / n_chunk) % p.Hq;
-  const int64_t b = wg / (n_chunk * p.Hq);
-  const int64_t hk = h / p.group;
-  const int tid = threadIdx.x;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31, hf = lane >> 5;
-  // active waves of this workgroup (the last chunk of a head may have fewer blocks)
-  const int nact = (int)min((int64_t)kFrWaves, n_wb - chunk * kFrWaves);
-  const int64_t wb = chunk * kFrWaves + w;
-  const bool active = w < nact;
-
-  int64_t kv_lim = p.Lk;
-  if (p.kv_valid) kv_lim = min(kv_lim, (int64_t)p.kv_valid[b]);
-  const int64_t kv_end = __builtin_amdgcn_readfirstlane((int)max(kv_lim, (int64_t)0));
-  const int n_tiles = (int)((kv_end + kBK - 1) / kBK);
-
-  if (tid < kFrSlots) {
-    filled[tid] = 0;
-    consumed[tid] = 0;
-  }
-  if (tid < kD) {
-    lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * kD + tid];
-    lds_vm[tid] = p.v_mean ? p.v_mean[(b * p.Hkv + hk) * kD + tid] : 0.f;
-  }
-  __syncthreads();  // counters and scales are set before any wave uses them (the only barrier)
-
-  // ---- loader side: wave w < 8 moves K block w and V block w of a tile (fragment-major, as above) ----
-  const int8_t* kbase = p.k8 + b * p.ksb + hk * p.ksh;
-  const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad;
-  const int64_t kbytes = (p.Lk - 1) * p.ksl + kD;
-  const v4u vrsrc = make_rsrc(vbase, (uint32_t)((int64_t)kD * p.Lpad));
-  const bool loader = w < kFrLoaders;
-  const uint32_t koff = (uint32_t)(((w & 1) * 32 + lq) * p.ksl + (2 * ((w >> 1) & 3) + hf) * 16);
-  const uint32_t voff = (uint32_t)((((w >> 1) & 3) * 32 + lq) * p.Lpad + (2 * hf + (w & 1)) * 16);
-  const uint32_t lk0 = lds_addr(&lds_k[0][0]) + (w & 7) * 1024, lv0 = lds_addr(&lds_v[0][0]) + (w & 7) * 1024;
-  auto dma = [&](int t) {
-    const int slot = t % kFrSlots;
-    const int64_t kso = (int64_t)t * kBK * p.ksl;
-    lds_dma16(koff, make_rsrc(kbase + kso, (uint32_t)(kbytes - kso)), 0, lk0 + slot * (kBK * kD));
-    lds_dma16(voff, vrsrc, (uint32_t)t * kBK, lv0 + slot * (kD * kBK));
-  };
-  auto signal_filled = [&](int t) {
-    if (lane == 0) atomicAdd(&filled[t % kFrSlots], 1u);
-  };
-  if (loader) {
-    for (int t = 0; t < min(n_tiles, kFrAhead); t++) dma(t);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    for (int t = 0; t < min(n_tiles, kFrAhead); t++) signal_filled(t);
-  }
-
-  // ---- compute side ----
-  const int8_t* qhead = p.q8 + b * p.qsb + h * p.qsh;
-  const float* qs_tab = p.q_scale + (b * p.Hq + h) * p.nQS;
-  const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
-  uint8_t* qstage = &lds_q[w][0];
-  if (active) {
-    // lane (lq, hf) holds bytes 32 m + 16 hf .. + 16 of query row lq (the MFMA B operand)
-    const int64_t row = wb * 32 + lq;
-#pragma unroll
-    for (int m = 0; m < 4; m++) {
-      const v4i val = row < p.Lq ? *reinterpret_cast<const v4i*>(qhead + row * p.qsl + m * 32 + hf * 16)
-                                 : v4i{0, 0, 0, 0};
-      *reinterpret_cast<v4i*>(qstage + m * 1024 + lane * 16) = val;
-    }
-  }
-  auto q_frag = [&](int m) { return *reinterpret_cast<const v4i*>(qstage + m * 1024 + lane * 16); };
-  const int64_t wrow0 = wb * 32, qrow = wrow0 + lq;
-  const int64_t qsi = p.qgran == QATTN_GRAN_THREAD ? wb * 8 + (lq & 7) : p.qgran == QATTN_GRAN_WARP ? wb : wb / 4;
-  const float qs = active ? qs_tab[qsi] * p.qk_mult : 0.f;
-  v16i kbias;
-#pragma unroll
-  for (int r = 0; r < 16; r++) kbias[r] = kAccBiasBits;
-  v16f o[4], lacc;
-  float m_run = kMInit;
-  // the key scales through the scalar cache (constant address space: scalar loads, no vector registers)
-  typedef const __attribute__((address_space(4))) float* cfloat_p;
-  const cfloat_p ks_c = (cfloat_p)ks_ptr;
-
-  // One key tile out of its ring slot (the arithmetic of the resident kernel's tile step).
-  auto tile = [&](int t, auto first_t) {
-    constexpr bool kFirst = decltype(first_t)::value;
-    const int slot = t % kFrSlots;
-    float cs_a, cs_b;
-    if constexpr (KT) {
-      const float k0 = ks_c[t * 4], k1 = ks_c[t * 4 + 1], k2 = ks_c[t * 4 + 2], k3 = ks_c[t * 4 + 3];
-      cs_a = qs * (hf ? k2 : k0);
-      cs_b = qs * (hf ? k3 : k1);
-    } else {
-      cs_a = cs_b = qs * ks_c[t];
-    }
-    v16i s[2];
-    {
-      __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const int m = j >> 1, kb = j & 1;
-        const v4i kf = *reinterpret_cast<const v4i*>(&lds_k[slot][j * 1024 + lane * 16]);
-        s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf, q_frag(m), m == 0 ? kbias : s[kb], 0, 0, 0);
-      }
-      __builtin_amdgcn_s_setprio(0);
-    }
-    const int64_t k0 = (int64_t)t * kBK;
-    const bool masked = k0 + kBK > kv_end;
-    bool select_mask = false;
-    if (masked) {
-      select_mask = !__all(cs_a > 0.f && cs_b > 0.f);
-      const int mval = select_mask ? INT32_MIN : kMaskedLogitBits;
-      const int lim = (int)min(kv_end - k0, (int64_t)kBK) - hf * 4;
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int r = 0; r < 16; r++)
-          if (kb * 32 + (r >> 2) * 8 + (r & 3) >= lim) s[kb][r] = mval;
-    }
-    auto all_masked = [](int x) { return x == INT32_MIN || x == kMaskedLogitBits; };
-    float m_tile;
-    if constexpr (!KT) {
-      int mx = max(s[0][0], s[0][1]);
-#pragma unroll
-      for (int r = 2; r < 16; r++) mx = max(mx, s[0][r]);
-#pragma unroll
-      for (int r = 0; r < 16; r++) mx = max(mx, s[1][r]);
-      const auto sw = __builtin_amdgcn_permlane32_swap(mx, mx, false, false);
-      mx = max((int)sw[0], (int)sw[1]);
-      m_tile = all_masked(mx) ? kMInit : fmaf(__int_as_float(mx), cs_a, -fmaf(kAccBias, cs_a, kFp8Offset - kLazyTau));
-    } else {
-      int ma = INT32_MIN, mb = INT32_MIN;
-#pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          if ((r & 3) < 2) ma = max(ma, s[kb][r]);
-          else mb = max(mb, s[kb][r]);
-        }
-      const float fa = all_masked(ma) ? kMInit : fmaf(__int_as_float(ma), cs_a, -fmaf(kAccBias, cs_a, kFp8Offset - kLazyTau));
-      const float fb = all_masked(mb) ? kMInit : fmaf(__int_as_float(mb), cs_b, -fmaf(kAccBias, cs_b, kFp8Offset - kLazyTau));
-      const float mt = fmaxf(fa, fb);
-      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
-      m_tile = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
-    }
-    if constexpr (kFirst) {
-      m_run = m_tile;
-    } else {
-      const bool grow = m_tile > m_run + kLazyTau;
-      if (__any(grow)) {
-        const float m_new = grow ? m_tile : m_run;
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) o[i][r] *= alpha;
-#pragma unroll
-        for (int r = 0; r < 16; r++) lacc[r] *= alpha;
-        m_run = m_new;
-      }
-    }
-    const float nc_a = -fmaf(kAccBias, cs_a, m_run), nc_b = -fmaf(kAccBias, cs_b, m_run);
-    v8i pf;
-    auto body = [&](auto mk) {
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const int kb = j >> 2, r0 = (j & 3) * 4;
-        float pv[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int sv = s[kb][r0 + e];
-          pv[e] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(sv), e < 2 ? cs_a : cs_b, e < 2 ? nc_a : nc_b));
-          if constexpr (decltype(mk)::value) pv[e] = sv == INT32_MIN ? 0.f : pv[e];
-        }
-        const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], __builtin_nondeterministic_value(0), false);
-        pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
-        // four logits at a time: the 168-register budget has no room for all 32 scaled logits at once
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    };
-    if (select_mask) body(std::true_type{});
-    else body(std::false_type{});
-    const v16f zero = {};
-#pragma unroll
-    for (int dblk = 0; dblk < 4; dblk++) {
-      const v4i a0 = *reinterpret_cast<const v4i*>(&lds_v[slot][(2 * dblk) * 1024 + lane * 16]);
-      const v4i a1 = *reinterpret_cast<const v4i*>(&lds_v[slot][(2 * dblk + 1) * 1024 + lane * 16]);
-      const v8i vf = v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-      o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf, kFirst ? zero : o[dblk], 0, 0, 0, 0, 0, 0);
-    }
-    lacc = row_sum_mfma(kFirst ? zero : lacc, pf);
-  };
-
-  for (int t = 0; t < n_tiles; t++) {
-    if (loader) {
-      // the DMA issued two tiles ago has landed (the last tile's pair may still be in flight)
-      if (t >= 2 && t - 2 + kFrAhead < n_tiles) {
-        if (t - 1 + kFrAhead < n_tiles) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        signal_filled(t - 2 + kFrAhead);
-      }
-      const int tl = t + kFrAhead;
-      if (tl < n_tiles) {
-        // the slot's previous tile (tl - kFrSlots) is done in every active wave
-        if (tl >= kFrSlots) fr_wait_ge(&consumed[tl % kFrSlots], (uint32_t)(nact * (tl / kFrSlots)));
-        dma(tl);
-      }
-    }
-    if (active) {
-      fr_wait_ge(&filled[t % kFrSlots], (uint32_t)(kFrLoaders * (t / kFrSlots + 1)));
-      if (t == 0) tile(0, std::true_type{});
-      else tile(t, std::false_type{});
-      // every read of the slot has returned before the slot is released
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      if (lane == 0) atomicAdd(&consumed[t % kFrSlots], 1u);
-    }
-  }
-  if (loader) {
-    // signals of the last DMAs (issued in the last two iterations)
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    for (int t = max(n_tiles, 2); t < n_tiles + 2; t++)
-      if (t - 2 + kFrAhead < n_tiles) signal_filled(t - 2 + kFrAhead);
-  }
-  if (!active) return;
-  if (n_tiles == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) o[i][r] = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; r++) lacc[r] = 0.f;
-  }
-
-  // ---- epilogue: O / l * v_scale (+ v_mean), 32 channels per pass through the 2 KiB stage ----
-  uint8_t* stage = qstage;
-  uint16_t* obase = static_cast<uint16_t*>(p.o) + b * p.osb + h * p.osh;
-  const float l_tot = lacc[0];
-  const float inv_l = l_tot > 0.f ? 1.0f / l_tot : 0.f;
-  auto store = [&](auto mean_t) {
-    constexpr bool kMean = decltype(mean_t)::value;
-#pragma unroll
-    for (int dblk = 0; dblk < 4; dblk++) {
-#pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const int d = dblk * 32 + g * 8 + hf * 4;
-        const v4f sc = *reinterpret_cast<const v4f*>(&lds_vs[d]);
-        const v4f vm = kMean ? *reinterpret_cast<const v4f*>(&lds_vm[d]) : v4f{0.f, 0.f, 0.f, 0.f};
-        float f[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) f[e] = epilogue_value<kMean>(o[dblk][g * 4 + e], inv_l, sc[e], vm[e]);
-        const v2u packed{pack_half2<IS_FP16_OUT>(f[0], f[1]), pack_half2<IS_FP16_OUT>(f[2], f[3])};
-        *reinterpret_cast<v2u*>(stage + lq * 64 + ((g ^ (lq & 3)) << 4) + hf * 8) = packed;
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-      for (int i = 0; i < 2; i++) {
-        const int id = i * 64 + lane, r = id >> 2, c = id & 3;
-        const v4u val = *reinterpret_cast<const v4u*>(stage + r * 64 + ((c ^ (r & 3)) << 4));
-        const int64_t row = wrow0 + r;
-        if (row < p.Lq) *reinterpret_cast<v4u*>(obase + row * p.osl + dblk * 32 + c * 8) = val;
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    }
-  };
-  if (p.v_mean) store(std::true_type{});
-  else store(std::false_type{});
-  if (p.lse && hf == 0 && qrow < p.Lq)
-    p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
-}
-
 // Merge the KV-split partials: one wave per query row, 2 channels per lane.
 template <bool IS_FP16_OUT>
 __global__ __launch_bounds__(256) void qattn_combine_kernel(AttnParams p) {
@@ -1752,7 +1447,7 @@ static thread_local int t_last_kernel = QATTN_KERNEL_AUTO;
 
 extern "C" int qattn_set_kernel(int kernel) {
   const int prev = t_kernel_override;
-  if (kernel >= QATTN_KERNEL_AUTO && kernel <= QATTN_KERNEL_STREAM) t_kernel_override = kernel;
+  if (kernel >= QATTN_KERNEL_AUTO && kernel <= QATTN_KERNEL_RESIDENT) t_kernel_override = kernel;
   return prev;
 }
 
@@ -1766,7 +1461,6 @@ static int pick_kernel(int pv, bool sparse, int ns, int causal, int64_t B, int64
   if (ov == QATTN_KERNEL_PINGPONG || ov == QATTN_KERNEL_ONE_BLOCK) return ov;
   if (ov == QATTN_KERNEL_MULTI_BLOCK && mq_ok && !causal) return QATTN_KERNEL_MULTI_BLOCK;
   if (ov == QATTN_KERNEL_RESIDENT && res_ok) return QATTN_KERNEL_RESIDENT;
-  if (ov == QATTN_KERNEL_STREAM && !causal) return QATTN_KERNEL_STREAM;
   if (res_ok) return QATTN_KERNEL_RESIDENT;
   if (qpw_auto > 1) return QATTN_KERNEL_MULTI_BLOCK;
   // The ping-pong kernel (two 128-row query blocks per workgroup) once its grid fills at least 7/8 of the
@@ -1818,15 +1512,6 @@ static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, siz
       QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
       if (out_dtype == QATTN_BF16) qattn_fwd_res_kernel<false, KT><<<g, kResThreads, 0, st>>>(p);
       else qattn_fwd_res_kernel<true, KT><<<g, kResThreads, 0, st>>>(p);
-      return check_launch("qattn_fwd");
-    }
-    if (kernel == QATTN_KERNEL_STREAM) {
-      p.nsplit = 1;
-      p.tiles_per_split = (int)p.nKB;
-      const int64_t g = p.B * p.Hq * (((p.Lq + 31) / 32 + kFrWaves - 1) / kFrWaves);
-      QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
-      if (out_dtype == QATTN_BF16) qattn_fwd_fr_kernel<false, KT><<<g, kFrThreads, 0, st>>>(p);
-      else qattn_fwd_fr_kernel<true, KT><<<g, kFrThreads, 0, st>>>(p);
       return check_launch("qattn_fwd");
     }
     if (kernel == QATTN_KERNEL_PINGPONG) {
