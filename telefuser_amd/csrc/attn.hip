@@ -179,7 +179,8 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // Row sums of P on the matrix pipe (FP8 P.V): D += ONES . P^T with ONES the all-ones 32 x 64 matrix in
 // fp4 (e2m1 1.0 = 0x2 per nibble, so the A operand takes 4 VGPRs) and P^T the e4m3 B operand of the
 // P.V MFMA: every row of the 32 x 32 result is the column sum of P^T, so each lane's 16 accumulators all
-// hold the running sum l of its query column (both key halves).  l is thus the sum of the e4m3-rounded P
+// hold the running sum l of its query column (both key halves); only element 0 is read, so an online
+// softmax rescale multiplies that one alone (the others keep accumulating, unread).  l is thus the sum of the e4m3-rounded P
 // (the reference's accumulate_d sums p before rounding; the difference is the mean FP8 rounding error of
 // P, far inside the attention tolerance), and 32 VALU adds per tile leave the softmax.
 __device__ __forceinline__ v16f row_sum_mfma(const v16f& acc, const v8i& pf) {
@@ -626,8 +627,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
 #pragma unroll
         for (int r = 0; r < 16; r++) o[i][r] *= alpha;
       if constexpr (PV == PV_FP8)
-#pragma unroll
-        for (int r = 0; r < 16; r++) lacc[r] *= alpha;
+        lacc[0] *= alpha;  // the row sum is read from element 0 only
       m_run = m_new;
     }
     const float nc_a = -fmaf(kAccBias, cs_a, m_run), nc_b = -fmaf(kAccBias, cs_b, m_run);
@@ -991,8 +991,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[i][r] *= alpha;
-#pragma unroll
-      for (int r = 0; r < 16; r++) lacc[r] *= alpha;
+      lacc[0] *= alpha;  // the row sum is read from element 0 only
       m_run = m_new;
     }
     const float nc_a = -fmaf(kAccBias, cs_a, m_run), nc_b = -fmaf(kAccBias, cs_b, m_run);
@@ -1270,8 +1269,7 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
           for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) o[i][r] *= alpha;
-#pragma unroll
-          for (int r = 0; r < 16; r++) lacc[r] *= alpha;
+          lacc[0] *= alpha;  // the row sum is read from element 0 only
           m_run = m_new;
         }
       }
