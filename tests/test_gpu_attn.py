@@ -169,6 +169,27 @@ def test_sageattn_api_and_lse(oracle):
     assert cosine(o.float().cpu().numpy(), truth) >= COS_E2E
 
 
+@pytest.mark.parametrize("gran", ["per_warp", "per_thread"])
+def test_sm90_entry_is_the_sm89_kernel(oracle, gran):
+    """sageattn_qk_int8_pv_fp8_cuda_sm90 runs the same gfx950 kernel and scale layout as the sm89 entry
+    (query scale blocks of 128 rows / 32-row warps, 64-key tiles), not the Hopper kernel's 64 / 16 / 128
+    layout (sageattn2.py:1611-1622): its output is the sm89 entry's, bit for bit, and within the
+    end-to-end tolerance of float64 attention; the two reference layouts group the quantization scales
+    differently, so the reference's two entries themselves differ by quantization noise of this size."""
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    q, k, v = qkv(1, 300, 500, 2, 2, seed=11, k_offset_std=0.5)
+    args = (q.to(dev), k.to(dev), v.to(dev))
+    kw = dict(tensor_layout="NHD", qk_quant_gran=gran, pv_accum_dtype="fp32+fp32")
+    o89 = sa.sageattn_qk_int8_pv_fp8_cuda(*args, **kw)
+    o90 = sa.sageattn_qk_int8_pv_fp8_cuda_sm90(*args, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o89, o90)
+    truth = oracle.attn_fp64(bf16_bits(q), bf16_bits(k), bf16_bits(v), 128 ** -0.5)
+    assert cosine(o90.float().cpu().numpy(), truth) >= COS_E2E
+
+
 def test_head_dim_64_padded(oracle):
     dev = require_gpu()
     from telefuser_amd import sageattn2 as sa
