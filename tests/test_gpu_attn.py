@@ -587,7 +587,7 @@ def test_resident_kernel_matches(oracle, case):
 
 
 @pytest.mark.parametrize("case", ["ragged", "padding", "empty_batch", "causal", "causal_odd", "gqa_hnd_thread",
-                                  "fp16_warp_gqa", "long"])
+                                  "fp16_warp_gqa", "long", "tiny", "causal_tiny", "one_key_valid", "gqa5_smooth_v"])
 def test_pingpong_kernel_matches(oracle, case):
     """The ping-pong kernel (two 4-wave groups per workgroup alternating matrix and vector stages) runs the
     same per-element arithmetic and accumulation order as qattn_fwd_kernel, so its output and LSE must be
@@ -596,7 +596,9 @@ def test_pingpong_kernel_matches(oracle, case):
     ragged lengths (masked tail tiles), key padding per batch (one batch with no valid key at all),
     top-left causal, causal with an odd number of query blocks and more keys than queries, GQA + HND +
     per-thread scales, GQA + per-warp scales + fp16 output, and a key range long enough for the
-    steady-state pipeline.  The long case is also checked against the oracle."""
+    steady-state pipeline; also one query over one key, a causal launch with fewer keys than queries, a
+    batch whose entries keep 1, 64 and 65 keys (tile boundaries), and GQA with five query heads per key
+    head and smoothed V.  The long case is also checked against the oracle."""
     dev = require_gpu()
     from telefuser_amd import _lib
     from telefuser_amd import sageattn2 as sa
@@ -610,6 +612,10 @@ def test_pingpong_kernel_matches(oracle, case):
         "gqa_hnd_thread": (1, 2000, 1500, 4, 2, "HND", False, None, "per_thread"),
         "fp16_warp_gqa": (1, 900, 1100, 6, 2, "NHD", False, None, "per_warp"),
         "long": (1, 700, 8200, 2, 2, "NHD", False, None, "per_block"),
+        "tiny": (1, 1, 1, 2, 2, "NHD", False, None, "per_block"),
+        "causal_tiny": (1, 5, 3, 2, 2, "NHD", True, None, "per_block"),
+        "one_key_valid": (3, 300, 200, 2, 2, "NHD", False, [1, 64, 65], "per_block"),
+        "gqa5_smooth_v": (1, 500, 900, 10, 2, "NHD", False, None, "per_block"),
     }[case]
     log(f"pingpong vs one-block: {case} B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} layout={layout} causal={causal} "
         f"kv_valid={kv_valid} gran={gran}")
@@ -625,10 +631,10 @@ def test_pingpong_kernel_matches(oracle, case):
         quant = sa.per_thread_int8 if gran == "per_thread" else sa.per_warp_int8
         q8, qs, k8, ks = quant(qd, kd, km, tensor_layout=layout)
         qk_mult = 128 ** -0.5 * LOG2E
-    v8, vs, _ = sa.per_channel_fp8(vd, tensor_layout=layout, smooth_v=False)
+    v8, vs, vm = sa.per_channel_fp8(vd, tensor_layout=layout, smooth_v=case == "gqa5_smooth_v")
     out_dtype = torch.float16 if case == "fp16_warp_gqa" else torch.bfloat16
     kw = dict(tensor_layout=layout, out_dtype=out_dtype, is_causal=causal, kv_valid_len=kv_valid,
-              return_lse=True, qk_mult=qk_mult, qk_quant_gran=gran, num_splits=1)
+              return_lse=True, qk_mult=qk_mult, qk_quant_gran=gran, num_splits=1, v_mean=vm)
     L = _lib.load()
     prev = L.qattn_set_kernel(KERNEL_ONE_BLOCK)
     try:
@@ -646,6 +652,18 @@ def test_pingpong_kernel_matches(oracle, case):
     assert torch.equal(l0, l1)
     if case == "empty_batch":  # no valid key: zero output, LSE -inf
         assert bool((o1[1] == 0).all()) and bool(torch.isneginf(l1[1]).all())
+    if case in ("tiny", "one_key_valid", "gqa5_smooth_v", "causal_tiny"):
+        ref, ref_lse = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(),
+                                        k8.contiguous().cpu().numpy(), ks.cpu().numpy(), v8=untile_v(v8),
+                                        v_scale=vs.cpu().numpy(), causal=causal, kv_valid=kv_valid, want_lse=True,
+                                        v_mean=None if vm is None else vm.cpu().numpy(),
+                                        lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED)
+        og = o1.float().cpu().numpy()
+        c = cosine(og, ref)
+        lerr = float(np.nanmax(np.abs(l1.cpu().numpy() - ref_lse)))
+        log(f"  ping-pong kernel vs quantized oracle: cosine={c:.6f} max_abs={float(np.abs(og - ref).max()):.3g} "
+            f"lse_max_abs={lerr:.3g}")
+        assert c >= COS_KERNEL and lerr < 2e-2
     if case == "long":
         ref = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
                                ks.cpu().numpy(), v8=untile_v(v8), v_scale=vs.cpu().numpy(),
