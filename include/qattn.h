@@ -301,7 +301,8 @@ int qattn_fwd_ex_blocks_per_workgroup(int64_t B, int64_t Lq, int64_t Lk, int64_t
  *   QATTN_KERNEL_MULTI_BLOCK: several query blocks of a head per workgroup through one K/V pipeline
  *                             (short, non-causal FP8 key ranges; see qattn_fwd_ex_blocks_per_workgroup)
  *   QATTN_KERNEL_PINGPONG:    two query blocks per workgroup (8 waves) whose wave groups alternate
- *                             matrix and vector stages; dense unsplit FP8 launches whose grid fills the chip
+ *                             matrix and vector stages; dense unsplit FP8 launches whose rounds of 256 CUs cost no more
+ *                             than the one-block grid's
  *   QATTN_KERNEL_RESIDENT:    the whole key range (at most 8 tiles of 64 keys) held in LDS, 12 waves per
  *                             workgroup each walking its own 32-row query blocks without barriers;
  *                             non-causal FP8 launches with Lk <= 512

@@ -1461,9 +1461,17 @@ static int pick_kernel(int pv, bool sparse, int ns, int causal, int64_t B, int64
   if (ov == QATTN_KERNEL_RESIDENT && res_ok) return QATTN_KERNEL_RESIDENT;
   if (res_ok) return QATTN_KERNEL_RESIDENT;
   if (qpw_auto > 1) return QATTN_KERNEL_MULTI_BLOCK;
-  // The ping-pong kernel (two 128-row query blocks per workgroup) once its grid fills at least 7/8 of the
-  // 256 CUs: C5's 228 workgroups run 7 % faster than the 444 one-block workgroups (1.7 rounds of two per CU).
-  return B * Hq * ((nQB + 1) / 2) >= 224 ? QATTN_KERNEL_PINGPONG : QATTN_KERNEL_ONE_BLOCK;
+  // The ping-pong kernel (one workgroup of two 128-row query blocks per CU) against one-block workgroups
+  // (one query block, two per CU), in rounds of the 256 CUs: a ping-pong round takes about T (one pair
+  // over the whole key range), a full round of one-block workgroups ~1.1 T (C2: 3.9 against 3.45 ms for
+  // the same rounds), a last round with a single one-block workgroup on a CU ~0.9 T (one wave per SIMD:
+  // 0.454 against 0.512 ms at 2048 x 32760 x 12).  At the C5 chunk shape with 8, 10, 11 and 12 heads (152
+  // to 228 pairs) the ping-pong grid is 4-9 % faster.
+  const int64_t pairs = B * Hq * ((nQB + 1) / 2), blocks = B * Hq * nQB;
+  const double pp_cost = (double)((pairs + 255) / 256);
+  const int64_t rem = blocks % 512;
+  const double ob_cost = (double)(blocks / 512) * 1.1 + (rem == 0 ? 0.0 : rem > 256 ? 1.1 : 0.9);
+  return pp_cost <= ob_cost ? QATTN_KERNEL_PINGPONG : QATTN_KERNEL_ONE_BLOCK;
 }
 
 // Resident-K/V launches: the 32-row wave blocks of each (batch, head) are cut into n_chunk workgroups

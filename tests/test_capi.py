@@ -104,7 +104,9 @@ def test_kernel_selection_rule(lib):
     assert lib.qattn_fwd_ex_kernel(1, 75600, 512, 40, 0, 1, 1, 0) != res       # causal: resident does not apply
     assert lib.qattn_fwd_ex_kernel(1, 75600, 512, 40, 1, 1, 0, 0) == one       # half P.V
     assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 12, 0, 1, 0, 0) == pp       # C5: 228 ping-pong workgroups (7/8 of the CUs)
-    assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 11, 0, 1, 0, 0) == one      # 209: below 7/8
+    assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 11, 0, 1, 0, 0) == pp       # 209 pairs: one round either way
+    assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 8, 0, 1, 0, 0) == pp        # 152 pairs against 296 blocks
+    assert lib.qattn_fwd_ex_kernel(1, 2048, 32760, 12, 0, 1, 0, 1) == one      # unsplit, 192 blocks: one per CU
     assert lib.qattn_fwd_ex_kernel(1, 1024, 32760, 2, 0, 1, 0, 0) == one       # KV split
     assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 0) == one        # C1: grid too small
     assert lib.qattn_fwd_ex_kernel(1, 32760, 32760, 12, 1, 1, 0, 0) == one     # half P.V
