@@ -296,13 +296,14 @@ int qattn_fwd_ex_blocks_per_workgroup(int64_t B, int64_t Lq, int64_t Lk, int64_t
 /*
  * Which kernel a qattn_fwd_ex launch runs (no counterpart in the reference, whose launch is one CTA
  * kernel per query block; for benchmarks and tests):
- *   QATTN_KERNEL_ONE_BLOCK:   one query block (128 rows, 4 waves) per workgroup; KV-split, half-P.V and
- *                             block-sparse launches always run it
+ *   QATTN_KERNEL_ONE_BLOCK:   one query block (128 rows, 4 waves) per workgroup; half-P.V and
+ *                             block-sparse launches always run it, KV-split launches unless they fit
+ *                             one round of 128-256 ping-pong workgroups
  *   QATTN_KERNEL_MULTI_BLOCK: several query blocks of a head per workgroup through one K/V pipeline
  *                             (short, non-causal FP8 key ranges; see qattn_fwd_ex_blocks_per_workgroup)
  *   QATTN_KERNEL_PINGPONG:    two query blocks per workgroup (8 waves) whose wave groups alternate
  *                             matrix and vector stages; dense unsplit FP8 launches whose rounds of 256 CUs cost no more
- *                             than the one-block grid's
+ *                             than the one-block grid's, and KV-split FP8 launches of 128-256 workgroups
  *   QATTN_KERNEL_RESIDENT:    the whole key range (at most 8 tiles of 64 keys) held in LDS, 12 waves per
  *                             workgroup each walking its own 32-row query blocks without barriers;
  *                             non-causal FP8 launches with Lk <= 512

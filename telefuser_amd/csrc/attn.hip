@@ -772,7 +772,7 @@ __device__ __forceinline__ void pp_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool IS_FP16_OUT, bool KT>
+template <bool IS_FP16_OUT, bool KT, bool SPLIT>
 __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   constexpr int KS = ks_per_tile(KT);
   constexpr int NB = kPPNBuf;
@@ -784,7 +784,11 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   __shared__ __align__(16) float lds_vm[kD];
 
   const int64_t nQP = (p.nQB + 1) / 2;
-  const int64_t tile_id = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t wg_id = xcd_remap(blockIdx.x, gridDim.x);
+  // KV split: split-major order, so the workgroups of one key range of a head run next to each other
+  const int64_t n_pairs = p.B * p.Hq * nQP;
+  const int split = SPLIT ? (int)(wg_id / n_pairs) : 0;
+  const int64_t tile_id = SPLIT ? wg_id - (int64_t)split * n_pairs : wg_id;
   const int64_t qp = tile_id % nQP;
   const int64_t rest = tile_id / nQP;
   const int64_t h = rest % p.Hq;
@@ -814,6 +818,9 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   constexpr int kNoDiag = INT32_MAX - 128;
   const int diag_s = p.causal ? __builtin_amdgcn_readfirstlane((int)min(wrow0 + p.q_offset, (int64_t)kNoDiag)) : kNoDiag;
   const int n_tiles = __builtin_amdgcn_readfirstlane(kv_end_wg > 0 ? (int)((kv_end_wg + kBK - 1) / kBK) : 0);
+  // this workgroup's key tiles t_lo .. t_end - 1 (the split's run, as in qattn_fwd_kernel)
+  const int t_lo = SPLIT ? split * p.tiles_per_split : 0;
+  const int t_end = SPLIT ? min(n_tiles, t_lo + p.tiles_per_split) : n_tiles;
 
   // Q fragments through the wave-private LDS stage (rows row-contiguous, chunk c of row r at c ^ (r & 7))
   uint8_t* stage = &lds_k[0][0] + w * 4096;
@@ -886,12 +893,13 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   for (int r = 0; r < 16; r++) kbias[r] = kAccBiasBits;
 
   __syncthreads();  // Q fragments are out of the LDS stage before the DMA reuses it
-  for (int64_t i = tid; i < n_tiles * KS; i += kPPThreads) lds_ks[i] = ks_ptr[i];
+  // the key scales of tiles t_lo .. t_end - 1, from lds_ks[0]
+  for (int i = tid; i < (t_end - t_lo) * KS; i += kPPThreads) lds_ks[i] = ks_ptr[(int64_t)t_lo * KS + i];
   if (tid < kD) {
     lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * kD + tid];
     lds_vm[tid] = p.v_mean ? p.v_mean[(b * p.Hkv + hk) * kD + tid] : 0.f;
   }
-  for (int t = 0; t < min(n_tiles, 2); t++) dma_tile(t);
+  for (int t = t_lo; t < min(t_end, t_lo + 2); t++) dma_tile(t);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
@@ -906,10 +914,10 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   };
   auto read_cs = [&](int t) {
     if constexpr (KT) {
-      cs_a = qs * lds_ks[t * 4 + 2 * hf];
-      cs_b = qs * lds_ks[t * 4 + 2 * hf + 1];
+      cs_a = qs * lds_ks[(t - t_lo) * 4 + 2 * hf];
+      cs_b = qs * lds_ks[(t - t_lo) * 4 + 2 * hf + 1];
     } else {
-      cs_a = cs_b = qs * lds_ks[t];
+      cs_a = cs_b = qs * lds_ks[t - t_lo];
     }
   };
   auto read_v = [&](int t) {
@@ -1017,7 +1025,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   };
 
   auto step = [&](int t, auto first_t) {
-    const bool issue = t + 2 < n_tiles;
+    const bool issue = t + 2 < t_end;
     if (issue) dma_tile(t + 2);
     // the matrix stage runs at raised wave priority: the vector-stage wave of the SIMD then cannot
     // delay the issue of its MFMAs (measured faster than equal priorities)
@@ -1033,19 +1041,38 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   };
   if (grp == 1) pp_barrier();
   // the first tile has no P.V of a previous one: peeled, so the loop body has no branch on it
-  if (n_tiles > 0) step(0, std::true_type{});
-  for (int t = 1; t < n_tiles; t++) step(t, std::false_type{});
+  if (t_lo < t_end) step(t_lo, std::true_type{});
+  for (int t = t_lo + 1; t < t_end; t++) step(t, std::false_type{});
   if (grp == 0) pp_barrier();
-  if (n_tiles > 0) {
-    read_v(n_tiles - 1);
+  if (t_end > t_lo) {
+    read_v(t_end - 1);
 #pragma unroll
     for (int dblk = 0; dblk < 4; dblk++)
       o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, o[dblk], 0, 0, 0, 0, 0, 0);
     lacc = row_sum_mfma(lacc, pf);
   }
 
-  // ---- epilogue: O / l * v_scale out through the wave's LDS stage (the K buffers are idle now) ----
   const float l_tot = lacc[0];
+  if constexpr (SPLIT) {
+    // the split's partial (unnormalised O, m, l) for the combine kernel, in qattn_fwd_kernel's layout
+    if (qrow >= p.Lq) return;
+    const int64_t row = (((int64_t)split * p.B + b) * p.Hq + h) * p.Lq + qrow;
+    float* wo = p.ws_o + row * kD;
+#pragma unroll
+    for (int dblk = 0; dblk < 4; dblk++)
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int d = dblk * 32 + g * 8 + hf * 4;
+        *reinterpret_cast<v4f*>(wo + d) = v4f{o[dblk][g * 4 + 0], o[dblk][g * 4 + 1], o[dblk][g * 4 + 2], o[dblk][g * 4 + 3]};
+      }
+    if (hf == 0) {
+      p.ws_ml[row * 2 + 0] = m_run;
+      p.ws_ml[row * 2 + 1] = l_tot;
+    }
+    return;
+  }
+
+  // ---- epilogue: O / l * v_scale out through the wave's LDS stage (the K buffers are idle now) ----
   const float inv_l = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   uint16_t* obase = static_cast<uint16_t*>(p.o) + b * p.osb + h * p.osh;
   auto store = [&](auto mean_t) {
@@ -1085,9 +1112,9 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
 }
 
-template <bool IS_FP16_OUT, bool KT>
+template <bool IS_FP16_OUT, bool KT, bool SPLIT>
 __global__ __launch_bounds__(kPPThreads) void qattn_fwd_pp_kernel(AttnParams p) {
-  qattn_fwd_pp<IS_FP16_OUT, KT>(p);
+  qattn_fwd_pp<IS_FP16_OUT, KT, SPLIT>(p);
 }
 
 // ---- resident K/V: short key ranges (at most kResMaxTiles tiles, e.g. text cross-attention) ----
@@ -1395,8 +1422,13 @@ static int64_t max_tiles_per_split(int pv, bool kt) {
   return floats / ks_per_tile(kt);
 }
 
-static int num_splits_for(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t max_tiles) {
-  const int64_t wgs = B * Hq * ((Lq + kBQ - 1) / kBQ);
+// Ping-pong KV-split launches take whole pairs of query blocks; an odd block count leaves the last pair's
+// second wave group idle, allowed when that is at most 1/6 of the groups.
+static bool pp_split_fits(int64_t nqb) { return nqb % 2 == 0 || nqb >= 5; }
+
+static int num_splits_for(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t max_tiles, bool pp) {
+  const int64_t nqb = (Lq + kBQ - 1) / kBQ;
+  const int64_t wgs = B * Hq * nqb;
   const int64_t nkb = (Lk + kBK - 1) / kBK;
   if (wgs <= 0 || nkb <= 0) return 1;
   // 256 CUs x 2 resident workgroups.  Split only when the grid leaves CUs without any workgroup: at
@@ -1406,17 +1438,26 @@ static int num_splits_for(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t
   const int64_t target = 1024;
   const int64_t min_s = (nkb + max_tiles - 1) / max_tiles;
   if (wgs >= target / 4) return (int)min_s;
+  if (pp && pp_split_fits(nqb)) {
+    // FP8 dense launches: splits for one round of at most 256 ping-pong workgroups (one per CU).  Against
+    // the earlier count (about 1024 one-block workgroups) 5-27 % faster at 512-4680 queries over 8k-32k keys,
+    // with either kernel (fewer splits, less combine traffic)
+    const int64_t pairs = B * Hq * ((nqb + 1) / 2);
+    const int64_t s = std::min<int64_t>(std::min<int64_t>(256 / pairs, nkb / 8), 32);
+    return (int)std::max<int64_t>(min_s, std::max<int64_t>(s, 1));
+  }
   int64_t s = (target + wgs - 1) / wgs;
   s = std::min<int64_t>(s, nkb / 8);
   return (int)std::max<int64_t>(min_s, std::min<int64_t>(s, 32));
 }
 
 extern "C" int qattn_fwd_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq) {
-  return num_splits_for(B, Lq, Lk, Hq, max_tiles_per_split(PV_FP8, false));
+  return num_splits_for(B, Lq, Lk, Hq, max_tiles_per_split(PV_FP8, false), true);
 }
 
 extern "C" int qattn_fwd_ex_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int v_kind, int qk_quant_gran) {
-  return num_splits_for(B, Lq, Lk, Hq, max_tiles_per_split(v_kind, qk_quant_gran == QATTN_GRAN_THREAD));
+  return num_splits_for(B, Lq, Lk, Hq, max_tiles_per_split(v_kind, qk_quant_gran == QATTN_GRAN_THREAD),
+                        v_kind == QATTN_V_FP8);
 }
 
 static int blocks_per_workgroup(int64_t bh, int64_t nqb, int64_t nkb);
@@ -1426,7 +1467,8 @@ extern "C" int qattn_fwd_ex_blocks_per_workgroup(int64_t B, int64_t Lq, int64_t 
   if (v_kind != QATTN_V_FP8 || causal || B <= 0 || Lq <= 0 || Lk <= 0 || Hq <= 0) return 1;
   const int64_t nkb = (Lk + kBK - 1) / kBK, nqb = (Lq + kBQ - 1) / kBQ;
   if (nkb > kMqMaxTiles) return 1;
-  if (num_splits_for(B, Lq, Lk, Hq, max_tiles_per_split(PV_FP8, qk_quant_gran == QATTN_GRAN_THREAD)) != 1) return 1;
+  if (num_splits_for(B, Lq, Lk, Hq, max_tiles_per_split(PV_FP8, qk_quant_gran == QATTN_GRAN_THREAD), true) != 1)
+    return 1;
   return blocks_per_workgroup(B * Hq, nqb, nkb);
 }
 
@@ -1454,8 +1496,18 @@ extern "C" int qattn_last_kernel(void) { return t_last_kernel; }
 // the kernel a launch runs, given its split count and whether the multi-block / resident layouts apply
 static int pick_kernel(int pv, bool sparse, int ns, int causal, int64_t B, int64_t Hq, int64_t nQB, int qpw_auto,
                        bool mq_ok, bool res_ok) {
-  if (pv != PV_FP8 || sparse || ns > 1) return QATTN_KERNEL_ONE_BLOCK;
+  if (pv != PV_FP8 || sparse) return QATTN_KERNEL_ONE_BLOCK;
   const int ov = t_kernel_override;
+  // KV-split launches: the ping-pong kernel when its grid of pairs x splits is one round of 128 to 256
+  // workgroups over whole pairs (the split count the automatic rule picks for it: 3-5 % faster than the
+  // one-block kernel with the same splits), else the one-block kernel (also for tiny grids such as C1's
+  // 16 ping-pong workgroups, where its 32 run 1 us faster)
+  if (ns > 1) {
+    if (ov == QATTN_KERNEL_PINGPONG) return QATTN_KERNEL_PINGPONG;
+    const int64_t g = B * Hq * ((nQB + 1) / 2) * ns;
+    const bool pp = ov == QATTN_KERNEL_AUTO && pp_split_fits(nQB) && g >= 128 && g <= 256;
+    return pp ? QATTN_KERNEL_PINGPONG : QATTN_KERNEL_ONE_BLOCK;
+  }
   if (ov == QATTN_KERNEL_PINGPONG || ov == QATTN_KERNEL_ONE_BLOCK) return ov;
   if (ov == QATTN_KERNEL_MULTI_BLOCK && mq_ok && !causal) return QATTN_KERNEL_MULTI_BLOCK;
   if (ov == QATTN_KERNEL_RESIDENT && res_ok) return QATTN_KERNEL_RESIDENT;
@@ -1521,12 +1573,25 @@ static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, siz
       return check_launch("qattn_fwd");
     }
     if (kernel == QATTN_KERNEL_PINGPONG) {
-      p.nsplit = 1;
-      p.tiles_per_split = (int)p.nKB;
-      const int64_t g = p.B * p.Hq * ((p.nQB + 1) / 2);
+      const int64_t g = p.B * p.Hq * ((p.nQB + 1) / 2) * ns;
       QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
-      if (out_dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT><<<g, kPPThreads, 0, st>>>(p);
-      else qattn_fwd_pp_kernel<true, KT><<<g, kPPThreads, 0, st>>>(p);
+      p.nsplit = ns;
+      p.tiles_per_split = (int)((p.nKB + ns - 1) / ns);
+      if (ns > 1) {
+        QATTN_REQUIRE(workspace && workspace_bytes >= qattn_fwd_workspace_size(p.B, p.Lq, p.Hq, D, ns),
+                      QATTN_ERR_WORKSPACE, "qattn_fwd with %d KV splits needs %zu workspace bytes", ns,
+                      qattn_fwd_workspace_size(p.B, p.Lq, p.Hq, D, ns));
+        p.ws_o = static_cast<float*>(workspace);
+        p.ws_ml = p.ws_o + (int64_t)ns * p.B * p.Hq * p.Lq * D;
+        if (out_dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT, true><<<g, kPPThreads, 0, st>>>(p);
+        else qattn_fwd_pp_kernel<true, KT, true><<<g, kPPThreads, 0, st>>>(p);
+        const int64_t rows = p.B * p.Hq * p.Lq;
+        if (out_dtype == QATTN_BF16) qattn_combine_kernel<false><<<(rows + 3) / 4, 256, 0, st>>>(p);
+        else qattn_combine_kernel<true><<<(rows + 3) / 4, 256, 0, st>>>(p);
+      } else {
+        if (out_dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT, false><<<g, kPPThreads, 0, st>>>(p);
+        else qattn_fwd_pp_kernel<true, KT, false><<<g, kPPThreads, 0, st>>>(p);
+      }
       return check_launch("qattn_fwd");
     }
   }
@@ -1577,7 +1642,7 @@ static void plan_fwd(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int pv, int 
                      int num_splits, int& ns, int& qpw, int& kernel) {
   const int64_t nQB = (Lq + kBQ - 1) / kBQ, nKB = (Lk + kBK - 1) / kBK;
   const int64_t max_tiles = sparse ? kSpMaxTiles : max_tiles_per_split(pv, gran == QATTN_GRAN_THREAD);
-  ns = num_splits > 0 ? num_splits : num_splits_for(B, Lq, Lk, Hq, max_tiles);
+  ns = num_splits > 0 ? num_splits : num_splits_for(B, Lq, Lk, Hq, max_tiles, pv == PV_FP8 && !sparse);
   ns = (int)std::min<int64_t>(ns, nKB);
   if (ns < 1) ns = 1;
   // a workgroup stages the k_scales of at most max_tiles key tiles
@@ -1810,7 +1875,7 @@ extern "C" int qattn_fwd_pv16(qattn_seq q8, const float* q_scale, qattn_seq k8, 
 }
 
 extern "C" int qattn_fwd_block_sparse_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq) {
-  return num_splits_for(B, Lq, Lk, Hq, kSpMaxTiles);
+  return num_splits_for(B, Lq, Lk, Hq, kSpMaxTiles, false);
 }
 
 extern "C" int qattn_fwd_block_sparse(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale,

@@ -107,13 +107,18 @@ def test_kernel_selection_rule(lib):
     assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 11, 0, 1, 0, 0) == pp       # 209 pairs: one round either way
     assert lib.qattn_fwd_ex_kernel(1, 4680, 32760, 8, 0, 1, 0, 0) == pp        # 152 pairs against 296 blocks
     assert lib.qattn_fwd_ex_kernel(1, 2048, 32760, 12, 0, 1, 0, 1) == one      # unsplit, 192 blocks: one per CU
-    assert lib.qattn_fwd_ex_kernel(1, 1024, 32760, 2, 0, 1, 0, 0) == one       # KV split
-    assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 0) == one        # C1: grid too small
+    assert lib.qattn_fwd_ex_kernel(1, 1024, 32760, 2, 0, 1, 0, 0) == pp        # KV split over 8 pairs: ping-pong
+    assert lib.qattn_fwd_ex_num_splits(1, 1024, 32760, 2, 0, 1) == 32          # 256 / 8 pairs, at most 32
+    assert lib.qattn_fwd_ex_num_splits(1, 4680, 32760, 4, 0, 1) == 3           # 76 pairs -> 228 workgroups
+    assert lib.qattn_fwd_ex_kernel(1, 128, 32760, 8, 0, 1, 0, 0) == one        # one block per head: idle pairs
+    assert lib.qattn_fwd_ex_kernel(1, 1024, 32760, 2, 1, 1, 0, 0) == one       # half P.V split
+    assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 0) == one        # C1: 16 ping-pong workgroups, too few
     assert lib.qattn_fwd_ex_kernel(1, 32760, 32760, 12, 1, 1, 0, 0) == one     # half P.V
     prev = lib.qattn_set_kernel(pp)
     try:
         assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 1) == pp
-        assert lib.qattn_fwd_ex_kernel(1, 1024, 32760, 2, 0, 1, 0, 0) == one   # a split launch cannot
+        assert lib.qattn_fwd_ex_kernel(1, 1024, 32760, 2, 0, 1, 0, 0) == pp    # forced: split ping-pong
+        assert lib.qattn_fwd_ex_kernel(1, 1024, 32760, 2, 1, 1, 0, 0) == one   # half P.V: no ping-pong form
         lib.qattn_set_kernel(multi)
         assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 1, 1) == one    # causal: multi-block does not apply
         assert lib.qattn_fwd_ex_kernel(1, 1024, 1024, 2, 0, 1, 0, 1) == multi
