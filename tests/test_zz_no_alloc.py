@@ -50,7 +50,7 @@ def test_noalloc_matches_workspace_entry_twice():
 
     L = _lib.load()
     cases = [  # (B, Lq, Lk, H, splits, kv_valid): a C5-length chunk on 2 heads with its automatic split
-        (1, 4680, 32760, 2, 0, None),  # (74 workgroups: 14 splits), then a smaller launch
+        (1, 4680, 32760, 2, 0, None),  # (38 pairs: 6 splits, ping-pong), then a smaller launch
         (2, 700, 9000, 3, 5, [9000, 4100]),
     ]
     for i, (B, Lq, Lk, H, splits, kvv) in enumerate(cases):
