@@ -287,7 +287,7 @@ int qattn_fwd_ex_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int v
 /*
  * Query blocks (128 rows) one workgroup of qattn_fwd_ex streams through a single K/V pipeline for an
  * automatic-split call with these sizes (1 = one block per workgroup).  Short, non-causal FP8 P.V key
- * ranges (at most 64 key tiles) over grids larger than the resident 512 workgroups use several, so the
+ * ranges (fewer than 24 key tiles) over grids larger than the resident 512 workgroups use several, so the
  * per-workgroup start-up and the epilogue overlap the next block's work; the result does not depend on
  * it.  No counterpart in the reference (its launch is one CTA per query block).
  */
