@@ -588,7 +588,8 @@ def test_resident_kernel_matches(oracle, case):
 
 @pytest.mark.parametrize("case", ["ragged", "padding", "empty_batch", "causal", "causal_odd", "gqa_hnd_thread",
                                   "fp16_warp_gqa", "long", "tiny", "causal_tiny", "one_key_valid", "gqa5_smooth_v",
-                                  "split3", "split_causal", "split_thread_gqa_hnd", "split_padding_empty"])
+                                  "split3", "split_causal", "split_thread_gqa_hnd", "split_padding_empty",
+                                  "split_causal_offset"])
 def test_pingpong_kernel_matches(oracle, case):
     """The ping-pong kernel (two 4-wave groups per workgroup alternating matrix and vector stages) runs the
     same per-element arithmetic and accumulation order as qattn_fwd_kernel, so its output and LSE must be
@@ -624,8 +625,11 @@ def test_pingpong_kernel_matches(oracle, case):
         "split_causal": (1, 1100, 1300, 2, 2, "NHD", True, None, "per_block"),
         "split_thread_gqa_hnd": (1, 900, 3000, 4, 2, "HND", False, None, "per_thread"),
         "split_padding_empty": (2, 400, 5000, 2, 2, "NHD", False, [2100, 0], "per_block"),
+        "split_causal_offset": (1, 700, 4000, 2, 2, "NHD", True, None, "per_block"),
     }[case]
-    ns = {"split3": 3, "split_causal": 2, "split_thread_gqa_hnd": 4, "split_padding_empty": 5}.get(case, 1)
+    ns = {"split3": 3, "split_causal": 2, "split_thread_gqa_hnd": 4, "split_padding_empty": 5,
+          "split_causal_offset": 4}.get(case, 1)
+    q_offset = 3000 if case == "split_causal_offset" else 0  # a chunk of queries after 3000 earlier keys
     log(f"pingpong vs one-block: {case} B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} layout={layout} causal={causal} "
         f"kv_valid={kv_valid} gran={gran}")
     q, k, v = qkv(B, Lq, Lk, Hq, Hkv, seed=4242, k_offset_std=0.5)
@@ -643,7 +647,7 @@ def test_pingpong_kernel_matches(oracle, case):
     v8, vs, vm = sa.per_channel_fp8(vd, tensor_layout=layout, smooth_v=case == "gqa5_smooth_v")
     out_dtype = torch.float16 if case == "fp16_warp_gqa" else torch.bfloat16
     kw = dict(tensor_layout=layout, out_dtype=out_dtype, is_causal=causal, kv_valid_len=kv_valid,
-              return_lse=True, qk_mult=qk_mult, qk_quant_gran=gran, num_splits=ns, v_mean=vm)
+              return_lse=True, qk_mult=qk_mult, qk_quant_gran=gran, num_splits=ns, v_mean=vm, q_offset=q_offset)
     L = _lib.load()
     prev = L.qattn_set_kernel(KERNEL_ONE_BLOCK)
     try:
@@ -662,13 +666,14 @@ def test_pingpong_kernel_matches(oracle, case):
     if case == "empty_batch":  # no valid key: zero output, LSE -inf
         assert bool((o1[1] == 0).all()) and bool(torch.isneginf(l1[1]).all())
     if case in ("tiny", "one_key_valid", "gqa5_smooth_v", "causal_tiny", "split3", "split_causal",
-                "split_thread_gqa_hnd", "split_padding_empty"):
+                "split_thread_gqa_hnd", "split_padding_empty", "split_causal_offset"):
         nkb = (Lk + 63) // 64
         if layout == "HND":
             o1, q8, k8 = o1.transpose(1, 2), q8.transpose(1, 2), k8.transpose(1, 2)
         ref, ref_lse = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(),
                                         k8.contiguous().cpu().numpy(), ks.cpu().numpy(), v8=untile_v(v8),
-                                        v_scale=vs.cpu().numpy(), causal=causal, kv_valid=kv_valid, want_lse=True,
+                                        v_scale=vs.cpu().numpy(), causal=causal, q_offset=q_offset,
+                                        kv_valid=kv_valid, want_lse=True,
                                         v_mean=None if vm is None else vm.cpu().numpy(), qk_mult=qk_mult,
                                         q_gran=GRAN_CODE[gran], k_gran=GRAN_CODE[gran],
                                         tiles_per_split=(nkb + ns - 1) // ns if ns > 1 else 0,
