@@ -175,6 +175,15 @@ __device__ __forceinline__ float epilogue_value(float o, float inv_l, float sc, 
   else return x;
 }
 
+// Two floats -> e4m3 in the low 16 bits of a fresh register (RNE, unclamped).  The high word is left as
+// whatever the register held: callers overwrite it with a second, word-selected conversion.  Written as
+// inline asm because the builtin ties the destination to an "old" operand, which costs a v_mov per pair.
+__device__ __forceinline__ int cvt_pk_fp8_lo(float a, float b) {
+  int r;
+  asm("v_cvt_pk_fp8_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
 }
@@ -652,9 +661,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
         for (int j = 0; j < 8; j++) {
           float pv[4];
           p4(j, pv, mk);
-          // the low word is written first and the high word then overwrites the rest of the register,
-          // so its incoming value does not matter (an undefined one needs no copy)
-          const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], __builtin_nondeterministic_value(0), false);
+          // low word first, then the high word overwrites the rest of the register
+          const int packed = cvt_pk_fp8_lo(pv[0], pv[1]);
           pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
         }
       };
@@ -954,6 +962,17 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     qk();
     // the logit scales of the tile, for the softmax of the next stage
     read_cs(t);
+    if constexpr (!kFirst) {
+      // LDS reads three ahead of the MFMA that consumes them: 3 reads, then (1 MFMA, 2 reads) x 7,
+      // then the remaining MFMAs (16 fragment reads + the key-scale read; 13 MFMAs with the row sum)
+      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+#pragma unroll
+      for (int i = 0; i < 7; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+    }
   };
   // stage V: V(t) fragments out of LDS (operands of the next stage M), mask, online softmax, P(t) to e4m3
   auto stage_v = [&](int t) {
@@ -1017,9 +1036,8 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
           pv[e] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(sv), e < 2 ? cs_a : cs_b, e < 2 ? nc_a : nc_b));
           if constexpr (decltype(mk)::value) pv[e] = sv == INT32_MIN ? 0.f : pv[e];
         }
-        // the low word is written first and the high word then overwrites the rest of the register, so
-        // its incoming value does not matter: an undefined one lets the compiler skip a copy per pair
-        const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], __builtin_nondeterministic_value(0), false);
+        // low word first, then the high word overwrites the rest of the register
+        const int packed = cvt_pk_fp8_lo(pv[0], pv[1]);
         pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
       }
     };
@@ -1316,7 +1334,7 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
             pv[e] = __builtin_amdgcn_exp2f(fmaf(__int_as_float(sv), e < 2 ? cs_a : cs_b, e < 2 ? nc_a : nc_b));
             if constexpr (decltype(mk)::value) pv[e] = sv == INT32_MIN ? 0.f : pv[e];
           }
-          const int packed = __builtin_amdgcn_cvt_pk_fp8_f32(pv[0], pv[1], __builtin_nondeterministic_value(0), false);
+          const int packed = cvt_pk_fp8_lo(pv[0], pv[1]);
           pf[j] = __builtin_amdgcn_cvt_pk_fp8_f32(pv[2], pv[3], packed, true);
         }
       };

@@ -34,3 +34,24 @@ def require_gpu():
 
 def log(msg):
     print(msg, flush=True)
+
+
+def lse_max_err(lse, ref_lse, out=None) -> float:
+    """Max |lse - ref_lse| over the rows that have keys, after checking the rows that have none.
+
+    A row with no valid key has LSE -inf on both sides (log of an empty sum) and, when `out` is given
+    ([..., rows, D] aligned with the LSE's rows), an all-zero output row.  No NaN is accepted on either
+    side, so a kernel that wrote NaN or a finite value for an empty row fails here."""
+    lse = np.asarray(lse, np.float64)
+    ref_lse = np.asarray(ref_lse, np.float64)
+    assert lse.shape == ref_lse.shape, (lse.shape, ref_lse.shape)
+    assert not np.isnan(lse).any(), "NaN in the kernel's LSE"
+    assert not np.isnan(ref_lse).any(), "NaN in the oracle's LSE"
+    empty = np.isneginf(ref_lse)
+    assert np.array_equal(np.isneginf(lse), empty), "rows without keys differ between kernel and oracle"
+    assert not np.isposinf(lse).any()
+    if out is not None and empty.any():
+        o = np.asarray(out)
+        assert np.all(o[empty] == 0), "a row without keys has a non-zero output"
+    fin = ~empty
+    return float(np.abs(lse[fin] - ref_lse[fin]).max()) if fin.any() else 0.0
