@@ -243,8 +243,12 @@ def _config_bench(name: str, calls: int = 5, warmup: int = 2) -> dict:
         call(True)
     torch.cuda.synchronize()
     ms_call = (time.perf_counter() - t0) * 1e3 / calls
-    kernel = _lib.KERNEL_NAMES.get(L.qattn_last_kernel(), "?")
-    splits = L.qattn_fwd_num_splits(cfg.B, cfg.Lq, cfg.Lk, cfg.Hq)
+    # the label comes from the rule the launch used (FP8 V, per-block scales, non-causal, automatic splits),
+    # and must agree with the kernel the last launch reports
+    splits = L.qattn_fwd_ex_num_splits(cfg.B, cfg.Lq, cfg.Lk, cfg.Hq, _lib.QATTN_V_FP8, _lib.QATTN_GRAN_BLOCK)
+    kernel_id = L.qattn_fwd_ex_kernel(cfg.B, cfg.Lq, cfg.Lk, cfg.Hq, _lib.QATTN_V_FP8, _lib.QATTN_GRAN_BLOCK, 0, 0)
+    assert kernel_id == L.qattn_last_kernel(), (kernel_id, L.qattn_last_kernel())
+    kernel = _lib.KERNEL_NAMES.get(kernel_id, "?")
     ms_attn = sum(a.elapsed_time(b) for a, b in t_attn) / len(t_attn)
     ops = cfg.ops()
     res = {"workload": cfg.name, "calls": calls, "ms_per_call": round(ms_call, 4), "attn_ms": round(ms_attn, 4),

@@ -346,8 +346,12 @@ int qattn_fwd_ex2(qattn_seq q8, const float* q_scale, qattn_seq k8, const float*
  * HIP graph capture, tight serving loops).  No counterpart in the reference.  KV-split partials go to a
  * device array inside the library (one per GPU, held until the process ends) of at most
  * qattn_fwd_noalloc_max_scratch() bytes (128 MiB): a launch whose qattn_fwd_workspace_size(B, Lq, Hq, D,
- * splits) exceeds it fails with QATTN_ERR_WORKSPACE.  Calls never allocate; calls that overlap on one GPU
- * (different streams or threads) share that array and race.  Results equal qattn_fwd_ex's.
+ * splits) exceeds it fails with QATTN_ERR_WORKSPACE.  Calls never allocate device memory.  Launches that use
+ * the array (KV-split launches) are ordered on the GPU in the order the host issues them, also from different
+ * streams or threads: each waits (hipStreamWaitEvent, no host wait) for the previous one's completion event.
+ * On a stream under graph capture that ordering is left to the graph: replays of a captured graph must not
+ * overlap other users of the array on the same GPU.  The array exists on every GPU where the library's code
+ * object is loaded, whether or not this entry is called.  Results equal qattn_fwd_ex's.
  */
 size_t qattn_fwd_noalloc_max_scratch(void);
 int qattn_fwd_ex_noalloc(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const void* v,

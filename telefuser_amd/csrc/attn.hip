@@ -1824,24 +1824,35 @@ extern "C" int qattn_fwd_varlen(qattn_seq q8, const float* q_scale, qattn_seq k8
 constexpr size_t kScratchBytes = 128ull << 20;
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 constexpr int kMaxDevices = 64;
-static std::mutex g_scratch_mu;
+static std::mutex g_scratch_mu;  // guards the per-device tables and orders the scratch users (below)
 static void* g_scratch_ptr[kMaxDevices];
+// Completion of the last launch that used a device's scratch.  Each launch that uses the scratch first makes
+// its stream wait for this event and then records it again, so launches from different streams (or threads)
+// take the array one after the other in the order the host issued them (hipStreamWaitEvent is asynchronous:
+// no host wait).  Created with the symbol lookup on the first call that needs the scratch on the device.
+static hipEvent_t g_scratch_done[kMaxDevices];
 
-// the scratch address on the calling thread's current device, looked up once per device
-static int scratch_on_current_device(void** out) {
+// the scratch address and its ordering event on the calling thread's current device, set up once per device;
+// the caller holds g_scratch_mu
+static int scratch_on_current_device(void** out, int* dev_out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   QATTN_REQUIRE(e == hipSuccess && dev >= 0 && dev < kMaxDevices, QATTN_ERR_LAUNCH, "hipGetDevice failed: %s",
                 hipGetErrorString(e));
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
     void* ptr = nullptr;
     e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     QATTN_REQUIRE(e == hipSuccess && ptr, QATTN_ERR_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
                   hipGetErrorString(e));
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    QATTN_REQUIRE(e == hipSuccess && ev, QATTN_ERR_LAUNCH, "hipEventCreate failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_done[dev] = ev;
     g_scratch_ptr[dev] = ptr;
   }
   *out = g_scratch_ptr[dev];
+  *dev_out = dev;
   return QATTN_OK;
 }
 
@@ -1865,14 +1876,35 @@ extern "C" int qattn_fwd_ex_noalloc(qattn_seq q8, const float* q_scale, qattn_se
   QATTN_REQUIRE(need <= kScratchBytes, QATTN_ERR_WORKSPACE,
                 "qattn_fwd_ex_noalloc: %d KV splits need %zu bytes of scratch, more than its %zu-byte limit "
                 "(use qattn_fwd_ex with a workspace, or fewer splits)", ns, need, kScratchBytes);
+  if (need == 0)  // no KV split: nothing of the scratch is used
+    return qattn_fwd_ex(q8, q_scale, k8, k_scale, v, v_kind, Lpad, v_scale, o, out_dtype, B, Lq, Lk, Hq, Hkv, D,
+                        qk_mult, qk_quant_gran, causal, q_offset, kv_valid, lse, ns, nullptr, 0, stream);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
   void* ws = nullptr;
-  if (need > 0) {
-    const int e = scratch_on_current_device(&ws);
-    if (e) return e;
+  int dev = -1;
+  int e = scratch_on_current_device(&ws, &dev);
+  if (e) return e;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // Order this launch after the previous scratch user on the device.  A stream under graph capture is left
+  // to the graph's own order (waiting there on an event recorded outside the capture is not allowed):
+  // replays of a captured graph must not overlap other users of the scratch.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t he = hipStreamIsCapturing(st, &cap);
+  QATTN_REQUIRE(he == hipSuccess, QATTN_ERR_LAUNCH, "hipStreamIsCapturing failed: %s", hipGetErrorString(he));
+  const bool order = cap == hipStreamCaptureStatusNone;
+  if (order) {
+    he = hipStreamWaitEvent(st, g_scratch_done[dev], 0);
+    QATTN_REQUIRE(he == hipSuccess, QATTN_ERR_LAUNCH, "hipStreamWaitEvent failed: %s", hipGetErrorString(he));
   }
   // the same launch as qattn_fwd_ex with this split count and the device array as its workspace
-  return qattn_fwd_ex(q8, q_scale, k8, k_scale, v, v_kind, Lpad, v_scale, o, out_dtype, B, Lq, Lk, Hq, Hkv, D,
-                      qk_mult, qk_quant_gran, causal, q_offset, kv_valid, lse, ns, ws, need, stream);
+  e = qattn_fwd_ex(q8, q_scale, k8, k_scale, v, v_kind, Lpad, v_scale, o, out_dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult,
+                   qk_quant_gran, causal, q_offset, kv_valid, lse, ns, ws, need, stream);
+  if (e) return e;
+  if (order) {
+    he = hipEventRecord(g_scratch_done[dev], st);
+    QATTN_REQUIRE(he == hipSuccess, QATTN_ERR_LAUNCH, "hipEventRecord failed: %s", hipGetErrorString(he));
+  }
+  return QATTN_OK;
 }
 
 extern "C" int qattn_fwd(qattn_seq q8, const float* q_scale, qattn_seq k8, const float* k_scale, const uint8_t* v8,

@@ -19,6 +19,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from . import sageattn2 as _sa
 
 LOG2E = 1.44269504
 _LAYOUT = {0: "NHD", 1: "HND"}
@@ -38,16 +39,29 @@ def _dims(x: torch.Tensor, layout: str):
     return b, l, h, d
 
 
+def _check_input(inp):
+    if inp.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"input must be bfloat16 or float16, got {inp.dtype}")
+    if inp.dim() != 4 or inp.stride(-1) != 1:
+        raise ValueError("input must be a 4-D tensor with a contiguous last dimension")
+
+
 def _quant(inp, mean, out, scale, sm_scale, has_sm, block_size, tensor_layout):
     L = _lib.load()
     lay = _layout(tensor_layout)
+    _check_input(inp)
     b, l, h, d = _dims(inp, lay)
+    if block_size <= 0:
+        raise ValueError(f"block_size must be positive, got {block_size}")
     if scale.shape != (b, h, (l + block_size - 1) // block_size) or scale.dtype != torch.float32:
         raise ValueError("scale must be float32 [B, H, ceil(L / block_size)]")
     if out.shape != inp.shape or out.dtype != torch.int8:
         raise ValueError("output must be int8 with the input's shape")
     mc = None
     if mean is not None:
+        if mean.numel() != b * h * d or not mean.is_floating_point() or mean.device != inp.device:
+            raise ValueError(f"mean must be a floating-point [B, H, D] = {(b, h, d)} tensor (or a keepdim form) on "
+                             f"{inp.device}, got {mean.dtype} {tuple(mean.shape)} on {mean.device}")
         mc = mean.to(inp.dtype).reshape(b, h, d).contiguous()
     _lib.check(L.qattn_quant_per_block_int8(
         _lib.seq(inp, lay), _lib.dtype_code(inp.dtype), b, l, h, d, _lib.ptr(mc), _lib.seq(out, lay), _lib.ptr(scale),
@@ -84,9 +98,12 @@ def quant_per_warp_int8_cuda(input: torch.Tensor, output: torch.Tensor, scale: t
         raise ValueError("quant_per_warp_int8_cuda supports block_size 128 with warp_block_size 32")
     L = _lib.load()
     lay = _layout(tensor_layout)
+    _check_input(input)
     b, l, h, d = _dims(input, lay)
     if scale.shape != (b, h, (l + 127) // 128 * 4) or scale.dtype != torch.float32:
         raise ValueError("scale must be float32 [B, H, ceil(L / 128) * 4]")
+    if output.shape != input.shape or output.dtype != torch.int8:
+        raise ValueError("output must be int8 with the input's shape")
     empty = torch.empty((b, 0, h, d) if lay == "NHD" else (b, h, 0, d), dtype=input.dtype, device=input.device)
     empty8 = torch.empty(empty.shape, dtype=torch.int8, device=input.device)
     dummy = torch.empty(1, dtype=torch.float32, device=input.device)
@@ -108,8 +125,20 @@ def _attn(query, key, value, output, query_scale, key_scale, value_scale, value_
     else:
         v_kind = _lib.QATTN_V_BF16 if value.dtype == torch.bfloat16 else _lib.QATTN_V_FP16
     lpad = value.shape[-1]
-    if value.shape[:3] != (b, hkv, d) or lpad < (lk + 63) // 64 * 64 or not value.is_contiguous():
+    if value.dim() != 4:
         raise ValueError(f"value must be this library's V tile layout [B, Hkv, D, Lpad] = {(b, hkv, d)} + Lpad")
+    # the same checks as the module's qattn_fwd (scale shapes per granularity, V tile, output), so that no
+    # operand of another granularity or size reaches the kernel (the reference's CHECK_SHAPE / CHECK_DTYPE,
+    # sm89_qk_int8_sv_f8_accum_f32_attn_inst_buf.cu:125-129)
+    gran = {1: "per_block", 2: "per_warp", 3: "per_thread"}[qk_quant_gran]
+    if not output.is_floating_point() or output.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"output must be bfloat16 or float16, got {output.dtype}")
+    _sa._check_attn_operands(query, query_scale, key, key_scale, value, value_scale, b, lq, lk, hq, hkv, d, gran,
+                             output, output.dtype)
+    if value_mean is not None and (value_scale is None or value_mean.dtype != torch.float32 or
+                                   tuple(value_mean.shape) != (b, hkv, d) or not value_mean.is_contiguous() or
+                                   value_mean.device != query.device):
+        raise ValueError(f"value_mean must be a contiguous float32 tensor of shape {(b, hkv, d)} (FP8 V only)")
     qk_mult = 1.0 if qk_quant_gran == 1 else float(sm_scale) * LOG2E
     lse = torch.empty((b, hq, lq) if return_lse else (0,), dtype=torch.float32, device=query.device)
     ns = L.qattn_fwd_ex_num_splits(b, lq, lk, hq, v_kind, qk_quant_gran)

@@ -396,6 +396,11 @@ def sageattn_qk_int8_pv_fp8_cuda(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
 
     Extra keyword arguments beyond the reference: ``kv_valid_len`` (int or per-batch sequence: keys at
     or beyond it are masked) and ``q_offset`` (causal diagonal offset, kv > q + q_offset is masked).
+
+    ``pv_accum_dtype="fp32+fp16"`` differs from the reference in its arithmetic: the reference sums each
+    64-key tile's P.V as two k=32 MMAs rounded to fp16 before adding it to the fp32 O
+    (attn_utils.cuh:886-953); here V is quantized with the same scale_max 2.25 but P.V accumulates in fp32
+    throughout, so results agree to within that fp16 rounding, not bit for bit.
     """
     return _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv_accum_dtype, smooth_k,
                          smooth_v, return_lse, kv_valid_len, q_offset, pv="fp8")

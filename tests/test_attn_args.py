@@ -58,3 +58,51 @@ def test_qattn_fwd_rejects_mismatched_operands(bad):
         kw["out"] = torch.empty(1, 10, 4, 128, dtype=torch.bfloat16)
     with pytest.raises(ValueError):
         sa.qattn_fwd(q8, qs, k8, ks, v, vs, **kw)
+
+
+@pytest.mark.parametrize("bad", ["q_scale_gran", "k_scale_short", "v_scale_shape", "out_small", "v_mean_shape",
+                                 "out_dtype"])
+def test_ops_reject_mismatched_operands(bad):
+    """torch.ops.telefuser_amd attention ops run the same operand checks as qattn_fwd before any launch."""
+    from telefuser_amd import ops  # noqa: F401  (registers the ops)
+
+    q8, qs, k8, ks, v, vs = _ops()
+    out = torch.empty(q8.shape, dtype=torch.bfloat16)
+    gran, vm = 1, None
+    if bad == "q_scale_gran":
+        gran = 3  # per-block scales handed to a per-thread launch
+    elif bad == "k_scale_short":
+        ks = ks[..., :1].contiguous()
+    elif bad == "v_scale_shape":
+        vs = vs[:, :1].contiguous()
+    elif bad == "out_small":
+        out = torch.empty(1, 10, 4, 128, dtype=torch.bfloat16)
+    elif bad == "v_mean_shape":
+        vm = torch.zeros(1, 1, 128)
+    elif bad == "out_dtype":
+        out = torch.empty(q8.shape, dtype=torch.float32)
+    with pytest.raises(ValueError):
+        if vm is None:
+            torch.ops.telefuser_amd.qk_int8_sv_f8_accum_f32_fuse_v_scale_attn(q8, k8, v, out, qs, ks, vs, 0, 0, gran,
+                                                                             128 ** -0.5, 0)
+        else:
+            torch.ops.telefuser_amd.qk_int8_sv_f8_accum_f32_fuse_v_scale_fuse_v_mean_attn(
+                q8, k8, v, out, qs, ks, vs, vm, 0, 0, gran, 128 ** -0.5, 0)
+
+
+@pytest.mark.parametrize("bad", ["input_dtype", "mean_size", "scale_shape"])
+def test_quant_ops_reject_bad_arguments(bad):
+    from telefuser_amd import ops  # noqa: F401
+
+    x = torch.zeros(1, 200, 2, 128, dtype=torch.bfloat16)
+    out = torch.empty(x.shape, dtype=torch.int8)
+    scale = torch.empty(1, 2, 4, dtype=torch.float32)
+    mean = torch.zeros(1, 2, 128, dtype=torch.bfloat16)
+    if bad == "input_dtype":
+        x = x.float()
+    elif bad == "mean_size":
+        mean = torch.zeros(1, 3, 128, dtype=torch.bfloat16)
+    elif bad == "scale_shape":
+        scale = torch.empty(1, 2, 3, dtype=torch.float32)
+    with pytest.raises(ValueError):
+        torch.ops.telefuser_amd.quant_per_block_int8_fuse_sub_mean_cuda(x, mean, out, scale, 64, 0)

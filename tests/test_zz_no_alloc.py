@@ -22,7 +22,7 @@ def _quantized(dev, B, Lq, Lk, H, seed):
     return q8, qs, k8, ks, v8, vs
 
 
-def _call(noalloc, t, B, Lq, Lk, H, splits, kv_valid):
+def _call(noalloc, t, B, Lq, Lk, H, splits, kv_valid, stream=None):
     from telefuser_amd import _lib
 
     L = _lib.load()
@@ -35,7 +35,8 @@ def _call(noalloc, t, B, Lq, Lk, H, splits, kv_valid):
             v8.shape[-1], _lib.ptr(vs), _lib.seq(o, "NHD"), _lib.QATTN_BF16, B, Lq, Lk, H, H, 128, 1.0,
             _lib.QATTN_GRAN_BLOCK, 0, 0, _lib.ptr(kvv), _lib.ptr(lse), splits)
     if noalloc:
-        _lib.check(L.qattn_fwd_ex_noalloc(*args, _lib.stream_of(q8)))
+        st = _lib.stream_of(q8) if stream is None else stream.cuda_stream
+        _lib.check(L.qattn_fwd_ex_noalloc(*args, st))
     else:
         ns = splits if splits > 0 else L.qattn_fwd_ex_num_splits(B, Lq, Lk, H, 0, 1)
         wsb = L.qattn_fwd_workspace_size(B, Lq, H, 128, ns)
@@ -84,3 +85,30 @@ def test_noalloc_rejects_launch_beyond_scratch():
                                 0, None, None, splits, _lib.stream_of(q8))
     assert rc == 7, rc  # QATTN_ERR_WORKSPACE, before any launch
     assert "scratch" in L.qattn_last_error().decode()
+
+
+def test_noalloc_calls_on_two_streams_are_ordered():
+    """Two KV-split launches issued back to back on two streams, with no host synchronisation between them:
+    the second waits on the GPU for the first one's use of the shared scratch, so both outputs equal the
+    workspace entry's bit for bit."""
+    dev = require_gpu()
+    from telefuser_amd import _lib
+
+    L = _lib.load()
+    cases = [(1, 4680, 32760, 2, 0, None), (1, 2000, 20000, 2, 6, None)]
+    data = []
+    for i, (B, Lq, Lk, H, splits, kvv) in enumerate(cases):
+        ns = splits if splits > 0 else L.qattn_fwd_ex_num_splits(B, Lq, Lk, H, 0, 1)
+        log(f"two-stream noalloc call {i}: B={B} Lq={Lq} Lk={Lk} H={H} splits={ns}")
+        assert ns > 1
+        t = _quantized(dev, B, Lq, Lk, H, seed=400 + i)
+        data.append((t, _call(False, t, B, Lq, Lk, H, splits, kvv)))
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    outs = []
+    for (t, _), (B, Lq, Lk, H, splits, kvv), st in zip(data, cases, streams):
+        outs.append(_call(True, t, B, Lq, Lk, H, splits, kvv, stream=st))
+    torch.cuda.synchronize()
+    for i, ((_, (o0, l0)), (o1, l1)) in enumerate(zip(data, outs)):
+        assert torch.equal(o0, o1), f"stream {i}: max diff {float((o0.float() - o1.float()).abs().max())}"
+        assert torch.equal(l0, l1)
