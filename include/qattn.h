@@ -36,7 +36,7 @@ enum qattn_status {
   QATTN_ERR_SHAPE = 2,      /* inconsistent or unsupported sizes */
   QATTN_ERR_STRIDE = 3,     /* strides not representable / not 16-byte aligned rows */
   QATTN_ERR_ALIGN = 4,      /* base pointer misaligned */
-  QATTN_ERR_HEAD_DIM = 5,   /* head_dim other than 128 (callers pad 64 < D < 128 up to 128) */
+  QATTN_ERR_HEAD_DIM = 5,   /* head_dim other than 128 (or 64 where supported): callers pad the others */
   QATTN_ERR_HEAD_RATIO = 6, /* num_qo_heads % num_kv_heads != 0 */
   QATTN_ERR_WORKSPACE = 7,  /* workspace missing or too small */
   QATTN_ERR_LAUNCH = 8,     /* HIP launch error */
@@ -161,7 +161,10 @@ int qattn_per_channel_fp8_ex(qattn_seq v, int dtype, int64_t B, int64_t L, int64
  *   lse:      NULL or fp32 [B, Hq, Lq] receiving log2(sum 2^s) of the quantized logits
  *   num_splits: 0 = automatic, 1 = no KV split, n > 1 = split keys over n workgroups
  *   workspace: needed when splitting, qattn_fwd_workspace_size bytes
- * D must be 128 (callers pad head_dim < 128, as sageattn2.py:1307-1316 does).
+ * D is 128, or 64 for FP8 V (dense launches: qattn_fwd / qattn_fwd_ex / _ex2 / _noalloc with v_kind FP8).
+ * Callers pad other heads as sageattn2.py:1307-1316 does: D < 64 to 64, 64 < D < 128 to 128.  Head
+ * dimension 64 runs the ping-pong kernel (unsplit or KV-split) with half the MFMA work and bytes per key
+ * tile; the kernel queries below (qattn_fwd_ex_kernel, the split counts) describe D = 128.
  */
 size_t qattn_fwd_workspace_size(int64_t B, int64_t Lq, int64_t Hq, int64_t D, int num_splits);
 int qattn_fwd_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq);

@@ -783,16 +783,25 @@ __device__ __forceinline__ void pp_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool IS_FP16_OUT, bool KT, bool SPLIT>
+template <bool IS_FP16_OUT, bool KT, bool SPLIT, int HD>
 __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
+  // HD: head dimension, 128 or 64.  Per 64-key tile a wave runs HD / 16 Q.K^T MFMAs (two key blocks x HD / 32
+  // k-steps) and HD / 32 P.V MFMAs; K and V tiles are HD / 16 fragments of 1 KiB each.
+  static_assert(HD == 128 || HD == 64, "head_dim 128 or 64");
+  constexpr int NQF = HD / 32;  // Q fragments (k-steps of 32) = P.V output blocks of 32 dims
+  constexpr int NKF = HD / 16;  // K fragments per tile = V fragments per tile
+  constexpr int ROWB = HD;      // bytes of one int8 Q row
   constexpr int KS = ks_per_tile(KT);
   constexpr int NB = kPPNBuf;
-  __shared__ __align__(16) uint8_t lds_k[NB][kBK * kD];
-  __shared__ __align__(16) uint8_t lds_v[NB][kD * kBK];
+  // the K buffers double as the waves' Q / O stage (4 KiB per wave), so they span at least 32 KiB
+  constexpr int kKBytes = NB * kBK * HD > 8 * 4096 ? NB * kBK * HD : 8 * 4096;
+  __shared__ __align__(16) uint8_t lds_kbuf[kKBytes];
+  auto lds_k = reinterpret_cast<uint8_t (*)[kBK * HD]>(lds_kbuf);
+  __shared__ __align__(16) uint8_t lds_v[NB][HD * kBK];
   auto buf_of = [](int t) { return (int)((unsigned)t % (unsigned)NB); };
   __shared__ float lds_ks[ks_lds_floats<PV_FP8>()];
-  __shared__ __align__(16) float lds_vs[kD];
-  __shared__ __align__(16) float lds_vm[kD];
+  __shared__ __align__(16) float lds_vs[HD];
+  __shared__ __align__(16) float lds_vm[HD];
 
   const int64_t nQP = (p.nQB + 1) / 2;
   const int64_t wg_id = xcd_remap(blockIdx.x, gridDim.x);
@@ -833,26 +842,28 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   const int t_lo = SPLIT ? split * p.tiles_per_split : 0;
   const int t_end = SPLIT ? min(n_tiles, t_lo + p.tiles_per_split) : n_tiles;
 
-  // Q fragments through the wave-private LDS stage (rows row-contiguous, chunk c of row r at c ^ (r & 7))
+  // Q fragments through the wave-private LDS stage (rows row-contiguous, 16-byte chunk c of row r at
+  // c ^ (r % chunks per row))
+  constexpr int QC = ROWB / 16;  // 16-byte chunks per Q row
   uint8_t* stage = &lds_k[0][0] + w * 4096;
-  v4i qf[4];
+  v4i qf[NQF];
   {
     const int8_t* qbase = p.q8 + b * p.qsb + h * p.qsh;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int r = i * 8 + (lane >> 3), c = lane & 7;
+    for (int i = 0; i < 32 * QC / 64; i++) {
+      const int r = i * (64 / QC) + lane / QC, c = lane % QC;
       const int64_t row = wrow0 + r;
       const v4i val = row < p.Lq ? *reinterpret_cast<const v4i*>(qbase + row * p.qsl + c * 16) : v4i{0, 0, 0, 0};
-      *reinterpret_cast<v4i*>(stage + r * 128 + ((c ^ (r & 7)) << 4)) = val;
+      *reinterpret_cast<v4i*>(stage + r * ROWB + ((c ^ (r % QC)) << 4)) = val;
     }
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
 #pragma unroll
-    for (int m = 0; m < 4; m++) {
+    for (int m = 0; m < NQF; m++) {
       const int c = 2 * m + hf;
-      qf[m] = *reinterpret_cast<const v4i*>(stage + lq * 128 + ((c ^ (lq & 7)) << 4));
+      qf[m] = *reinterpret_cast<const v4i*>(stage + lq * ROWB + ((c ^ (lq % QC)) << 4));
     }
 #pragma unroll
-    for (int m = 0; m < 4; m++) asm volatile("" ::"v"(qf[m]));
+    for (int m = 0; m < NQF; m++) asm volatile("" ::"v"(qf[m]));
   }
   const int64_t qbs = min(qb, p.nQB - 1);
   const int64_t qsi = p.qgran == QATTN_GRAN_THREAD ? (qbs * 4 + wl) * 8 + (lq & 7)
@@ -867,32 +878,37 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   //   K block j (0..7): lane l gets K row (j & 1) * 32 + l % 32, bytes 16 (2 (j >> 1) + l / 32) .. + 16
   //   V block 2 dblk + h (h = 0, 1): lane l gets V^T row dblk * 32 + l % 32, bytes 16 (2 (l / 32) + h) .. + 16
   //     of the tile (the two halves of the lane's P.V A operand)
-  // LDS DMA: wave w fills block w of the K tile and block w of the V tile.
+  // LDS DMA: with HD = 128 wave w fills block w of the K tile and block w of the V tile (two DMAs per wave
+  // and tile); with HD = 64 the tiles have four blocks each, waves 0-3 fill the K blocks and waves 4-7 the
+  // V blocks (one DMA per wave and tile).
+  constexpr int kDmaPerTile = HD == 128 ? 2 : 1;
   const int8_t* kbase = p.k8 + b * p.ksb + hk * p.ksh;
-  const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.Hkv + hk) * (int64_t)kD * p.Lpad;
-  const int64_t kbytes = (p.Lk - 1) * p.ksl + kD;
-  const v4u vrsrc = make_rsrc(vbase, (uint32_t)((int64_t)kD * p.Lpad));
+  const uint8_t* vbase = static_cast<const uint8_t*>(p.v) + (b * p.Hkv + hk) * (int64_t)HD * p.Lpad;
+  const int64_t kbytes = (p.Lk - 1) * p.ksl + HD;
+  const v4u vrsrc = make_rsrc(vbase, (uint32_t)((int64_t)HD * p.Lpad));
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  const int kblk = HD == 128 ? wu : wu & 3;  // the K block and V block this wave fills
   uint32_t koff, voff;
   {
-    const int kr = (w & 1) * 32 + lq, kc = 2 * (w >> 1) + hf;
+    const int kr = (kblk & 1) * 32 + lq, kc = 2 * (kblk >> 1) + hf;
     koff = (uint32_t)(kr * p.ksl + kc * 16);
-    const int vd = (w >> 1) * 32 + lq, vc = 2 * hf + (w & 1);
+    const int vd = (kblk >> 1) * 32 + lq, vc = 2 * hf + (kblk & 1);
     voff = (uint32_t)(vd * p.Lpad + vc * 16);
   }
   const int64_t k_step = kBK * p.ksl;
-  const int wu = __builtin_amdgcn_readfirstlane(w);
-  const uint32_t lds_k0 = lds_addr(&lds_k[0][0]) + wu * 1024;
-  const uint32_t lds_v0 = lds_addr(&lds_v[0][0]) + wu * 1024;
+  const uint32_t lds_k0 = lds_addr(&lds_k[0][0]) + kblk * 1024;
+  const uint32_t lds_v0 = lds_addr(&lds_v[0][0]) + kblk * 1024;
+  const bool dma_k = HD == 128 || wu < 4, dma_v = HD == 128 || wu >= 4;
   auto dma_tile = [&](int t) {
     const int buf = buf_of(t);
     const int64_t kso = (int64_t)t * k_step;
-    lds_dma16(koff, make_rsrc(kbase + kso, (uint32_t)(kbytes - kso)), 0, lds_k0 + buf * (kBK * kD));
-    lds_dma16(voff, vrsrc, (uint32_t)t * kBK, lds_v0 + buf * (kD * kBK));
+    if (dma_k) lds_dma16(koff, make_rsrc(kbase + kso, (uint32_t)(kbytes - kso)), 0, lds_k0 + buf * (kBK * HD));
+    if (dma_v) lds_dma16(voff, vrsrc, (uint32_t)t * kBK, lds_v0 + buf * (HD * kBK));
   };
 
-  v16f o[4];
+  v16f o[NQF];
 #pragma unroll
-  for (int i = 0; i < 4; i++)
+  for (int i = 0; i < NQF; i++)
 #pragma unroll
     for (int r = 0; r < 16; r++) o[i][r] = 0.f;
   float m_run = kMInit;
@@ -906,22 +922,22 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   __syncthreads();  // Q fragments are out of the LDS stage before the DMA reuses it
   // the key scales of tiles t_lo .. t_end - 1, from lds_ks[0]
   for (int i = tid; i < (t_end - t_lo) * KS; i += kPPThreads) lds_ks[i] = ks_ptr[(int64_t)t_lo * KS + i];
-  if (tid < kD) {
-    lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * kD + tid];
-    lds_vm[tid] = p.v_mean ? p.v_mean[(b * p.Hkv + hk) * kD + tid] : 0.f;
+  if (tid < HD) {
+    lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * HD + tid];
+    lds_vm[tid] = p.v_mean ? p.v_mean[(b * p.Hkv + hk) * HD + tid] : 0.f;
   }
   for (int t = t_lo; t < min(t_end, t_lo + 2); t++) dma_tile(t);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
   v16i s[2];
-  v8i pf, vf[4];
-  v4i kf[8];
+  v8i pf, vf[NQF];
+  v4i kf[NKF];
   float cs_a, cs_b;  // logit scales of the tile in the softmax
   auto read_k = [&](int t) {
     const uint8_t* kb = &lds_k[buf_of(t)][lane * 16];
 #pragma unroll
-    for (int j = 0; j < 8; j++) kf[j] = *reinterpret_cast<const v4i*>(kb + j * 1024);
+    for (int j = 0; j < NKF; j++) kf[j] = *reinterpret_cast<const v4i*>(kb + j * 1024);
   };
   auto read_cs = [&](int t) {
     if constexpr (KT) {
@@ -934,7 +950,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   auto read_v = [&](int t) {
     const uint8_t* vb = &lds_v[buf_of(t)][lane * 16];
 #pragma unroll
-    for (int dblk = 0; dblk < 4; dblk++) {
+    for (int dblk = 0; dblk < NQF; dblk++) {
       const v4i a0 = *reinterpret_cast<const v4i*>(vb + (2 * dblk) * 1024);
       const v4i a1 = *reinterpret_cast<const v4i*>(vb + (2 * dblk + 1) * 1024);
       vf[dblk] = v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
@@ -943,13 +959,13 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   // stage M: P(t-1).V(t-1) and its row sum (operands from the previous stage V), then S^T(t) = K(t).Q^T
   auto pv = [&]() {
 #pragma unroll
-    for (int dblk = 0; dblk < 4; dblk++)
+    for (int dblk = 0; dblk < NQF; dblk++)
       o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, o[dblk], 0, 0, 0, 0, 0, 0);
     lacc = row_sum_mfma(lacc, pf);
   };
   auto qk = [&]() {
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
+    for (int j = 0; j < NKF; j++) {
       const int m = j >> 1, kb = j & 1;
       s[kb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kf[j], qf[m], m == 0 ? kbias : s[kb], 0, 0, 0);
     }
@@ -962,7 +978,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     qk();
     // the logit scales of the tile, for the softmax of the next stage
     read_cs(t);
-    if constexpr (!kFirst) {
+    if constexpr (!kFirst && HD == 128) {
       // LDS reads three ahead of the MFMA that consumes them: 3 reads, then (1 MFMA, 2 reads) x 7,
       // then the remaining MFMAs (16 fragment reads + the key-scale read; 13 MFMAs with the row sum)
       __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
@@ -1018,7 +1034,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
       const float m_new = grow ? m_tile : m_run;
       const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+      for (int i = 0; i < NQF; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[i][r] *= alpha;
       lacc[0] *= alpha;  // the row sum is read from element 0 only
@@ -1054,7 +1070,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     stage_m(t, first_t);
     __builtin_amdgcn_s_setprio(0);
     // this wave's share of tile t + 1 has landed (tile t + 2 may stay in flight)
-    if (issue) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    if (issue) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kDmaPerTile) : "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     pp_barrier();
     stage_v(t);
@@ -1068,7 +1084,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   if (t_end > t_lo) {
     read_v(t_end - 1);
 #pragma unroll
-    for (int dblk = 0; dblk < 4; dblk++)
+    for (int dblk = 0; dblk < NQF; dblk++)
       o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, o[dblk], 0, 0, 0, 0, 0, 0);
     lacc = row_sum_mfma(lacc, pf);
   }
@@ -1078,9 +1094,9 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     // the split's partial (unnormalised O, m, l) for the combine kernel, in qattn_fwd_kernel's layout
     if (qrow >= p.Lq) return;
     const int64_t row = (((int64_t)split * p.B + b) * p.Hq + h) * p.Lq + qrow;
-    float* wo = p.ws_o + row * kD;
+    float* wo = p.ws_o + row * HD;
 #pragma unroll
-    for (int dblk = 0; dblk < 4; dblk++)
+    for (int dblk = 0; dblk < NQF; dblk++)
 #pragma unroll
       for (int g = 0; g < 4; g++) {
         const int d = dblk * 32 + g * 8 + hf * 4;
@@ -1099,7 +1115,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   auto store = [&](auto mean_t) {
   constexpr bool kMean = decltype(mean_t)::value;
 #pragma unroll
-  for (int pass = 0; pass < 2; pass++) {
+  for (int pass = 0; pass < HD / 64; pass++) {
 #pragma unroll
     for (int db = 0; db < 2; db++) {
       const int dblk = pass * 2 + db;
@@ -1133,9 +1149,9 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
 }
 
-template <bool IS_FP16_OUT, bool KT, bool SPLIT>
+template <bool IS_FP16_OUT, bool KT, bool SPLIT, int HD = kD>
 __global__ __launch_bounds__(kPPThreads) void qattn_fwd_pp_kernel(AttnParams p) {
-  qattn_fwd_pp<IS_FP16_OUT, KT, SPLIT>(p);
+  qattn_fwd_pp<IS_FP16_OUT, KT, SPLIT, HD>(p);
 }
 
 // ---- resident K/V: short key ranges (at most kResMaxTiles tiles, e.g. text cross-attention) ----
@@ -1400,8 +1416,9 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
 }
 
 // Merge the KV-split partials: one wave per query row, 2 channels per lane.
-template <bool IS_FP16_OUT>
+template <bool IS_FP16_OUT, int HD = kD>
 __global__ __launch_bounds__(256) void qattn_combine_kernel(AttnParams p) {
+  constexpr int E = HD / 64;  // output elements per lane
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // over B*Hq*Lq
   const int lane = threadIdx.x & 63;
   const int64_t total = p.B * p.Hq * p.Lq;
@@ -1413,23 +1430,27 @@ __global__ __launch_bounds__(256) void qattn_combine_kernel(AttnParams p) {
   const int64_t sstride = total;
   float M = kMInit;
   for (int s = 0; s < p.nsplit; s++) M = fmaxf(M, p.ws_ml[(s * sstride + row) * 2]);
-  float L = 0.f, a0 = 0.f, a1 = 0.f;
+  float L = 0.f, a[E];
+#pragma unroll
+  for (int e = 0; e < E; e++) a[e] = 0.f;
   for (int s = 0; s < p.nsplit; s++) {
     const float ms = p.ws_ml[(s * sstride + row) * 2], ls = p.ws_ml[(s * sstride + row) * 2 + 1];
     const float f = __builtin_amdgcn_exp2f(ms - M);
     L += ls * f;
-    const float* wo = p.ws_o + (s * sstride + row) * kD + lane * 2;
-    a0 += wo[0] * f;
-    a1 += wo[1] * f;
+    const float* wo = p.ws_o + (s * sstride + row) * HD + lane * E;
+#pragma unroll
+    for (int e = 0; e < E; e++) a[e] += wo[e] * f;
   }
   const float inv = L > 0.f ? 1.0f / L : 0.f;
-  const float* vs = p.v_scale ? p.v_scale + (b * p.Hkv + hk) * kD + lane * 2 : nullptr;
-  uint16_t* orow = static_cast<uint16_t*>(p.o) + b * p.osb + qrow * p.osl + h * p.osh + lane * 2;
-  const float* vm = p.v_mean ? p.v_mean + (b * p.Hkv + hk) * kD + lane * 2 : nullptr;
-  const float r0 = vm ? epilogue_value<true>(a0, inv, vs ? vs[0] : 1.f, vm[0]) : epilogue_value<false>(a0, inv, vs ? vs[0] : 1.f, 0.f);
-  const float r1 = vm ? epilogue_value<true>(a1, inv, vs ? vs[1] : 1.f, vm[1]) : epilogue_value<false>(a1, inv, vs ? vs[1] : 1.f, 0.f);
-  orow[0] = f32_to_half<IS_FP16_OUT>(r0);
-  orow[1] = f32_to_half<IS_FP16_OUT>(r1);
+  const float* vs = p.v_scale ? p.v_scale + (b * p.Hkv + hk) * HD + lane * E : nullptr;
+  uint16_t* orow = static_cast<uint16_t*>(p.o) + b * p.osb + qrow * p.osl + h * p.osh + lane * E;
+  const float* vm = p.v_mean ? p.v_mean + (b * p.Hkv + hk) * HD + lane * E : nullptr;
+#pragma unroll
+  for (int e = 0; e < E; e++) {
+    const float r = vm ? epilogue_value<true>(a[e], inv, vs ? vs[e] : 1.f, vm[e])
+                       : epilogue_value<false>(a[e], inv, vs ? vs[e] : 1.f, 0.f);
+    orow[e] = f32_to_half<IS_FP16_OUT>(r);
+  }
   if (p.lse && lane == 0) p.lse[(b * p.Hq + h) * p.Lq + qrow] = L > 0.f ? __builtin_log2f(L) + M : -INFINITY;
 }
 
@@ -1604,11 +1625,21 @@ static int launch_fwd(AttnParams& p, int out_dtype, int ns, void* workspace, siz
                       qattn_fwd_workspace_size(p.B, p.Lq, p.Hq, D, ns));
         p.ws_o = static_cast<float*>(workspace);
         p.ws_ml = p.ws_o + (int64_t)ns * p.B * p.Hq * p.Lq * D;
-        if (out_dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT, true><<<g, kPPThreads, 0, st>>>(p);
-        else qattn_fwd_pp_kernel<true, KT, true><<<g, kPPThreads, 0, st>>>(p);
         const int64_t rows = p.B * p.Hq * p.Lq;
-        if (out_dtype == QATTN_BF16) qattn_combine_kernel<false><<<(rows + 3) / 4, 256, 0, st>>>(p);
-        else qattn_combine_kernel<true><<<(rows + 3) / 4, 256, 0, st>>>(p);
+        if (D == 64) {
+          if (out_dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT, true, 64><<<g, kPPThreads, 0, st>>>(p);
+          else qattn_fwd_pp_kernel<true, KT, true, 64><<<g, kPPThreads, 0, st>>>(p);
+          if (out_dtype == QATTN_BF16) qattn_combine_kernel<false, 64><<<(rows + 3) / 4, 256, 0, st>>>(p);
+          else qattn_combine_kernel<true, 64><<<(rows + 3) / 4, 256, 0, st>>>(p);
+        } else {
+          if (out_dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT, true><<<g, kPPThreads, 0, st>>>(p);
+          else qattn_fwd_pp_kernel<true, KT, true><<<g, kPPThreads, 0, st>>>(p);
+          if (out_dtype == QATTN_BF16) qattn_combine_kernel<false><<<(rows + 3) / 4, 256, 0, st>>>(p);
+          else qattn_combine_kernel<true><<<(rows + 3) / 4, 256, 0, st>>>(p);
+        }
+      } else if (D == 64) {
+        if (out_dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT, false, 64><<<g, kPPThreads, 0, st>>>(p);
+        else qattn_fwd_pp_kernel<true, KT, false, 64><<<g, kPPThreads, 0, st>>>(p);
       } else {
         if (out_dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT, false><<<g, kPPThreads, 0, st>>>(p);
         else qattn_fwd_pp_kernel<true, KT, false><<<g, kPPThreads, 0, st>>>(p);
@@ -1691,7 +1722,8 @@ static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale,
                      const int32_t* kv_valid, float* lse, int num_splits, int pv, int gran, int& kernel,
                      bool sparse = false) {
   QATTN_REQUIRE(out_dtype == QATTN_BF16 || out_dtype == QATTN_FP16, QATTN_ERR_DTYPE, "out dtype must be bf16 or fp16");
-  QATTN_REQUIRE(D == kD, QATTN_ERR_HEAD_DIM, "qattn_fwd needs head_dim 128 (pad smaller heads), got %lld",
+  QATTN_REQUIRE(D == kD || (D == 64 && pv == PV_FP8 && !sparse), QATTN_ERR_HEAD_DIM,
+                "qattn_fwd needs head_dim 128, or 64 with FP8 V on a dense launch (pad other heads), got %lld",
                 (long long)D);
   QATTN_REQUIRE(gran == QATTN_GRAN_BLOCK || gran == QATTN_GRAN_WARP || gran == QATTN_GRAN_THREAD, QATTN_ERR_ARG,
                 "qk_quant_gran must be 1 (per block), 2 (per warp) or 3 (per thread), got %d", gran);
@@ -1737,6 +1769,14 @@ static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale,
   p.qk_mult = qk_mult;
 
   plan_fwd(B, Lq, Lk, Hq, pv, gran, causal, sparse, num_splits, ns, p.qpw, kernel);
+  if (D == 64) {
+    // head_dim 64 runs the ping-pong kernel only (its unsplit and KV-split forms)
+    QATTN_REQUIRE(t_kernel_override == QATTN_KERNEL_AUTO || t_kernel_override == QATTN_KERNEL_PINGPONG,
+                  QATTN_ERR_HEAD_DIM, "head_dim 64 runs the ping-pong kernel only (kernel override %d)",
+                  t_kernel_override);
+    kernel = QATTN_KERNEL_PINGPONG;
+    p.qpw = 1;
+  }
   return QATTN_OK;
 }
 

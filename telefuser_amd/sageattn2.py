@@ -306,13 +306,17 @@ def qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout
     return (o, lse) if return_lse else o
 
 
-def _pad_head_dim(x: torch.Tensor) -> torch.Tensor:
+def _pad_head_dim(x: torch.Tensor, native64: bool = False) -> torch.Tensor:
+    """Zero-pad the head dimension to what the kernels take.  With ``native64`` (the FP8 P.V path, whose
+    kernel has a head_dim-64 form) heads of at most 64 are padded to 64 and larger ones to 128, as the
+    reference pads (sageattn2.py:1307-1316); otherwise every head is padded to 128."""
     d = x.size(-1)
-    if d == 128:
-        return x
     if d > 128:
         raise ValueError(f"Unsupported head_dim: {d}")
-    return torch.nn.functional.pad(x, (0, 128 - d))
+    target = 64 if native64 and d <= 64 else 128
+    if d == target:
+        return x
+    return torch.nn.functional.pad(x, (0, target - d))
 
 
 def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv_accum_dtype, smooth_k, smooth_v,
@@ -329,7 +333,8 @@ def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv
     if not (q.dtype == k.dtype == v.dtype):
         raise AssertionError("All tensors must have the same dtype.")
     head_dim_og = q.size(-1)
-    q, k, v = _pad_head_dim(q), _pad_head_dim(k), _pad_head_dim(v)
+    native64 = pv == "fp8"
+    q, k, v = _pad_head_dim(q, native64), _pad_head_dim(k, native64), _pad_head_dim(v, native64)
     if not (q.stride(-1) == 1 and k.stride(-1) == 1 and v.stride(-1) == 1):
         raise AssertionError("Last dim of qkv must be contiguous.")
     if sm_scale is None:
@@ -462,7 +467,8 @@ def sageattn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlen
     if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape:
         raise ValueError("q must be [total_q, Hq, D] and k/v [total_k, Hkv, D]")
     head_dim_og = q.size(-1)
-    q, k, v = _pad_head_dim(q), _pad_head_dim(k), _pad_head_dim(v)
+    native64 = pv == "fp8"
+    q, k, v = _pad_head_dim(q, native64), _pad_head_dim(k, native64), _pad_head_dim(v, native64)
     if not (q.stride(-1) == 1 and k.stride(-1) == 1 and v.stride(-1) == 1):
         raise AssertionError("Last dim of qkv must be contiguous.")
     if not (cu_seqlens_q.is_contiguous() and cu_seqlens_k.is_contiguous()):

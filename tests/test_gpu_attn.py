@@ -191,15 +191,51 @@ def test_sm90_entry_is_the_sm89_kernel(oracle, gran):
     assert cosine(o90.float().cpu().numpy(), truth) >= COS_E2E
 
 
-def test_head_dim_64_padded(oracle):
+@pytest.mark.parametrize("case", ["ragged", "gqa_hnd_padding", "causal_offset", "split", "per_thread",
+                                  "per_warp_fp16"])
+def test_head_dim_64_native(oracle, case):
+    """head_dim 64 on the native D = 64 form of the ping-pong kernel (half the MFMA chain, 64-row V tiles),
+    against the oracle on the same quantized operands and against float64 truth (through _run_and_check)."""
+    from telefuser_amd import _lib
+
+    kw = {}
+    if case == "ragged":
+        q, k, v = qkv(1, 1000, 777, 2, 2, D=64, seed=60, k_offset_std=0.5)
+    elif case == "gqa_hnd_padding":
+        q, k, v = qkv(2, 300, 1500, 4, 2, D=64, seed=61, k_offset_std=1.0)
+        kw = dict(layout="HND", kv_valid=[1500, 700])
+    elif case == "causal_offset":
+        q, k, v = qkv(1, 500, 900, 2, 2, D=64, seed=62)
+        kw = dict(causal=True, q_offset=400)
+    elif case == "split":
+        q, k, v = qkv(1, 520, 6000, 3, 3, D=64, seed=63, k_offset_std=0.5)
+        kw = dict(num_splits=4, kv_valid=[5000])
+    elif case == "per_thread":
+        q, k, v = qkv(1, 700, 1300, 2, 1, D=64, seed=64, k_offset_std=0.5)
+        kw = dict(gran="per_thread")
+    else:
+        q, k, v = qkv(1, 300, 400, 2, 2, D=64, seed=65, dtype=torch.float16)
+        kw = dict(gran="per_warp")
+    _run_and_check(oracle, q, k, v, **kw)
+    assert _lib.load().qattn_last_kernel() == KERNEL_PINGPONG
+
+
+@pytest.mark.parametrize("d", [48, 64, 96])
+def test_small_head_dims_through_the_drop_in(oracle, d):
+    """sageattn_qk_int8_pv_fp8_cuda pads head_dim <= 64 to 64 (native kernel form) and 64 < D < 128 to 128, as
+    sageattn2.py:1307-1316 does; the half-P.V entry pads to 128.  Output shape and accuracy against float64
+    truth."""
     dev = require_gpu()
     from telefuser_amd import sageattn2 as sa
 
-    q, k, v = qkv(1, 200, 300, 2, 2, D=64, seed=10)
-    o = sa.sageattn_qk_int8_pv_fp8_cuda(q.to(dev), k.to(dev), v.to(dev), tensor_layout="NHD")
-    assert o.shape == q.shape
-    truth = oracle.attn_fp64(bf16_bits(q), bf16_bits(k), bf16_bits(v), 64 ** -0.5)
-    assert cosine(o.float().cpu().numpy(), truth) >= COS_E2E
+    q, k, v = qkv(1, 200, 300, 2, 2, D=d, seed=10 + d)
+    truth = oracle.attn_fp64(bf16_bits(q), bf16_bits(k), bf16_bits(v), d ** -0.5)
+    for fn in (sa.sageattn_qk_int8_pv_fp8_cuda, sa.sageattn_qk_int8_pv_fp16_cuda):
+        o = fn(q.to(dev), k.to(dev), v.to(dev), tensor_layout="NHD")
+        assert o.shape == q.shape
+        c = cosine(o.float().cpu().numpy(), truth)
+        log(f"  head_dim {d} via {fn.__name__}: cos_truth={c:.6f}")
+        assert c >= COS_E2E
 
 
 def test_full_size_wan_480p_against_sdpa():
