@@ -188,16 +188,39 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p);
 }
 
-// Row sums of P on the matrix pipe (FP8 P.V): D += ONES . P^T with ONES the all-ones 32 x 64 matrix in
-// fp4 (e2m1 1.0 = 0x2 per nibble, so the A operand takes 4 VGPRs) and P^T the e4m3 B operand of the
-// P.V MFMA: every row of the 32 x 32 result is the column sum of P^T, so each lane's 16 accumulators all
-// hold the running sum l of its query column (both key halves); only element 0 is read, so an online
-// softmax rescale multiplies that one alone (the others keep accumulating, unread).  l is thus the sum of the e4m3-rounded P
-// (the reference's accumulate_d sums p before rounding; the difference is the mean FP8 rounding error of
-// P, far inside the attention tolerance), and 32 VALU adds per tile leave the softmax.
-__device__ __forceinline__ v16f row_sum_mfma(const v16f& acc, const v8i& pf) {
-  const v8i ones = {0x22222222, 0x22222222, 0x22222222, 0x22222222, 0, 0, 0, 0};
-  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(ones, pf, acc, 4, 0, 0, 0, 0, 0);
+// Row sums of P on the matrix pipe (FP8 P.V): one v_mfma_scale_f32_16x16x128_f8f6f4 per tile, D += A . B with
+// B the e4m3 P^T operand of the P.V MFMA read in the 16 x 16 x 128 layout (lane l feeds column l % 16; its 32
+// bytes are, in the 32 x 32 layout, 32 keys of query l % 32, so columns collect query c from lanes c and
+// c + 32 and query c + 16 from lanes c + 16 and c + 48) and A an fp4 (e2m1) selector.  In this layout fp4
+// nibbles 0-15 of A lane 16 a + r meet bytes 0-15 (a = 0, 1: of B lane groups 0, 2) or 16-31 (a = 2, 3) of
+// lane groups 0 / 2, and nibbles 16-31 the same bytes of lane groups 1 / 3 (measured on gfx950).  So row 0 of
+// A is 1.0 on nibbles 0-15 of lanes 0, 16, 32, 48 and row 1 on nibbles 16-31 of lanes 1, 17, 33, 49: row 0
+// of the result is the running sum l of queries 0..15, row 1 that of queries 16..31, and lane c < 16 holds
+// them in elements 0 and 1.  l is thus the sum of the e4m3-rounded P (the reference's accumulate_d sums p
+// before rounding; the difference is the mean FP8 rounding error of P, far inside the attention tolerance);
+// the row sums leave the softmax's VALU stream, and the MFMA costs half the 32 x 32 x 64 form.
+__device__ __forceinline__ v8i row_sum_selector() {
+  const int r = threadIdx.x & 15;
+  const int lo = r == 0 ? 0x22222222 : 0, hi = r == 1 ? 0x22222222 : 0;
+  return v8i{lo, lo, hi, hi, 0, 0, 0, 0};
+}
+__device__ __forceinline__ v4f row_sum_mfma(const v4f& acc, const v8i& pf, const v8i& sel) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(sel, pf, acc, 4, 0, 0, 0, 0, 0);
+}
+// online-softmax rescale of the row sums: element 0 of lane c belongs to query c (the lane's own), element 1
+// to query c + 16, whose factor lane c + 16 holds
+__device__ __forceinline__ void row_sum_rescale(v4f& acc, float alpha) {
+  const int lane = threadIdx.x & 63;
+  const float a_hi = __int_as_float(__builtin_amdgcn_ds_bpermute(((lane & 15) + 16) * 4, __float_as_int(alpha)));
+  acc[0] *= alpha;
+  acc[1] *= a_hi;
+}
+// the row sum of query lq (lanes lq and lq + 32 both get it)
+__device__ __forceinline__ float row_sum_value(const v4f& acc, int lq) {
+  const int src = (lq & 15) * 4;
+  const float v0 = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(acc[0])));
+  const float v1 = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(acc[1])));
+  return lq < 16 ? v0 : v1;
 }
 
 // P.V flavours: e4m3 P x e4m3 V (the reference's fp8 kernel, with the 8.807 offset and v_scale), or
@@ -418,9 +441,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
 #pragma unroll
     for (int r = 0; r < 16; r++) o[i][r] = 0.f;
   float m_run = kMInit, l_run = 0.f;
-  v16f lacc;  // FP8 P.V: row sums of P on the matrix pipe (row_sum_mfma); l_run for the half P.V kinds
-#pragma unroll
-  for (int r = 0; r < 16; r++) lacc[r] = 0.f;
+  v4f lacc = {0.f, 0.f, 0.f, 0.f};  // FP8 P.V: row sums of P on the matrix pipe (row_sum_mfma)
+  const v8i rs_sel = row_sum_selector();
   v16i kbias;
 #pragma unroll
   for (int r = 0; r < 16; r++) kbias[r] = kAccBiasBits;
@@ -458,7 +480,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   auto finish = [&]() {
     float l_tot;
     if constexpr (PV == PV_FP8) {
-      l_tot = lacc[0];
+      l_tot = row_sum_value(lacc, lq);
     } else {
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l_run), __float_as_uint(l_run), false, false);
       l_tot = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
@@ -534,8 +556,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
       for (int r = 0; r < 16; r++) o[i][r] = 0.f;
     m_run = kMInit;
     l_run = 0.f;
-#pragma unroll
-    for (int r = 0; r < 16; r++) lacc[r] = 0.f;
+    lacc = v4f{0.f, 0.f, 0.f, 0.f};
   };
 
   int buf = 0;
@@ -638,8 +659,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[i][r] *= alpha;
-      if constexpr (PV == PV_FP8)
-        lacc[0] *= alpha;  // the row sum is read from element 0 only
+      if constexpr (PV == PV_FP8) row_sum_rescale(lacc, alpha);
       m_run = m_new;
     }
     const float nc_a = -fmaf(kAccBias, cs_a, m_run), nc_b = -fmaf(kAccBias, cs_b, m_run);
@@ -680,7 +700,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
 #pragma unroll
       for (int dblk = 0; dblk < 4; dblk++)
         o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, o[dblk], 0, 0, 0, 0, 0, 0);
-      lacc = row_sum_mfma(lacc, pf);
+      lacc = row_sum_mfma(lacc, pf, rs_sel);
     } else {
       // P^T in the half dtype: chunk c (16 keys of the MFMA's K dimension) = slots 8c .. 8c+7
       typedef __attribute__((ext_vector_type(8))) __bf16 v8bf;
@@ -912,9 +932,8 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
 #pragma unroll
     for (int r = 0; r < 16; r++) o[i][r] = 0.f;
   float m_run = kMInit;
-  v16f lacc;
-#pragma unroll
-  for (int r = 0; r < 16; r++) lacc[r] = 0.f;
+  v4f lacc = {0.f, 0.f, 0.f, 0.f};
+  const v8i rs_sel = row_sum_selector();
   v16i kbias;
 #pragma unroll
   for (int r = 0; r < 16; r++) kbias[r] = kAccBiasBits;
@@ -961,7 +980,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
 #pragma unroll
     for (int dblk = 0; dblk < NQF; dblk++)
       o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, o[dblk], 0, 0, 0, 0, 0, 0);
-    lacc = row_sum_mfma(lacc, pf);
+    lacc = row_sum_mfma(lacc, pf, rs_sel);
   };
   auto qk = [&]() {
 #pragma unroll
@@ -1037,7 +1056,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
       for (int i = 0; i < NQF; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[i][r] *= alpha;
-      lacc[0] *= alpha;  // the row sum is read from element 0 only
+      row_sum_rescale(lacc, alpha);
       m_run = m_new;
     }
     const float nc_a = -fmaf(kAccBias, cs_a, m_run), nc_b = -fmaf(kAccBias, cs_b, m_run);
@@ -1086,10 +1105,10 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
 #pragma unroll
     for (int dblk = 0; dblk < NQF; dblk++)
       o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf[dblk], pf, o[dblk], 0, 0, 0, 0, 0, 0);
-    lacc = row_sum_mfma(lacc, pf);
+    lacc = row_sum_mfma(lacc, pf, rs_sel);
   }
 
-  const float l_tot = lacc[0];
+  const float l_tot = row_sum_value(lacc, lq);
   if constexpr (SPLIT) {
     // the split's partial (unnormalised O, m, l) for the combine kernel, in qattn_fwd_kernel's layout
     if (qrow >= p.Lq) return;
@@ -1188,6 +1207,7 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
   const int64_t hk = h / p.group;
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, lq = lane & 31, hf = lane >> 5;
+  const v8i rs_sel = row_sum_selector();
 
   // key range (wave-uniform, in scalar registers: kv_valid comes through a vector load)
   int64_t kv_lim = p.Lk;
@@ -1253,7 +1273,8 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
     const int64_t qsi = p.qgran == QATTN_GRAN_THREAD ? wb * 8 + (lq & 7) : p.qgran == QATTN_GRAN_WARP ? wb : wb / 4;
     const float qs = qs_tab[qsi] * p.qk_mult;
 
-    v16f o[4], lacc;
+    v16f o[4];
+    v4f lacc;
     float m_run = kMInit;
     // One key tile.  The first tile of a block is peeled: its running max is the tile max and its P.V
     // starts from zero accumulators, which is what the general step computes there (the rescale factor
@@ -1333,7 +1354,7 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
           for (int i = 0; i < 4; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) o[i][r] *= alpha;
-          lacc[0] *= alpha;  // the row sum is read from element 0 only
+          row_sum_rescale(lacc, alpha);
           m_run = m_new;
         }
       }
@@ -1364,7 +1385,7 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
         const v8i vf = v8i{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
         o[dblk] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(vf, pf, kFirst ? zero : o[dblk], 0, 0, 0, 0, 0, 0);
       }
-      lacc = row_sum_mfma(kFirst ? zero : lacc, pf);
+      lacc = row_sum_mfma(kFirst ? v4f{0.f, 0.f, 0.f, 0.f} : lacc, pf, rs_sel);
     };
     if (n_tiles > 0) {
       tile(0, std::true_type{});
@@ -1374,12 +1395,11 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
       for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int r = 0; r < 16; r++) o[i][r] = 0.f;
-#pragma unroll
-      for (int r = 0; r < 16; r++) lacc[r] = 0.f;
+      lacc = v4f{0.f, 0.f, 0.f, 0.f};
     }
 
     // ---- epilogue: O / l * v_scale (+ v_mean), 32 channels per pass through the 2 KiB stage ----
-    const float l_tot = lacc[0];
+    const float l_tot = row_sum_value(lacc, lq);
     const float inv_l = l_tot > 0.f ? 1.0f / l_tot : 0.f;
     auto store = [&](auto mean_t) {
     constexpr bool kMean = decltype(mean_t)::value;

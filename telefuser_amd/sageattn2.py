@@ -467,8 +467,7 @@ def sageattn_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlen
     if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape:
         raise ValueError("q must be [total_q, Hq, D] and k/v [total_k, Hkv, D]")
     head_dim_og = q.size(-1)
-    native64 = pv == "fp8"
-    q, k, v = _pad_head_dim(q, native64), _pad_head_dim(k, native64), _pad_head_dim(v, native64)
+    q, k, v = _pad_head_dim(q), _pad_head_dim(k), _pad_head_dim(v)
     if not (q.stride(-1) == 1 and k.stride(-1) == 1 and v.stride(-1) == 1):
         raise AssertionError("Last dim of qkv must be contiguous.")
     if not (cu_seqlens_q.is_contiguous() and cu_seqlens_k.is_contiguous()):
