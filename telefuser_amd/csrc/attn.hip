@@ -60,7 +60,11 @@ constexpr int kBK = 64;
 constexpr int kThreads = 256;
 constexpr float kFp8Offset = 8.807f;  // attn_utils.cuh:35 S_FP8_OFFSET
 constexpr float kMInit = -3.0e38f;
-constexpr float kLazyTau = 1.0f;  // lazy-rescale threshold (log2 units), see the softmax below
+// Lazy-rescale threshold (log2 units), see the softmax below.  After a move of the running max the largest p of
+// the row is 448 / 2^kLazyTau.  Measured against 1 (C4, text cross attention over 512 keys: a few tiles per
+// row, so the max moves on most of them at 1): 8 % faster at 3, RMS error against float64 truth 3.84 % ->
+// 3.90 % (cosine 0.99926 -> 0.99924); C2 / C5 within 1 %, error unchanged.
+constexpr float kLazyTau = 3.0f;
 // The QK accumulators start at kAccBiasBits instead of 0: the int32 result bias + s, read as fp32,
 // is exactly kAccBias + s for |s| < 2^22 (here |s| <= 2^21), so the logits reach the softmax as floats
 // without an int -> float conversion per element; the bias is folded into the exp2 offset.

@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 COS_KERNEL = 0.99995  # same quantized operands and schedule: only exp2 ulps / fp32 sums differ
 COS_E2E = 0.999
 LOG2E = 1.44269504
-KERNEL_LAZY_TAU = 1.0  # lazy running-max threshold of qattn_fwd_kernel (kLazyTau in attn.hip)
+KERNEL_LAZY_TAU = 3.0  # lazy running-max threshold of the FP8 / half attention kernels (kLazyTau in attn.hip)
 # FP8 P.V kernels sum the e4m3-rounded P on the matrix pipe (row_sum_mfma in attn.hip); the oracle restates it
 KERNEL_LSUM_ROUNDED = True
 LSE_ROUNDED_SUM_BOUND = 0.0931  # log2(16/15): bound of the rounded-vs-unrounded row-sum LSE difference

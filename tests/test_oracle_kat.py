@@ -439,10 +439,11 @@ def test_lazy_running_max_schedule(oracle):
     v8, vs = oracle.per_channel_fp8(vb)
     ref = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs)
     assert np.array_equal(ref, oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, lazy_tau=0.0))
-    lazy = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, lazy_tau=1.0)
-    assert 0.9995 < cosine(lazy, ref) < 1.0
     truth = oracle.attn_fp64(qb, kb, vb, 128 ** -0.5)
-    assert cosine(lazy, truth) >= 0.999
+    for tau in (1.0, 3.0):  # 3 is the device kernels' threshold
+        lazy = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, lazy_tau=tau)
+        assert 0.999 < cosine(lazy, ref) < 1.0  # a different P rounding, not a different result
+        assert cosine(lazy, truth) >= 0.999
 
 
 def test_rounded_row_sum_mode(oracle):
