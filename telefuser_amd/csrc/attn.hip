@@ -4,7 +4,7 @@
 // attn_utils.cuh:362-452 update_mdo, :469-481 RS_32_to_8, :711-756 normalize_d):
 //   s    = int32(Q8 . K8^T) * (q_scale * k_scale * qk_mult)          (log2 domain)
 //   m'   = max(m, rowmax(s) - 8.807);   p = exp2(s - m')  in (0, 448]
-//          (here with a lazy update rule: m' = rowmax(s) - 7.807 only if that exceeds m by > 1, which
+//          (here with a lazy update rule: m' = rowmax(s) - 5.807 only if that exceeds m by > 3, which
 //          keeps p <= 448 and skips the O rescale on almost every tile; oracle/ restates the rule)
 //   l    = l * exp2(m - m') + sum(p)
 //   O    = O * exp2(m - m') + e4m3(p) . e4m3(V)                        (fp32 accumulation)

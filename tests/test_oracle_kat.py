@@ -431,7 +431,7 @@ def test_split_schedule_restatement(oracle):
 
 def test_lazy_running_max_schedule(oracle):
     """The lazy running-max rule (device kernel schedule) only changes which fp8 rounding P gets:
-    tau = 0 with the offset unchanged is the reference rule exactly; tau = 1 stays within the gate."""
+    tau = 0 with the offset unchanged is the reference rule exactly; tau = 1 and tau = 3 (the device kernels' threshold) stay within the gate."""
     q, k, v = qkv(1, 256, 2048, 2, 2, seed=37, k_offset_std=0.5)
     qb, kb, vb = bf16_bits(q), bf16_bits(k), bf16_bits(v)
     q8, qs = oracle.quant_per_block_int8(qb, sm_scale=128 ** -0.5 * LOG2E, blk=128)
