@@ -46,7 +46,21 @@ enum qattn_status {
 enum qattn_dtype { QATTN_BF16 = 0, QATTN_FP16 = 1 };
 
 /* Q/K scale granularity: the reference's QuantGranularity codes (attn_utils.cuh:41-64) */
-enum qattn_gran { QATTN_GRAN_BLOCK = 1, QATTN_GRAN_WARP = 2, QATTN_GRAN_THREAD = 3 };
+enum qattn_gran {
+  QATTN_GRAN_BLOCK = 1,
+  QATTN_GRAN_WARP = 2,
+  QATTN_GRAN_THREAD = 3,
+  /* the same granularities with the scale tables of the reference's sm90 entry (sageattn2.py:1608-1624):
+   * 64-row Q blocks of four 16-row warps, 128-row K blocks (shapes at qattn_quant_qk_per_warp_int8_ex) */
+  QATTN_GRAN_WARP_SM90 = 4,
+  QATTN_GRAN_THREAD_SM90 = 5
+};
+
+/* scale-table layout of the per-warp / per-thread quantizers (the *_ex entries) */
+enum qattn_scale_layout {
+  QATTN_SCALES_SM89 = 0, /* BLKQ 128, WARPQ 32, BLKK 64: the sm80/sm89 kernels' tables */
+  QATTN_SCALES_SM90 = 1  /* BLKQ 64, WARPQ 16, BLKK 128 (WARPK 128): the sm90 kernel's tables */
+};
 
 /* V operand of qattn_fwd_ex */
 enum qattn_v_kind { QATTN_V_FP8 = 0, QATTN_V_BF16 = 1, QATTN_V_FP16 = 2 };
@@ -112,6 +126,27 @@ int qattn_quant_qk_per_warp_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B,
 int qattn_quant_qk_per_thread_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq, int64_t Lk,
                                    int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean, qattn_seq q_out,
                                    qattn_seq k_out, float* q_scale, float* k_scale, qattn_stream_t stream);
+
+/*
+ * The two quantizers above with a choice of scale layout.  QATTN_SCALES_SM89 is what the plain entries
+ * do.  QATTN_SCALES_SM90 gives the tables of the reference's sm90 entry, which calls
+ * per_warp_int8(BLKQ=64, WARPQ=16, BLKK=128) and per_thread_int8(BLKQ=64, WARPQ=16, BLKK=128, WARPK=128)
+ * (tf-kernel/tf_kernel/sageattn2.py:1608-1624, quant_per_thread.py:267-369):
+ *   per-warp:   q_scale [B, Hq, ceil(Lq/64)*4]  (index row / 16),
+ *               k_scale [B, Hkv, ceil(Lk/128)]   (index row / 128);
+ *   per-thread: q_scale [B, Hq, ceil(Lq/64)*32] (index (row / 16) * 8 + row % 8),
+ *               k_scale [B, Hkv, ceil(Lk/128)*4] (index (row / 128) * 4 + (row % 8) / 2).
+ * Rounding and smoothing are those of the plain entry.  qattn_fwd_ex reads these tables with
+ * qk_quant_gran QATTN_GRAN_WARP_SM90 / QATTN_GRAN_THREAD_SM90.
+ */
+int qattn_quant_qk_per_warp_int8_ex(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq, int64_t Lk,
+                                    int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean, qattn_seq q_out,
+                                    qattn_seq k_out, float* q_scale, float* k_scale, int scale_layout,
+                                    qattn_stream_t stream);
+int qattn_quant_qk_per_thread_int8_ex(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq, int64_t Lk,
+                                      int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean, qattn_seq q_out,
+                                      qattn_seq k_out, float* q_scale, float* k_scale, int scale_layout,
+                                      qattn_stream_t stream);
 
 /*
  * Mean over the sequence, rounded to the input dtype: mean[b, h, d] (contiguous [B, H, D]).
@@ -280,7 +315,12 @@ int qattn_v_fp8_cache_update(qattn_seq v, int dtype, int64_t B, int64_t fill, in
  *   QATTN_GRAN_BLOCK:  q_scale [B, Hq, ceil(Lq/128)],     k_scale [B, Hkv, ceil(Lk/64)]
  *   QATTN_GRAN_WARP:   q_scale [B, Hq, ceil(Lq/128)*4],   k_scale [B, Hkv, ceil(Lk/64)]
  *   QATTN_GRAN_THREAD: q_scale [B, Hq, ceil(Lq/128)*32],  k_scale [B, Hkv, ceil(Lk/64)*4]
- * (layouts of qattn_quant_qk_per_warp_int8 / qattn_quant_qk_per_thread_int8).  For per-warp and
+ * (layouts of qattn_quant_qk_per_warp_int8 / qattn_quant_qk_per_thread_int8), and the sm90 tables of
+ * qk_int8_sv_f8_accum_f32_fuse_v_scale_attn_inst_buf (sageattn2.py:1608-1624,1676-1689):
+ *   QATTN_GRAN_WARP_SM90:   q_scale [B, Hq, ceil(Lq/64)*4],   k_scale [B, Hkv, ceil(Lk/128)]
+ *   QATTN_GRAN_THREAD_SM90: q_scale [B, Hq, ceil(Lq/64)*32],  k_scale [B, Hkv, ceil(Lk/128)*4]
+ * (qattn_quant_qk_per_warp_int8_ex / _per_thread_int8_ex with QATTN_SCALES_SM90; FP8 or half V, dense
+ * sequences only).  For per-warp and
  * per-thread scales sm_scale is not in Q: pass qk_mult = sm_scale * 1.44269504.
  *   v_kind QATTN_V_FP8: v = e4m3 tile layout + v_scale;  QATTN_V_BF16 / _FP16: v from qattn_v_tile_half.
  * The number of KV splits depends on v_kind and the granularity: size the workspace with

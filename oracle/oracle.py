@@ -48,6 +48,8 @@ def lib():
         L.oq_norm_rope.argtypes = [vp, i32, i64, i64, i64, i64, vp, vp, vp, f32, vp]
         L.oq_quant_per_thread_int8.argtypes = [vp, i32, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, i32, vp,
                                                i64, i64, i64, vp]
+        L.oq_quant_per_thread_int8_ex.argtypes = [vp, i32, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, i32,
+                                                  i64, i64, vp, i64, i64, i64, vp]
         L.oq_attn_fp64.argtypes = [vp, vp, vp, i32, i64, i64, i64, i64, i64, i64, f64, i32, i64, vp, vp]
         L.oq_f32_to_e4m3.argtypes = [f32]
         L.oq_f32_to_e4m3.restype = ctypes.c_uint8
@@ -127,17 +129,25 @@ def norm_rope(x_bits, w_bits, cos, sin, head_dim, eps=1e-6, is_fp16=False):
     return out
 
 
-def quant_per_thread_int8(x_bits, km_bits=None, is_key=False, layout="NHD", is_fp16=False):
+def quant_per_thread_int8(x_bits, km_bits=None, is_key=False, layout="NHD", is_fp16=False, sm90=False):
     """Triton per-thread quantizer (triton/quant_per_thread.py:22-158,267-369).  Returns (int8 tensor same
-    layout, fp32 scale [B, H, n]) with n = ceil(L/128)*32 for queries, ceil(L/64)*4 for keys."""
+    layout, fp32 scale [B, H, n]) with n = ceil(L/128)*32 for queries, ceil(L/64)*4 for keys; with
+    ``sm90`` the sm90 entry's blocks (BLKQ 64, WARPQ 16, BLKK = WARPK 128; sageattn2.py:1614-1624):
+    n = ceil(L/64)*32 for queries, ceil(L/128)*4 for keys."""
     x_bits = _bits(x_bits)
     B, L, H, D, sb, sl, sh = _dims_nhd(x_bits, layout)
     out = np.zeros(x_bits.shape, np.int8)
-    n = (L + 63) // 64 * 4 if is_key else (L + 127) // 128 * 32
+    if is_key:
+        blk = 128 if sm90 else 64
+        nblk = (L + blk - 1) // blk
+    else:
+        blkq, blk = (64, 16) if sm90 else (128, 32)
+        nblk = (L + blkq - 1) // blkq * (blkq // blk)
+    n = nblk * (4 if is_key else 8)
     scale = np.zeros((B, H, n), np.float32)
     km_arr = None if km_bits is None else np.ascontiguousarray(km_bits.reshape(B, H, D))
-    lib().oq_quant_per_thread_int8(_p(x_bits), int(is_fp16), B, L, H, D, sb, sl, sh, _p(km_arr), H * D, D,
-                                   int(bool(is_key)), _p(out), sb, sl, sh, _p(scale))
+    lib().oq_quant_per_thread_int8_ex(_p(x_bits), int(is_fp16), B, L, H, D, sb, sl, sh, _p(km_arr), H * D, D,
+                                      int(bool(is_key)), blk, nblk, _p(out), sb, sl, sh, _p(scale))
     return out, scale
 
 

@@ -247,11 +247,17 @@ void oq_quant_per_block_int8_triton(const uint16_t* in, int is_fp16, int64_t B, 
  *   scale = max|x| / 127 + 1e-7; q = trunc(x / scale + 0.5 * sign)  (:63-70, :145-158)
  * Masked tail rows load as 0 and do not change the max.
  */
-void oq_quant_per_thread_int8(const uint16_t* in, int is_fp16, int64_t B, int64_t L, int64_t H, int64_t D,
-                              int64_t sb, int64_t sl, int64_t sh, const uint16_t* km, int64_t kmb, int64_t kmh,
-                              int is_key, int8_t* out, int64_t ob, int64_t ol, int64_t oh, float* scale) {
-  const int64_t blk = is_key ? 64 : 32, ncls = is_key ? 4 : 8;
-  const int64_t nblk = is_key ? (L + 63) / 64 : (L + 127) / 128 * 4;
+/*
+ * General form: scale blocks of blk rows (WARPQ for queries; WARPK = BLKK for keys), nblk of them per
+ * (b, h) (ceil(L / BLKQ) * (BLKQ / WARPQ) for queries, ceil(L / BLKK) for keys: the grid of
+ * quant_per_thread.py:317-350).  The sm90 entry calls it with BLKQ 64, WARPQ 16, BLKK = WARPK = 128
+ * (sageattn2.py:1614-1624).
+ */
+void oq_quant_per_thread_int8_ex(const uint16_t* in, int is_fp16, int64_t B, int64_t L, int64_t H, int64_t D,
+                                 int64_t sb, int64_t sl, int64_t sh, const uint16_t* km, int64_t kmb, int64_t kmh,
+                                 int is_key, int64_t blk, int64_t nblk, int8_t* out, int64_t ob, int64_t ol,
+                                 int64_t oh, float* scale) {
+  const int64_t ncls = is_key ? 4 : 8;
 #pragma omp parallel for collapse(3) schedule(static)
   for (int64_t b = 0; b < B; b++)
     for (int64_t h = 0; h < H; h++)
@@ -289,6 +295,13 @@ void oq_quant_per_thread_int8(const uint16_t* in, int is_fp16, int64_t B, int64_
             }
           }
         }
+}
+
+void oq_quant_per_thread_int8(const uint16_t* in, int is_fp16, int64_t B, int64_t L, int64_t H, int64_t D,
+                              int64_t sb, int64_t sl, int64_t sh, const uint16_t* km, int64_t kmb, int64_t kmh,
+                              int is_key, int8_t* out, int64_t ob, int64_t ol, int64_t oh, float* scale) {
+  oq_quant_per_thread_int8_ex(in, is_fp16, B, L, H, D, sb, sl, sh, km, kmb, kmh, is_key, is_key ? 64 : 32,
+                              is_key ? (L + 63) / 64 : (L + 127) / 128 * 4, out, ob, ol, oh, scale);
 }
 
 /*
@@ -427,6 +440,10 @@ void oq_per_channel_fp8(const uint16_t* in, int is_fp16, int64_t B, int64_t L, i
  *   entries;  3 (per thread): (row / 32) * 8 + row % 8, ceil(Lq/128)*32 entries.
  *   k_gran 1 / 2: k_scale [B,Hkv,nKB] one per key tile (blkk);  3: tile * 4 + (key % 8) / 2, nKB*4 entries.
  *   (per-warp K is per-block K; quant_per_thread.py:267-369, fused.cu:698-780.)
+ *   The sm90 entry's tables (BLKQ 64, WARPQ 16, BLKK = WARPK 128; sageattn2.py:1608-1624):
+ *   q_gran 4 (per warp): row / 16, ceil(Lq/64)*4 entries;  5 (per thread): (row / 16) * 8 + row % 8,
+ *   ceil(Lq/64)*32 entries;  k_gran 4: key / 128, ceil(Lk/128) entries;  5: (key / 128) * 4 + (key % 8) / 2,
+ *   ceil(Lk/128)*4 entries.
  * pv_mode 0: v8 is the plain transposed [B,Hkv,D,Lpad] e4m3 tensor, v_scale [B,Hkv,D].
  * pv_mode 1: vh is (b,l,h,d) at vh[b*vsb + l*vsl + h*vsh + d] (bf16 or fp16 bits).
  * kv_valid: per-batch number of valid keys (NULL = Lk); causal: top-left aligned kv > q + q_offset masked.
@@ -456,8 +473,12 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
   int64_t nQB = (Lq + blkq - 1) / blkq;
   int64_t nKB = (Lk + blkk - 1) / blkk;
   /* scale entries per (b, h): per-block / per-warp (32 rows) / per-thread (32-row block x 8 classes) */
-  const int64_t nQS = q_gran == 3 ? (Lq + 127) / 128 * 32 : q_gran == 2 ? (Lq + 127) / 128 * 4 : nQB;
-  const int64_t nKS = k_gran == 3 ? nKB * 4 : nKB;
+  const int64_t nQS = q_gran == 5   ? (Lq + 63) / 64 * 32
+                      : q_gran == 4 ? (Lq + 63) / 64 * 4
+                      : q_gran == 3 ? (Lq + 127) / 128 * 32
+                      : q_gran == 2 ? (Lq + 127) / 128 * 4
+                                    : nQB;
+  const int64_t nKS = k_gran == 5 ? (Lk + 127) / 128 * 4 : k_gran == 4 ? (Lk + 127) / 128 : k_gran == 3 ? nKB * 4 : nKB;
   int64_t group = Hq / Hkv;
   int64_t rows = qrows_limit > 0 && qrows_limit < Lq ? qrows_limit : Lq;
   int64_t nRB = (rows + RB - 1) / RB;
@@ -511,14 +532,21 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
               if (causal && i + q_offset + 1 < k1) k1 = i + q_offset + 1;
               if (k1 <= k0) continue;
               const int8_t* qrow = q8 + b * qsb + i * qsl + h * qsh;
-              const int64_t qi = q_gran == 3 ? (i / 32) * 8 + i % 8 : q_gran == 2 ? i / 32 : i / blkq;
+              const int64_t qi = q_gran == 5   ? (i / 16) * 8 + i % 8
+                                 : q_gran == 4 ? i / 16
+                                 : q_gran == 3 ? (i / 32) * 8 + i % 8
+                                 : q_gran == 2 ? i / 32
+                                               : i / blkq;
               const double qsv = (double)q_scale[(b * Hq + h) * nQS + qi];
               double mx = -1e300;
               for (int64_t j = k0; j < k1; j++) {
                 const int8_t* krow = k8 + b * ksb + j * ksl + hk * ksh;
                 int32_t acc = 0;
                 for (int64_t d = 0; d < D; d++) acc += (int32_t)qrow[d] * (int32_t)krow[d];
-                const double ks = ksrow[k_gran == 3 ? t * 4 + (j % 8) / 2 : t];
+                const double ks = ksrow[k_gran == 5   ? (j / 128) * 4 + (j % 8) / 2
+                                        : k_gran == 4 ? j / 128
+                                        : k_gran == 3 ? t * 4 + (j % 8) / 2
+                                                      : t];
                 s[j - k0] = (double)acc * (qsv * ks * qk_mult);
                 if (s[j - k0] > mx) mx = s[j - k0];
               }

@@ -20,6 +20,8 @@ QATTN_FP16 = 1
 QATTN_QUANT_CUDA = 0
 QATTN_QUANT_TRITON = 1
 QATTN_GRAN_BLOCK, QATTN_GRAN_WARP, QATTN_GRAN_THREAD = 1, 2, 3
+QATTN_GRAN_WARP_SM90, QATTN_GRAN_THREAD_SM90 = 4, 5
+QATTN_SCALES_SM89, QATTN_SCALES_SM90 = 0, 1
 QATTN_V_FP8, QATTN_V_BF16, QATTN_V_FP16 = 0, 1, 2
 QATTN_KERNEL_AUTO, QATTN_KERNEL_ONE_BLOCK, QATTN_KERNEL_MULTI_BLOCK, QATTN_KERNEL_PINGPONG = 0, 1, 2, 3
 QATTN_KERNEL_RESIDENT = 4
@@ -105,6 +107,9 @@ def load() -> ctypes.CDLL:
                                            sz, vp]
     L.qattn_quant_qk_per_warp_int8.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, vp]
     L.qattn_quant_qk_per_thread_int8.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, vp]
+    L.qattn_quant_qk_per_warp_int8_ex.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, i32, vp]
+    L.qattn_quant_qk_per_thread_int8_ex.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, i32,
+                                                    vp]
     L.qattn_fwd_ex_num_splits.argtypes = [i64, i64, i64, i64, i32, i32]
     L.qattn_fwd_ex_num_splits.restype = i32
     L.qattn_fwd_ex_blocks_per_workgroup.argtypes = [i64, i64, i64, i64, i32, i32, i32]
@@ -150,6 +155,7 @@ def load() -> ctypes.CDLL:
                  "qattn_fwd_varlen"):
         getattr(L, name).restype = i32
     for name in ("qattn_row_rstd", "qattn_norm_rope_seq_mean", "qattn_norm_rope_quant_qk", "qattn_fwd_block_sparse", "qattn_quant_qk_per_warp_int8", "qattn_quant_qk_per_thread_int8", "qattn_fwd_ex",
+                 "qattn_quant_qk_per_warp_int8_ex", "qattn_quant_qk_per_thread_int8_ex",
                  "qattn_v_fp8_cache_update", "qattn_quant_per_block_int8", "qattn_quant_qk_per_block_int8", "qattn_seq_mean",
                  "qattn_per_channel_fp8", "qattn_fwd", "qattn_v_tile_half", "qattn_fwd_pv16"):
         getattr(L, name).restype = i32

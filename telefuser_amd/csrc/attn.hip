@@ -95,6 +95,8 @@ struct AttnParams {
   int64_t B, Lq, Lk, Hq, Hkv, nQB, nKB;
   int64_t nQS, nKS;  // scale entries per (b, h)
   int qgran;         // QATTN_GRAN_BLOCK / _WARP / _THREAD (q_scale indexing)
+  int qrs;           // log2 of the rows of a warp cell of q_scale: 5 (sm89 tables) or 4 (sm90 tables)
+  int kts;           // key tiles (64 keys) per k_scale block, as a shift: 0 (64-key blocks) or 1 (128)
   int64_t q_offset;
   int group;
   int nsplit;
@@ -126,6 +128,21 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t bid, int64_t n) {
 
 // Buffer resource (V#) for raw, unswizzled byte addressing of [base, base + bytes): loads whose offset
 // is at or past `bytes` return zeros instead of touching memory.
+// q_scale entry of query row `row` (< nQB * 128): one per 128-row block, per warp cell of 2^qrs rows, or
+// per row class (rows of a warp cell with equal row % 8: the reference's per-thread grouping).  Clamped
+// to the table: the sm90 tables cover ceil(Lq / 64) * 64 rows, and the rows past that are masked.
+__device__ __forceinline__ int64_t q_scale_index(const AttnParams& p, int64_t row) {
+  const int64_t i = p.qgran == QATTN_GRAN_THREAD ? ((row >> p.qrs) << 3) + (row & 7)
+                    : p.qgran == QATTN_GRAN_WARP ? row >> p.qrs
+                                                 : row >> 7;
+  return i < p.nQS ? i : p.nQS - 1;
+}
+
+// k_scale entry c (< ks) of key tile t in a table of ks entries per k_scale block
+__device__ __forceinline__ int64_t k_scale_index(const AttnParams& p, int64_t t, int c, int ks) {
+  return (t >> p.kts) * ks + c;
+}
+
 __device__ __forceinline__ v4u make_rsrc(const void* base, uint32_t bytes) {
   const uint64_t a = reinterpret_cast<uint64_t>(base);
   v4u r;
@@ -365,15 +382,11 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
 #pragma unroll
     for (int m = 0; m < 4; m++) asm volatile("" ::"v"(qf[m]));
   }
-  // q_scale of this lane's query row: one per 128-row block, per wave (32 rows), or per row class
-  // (rows with equal row % 8 inside the wave's 32 rows: the reference's per-thread grouping)
-  const int64_t qsi = p.qgran == QATTN_GRAN_THREAD ? (qb * 4 + w) * 8 + (lq & 7)
-                      : p.qgran == QATTN_GRAN_WARP ? qb * 4 + w
-                                                   : qb;
-  float qs = qs_tab[qsi * qs_stride] * p.qk_mult;
+  // q_scale of this lane's query row
+  float qs = qs_tab[q_scale_index(p, qb * kBQ + w * 32 + lq) * qs_stride] * p.qk_mult;
   // q_scale entries per query block, and this lane's entry within its block
-  const int qs_per = p.qgran == QATTN_GRAN_THREAD ? 32 : p.qgran == QATTN_GRAN_WARP ? 4 : 1;
-  const int qs_sub = p.qgran == QATTN_GRAN_THREAD ? w * 8 + (lq & 7) : p.qgran == QATTN_GRAN_WARP ? w : 0;
+  const int qs_per = p.qgran == QATTN_GRAN_THREAD ? (kBQ >> p.qrs) * 8 : p.qgran == QATTN_GRAN_WARP ? kBQ >> p.qrs : 1;
+  const int qs_sub = p.qgran == QATTN_GRAN_BLOCK ? 0 : (int)q_scale_index(p, w * 32 + lq);
   const float* ks_ptr = ks_tab;
 
   // global -> LDS copies go through the LDS-DMA path (buffer_load_dwordx4 ... lds): lane j of a wave
@@ -459,7 +472,7 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
   if constexpr (SP) {
     for (int64_t i = tid; i < t_end - t_begin; i += kThreads) lds_ks[i] = ks_ptr[lds_tid[i] * ks_stride];
   } else {
-    for (int64_t i = tid; i < (t_end - t_begin) * KS; i += kThreads) lds_ks[i] = ks_ptr[(t_begin * KS + i) * ks_stride];
+    for (int64_t i = tid; i < (t_end - t_begin) * KS; i += kThreads) lds_ks[i] = ks_ptr[k_scale_index(p, t_begin + i / KS, i % KS, KS) * ks_stride];
   }
   if constexpr (PV == PV_FP8 && !SPLIT)
     if (tid < kD) {
@@ -468,7 +481,8 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
     }
   if constexpr (MQ) {
     const float* qsp = p.q_scale + (b * p.Hq + h) * p.nQS + qb0 * qs_per;
-    for (int64_t i = tid; i < (qb_end - qb0) * qs_per; i += kThreads) lds_qs[i] = qsp[i];
+    const int64_t n_qs = std::min<int64_t>((qb_end - qb0) * qs_per, p.nQS - qb0 * qs_per);
+    for (int64_t i = tid; i < n_qs; i += kThreads) lds_qs[i] = qsp[i];
   }
   // The loop runs over (query block, key tile) pairs: a multi-block launch walks the same key tiles once
   // per query block, and its DMA stream runs on across the block boundaries.
@@ -890,9 +904,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     for (int m = 0; m < NQF; m++) asm volatile("" ::"v"(qf[m]));
   }
   const int64_t qbs = min(qb, p.nQB - 1);
-  const int64_t qsi = p.qgran == QATTN_GRAN_THREAD ? (qbs * 4 + wl) * 8 + (lq & 7)
-                      : p.qgran == QATTN_GRAN_WARP ? qbs * 4 + wl
-                                                   : qbs;
+  const int64_t qsi = q_scale_index(p, qbs * kBQ + wl * 32 + lq);
   const float qs = p.q_scale[(b * p.Hq + h) * p.nQS + qsi] * p.qk_mult;
   const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
 
@@ -944,7 +956,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
 
   __syncthreads();  // Q fragments are out of the LDS stage before the DMA reuses it
   // the key scales of tiles t_lo .. t_end - 1, from lds_ks[0]
-  for (int i = tid; i < (t_end - t_lo) * KS; i += kPPThreads) lds_ks[i] = ks_ptr[(int64_t)t_lo * KS + i];
+  for (int i = tid; i < (t_end - t_lo) * KS; i += kPPThreads) lds_ks[i] = ks_ptr[k_scale_index(p, t_lo + i / KS, i % KS, KS)];
   if (tid < HD) {
     lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * HD + tid];
     lds_vm[tid] = p.v_mean ? p.v_mean[(b * p.Hkv + hk) * HD + tid] : 0.f;
@@ -1240,7 +1252,7 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
       }
     }
     const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
-    if (tid < n_tiles * KS) lds_ks[tid] = ks_ptr[tid];
+    if (tid < n_tiles * KS) lds_ks[tid] = ks_ptr[k_scale_index(p, tid / KS, tid % KS, KS)];
     if (tid < kD) {
       lds_vs[tid] = p.v_scale[(b * p.Hkv + hk) * kD + tid];
       lds_vm[tid] = p.v_mean ? p.v_mean[(b * p.Hkv + hk) * kD + tid] : 0.f;
@@ -1274,8 +1286,7 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
   for (; wb < wb_end; wb += NW) {
     load_q(wb, qf);
     const int64_t wrow0 = wb * 32, qrow = wrow0 + lq;
-    const int64_t qsi = p.qgran == QATTN_GRAN_THREAD ? wb * 8 + (lq & 7) : p.qgran == QATTN_GRAN_WARP ? wb : wb / 4;
-    const float qs = qs_tab[qsi] * p.qk_mult;
+    const float qs = qs_tab[q_scale_index(p, wb * 32 + lq)] * p.qk_mult;
 
     v16f o[4];
     v4f lacc;
@@ -1482,6 +1493,8 @@ __global__ __launch_bounds__(256) void qattn_combine_kernel(AttnParams p) {
 
 using namespace qattn;
 
+static bool is_thread_gran(int g) { return g == QATTN_GRAN_THREAD || g == QATTN_GRAN_THREAD_SM90; }
+
 // key tiles one workgroup can cover (its k_scales are staged in LDS)
 static int64_t max_tiles_per_split(int pv, bool kt) {
   const int floats = pv == PV_FP8 ? ks_lds_floats<PV_FP8>() : ks_lds_floats<PV_BF16>();
@@ -1522,7 +1535,7 @@ extern "C" int qattn_fwd_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t H
 }
 
 extern "C" int qattn_fwd_ex_num_splits(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int v_kind, int qk_quant_gran) {
-  return num_splits_for(B, Lq, Lk, Hq, max_tiles_per_split(v_kind, qk_quant_gran == QATTN_GRAN_THREAD),
+  return num_splits_for(B, Lq, Lk, Hq, max_tiles_per_split(v_kind, is_thread_gran(qk_quant_gran)),
                         v_kind == QATTN_V_FP8);
 }
 
@@ -1533,7 +1546,7 @@ extern "C" int qattn_fwd_ex_blocks_per_workgroup(int64_t B, int64_t Lq, int64_t 
   if (v_kind != QATTN_V_FP8 || causal || B <= 0 || Lq <= 0 || Lk <= 0 || Hq <= 0) return 1;
   const int64_t nkb = (Lk + kBK - 1) / kBK, nqb = (Lq + kBQ - 1) / kBQ;
   if (nkb >= kMqAutoMaxTiles) return 1;
-  if (num_splits_for(B, Lq, Lk, Hq, max_tiles_per_split(PV_FP8, qk_quant_gran == QATTN_GRAN_THREAD), true) != 1)
+  if (num_splits_for(B, Lq, Lk, Hq, max_tiles_per_split(PV_FP8, is_thread_gran(qk_quant_gran)), true) != 1)
     return 1;
   return blocks_per_workgroup(B * Hq, nqb, nkb);
 }
@@ -1717,13 +1730,15 @@ static int blocks_per_workgroup(int64_t bh, int64_t nqb, int64_t nkb) {
 static void plan_fwd(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int pv, int gran, int causal, bool sparse,
                      int num_splits, int& ns, int& qpw, int& kernel) {
   const int64_t nQB = (Lq + kBQ - 1) / kBQ, nKB = (Lk + kBK - 1) / kBK;
-  const int64_t max_tiles = sparse ? kSpMaxTiles : max_tiles_per_split(pv, gran == QATTN_GRAN_THREAD);
+  const int64_t max_tiles = sparse ? kSpMaxTiles : max_tiles_per_split(pv, is_thread_gran(gran));
   ns = num_splits > 0 ? num_splits : num_splits_for(B, Lq, Lk, Hq, max_tiles, pv == PV_FP8 && !sparse);
   ns = (int)std::min<int64_t>(ns, nKB);
   if (ns < 1) ns = 1;
   // a workgroup stages the k_scales of at most max_tiles key tiles
   ns = (int)std::max<int64_t>(ns, (nKB + max_tiles - 1) / max_tiles);
-  const bool mq_ok = ns == 1 && !sparse && !causal && pv == PV_FP8 && nKB <= kMqMaxTiles;
+  // (the multi-block kernel stages at most 32 q_scales per query block)
+  const bool mq_ok = ns == 1 && !sparse && !causal && pv == PV_FP8 && nKB <= kMqMaxTiles &&
+                     gran != QATTN_GRAN_THREAD_SM90;
   const bool res_ok = ns == 1 && !sparse && !causal && pv == PV_FP8 && nKB <= kResMaxTiles;
   const int qpw_mq = mq_ok ? blocks_per_workgroup(B * Hq, nQB, nKB) : 1;
   const int qpw_auto = nKB < kMqAutoMaxTiles ? qpw_mq : 1;
@@ -1749,8 +1764,9 @@ static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale,
   QATTN_REQUIRE(D == kD || (D == 64 && pv == PV_FP8 && !sparse), QATTN_ERR_HEAD_DIM,
                 "qattn_fwd needs head_dim 128, or 64 with FP8 V on a dense launch (pad other heads), got %lld",
                 (long long)D);
-  QATTN_REQUIRE(gran == QATTN_GRAN_BLOCK || gran == QATTN_GRAN_WARP || gran == QATTN_GRAN_THREAD, QATTN_ERR_ARG,
-                "qk_quant_gran must be 1 (per block), 2 (per warp) or 3 (per thread), got %d", gran);
+  QATTN_REQUIRE(gran >= QATTN_GRAN_BLOCK && gran <= QATTN_GRAN_THREAD_SM90, QATTN_ERR_ARG,
+                "qk_quant_gran must be 1 (per block), 2 (per warp), 3 (per thread), 4 (per warp, sm90 tables) or "
+                "5 (per thread, sm90 tables), got %d", gran);
   QATTN_REQUIRE(B >= 0 && Lq >= 0 && Lk >= 0 && Hq > 0 && Hkv > 0, QATTN_ERR_SHAPE, "bad sizes");
   QATTN_REQUIRE(Hq % Hkv == 0, QATTN_ERR_HEAD_RATIO, "num_qo_heads (%lld) must be divisible by num_kv_heads (%lld)",
                 (long long)Hq, (long long)Hkv);
@@ -1784,9 +1800,19 @@ static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale,
   p.B = B; p.Lq = Lq; p.Lk = Lk; p.Hq = Hq; p.Hkv = Hkv;
   p.nQB = (Lq + kBQ - 1) / kBQ;
   p.nKB = (Lk + kBK - 1) / kBK;
-  p.qgran = gran;
-  p.nQS = gran == QATTN_GRAN_THREAD ? p.nQB * 32 : gran == QATTN_GRAN_WARP ? p.nQB * 4 : p.nQB;
-  p.nKS = gran == QATTN_GRAN_THREAD ? p.nKB * 4 : p.nKB;
+  const bool sm90 = gran == QATTN_GRAN_WARP_SM90 || gran == QATTN_GRAN_THREAD_SM90;
+  p.qgran = sm90 ? gran - 2 : gran;
+  p.qrs = sm90 ? 4 : 5;
+  p.kts = sm90 ? 1 : 0;
+  if (sm90) {
+    // 64-row Q blocks of four 16-row warps, 128-key K blocks
+    const int64_t nq64 = (Lq + 63) / 64, nk128 = (Lk + 127) / 128;
+    p.nQS = p.qgran == QATTN_GRAN_THREAD ? nq64 * 32 : nq64 * 4;
+    p.nKS = p.qgran == QATTN_GRAN_THREAD ? nk128 * 4 : nk128;
+  } else {
+    p.nQS = gran == QATTN_GRAN_THREAD ? p.nQB * 32 : gran == QATTN_GRAN_WARP ? p.nQB * 4 : p.nQB;
+    p.nKS = gran == QATTN_GRAN_THREAD ? p.nKB * 4 : p.nKB;
+  }
   p.q_offset = q_offset;
   p.group = (int)(Hq / Hkv);
   p.causal = causal ? 1 : 0;
@@ -1807,7 +1833,7 @@ static int setup_fwd(AttnParams& p, int& ns, qattn_seq q8, const float* q_scale,
 template <int PV>
 static int launch_gran(AttnParams& p, int gran, int out_dtype, int ns, void* ws, size_t wsb, hipStream_t st,
                        int64_t D, int kernel) {
-  if (gran == QATTN_GRAN_THREAD) return launch_fwd<PV, true>(p, out_dtype, ns, ws, wsb, st, D, kernel);
+  if (is_thread_gran(gran)) return launch_fwd<PV, true>(p, out_dtype, ns, ws, wsb, st, D, kernel);
   return launch_fwd<PV, false>(p, out_dtype, ns, ws, wsb, st, D, kernel);
 }
 

@@ -55,8 +55,8 @@ __device__ __forceinline__ void norm_rope8(const NormRope& nr, int64_t b, int64_
 }
 
 // One quantizer job (Q or K).  A workgroup covers blk rows of one (batch entry, head): one scale block of
-// the quantizer's block size (128, 64 or 32 rows), or, with nsub = 4, 128 rows that are four 32-row scale
-// blocks (the warp blocks of the per-warp / per-thread Q layouts).
+// the quantizer's block size (128, 64 or 32 rows), or, with nsub = 4, blk = 4 cr rows that are four cr-row
+// scale blocks (the warp blocks of the per-warp / per-thread Q layouts: cr = 32, or 16 in the sm90 layout).
 struct QuantJob {
   const uint16_t* in;
   int64_t sb, sl, sh;
@@ -68,6 +68,7 @@ struct QuantJob {
   int64_t nblk;          // workgroup blocks per (batch entry, head)
   int64_t scale_blocks;  // scale blocks per (batch entry, head) in the scale tensor
   int blk, nsub;
+  int cr;  // rows per scale cell of a grouped block (32 or 16), 0 for one scale per block
   int has_sm_scale;
   float sm_scale;
   int64_t nwg;  // B * H * nblk
@@ -127,14 +128,17 @@ __device__ __forceinline__ float div_by(float a, float b, float y1) {
 }
 
 // One workgroup per block of one (batch entry, head) of a job; a launch covers up to two jobs (Q and K)
-// of equal nsub: workgroups [0, job[0].nwg) take job 0, the rest job 1.  Two passes over registers: |x|
-// maxima, then the scales and the quantized bytes.  GROUPED (nsub = 4): the block's 128 rows are four
+// of equal cell layout (cr): workgroups [0, job[0].nwg) take job 0, the rest job 1.  Two passes over registers: |x|
+// maxima, then the scales and the quantized bytes.  GROUPED (CR = 32 or 16 rows per cell, nsub = blk / CR
+// cells): the block's rows are cells of CR rows with scales of their own, e.g. four
 // 32-row scale blocks; a wave's rows of one pass lie in one of them.
 // The plain kernel is held to 64 VGPRs: 4 workgroups (8 waves per SIMD) per CU instead of 3, worth more than
 // the two registers it spills.
-template <bool IS_FP16, int VARIANT, int D, bool GROUPED>
-__global__ __launch_bounds__(quant_threads<VARIANT>()) __attribute__((amdgpu_waves_per_eu(GROUPED ? 7 : 8)))
+template <bool IS_FP16, int VARIANT, int D, int CR>
+__global__ __launch_bounds__(quant_threads<VARIANT>()) __attribute__((amdgpu_waves_per_eu(CR ? 7 : 8)))
 void quant_per_block_kernel(QuantArgs args) {
+  constexpr bool GROUPED = CR != 0;
+  constexpr int NCELL = GROUPED ? 128 / CR : 1;  // cells of a 128-row block
   constexpr int kQuantThreads = quant_threads<VARIANT>();
   constexpr int TPR = D / 8;                       // threads (16-byte chunks) per row
   constexpr int MAXC = 128 * TPR / kQuantThreads;  // chunks per thread at 128 rows
@@ -168,7 +172,7 @@ void quant_per_block_kernel(QuantArgs args) {
     h = bh - b * H;
   }
   const int tid = threadIdx.x;
-  const int blk = GROUPED ? 128 : J.blk;
+  const int blk = J.blk;
   // this entry's rows: in_b[l * sl], l < Lb (a dense batch entry, or one packed sequence)
   const uint16_t* in_b = J.in + (int64_t)b * J.sb;
   int8_t* out_b = J.out + (int64_t)b * J.ob;
@@ -253,13 +257,13 @@ void quant_per_block_kernel(QuantArgs args) {
     const int cw = 1 << J.cls_shift;
     auto class_max = [&](int g, int k) {
       float a = 0.f;
-      const int r0 = GROUPED ? 32 * g : 0, r1 = GROUPED ? r0 + 32 : RPP;
+      const int r0 = GROUPED ? CR * g : 0, r1 = GROUPED ? r0 + CR : RPP;
       for (int o = r0; o < r1; o += 8)
         for (int m = 0; m < cw; m++) a = fmaxf(a, row_max[o + k * cw + m]);
       return a;
     };
 #pragma unroll
-    for (int i = 0; i < NA; i++) sc[i] = scale_of(class_max(GROUPED ? (RPP * i + row0) / 32 : 0, cls));
+    for (int i = 0; i < NA; i++) sc[i] = scale_of(class_max(GROUPED ? (RPP * i + row0) / (GROUPED ? CR : 1) : 0, cls));
     if (tid < J.nsub * J.ncls) scale_at[tid] = scale_of(class_max(tid / J.ncls, tid % J.ncls));
   } else {  // one scale per scale block: wave maxima, then over the waves (of each 32-row cell)
     __shared__ float wave_maxes[NA][NW];
@@ -269,31 +273,37 @@ void quant_per_block_kernel(QuantArgs args) {
       if ((tid & 63) == 0) wave_maxes[i][tid >> 6] = a;
     }
     __syncthreads();
-    float cell[GROUPED ? 4 : 1];  // cell c: rows [32 c, 32 c + 32) = the waves w of chunk i with (RPP i + RPW w) / 32 == c
+    float cell[NCELL];  // cell c: rows [CR c, CR c + CR) = the waves w of chunk i with (RPP i + RPW w) / CR == c
 #pragma unroll
-    for (int c = 0; c < (GROUPED ? 4 : 1); c++) {
+    for (int c = 0; c < NCELL; c++) {
       cell[c] = amax0;
 #pragma unroll
       for (int i = 0; i < NA; i++)
 #pragma unroll
         for (int ww = 0; ww < NW; ww++)
-          if (!GROUPED || (RPP * i + RPW * ww) / 32 == c) cell[c] = fmaxf(cell[c], wave_maxes[i][ww]);
+          if (!GROUPED || (RPP * i + RPW * ww) / (GROUPED ? CR : 1) == c) cell[c] = fmaxf(cell[c], wave_maxes[i][ww]);
     }
 #pragma unroll
     for (int i = 0; i < NA; i++) {
       float a = cell[0];
-      if constexpr (GROUPED) {
+      if constexpr (CR == 32) {
         // this thread's cell of chunk i: (RPP i + row0) / 32, row0 / 32 = RPW (tid / 64) / 32
         a = cell[(RPP * i) / 32];
         if constexpr (RPP > 32) {
           if ((RPW * (tid >> 6)) / 32 == 1) a = cell[(RPP * i) / 32 + 1];
         }
+      } else if constexpr (GROUPED) {
+        // this wave's cell of chunk i (a wave's RPW rows of a pass lie in one cell)
+        const int idx = (RPP * i + RPW * (tid >> 6)) / CR;
+#pragma unroll
+        for (int c = 1; c < NCELL; c++)
+          if (idx == c) a = cell[c];
       }
       sc[i] = VARIANT == QATTN_QUANT_CUDA ? 127.0f / a : scale_of(a);
     }
 #pragma unroll
-    for (int c = 0; c < (GROUPED ? 4 : 1); c++)
-      if (tid == c) scale_at[c] = scale_of(cell[c]);
+    for (int c = 0; c < NCELL; c++)
+      if (tid == c && c < J.nsub) scale_at[c] = scale_of(cell[c]);
   }
 
 #pragma unroll
@@ -753,6 +763,7 @@ static bool fill_job(QuantJob& J, const qattn_seq& in, const qattn_seq& out, int
   J.L = L; J.H = H;
   J.blk = blk;
   J.nsub = 1;
+  J.cr = 0;
   J.nblk = (L + blk - 1) / blk;
   J.scale_blocks = J.nblk;
   J.has_sm_scale = has_sm;
@@ -769,18 +780,21 @@ static bool fill_job(QuantJob& J, const qattn_seq& in, const qattn_seq& out, int
 // Q in the per-warp / per-thread layouts: the reference grid's 128-row CTA blocks, each four 32-row warp
 // blocks with scales of their own (trailing warp blocks past L get the scale of an empty block).  One
 // workgroup covers a CTA block.
-static void warp_block_job(QuantJob& J, int64_t B) {
-  J.blk = 128;
+static void warp_block_job(QuantJob& J, int64_t B, int warp_rows = 32) {
+  // warp_rows 32: the sm80/sm89 layout (128-row blocks of four 32-row warps); 16: the sm90 layout
+  // (64-row blocks of four 16-row warps, sageattn2.py:1608-1624)
+  J.blk = warp_rows * 4;
   J.nsub = 4;
-  J.nblk = (J.L + 127) / 128;
+  J.cr = warp_rows;
+  J.nblk = (J.L + J.blk - 1) / J.blk;
   J.scale_blocks = J.nblk * 4;
   J.nwg = B * J.H * J.nblk;
 }
 
-template <int D, bool GROUPED>
+template <int D, int CR>
 static void launch_quant(const QuantArgs& a, int dtype, int variant, int64_t nwg, hipStream_t st) {
   dim3 grid((unsigned)nwg);
-#define QATTN_QK(F16, V) quant_per_block_kernel<F16, V, D, GROUPED><<<grid, quant_threads<V>(), 0, st>>>(a)
+#define QATTN_QK(F16, V) quant_per_block_kernel<F16, V, D, CR><<<grid, quant_threads<V>(), 0, st>>>(a)
   if (dtype == QATTN_BF16) {
     if (variant == QATTN_QUANT_CUDA) QATTN_QK(false, QATTN_QUANT_CUDA);
     else if (variant == QATTN_QUANT_TRITON) QATTN_QK(false, QATTN_QUANT_TRITON);
@@ -796,23 +810,26 @@ static void launch_quant(const QuantArgs& a, int dtype, int variant, int64_t nwg
 // One launch per scale-block layout among the jobs (Q in warp blocks next to K in plain blocks takes two:
 // each kernel keeps the register budget of its own layout).
 static int run_quant(QuantArgs& a, int dtype, int64_t D, int variant, hipStream_t st) {
-  for (int nsub : {1, 4}) {
+  for (int cr : {0, 32, 16}) {
     QuantArgs s{};
     s.njobs = 0;
     int64_t nwg = 0;
     for (int j = 0; j < a.njobs; j++)
-      if (a.job[j].nsub == nsub && a.job[j].nwg > 0) {
+      if (a.job[j].cr == cr && a.job[j].nwg > 0) {
         s.job[s.njobs++] = a.job[j];
         nwg += a.job[j].nwg;
       }
     if (nwg == 0) continue;
     QATTN_REQUIRE(nwg < (1ll << 31), QATTN_ERR_SHAPE, "quantizer grid too large");
-    if (nsub == 4) {
-      if (D == 128) launch_quant<128, true>(s, dtype, variant, nwg, st);
-      else launch_quant<64, true>(s, dtype, variant, nwg, st);
+    if (cr == 32) {
+      if (D == 128) launch_quant<128, 32>(s, dtype, variant, nwg, st);
+      else launch_quant<64, 32>(s, dtype, variant, nwg, st);
+    } else if (cr == 16) {
+      if (D == 128) launch_quant<128, 16>(s, dtype, variant, nwg, st);
+      else launch_quant<64, 16>(s, dtype, variant, nwg, st);
     } else {
-      if (D == 128) launch_quant<128, false>(s, dtype, variant, nwg, st);
-      else launch_quant<64, false>(s, dtype, variant, nwg, st);
+      if (D == 128) launch_quant<128, 0>(s, dtype, variant, nwg, st);
+      else launch_quant<64, 0>(s, dtype, variant, nwg, st);
     }
   }
   return check_launch("quant_per_block_int8");
@@ -872,45 +889,59 @@ extern "C" int qattn_quant_qk_per_block_int8(qattn_seq q, qattn_seq k, int dtype
   return run_quant(a, dtype, D, variant, (hipStream_t)stream);
 }
 
-extern "C" int qattn_quant_qk_per_warp_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq, int64_t Lk,
-                                             int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean, qattn_seq q_out,
-                                             qattn_seq k_out, float* q_scale, float* k_scale, qattn_stream_t stream) {
+extern "C" int qattn_quant_qk_per_warp_int8_ex(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq,
+                                                int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean,
+                                                qattn_seq q_out, qattn_seq k_out, float* q_scale, float* k_scale,
+                                                int scale_layout, qattn_stream_t stream) {
   int rc;
   if ((rc = check_common(dtype, D, QATTN_QUANT_CUDA, 64))) return rc;
+  QATTN_REQUIRE(scale_layout == QATTN_SCALES_SM89 || scale_layout == QATTN_SCALES_SM90, QATTN_ERR_ARG,
+                "scale_layout must be 0 (sm89) or 1 (sm90), got %d", scale_layout);
   QATTN_REQUIRE(B >= 0 && Lq >= 0 && Lk >= 0 && Hq >= 0 && Hkv >= 0, QATTN_ERR_SHAPE, "negative size");
   QATTN_REQUIRE(q_scale && k_scale, QATTN_ERR_ARG, "scale is null");
+  const bool sm90 = scale_layout == QATTN_SCALES_SM90;
   QuantArgs a{};
   a.njobs = 0;
   if (B * Lq * Hq > 0) {
     if ((rc = check_seq("q", q, 2)) || (rc = check_seq("q_out", q_out, 1))) return rc;
     QuantJob& J = a.job[a.njobs++];
     fill_job(J, q, q_out, B, Lq, Hq, nullptr, q_scale, 1.0f, 0, 32);
-    warp_block_job(J, B);
+    warp_block_job(J, B, sm90 ? 16 : 32);
   }
   if (B * Lk * Hkv > 0) {
     if ((rc = check_seq("k", k, 2)) || (rc = check_seq("k_out", k_out, 1))) return rc;
     QATTN_REQUIRE(k_mean == nullptr || aligned16(k_mean), QATTN_ERR_ALIGN, "k_mean must be 16-byte aligned");
-    fill_job(a.job[a.njobs++], k, k_out, B, Lk, Hkv, k_mean, k_scale, 1.0f, 0, 64);
+    fill_job(a.job[a.njobs++], k, k_out, B, Lk, Hkv, k_mean, k_scale, 1.0f, 0, sm90 ? 128 : 64);
   }
   if (a.njobs == 0) return QATTN_OK;
   return run_quant(a, dtype, D, QATTN_QUANT_CUDA, (hipStream_t)stream);
 }
 
-extern "C" int qattn_quant_qk_per_thread_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq,
-                                               int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean,
-                                               qattn_seq q_out, qattn_seq k_out, float* q_scale, float* k_scale,
-                                               qattn_stream_t stream) {
+extern "C" int qattn_quant_qk_per_warp_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq, int64_t Lk,
+                                             int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean, qattn_seq q_out,
+                                             qattn_seq k_out, float* q_scale, float* k_scale, qattn_stream_t stream) {
+  return qattn_quant_qk_per_warp_int8_ex(q, k, dtype, B, Lq, Lk, Hq, Hkv, D, k_mean, q_out, k_out, q_scale, k_scale,
+                                         QATTN_SCALES_SM89, stream);
+}
+
+extern "C" int qattn_quant_qk_per_thread_int8_ex(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq,
+                                                  int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean,
+                                                  qattn_seq q_out, qattn_seq k_out, float* q_scale, float* k_scale,
+                                                  int scale_layout, qattn_stream_t stream) {
   int rc;
   if ((rc = check_common(dtype, D, QATTN_QUANT_TRITON, 64))) return rc;
+  QATTN_REQUIRE(scale_layout == QATTN_SCALES_SM89 || scale_layout == QATTN_SCALES_SM90, QATTN_ERR_ARG,
+                "scale_layout must be 0 (sm89) or 1 (sm90), got %d", scale_layout);
   QATTN_REQUIRE(B >= 0 && Lq >= 0 && Lk >= 0 && Hq >= 0 && Hkv >= 0, QATTN_ERR_SHAPE, "negative size");
   QATTN_REQUIRE(q_scale && k_scale, QATTN_ERR_ARG, "scale is null");
+  const bool sm90 = scale_layout == QATTN_SCALES_SM90;
   QuantArgs a{};
   a.njobs = 0;
   if (B * Lq * Hq > 0) {
     if ((rc = check_seq("q", q, 2)) || (rc = check_seq("q_out", q_out, 1))) return rc;
     QuantJob& J = a.job[a.njobs++];
     fill_job(J, q, q_out, B, Lq, Hq, nullptr, q_scale, 1.0f, 0, 32);
-    warp_block_job(J, B);
+    warp_block_job(J, B, sm90 ? 16 : 32);
     J.ncls = 8;
     J.cls_shift = 0;
   }
@@ -918,12 +949,20 @@ extern "C" int qattn_quant_qk_per_thread_int8(qattn_seq q, qattn_seq k, int dtyp
     if ((rc = check_seq("k", k, 2)) || (rc = check_seq("k_out", k_out, 1))) return rc;
     QATTN_REQUIRE(k_mean == nullptr || aligned16(k_mean), QATTN_ERR_ALIGN, "k_mean must be 16-byte aligned");
     QuantJob& J = a.job[a.njobs++];
-    fill_job(J, k, k_out, B, Lk, Hkv, k_mean, k_scale, 1.0f, 0, 64);
+    fill_job(J, k, k_out, B, Lk, Hkv, k_mean, k_scale, 1.0f, 0, sm90 ? 128 : 64);
     J.ncls = 4;
     J.cls_shift = 1;
   }
   if (a.njobs == 0) return QATTN_OK;
   return run_quant(a, dtype, D, QATTN_QUANT_TRITON_THREAD, (hipStream_t)stream);
+}
+
+extern "C" int qattn_quant_qk_per_thread_int8(qattn_seq q, qattn_seq k, int dtype, int64_t B, int64_t Lq,
+                                               int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, const void* k_mean,
+                                               qattn_seq q_out, qattn_seq k_out, float* q_scale, float* k_scale,
+                                               qattn_stream_t stream) {
+  return qattn_quant_qk_per_thread_int8_ex(q, k, dtype, B, Lq, Lk, Hq, Hkv, D, k_mean, q_out, k_out, q_scale,
+                                           k_scale, QATTN_SCALES_SM89, stream);
 }
 
 static int64_t col_chunks(int64_t L) { return (L + kColChunk - 1) / kColChunk; }

@@ -97,24 +97,37 @@ def per_block_int8(q: torch.Tensor, k: torch.Tensor, km: Optional[torch.Tensor] 
 
 def per_warp_int8(q: torch.Tensor, k: torch.Tensor, km: Optional[torch.Tensor] = None, BLKQ: int = 128,
                   WARPQ: int = 32, BLKK: int = 64, tensor_layout: str = "HND"):
-    """sageattn2.per_warp_int8 (sageattn2.py:190-280): Q per 32-row warp block (no sm_scale folded in),
-    K per 64-row block after km.  Returns (q_int8, q_scale [B, Hq, ceil(Lq/128)*4], k_int8, k_scale)."""
-    if (BLKQ, WARPQ, BLKK) != (128, 32, 64):
-        raise ValueError("per_warp_int8 supports BLKQ=128, WARPQ=32, BLKK=64")
-    return _quant_gran(q, k, km, tensor_layout, "qattn_quant_qk_per_warp_int8", 4, 1)
+    """sageattn2.per_warp_int8 (sageattn2.py:190-280): Q per WARPQ-row warp block (no sm_scale folded in),
+    K per BLKK-row block after km.  Block shapes: (BLKQ, WARPQ, BLKK) = (128, 32, 64), the sm80/sm89
+    kernels' tables, or (64, 16, 128), the sm90 entry's (sageattn2.py:1608-1611).  Returns (q_int8,
+    q_scale [B, Hq, ceil(Lq/BLKQ)*4], k_int8, k_scale [B, Hkv, ceil(Lk/BLKK)])."""
+    shapes = {(128, 32, 64): False, (64, 16, 128): True}
+    if (BLKQ, WARPQ, BLKK) not in shapes:
+        raise ValueError("per_warp_int8 supports (BLKQ, WARPQ, BLKK) = (128, 32, 64) or (64, 16, 128)")
+    return _quant_gran(q, k, km, tensor_layout, "qattn_quant_qk_per_warp_int8_ex", 4, 1, shapes[(BLKQ, WARPQ, BLKK)])
 
 
 def per_thread_int8(q: torch.Tensor, k: torch.Tensor, km: Optional[torch.Tensor] = None, BLKQ: int = 128,
                     WARPQ: int = 32, BLKK: int = 64, WARPK: int = 64, sm_scale=None, tensor_layout: str = "HND"):
     """triton.quant_per_thread.per_thread_int8 (quant_per_thread.py:267-369): per-thread scale classes,
     scale = amax/127 + 1e-7, round half away, K = half-rounded (k - km); sm_scale is not folded in.
-    Returns (q_int8, q_scale [B, Hq, ceil(Lq/128)*32], k_int8, k_scale [B, Hkv, ceil(Lk/64)*4])."""
-    if (BLKQ, WARPQ, BLKK, WARPK) != (128, 32, 64, 64):
-        raise ValueError("per_thread_int8 supports BLKQ=128, WARPQ=32, BLKK=64, WARPK=64")
-    return _quant_gran(q, k, km, tensor_layout, "qattn_quant_qk_per_thread_int8", 32, 4)
+    Block shapes: (BLKQ, WARPQ, BLKK, WARPK) = (128, 32, 64, 64) or the sm90 entry's (64, 16, 128, 128)
+    (sageattn2.py:1614-1624).  Returns (q_int8, q_scale [B, Hq, ceil(Lq/BLKQ)*(BLKQ/WARPQ)*8], k_int8,
+    k_scale [B, Hkv, ceil(Lk/BLKK)*4])."""
+    shapes = {(128, 32, 64, 64): False, (64, 16, 128, 128): True}
+    if (BLKQ, WARPQ, BLKK, WARPK) not in shapes:
+        raise ValueError("per_thread_int8 supports (BLKQ, WARPQ, BLKK, WARPK) = (128, 32, 64, 64) or "
+                         "(64, 16, 128, 128)")
+    return _quant_gran(q, k, km, tensor_layout, "qattn_quant_qk_per_thread_int8_ex", 32, 4,
+                       shapes[(BLKQ, WARPQ, BLKK, WARPK)])
 
 
-def _quant_gran(q, k, km, tensor_layout, entry, q_per_blk, k_per_blk):
+def _scale_blocks(lq, lk, sm90):
+    """Q and K scale blocks per (batch entry, head): 128-row Q / 64-row K blocks, or 64 / 128 (sm90)."""
+    return (-(-lq // 64), -(-lk // 128)) if sm90 else (-(-lq // 128), -(-lk // 64))
+
+
+def _quant_gran(q, k, km, tensor_layout, entry, q_per_blk, k_per_blk, sm90=False):
     L = _lib.load()
     if q.dtype != k.dtype:
         raise ValueError("q and k must have the same dtype")
@@ -122,13 +135,14 @@ def _quant_gran(q, k, km, tensor_layout, entry, q_per_blk, k_per_blk):
     _, lk, hkv, _ = _dims(k, tensor_layout)
     q_int8 = torch.empty(q.shape, dtype=torch.int8, device=q.device)
     k_int8 = torch.empty(k.shape, dtype=torch.int8, device=k.device)
-    q_scale = torch.empty((b, hq, (lq + 127) // 128 * q_per_blk), dtype=torch.float32, device=q.device)
-    k_scale = torch.empty((b, hkv, (lk + 63) // 64 * k_per_blk), dtype=torch.float32, device=q.device)
+    nqb, nkb = _scale_blocks(lq, lk, sm90)
+    q_scale = torch.empty((b, hq, nqb * q_per_blk), dtype=torch.float32, device=q.device)
+    k_scale = torch.empty((b, hkv, nkb * k_per_blk), dtype=torch.float32, device=q.device)
     kmc = None if km is None else _mean_3d(km.to(k.dtype), b, hkv, d, tensor_layout)
     _lib.check(getattr(L, entry)(
         _lib.seq(q, tensor_layout), _lib.seq(k, tensor_layout), _lib.dtype_code(q.dtype), b, lq, lk, hq, hkv, d,
         _lib.ptr(kmc), _lib.seq(q_int8, tensor_layout), _lib.seq(k_int8, tensor_layout), _lib.ptr(q_scale),
-        _lib.ptr(k_scale), _lib.stream_of(q)))
+        _lib.ptr(k_scale), _lib.QATTN_SCALES_SM90 if sm90 else _lib.QATTN_SCALES_SM89, _lib.stream_of(q)))
     return q_int8, q_scale, k_int8, k_scale
 
 
@@ -233,10 +247,11 @@ def _kv_valid_tensor(kv_valid_len, b: int, device) -> Optional[torch.Tensor]:
 _GRAN = {"per_block": _lib.QATTN_GRAN_BLOCK, "per_warp": _lib.QATTN_GRAN_WARP, "per_thread": _lib.QATTN_GRAN_THREAD}
 
 
-def _check_attn_operands(q_int8, q_scale, k_int8, k_scale, v, v_scale, b, lq, lk, hq, hkv, d, gran, out, out_dtype):
+def _check_attn_operands(q_int8, q_scale, k_int8, k_scale, v, v_scale, b, lq, lk, hq, hkv, d, gran, out, out_dtype,
+                         sm90=False):
     """Shapes, dtypes and devices of qattn_fwd's operands: a scale tensor of another granularity or a V
     tile of the wrong size would make the kernel read outside them."""
-    nqb, nkb = -(-lq // BLKQ), -(-lk // BLKK)
+    nqb, nkb = _scale_blocks(lq, lk, sm90)
     q_per = {"per_block": 1, "per_warp": 4, "per_thread": 32}[gran]
     k_per = 4 if gran == "per_thread" else 1
     dev = q_int8.device
@@ -246,7 +261,7 @@ def _check_attn_operands(q_int8, q_scale, k_int8, k_scale, v, v_scale, b, lq, lk
         if t.dtype != torch.float32 or tuple(t.shape) != shape or not t.is_contiguous():
             raise ValueError(f"{name} must be a contiguous float32 tensor of shape {shape} for qk_quant_gran="
                              f"{gran!r}, got {t.dtype} {tuple(t.shape)}")
-    lpad = nkb * BLKK
+    lpad = -(-lk // BLKK) * BLKK
     if v.dim() != 4 or tuple(v.shape[:3]) != (b, hkv, d) or v.shape[3] < lpad or v.shape[3] % BLKK or \
             not v.is_contiguous():
         raise ValueError(f"the V tile must be a contiguous [B, Hkv, D, Lpad] = [{b}, {hkv}, {d}, >= {lpad} (multiple "
@@ -269,12 +284,15 @@ def _check_attn_operands(q_int8, q_scale, k_int8, k_scale, v, v_scale, b, lq, lk
 
 def qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout="HND", out_dtype=torch.bfloat16,
               qk_mult=1.0, is_causal=False, q_offset=0, kv_valid_len=None, return_lse=False, num_splits=0,
-              qk_quant_gran="per_block", out: Optional[torch.Tensor] = None, v_mean: Optional[torch.Tensor] = None):
+              qk_quant_gran="per_block", out: Optional[torch.Tensor] = None, v_mean: Optional[torch.Tensor] = None,
+              scale_layout: str = "sm89"):
     """Attention on already-quantized operands (the torch.ops.tf_kernel.qk_int8_sv_f8_accum_f32_fuse_v_scale
     _attn op, common_extension.cc:239-258).  With v_scale=None, v_fp8 is the half-dtype V tile from
     ``v_tile_half`` and P.V runs in that dtype (qk_int8_sv_f16_accum_f32_attn, common_extension.cc:214-218).
     ``qk_quant_gran`` names the layout of q_scale / k_scale ("per_block", "per_warp", "per_thread"); for
-    the last two pass qk_mult = sm_scale * 1.44269504.  Returns o (and the log2-domain LSE [B, Hq, Lq])."""
+    the last two pass qk_mult = sm_scale * 1.44269504.  ``scale_layout="sm90"`` reads per-warp / per-thread
+    tables of the sm90 block shapes (per_warp_int8 / per_thread_int8 with BLKQ=64, WARPQ=16, BLKK=128).
+    Returns o (and the log2-domain LSE [B, Hq, Lq])."""
     L = _lib.load()
     b, lq, hq, d = _dims(q_int8, tensor_layout)
     _, lk, hkv, _ = _dims(k_int8, tensor_layout)
@@ -282,9 +300,14 @@ def qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout
         raise ValueError(f"num_qo_heads ({hq}) must be divisible by num_kv_heads ({hkv})")
     if qk_quant_gran not in _GRAN:
         raise ValueError(f"qk_quant_gran must be one of {sorted(_GRAN)}, got {qk_quant_gran!r}")
-    gran = _GRAN[qk_quant_gran]
+    if scale_layout not in ("sm89", "sm90"):
+        raise ValueError(f"scale_layout must be 'sm89' or 'sm90', got {scale_layout!r}")
+    sm90 = scale_layout == "sm90"
+    if sm90 and qk_quant_gran == "per_block":
+        raise ValueError("scale_layout='sm90' needs qk_quant_gran 'per_warp' or 'per_thread'")
+    gran = _GRAN[qk_quant_gran] + (2 if sm90 else 0)
     _check_attn_operands(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, b, lq, lk, hq, hkv, d, qk_quant_gran, out,
-                         out_dtype)
+                         out_dtype, sm90)
     if v_mean is not None and (v_scale is None or v_mean.dtype != torch.float32 or
                                tuple(v_mean.shape) != (b, hkv, d) or not v_mean.is_contiguous()):
         raise ValueError(f"v_mean must be a contiguous float32 tensor of shape {(b, hkv, d)} (FP8 V only)")
@@ -320,7 +343,7 @@ def _pad_head_dim(x: torch.Tensor, native64: bool = False) -> torch.Tensor:
 
 
 def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv_accum_dtype, smooth_k, smooth_v,
-                  return_lse, kv_valid_len, q_offset, pv, quant_variant="cuda"):
+                  return_lse, kv_valid_len, q_offset, pv, quant_variant="cuda", sm90=False):
     dtype = q.dtype
     if not q.is_cuda:
         raise AssertionError("Input tensors must be on cuda.")
@@ -355,7 +378,17 @@ def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv
             warnings.warn(f"pv_accum_dtype is '{pv_accum_dtype}', smooth_v will be ignored.")
             smooth_v = False
         scale_max = 2.25 if pv_accum_dtype == "fp32+fp16" else 448.0
-    if pv == "fp8" and quant_variant == "cuda":
+    if sm90:
+        # the sm90 entry's quantizers and tables (sageattn2.py:1579-1660): V without smoothing
+        km = k_mean(k, tensor_layout) if smooth_k else None
+        if qk_quant_gran == "per_thread":
+            q_int8, q_scale, k_int8, k_scale = per_thread_int8(q, k, km, BLKQ=64, WARPQ=16, BLKK=128, WARPK=128,
+                                                               tensor_layout=tensor_layout)
+        else:
+            q_int8, q_scale, k_int8, k_scale = per_warp_int8(q, k, km, BLKQ=64, WARPQ=16, BLKK=128,
+                                                             tensor_layout=tensor_layout)
+        v_fp8, v_scale, vm = per_channel_fp8(v, tensor_layout=tensor_layout, smooth_v=False)
+    elif pv == "fp8" and quant_variant == "cuda":
         # K mean, Q/K INT8 and V FP8 in one fused prologue (four launches)
         q_int8, q_scale, k_int8, k_scale, km, v_fp8, v_scale, vm = sage_quant(
             q, k, v, tensor_layout=tensor_layout, qk_quant_gran=qk_quant_gran, sm_scale=sm_scale, smooth_k=smooth_k,
@@ -377,7 +410,8 @@ def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv
             v_fp8, v_scale = v_tile_half(v, tensor_layout), None
     res = qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, tensor_layout=tensor_layout, out_dtype=dtype,
                     qk_mult=qk_mult, is_causal=is_causal, q_offset=q_offset, kv_valid_len=kv_valid_len,
-                    return_lse=return_lse, qk_quant_gran=qk_quant_gran, v_mean=vm)
+                    return_lse=return_lse, qk_quant_gran=qk_quant_gran, v_mean=vm,
+                    scale_layout="sm90" if sm90 else "sm89")
     o, lse = res if return_lse else (res, None)
     o = o[..., :head_dim_og]
     if not return_lse:
@@ -411,9 +445,24 @@ def sageattn_qk_int8_pv_fp8_cuda(q: torch.Tensor, k: torch.Tensor, v: torch.Tens
                          smooth_v, return_lse, kv_valid_len, q_offset, pv="fp8")
 
 
-def sageattn_qk_int8_pv_fp8_cuda_sm90(*args, **kwargs):
-    """Same entry as sageattn_qk_int8_pv_fp8_cuda (the reference's Hopper variant, sageattn2.py:1460)."""
-    return sageattn_qk_int8_pv_fp8_cuda(*args, **kwargs)
+def sageattn_qk_int8_pv_fp8_cuda_sm90(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str = "HND",
+                                      is_causal: bool = False, qk_quant_gran: str = "per_thread",
+                                      sm_scale: Optional[float] = None, pv_accum_dtype: str = "fp32+fp32",
+                                      smooth_k: bool = True, return_lse: bool = False, kv_valid_len=None,
+                                      q_offset: int = 0, **kwargs: Any):
+    """The reference's sm90 entry (sageattn2.py:1460-1697): INT8 Q.K^T with the sm90 scale tables
+    (per_warp_int8 / per_thread_int8 with BLKQ=64, WARPQ=16, BLKK=128), per-channel FP8 V without
+    smoothing, P.V accumulated in fp32 ("fp32+fp32", the only accumulation it takes: "fp32" raises
+    NotImplementedError there and here).  Heads of at most 64 run at 64, larger ones at 128, as there.
+    ``kv_valid_len`` / ``q_offset`` as in sageattn_qk_int8_pv_fp8_cuda."""
+    if qk_quant_gran not in ("per_warp", "per_thread"):
+        raise AssertionError("qk_quant_gran must be either 'per_warp' or 'per_thread'.")
+    if pv_accum_dtype == "fp32":
+        raise NotImplementedError("Please use pv_accum_dtype='fp32+fp32' for sm90.")
+    if pv_accum_dtype != "fp32+fp32":
+        raise ValueError(f"pv_accum_dtype must be 'fp32+fp32' for sm90, got {pv_accum_dtype!r}")
+    return _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv_accum_dtype, smooth_k,
+                         False, return_lse, kv_valid_len, q_offset, pv="fp8", sm90=True)
 
 
 def sageattn_qk_int8_pv_fp16_cuda(q, k, v, tensor_layout: str = "HND", is_causal: bool = False,

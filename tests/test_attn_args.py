@@ -106,3 +106,19 @@ def test_quant_ops_reject_bad_arguments(bad):
         scale = torch.empty(1, 2, 3, dtype=torch.float32)
     with pytest.raises(ValueError):
         torch.ops.telefuser_amd.quant_per_block_int8_fuse_sub_mean_cuda(x, mean, out, scale, 64, 0)
+
+
+@pytest.mark.parametrize("bad", ["sm89_tables", "per_block", "layout_name"])
+def test_qattn_fwd_sm90_layout_checks(bad):
+    """scale_layout="sm90" takes per-warp / per-thread tables of the sm90 block shapes only."""
+    from telefuser_amd import sageattn2 as sa
+
+    q8, qs, k8, ks, v, vs = _ops(Lq=300, Lk=200, gran="per_thread")  # sm89 shapes: 3*32 / 4*4 entries
+    kw = dict(tensor_layout="NHD", qk_quant_gran="per_thread", scale_layout="sm90")
+    if bad == "per_block":
+        q8, qs, k8, ks, v, vs = _ops(gran="per_block")
+        kw["qk_quant_gran"] = "per_block"
+    elif bad == "layout_name":
+        kw["scale_layout"] = "sm100"
+    with pytest.raises(ValueError):
+        sa.qattn_fwd(q8, qs, k8, ks, v, vs, **kw)

@@ -83,7 +83,11 @@ def test_fwd_ex_granularity_validation_and_splits(lib):
         return lib.qattn_fwd_ex(s, buf, s, buf, buf, v_kind, 128, buf, s, 0, 1, 128, 128, 2, 2, 128, 1.0, gran, 0, 0,
                                 None, None, ns, None, 0, None)
 
-    assert call(0, 4) == 9 and b"qk_quant_gran" in lib.qattn_last_error()
+    assert call(0, 6) == 9 and b"qk_quant_gran" in lib.qattn_last_error()
+    assert call(0, 0) == 9
+    # the sm90 tables (codes 4, 5) are per warp / per thread: same split counts as codes 2, 3
+    assert lib.qattn_fwd_ex_num_splits(1, 32760, 2000 * 64, 12, 0, 5) == \
+        lib.qattn_fwd_ex_num_splits(1, 32760, 2000 * 64, 12, 0, 3)
     assert call(3, 1) == 1
     assert call(1, 3, ns=2) == 7  # a split launch still needs its workspace
     # per-thread K scales take 4x the LDS staging per tile: long keys need more splits

@@ -27,7 +27,7 @@ KERNEL_ONE_BLOCK, KERNEL_MULTI_BLOCK, KERNEL_PINGPONG, KERNEL_RESIDENT = 1, 2, 3
 
 
 def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None, num_splits=0, q_offset=0,
-                   check_truth=True, pv="fp8", gran="per_block"):
+                   check_truth=True, pv="fp8", gran="per_block", sm90=False):
     dev = require_gpu()
     from telefuser_amd import _lib
     from telefuser_amd import sageattn2 as sa
@@ -35,7 +35,7 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
     B, Lq, Hq, D = q.shape
     Lk, Hkv = k.shape[1], k.shape[2]
     log(f"attn B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} layout={layout} causal={causal} kv_valid={kv_valid} "
-        f"splits={num_splits} gran={gran} pv={pv}")
+        f"splits={num_splits} gran={gran} pv={pv} D={D} sm90={sm90}")
     qd, kd, vd = (t.to(dev) for t in (q, k, v))
     if layout == "HND":
         qd, kd, vd = (t.transpose(1, 2).contiguous() for t in (qd, kd, vd))
@@ -45,15 +45,19 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
         q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=D ** -0.5, tensor_layout=layout)
     else:
         quant = sa.per_thread_int8 if gran == "per_thread" else sa.per_warp_int8
-        q8, qs, k8, ks = quant(qd, kd, km, tensor_layout=layout)
+        # the sm90 entry's block shapes (sageattn2.py:1608-1624)
+        shapes = (dict(BLKQ=64, WARPQ=16, BLKK=128, **(dict(WARPK=128) if gran == "per_thread" else {}))
+                  if sm90 else {})
+        q8, qs, k8, ks = quant(qd, kd, km, tensor_layout=layout, **shapes)
         qk_mult = D ** -0.5 * sa.LOG2E
+    gcode = GRAN_CODE[gran] + (2 if sm90 else 0)
     if pv == "fp8":
         v8, vs, _ = sa.per_channel_fp8(vd, tensor_layout=layout, smooth_v=False)
     else:
         v8, vs = sa.v_tile_half(vd, tensor_layout=layout), None
     o, lse = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout=layout, out_dtype=q.dtype, is_causal=causal,
                           q_offset=q_offset, kv_valid_len=kv_valid, num_splits=num_splits, return_lse=True,
-                          qk_mult=qk_mult, qk_quant_gran=gran)
+                          qk_mult=qk_mult, qk_quant_gran=gran, scale_layout="sm90" if sm90 else "sm89")
     torch.cuda.synchronize()
     if layout == "HND":
         o, q8, k8 = o.transpose(1, 2), q8.transpose(1, 2), k8.transpose(1, 2)
@@ -61,7 +65,7 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
     L = _lib.load()
     nkb = (Lk + 63) // 64
     v_kind = 0 if pv == "fp8" else (2 if q.dtype == torch.float16 else 1)
-    ns = num_splits if num_splits > 0 else L.qattn_fwd_ex_num_splits(B, Lq, Lk, Hq, v_kind, GRAN_CODE[gran])
+    ns = num_splits if num_splits > 0 else L.qattn_fwd_ex_num_splits(B, Lq, Lk, Hq, v_kind, gcode)
     ns = min(ns, nkb)
     tps = (nkb + ns - 1) // ns if ns > 1 else 0  # the GPU's KV-split schedule, restated on the CPU
     f16 = q.dtype == torch.float16
@@ -71,8 +75,8 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
     ref, ref_lse = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
                                     ks.cpu().numpy(), **vargs, causal=causal, q_offset=q_offset,
                                     kv_valid=kv_valid, want_lse=True, tiles_per_split=tps,
-                                    lazy_tau=KERNEL_LAZY_TAU, qk_mult=qk_mult, q_gran=GRAN_CODE[gran],
-                                    k_gran=GRAN_CODE[gran], lsum_rounded=KERNEL_LSUM_ROUNDED and pv == "fp8")
+                                    lazy_tau=KERNEL_LAZY_TAU, qk_mult=qk_mult, q_gran=gcode,
+                                    k_gran=gcode, lsum_rounded=KERNEL_LSUM_ROUNDED and pv == "fp8")
     c = cosine(og, ref)
     err = float(np.abs(og - ref).max())
     og_bhld = og.transpose(0, 2, 1, 3)  # rows in the LSE's [B, H, Lq] order
@@ -82,8 +86,8 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
     # the reference's own schedule (no split, eager running max) on the same quantized operands
     ref0, ref0_lse = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(),
                                       k8.contiguous().cpu().numpy(), ks.cpu().numpy(), **vargs, causal=causal,
-                                      q_offset=q_offset, kv_valid=kv_valid, qk_mult=qk_mult, q_gran=GRAN_CODE[gran],
-                                      k_gran=GRAN_CODE[gran], want_lse=True)
+                                      q_offset=q_offset, kv_valid=kv_valid, qk_mult=qk_mult, q_gran=gcode,
+                                      k_gran=gcode, want_lse=True)
     c0 = cosine(og, ref0)
     lerr0 = lse_max_err(lse.cpu().numpy(), ref0_lse, og_bhld)
     log(f"  vs reference-schedule quantized math: cosine={c0:.6f} max_abs={float(np.abs(og - ref0).max()):.4g} "
@@ -170,25 +174,60 @@ def test_sageattn_api_and_lse(oracle):
     assert cosine(o.float().cpu().numpy(), truth) >= COS_E2E
 
 
+SM90_CASES = {
+    # name: (B, Lq, Lk, Hq, Hkv, D, layout, causal, num_splits, gran, pv)
+    "thread_ragged": (1, 200, 333, 2, 2, 128, "NHD", False, 0, "per_thread", "fp8"),
+    "warp_ragged": (1, 200, 333, 2, 2, 128, "NHD", False, 0, "per_warp", "fp8"),
+    "thread_short_q": (2, 40, 300, 2, 1, 128, "HND", False, 0, "per_thread", "fp8"),   # table < 128 rows
+    "warp_causal": (1, 300, 300, 2, 2, 128, "NHD", True, 0, "per_warp", "fp8"),
+    "thread_split": (1, 130, 2100, 2, 2, 128, "NHD", False, 3, "per_thread", "fp8"),
+    "thread_d64": (1, 500, 700, 2, 2, 64, "NHD", False, 0, "per_thread", "fp8"),
+    "thread_fp16_pv": (1, 300, 400, 4, 2, 128, "NHD", False, 0, "per_thread", "fp16"),
+    "warp_many_blocks": (2, 1000, 1200, 4, 2, 128, "NHD", False, 0, "per_warp", "fp8"),
+}
+
+
+@pytest.mark.parametrize("case", sorted(SM90_CASES))
+def test_sm90_scale_tables(oracle, case):
+    """qattn_fwd reading the sm90 entry's scale tables (64-row Q blocks of 16-row warps, 128-key K blocks;
+    sageattn2.py:1608-1624) against the oracle fed the same tables with q_gran / k_gran 4 or 5."""
+    B, Lq, Lk, Hq, Hkv, D, layout, causal, ns, gran, pv = SM90_CASES[case]
+    dt = torch.float16 if pv == "fp16" else torch.bfloat16
+    q, k, v = qkv(B, Lq, Lk, Hq, Hkv, D=D, seed=31, k_offset_std=0.5, dtype=dt)
+    _run_and_check(oracle, q, k, v, layout=layout, causal=causal, num_splits=ns, gran=gran, pv=pv, sm90=True)
+
+
 @pytest.mark.parametrize("gran", ["per_warp", "per_thread"])
-def test_sm90_entry_is_the_sm89_kernel(oracle, gran):
-    """sageattn_qk_int8_pv_fp8_cuda_sm90 runs the same gfx950 kernel and scale layout as the sm89 entry
-    (query scale blocks of 128 rows / 32-row warps, 64-key tiles), not the Hopper kernel's 64 / 16 / 128
-    layout (sageattn2.py:1611-1622): its output is the sm89 entry's, bit for bit, and within the
-    end-to-end tolerance of float64 attention; the two reference layouts group the quantization scales
-    differently, so the reference's two entries themselves differ by quantization noise of this size."""
+def test_sm90_entry(oracle, gran):
+    """sageattn_qk_int8_pv_fp8_cuda_sm90 is the sm90 pipeline of the reference (sageattn2.py:1579-1697):
+    K mean, the sm90-shape quantizers, V per channel without smoothing, attention on the sm90 tables.  Its
+    output equals those steps run one by one, bit for bit, and float64 attention to the end-to-end bound;
+    the LSE carries the q . k_mean correction.  "fp32" accumulation is refused as there."""
     dev = require_gpu()
     from telefuser_amd import sageattn2 as sa
 
+    log(f"sm90 entry {gran}")
     q, k, v = qkv(1, 300, 500, 2, 2, seed=11, k_offset_std=0.5)
-    args = (q.to(dev), k.to(dev), v.to(dev))
-    kw = dict(tensor_layout="NHD", qk_quant_gran=gran, pv_accum_dtype="fp32+fp32")
-    o89 = sa.sageattn_qk_int8_pv_fp8_cuda(*args, **kw)
-    o90 = sa.sageattn_qk_int8_pv_fp8_cuda_sm90(*args, **kw)
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    o90, lse = sa.sageattn_qk_int8_pv_fp8_cuda_sm90(qd, kd, vd, tensor_layout="NHD", qk_quant_gran=gran,
+                                                    return_lse=True)
+    km = sa.k_mean(kd, "NHD")
+    shapes = dict(BLKQ=64, WARPQ=16, BLKK=128, **(dict(WARPK=128) if gran == "per_thread" else {}))
+    quant = sa.per_thread_int8 if gran == "per_thread" else sa.per_warp_int8
+    q8, qs, k8, ks = quant(qd, kd, km, tensor_layout="NHD", **shapes)
+    v8, vs, _ = sa.per_channel_fp8(vd, tensor_layout="NHD", smooth_v=False)
+    o = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout="NHD", out_dtype=q.dtype, qk_mult=128 ** -0.5 * LOG2E,
+                     qk_quant_gran=gran, scale_layout="sm90")
     torch.cuda.synchronize()
-    assert torch.equal(o89, o90)
+    assert torch.equal(o90, o)
     truth = oracle.attn_fp64(bf16_bits(q), bf16_bits(k), bf16_bits(v), 128 ** -0.5)
     assert cosine(o90.float().cpu().numpy(), truth) >= COS_E2E
+    # natural-log LSE of the unsmoothed logits, against float64
+    s = torch.einsum("bqhd,bkhd->bhqk", q.double(), k.double()) * 128 ** -0.5
+    lse_ref = torch.logsumexp(s, dim=-1)
+    assert (lse.double().cpu() - lse_ref).abs().max().item() < 0.1
+    with pytest.raises(NotImplementedError):
+        sa.sageattn_qk_int8_pv_fp8_cuda_sm90(qd, kd, vd, pv_accum_dtype="fp32")
 
 
 @pytest.mark.parametrize("case", ["ragged", "gqa_hnd_padding", "causal_offset", "split", "per_thread",

@@ -96,6 +96,53 @@ def test_per_thread_and_per_warp_quant_bit_exact(oracle, B, Lq, Lk, Hq, Hkv, lay
     assert np.array_equal(k8.cpu().numpy(), ok8)
 
 
+@pytest.mark.parametrize("B,Lq,Lk,Hq,Hkv,layout,dtype,D", [
+    (1, 1024, 1024, 2, 2, "NHD", torch.bfloat16, 128),
+    (2, 1000, 777, 4, 2, "NHD", torch.bfloat16, 128),   # ragged: empty trailing 16-row warps, partial K blocks
+    (1, 40, 130, 3, 3, "HND", torch.bfloat16, 128),     # one 64-row Q block
+    (1, 517, 333, 2, 1, "NHD", torch.float16, 128),
+    (2, 1000, 777, 4, 2, "NHD", torch.bfloat16, 64),
+    (1, 300, 130, 3, 3, "HND", torch.float16, 64),
+])
+def test_sm90_per_thread_and_per_warp_quant_bit_exact(oracle, B, Lq, Lk, Hq, Hkv, layout, dtype, D):
+    """The sm90 entry's quantizer shapes (sageattn2.py:1608-1624): per_thread_int8(BLKQ=64, WARPQ=16,
+    BLKK=128, WARPK=128) and per_warp_int8(BLKQ=64, WARPQ=16, BLKK=128)."""
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    log(f"sm90 per_thread/per_warp quant B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} D={D} {layout} {dtype}")
+    q, k, _ = qkv(B, Lq, Lk, Hq, Hkv, D=D, seed=104, k_offset_std=0.5, dtype=dtype)
+    if layout == "HND":
+        q, k = q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
+    qd, kd = q.to(dev), k.to(dev)
+    km = sa.k_mean(kd, layout)
+    f16 = dtype == torch.float16
+    kmb = _as_bits(km)
+    q8, qs, k8, ks = sa.per_thread_int8(qd, kd, km, BLKQ=64, WARPQ=16, BLKK=128, WARPK=128, tensor_layout=layout)
+    torch.cuda.synchronize()
+    oq8, oqs = oracle.quant_per_thread_int8(_as_bits(q), layout=layout, is_fp16=f16, sm90=True)
+    ok8, oks = oracle.quant_per_thread_int8(_as_bits(k), km_bits=kmb, is_key=True, layout=layout, is_fp16=f16,
+                                            sm90=True)
+    assert qs.shape[-1] == (Lq + 63) // 64 * 32 and ks.shape[-1] == (Lk + 127) // 128 * 4
+    assert np.array_equal(qs.cpu().numpy(), oqs)
+    assert np.array_equal(ks.cpu().numpy(), oks)
+    assert np.array_equal(q8.cpu().numpy(), oq8)
+    assert np.array_equal(k8.cpu().numpy(), ok8)
+    # per warp: QuantInt8Kernel over 16-row blocks, padded to 4 per 64-row block; K over 128-row blocks
+    q8, qs, k8, ks = sa.per_warp_int8(qd, kd, km, BLKQ=64, WARPQ=16, BLKK=128, tensor_layout=layout)
+    torch.cuda.synchronize()
+    oq8, oqs = oracle.quant_per_block_int8(_as_bits(q), blk=16, layout=layout, is_fp16=f16)
+    ok8, oks = oracle.quant_per_block_int8(_as_bits(k), km_bits=kmb, blk=128, layout=layout, is_fp16=f16)
+    n16 = oqs.shape[-1]
+    qs = qs.cpu().numpy()
+    assert qs.shape[-1] == (Lq + 63) // 64 * 4
+    assert np.array_equal(qs[..., :n16], oqs)
+    assert (qs[..., n16:] == np.float32(np.float32(1e-7) / np.float32(127.0))).all()
+    assert np.array_equal(ks.cpu().numpy(), oks)
+    assert np.array_equal(q8.cpu().numpy(), oq8)
+    assert np.array_equal(k8.cpu().numpy(), ok8)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_quant_nan_and_inf_inputs_match_oracle(oracle, dtype):
     """NaN elements quantize to 0 and drop out of the block maximum (cvt.rni.sat.s8 and fmaxf semantics); an

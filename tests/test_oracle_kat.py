@@ -510,24 +510,32 @@ def test_per_thread_zero_rows_and_half_away(oracle):
     assert q8[0, 1, 0, 0] == 127 and q8[0, 1, 0, 1] == -127 and q8[0, 1, 0, 2] == int(np.trunc(t + 0.5))
 
 
-@pytest.mark.parametrize("L,is_key", [(300, False), (300, True), (1000, True), (129, False)])
-def test_per_thread_random_matches_numpy_restatement(oracle, L, is_key):
-    """Vectorised float32 numpy version with the class mapping built by reshapes (not index formulas)."""
+@pytest.mark.parametrize("L,is_key,sm90", [(300, False, False), (300, True, False), (1000, True, False),
+                                           (129, False, False), (300, False, True), (300, True, True),
+                                           (1000, True, True), (129, False, True), (40, False, True)])
+def test_per_thread_random_matches_numpy_restatement(oracle, L, is_key, sm90):
+    """Vectorised float32 numpy version with the class mapping built by reshapes (not index formulas).
+    sm90: 16-row query warp blocks in 64-row CTA blocks, 128-row key blocks (sageattn2.py:1614-1624)."""
     g = torch.Generator().manual_seed(L)
     x = (torch.randn((2, L, 3, 128), generator=g) * 2).to(torch.bfloat16)
     km = (torch.randn((2, 1, 3, 128), generator=g)).to(torch.bfloat16) if is_key else None
     xd = (x - km) if is_key else x  # torch bf16 op, as the reference wrapper does
-    q8, sc = oracle.quant_per_thread_int8(bf16_bits(x), None if km is None else bf16_bits(km[:, 0]), is_key=is_key)
+    q8, sc = oracle.quant_per_thread_int8(bf16_bits(x), None if km is None else bf16_bits(km[:, 0]), is_key=is_key,
+                                          sm90=sm90)
     xf = xd.float().numpy()
-    blk = 64 if is_key else 32
-    nb = -(-L // 64) if is_key else -(-L // 128) * 4
+    if sm90:
+        blk = 128 if is_key else 16
+        nb = -(-L // 128) if is_key else -(-L // 64) * 4
+    else:
+        blk = 64 if is_key else 32
+        nb = -(-L // 64) if is_key else -(-L // 128) * 4
     pad = np.zeros((2, nb * blk, 3, 128), np.float32)
     pad[:, :L] = xf
-    if is_key:  # [b, n, j(8), cls(4), pair(2), h, d]
-        v = pad.reshape(2, nb, 8, 4, 2, 3, 128)
+    if is_key:  # [b, n, j(blk/8), cls(4), pair(2), h, d]
+        v = pad.reshape(2, nb, blk // 8, 4, 2, 3, 128)
         amax = np.abs(v).max(axis=(2, 4, 6))                 # [b, n, cls, h]
-    else:       # [b, n, j(4), cls(8), h, d]
-        v = pad.reshape(2, nb, 4, 8, 3, 128)
+    else:       # [b, n, j(blk/8), cls(8), h, d]
+        v = pad.reshape(2, nb, blk // 8, 8, 3, 128)
         amax = np.abs(v).max(axis=(2, 5))
     scale = (amax / np.float32(127.0) + np.float32(1e-7)).astype(np.float32)
     want_sc = scale.transpose(0, 3, 1, 2).reshape(2, 3, -1)
@@ -573,6 +581,89 @@ def test_attention_oracle_granularity_indexing(oracle):
     kscale[sel] *= 0.25
     kf = k8[0, :, 0].astype(np.float64) * kscale[:, None]
     s = qf @ kf.T
+    p = np.exp2(s - s.max(axis=1, keepdims=True))
+    vf = oracle.e4m3_to_f32(v8[0, 0, :, :300]).T.astype(np.float64) * vs[0, 0][None, :]
+    ref = (p @ vf) / p.sum(axis=1, keepdims=True)
+    assert cosine(o3[0, :, 0], ref) > 0.9995
+
+
+def test_sm90_per_thread_tables_refine_sm89(oracle):
+    """The sm89 and sm90 per-thread tables partition the same rows into nested cells: an sm89 query cell
+    (32-row warp, class c) is the union of the sm90 cells (two 16-row warps, class c), and an sm90 key
+    cell (128-row block, class c) the union of two sm89 ones (64-row blocks).  scale = amax / 127 + 1e-7
+    is monotone in amax, so the coarser cell's scale is the maximum of its parts' scales exactly."""
+    g = torch.Generator().manual_seed(5)
+    L = 333
+    x = (torch.randn((1, L, 2, 128), generator=g) * torch.linspace(0.2, 3.0, L)[None, :, None, None])
+    xb = bf16_bits(x.to(torch.bfloat16))
+    _, q89 = oracle.quant_per_thread_int8(xb)
+    _, q90 = oracle.quant_per_thread_int8(xb, sm90=True)
+    _, k89 = oracle.quant_per_thread_int8(xb, is_key=True)
+    _, k90 = oracle.quant_per_thread_int8(xb, is_key=True, sm90=True)
+    assert q89.shape == (1, 2, 3 * 32) and q90.shape == (1, 2, 6 * 32)
+    assert k89.shape == (1, 2, 6 * 4) and k90.shape == (1, 2, 3 * 4)
+    q90w = q90.reshape(1, 2, -1, 2, 8)                     # [b, h, 32-row warp, half, class]
+    assert np.array_equal(q89.reshape(1, 2, -1, 8), q90w.max(axis=3))
+    k89b = k89.reshape(1, 2, -1, 2, 4)                     # [b, h, 128-row block, half, class]
+    assert np.array_equal(k90.reshape(1, 2, -1, 4), k89b.max(axis=3))
+
+
+def test_attention_oracle_sm90_indexing(oracle):
+    """q_gran / k_gran 4, 5 (the sm90 tables): scale tables that give every row the same scale as an sm89
+    table give the same O, and a change in one sm90 cell touches exactly the rows / keys of that cell."""
+    q, k, v = qkv(1, 200, 300, 2, 1, seed=12)
+    qb, kb, vb = bf16_bits(q), bf16_bits(k), bf16_bits(v)
+    q8, _ = oracle.quant_per_thread_int8(qb)
+    k8, _ = oracle.quant_per_thread_int8(kb, is_key=True)
+    v8, vs = oracle.per_channel_fp8(vb)
+    rng = np.random.default_rng(3)
+    # per-row scale functions: query f(row // 32, row % 8), key g(key // 128, (key % 8) // 2)
+    fq = rng.uniform(0.01, 0.03, size=(2, 7, 8)).astype(np.float32)   # [head, row // 32, row % 8]
+    fk = rng.uniform(0.01, 0.03, size=(1, 3, 4)).astype(np.float32)   # [kv head, key // 128, class]
+    qs89 = np.zeros((1, 2, 2 * 32), np.float32)                        # ceil(200/128) = 2 blocks x 32
+    qs90 = np.zeros((1, 2, 4 * 32), np.float32)                        # ceil(200/64) = 4 blocks x 32
+    for w in range(8):                     # 32-row warps of the sm89 table
+        qs89[0, :, w * 8:(w + 1) * 8] = fq[:, min(w, 6)]
+    for w in range(16):                    # 16-row warps of the sm90 table
+        qs90[0, :, w * 8:(w + 1) * 8] = fq[:, min(w // 2, 6)]
+    ks89 = np.zeros((1, 1, 5 * 4), np.float32)                         # ceil(300/64) = 5 blocks x 4
+    ks90 = np.zeros((1, 1, 3 * 4), np.float32)                         # ceil(300/128) = 3 blocks x 4
+    for t in range(5):
+        ks89[0, :, t * 4:(t + 1) * 4] = fk[:, t // 2]
+    for t in range(3):
+        ks90[0, :, t * 4:(t + 1) * 4] = fk[:, t]
+    qk = 128 ** -0.5 * LOG2E
+    base = oracle.qattn_fwd(q8, qs89, k8, ks89, v8, vs, qk_mult=qk, q_gran=3, k_gran=3)
+    o = oracle.qattn_fwd(q8, qs90, k8, ks90, v8, vs, qk_mult=qk, q_gran=5, k_gran=5)
+    assert np.array_equal(o, base)
+    # per-warp: one scale per 16-row warp / 128-key block
+    qw89 = fq[None, :, [min(w, 6) for w in range(8)], 0]
+    qw90 = fq[None, :, [min(w // 2, 6) for w in range(16)], 0]
+    kw89 = fk[None, :, [t // 2 for t in range(5)], 0]
+    kw90 = fk[None, :, :, 0]
+    base_w = oracle.qattn_fwd(q8, np.ascontiguousarray(qw89), k8, np.ascontiguousarray(kw89), v8, vs, qk_mult=qk,
+                              q_gran=2, k_gran=2)
+    o_w = oracle.qattn_fwd(q8, np.ascontiguousarray(qw90), k8, np.ascontiguousarray(kw90), v8, vs, qk_mult=qk,
+                           q_gran=4, k_gran=4)
+    assert np.array_equal(o_w, base_w)
+    # one sm90 query cell: 16-row warp 3, class 5 = rows 53, 61 of head 1
+    qs2 = qs90.copy()
+    qs2[0, 1, 3 * 8 + 5] *= 2.0
+    o2 = oracle.qattn_fwd(q8, qs2, k8, ks90, v8, vs, qk_mult=qk, q_gran=5, k_gran=5)
+    changed = np.nonzero(np.abs(o2 - o).max(axis=-1) > 0)
+    assert sorted(set(zip(changed[1].tolist(), changed[2].tolist()))) == [(53, 1), (61, 1)]
+    # one sm90 key cell: 128-key block 1, class 3 = keys 128 + 8j + 6, 128 + 8j + 7: the logits of
+    # exactly those keys scale (against a float64 softmax over the dequantized logits)
+    ks2 = ks90.copy()
+    ks2[0, 0, 4 + 3] *= 0.25
+    o3 = oracle.qattn_fwd(q8, qs90, k8, ks2, v8, vs, qk_mult=qk, q_gran=5, k_gran=5)
+    rows = np.arange(200)
+    qrow_scale = qs90[0, 0][(rows // 16) * 8 + rows % 8].astype(np.float64)
+    keys = np.arange(300)
+    kscale = fk[0][keys // 128, (keys % 8) // 2].astype(np.float64)
+    kscale[[128 + 8 * j + 6 + e for j in range(16) for e in range(2)]] *= 0.25
+    s = (q8[0, :, 0].astype(np.float64) * qrow_scale[:, None]) @ (k8[0, :, 0].astype(np.float64)
+                                                                * kscale[:, None]).T * qk
     p = np.exp2(s - s.max(axis=1, keepdims=True))
     vf = oracle.e4m3_to_f32(v8[0, 0, :, :300]).T.astype(np.float64) * vs[0, 0][None, :]
     ref = (p @ vf) / p.sum(axis=1, keepdims=True)
