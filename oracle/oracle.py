@@ -44,7 +44,7 @@ def lib():
                                             vp]
         L.oq_qattn_fwd.argtypes = [vp, i64, i64, i64, vp, i64, vp, i64, i64, i64, vp, i64, vp, i64, vp, vp, i32,
                                    i64, i64, i64, i64, i64, i64, i64, i64, i64, f64, i32, i32, i64, vp, i64, i64,
-                                   i64, i64, f64, i32, i32, i32, vp, i64, i64, vp, i32, vp, vp]
+                                   i64, i64, f64, i32, i32, i32, vp, i64, i64, vp, i32, i32, vp, vp]
         L.oq_norm_rope.argtypes = [vp, i32, i64, i64, i64, i64, vp, vp, vp, f32, vp]
         L.oq_quant_per_thread_int8.argtypes = [vp, i32, i64, i64, i64, i64, i64, i64, i64, vp, i64, i64, i32, vp,
                                                i64, i64, i64, vp]
@@ -170,7 +170,7 @@ def per_channel_fp8(v_bits, scale_max=448.0, layout="NHD", is_fp16=False, pad=64
 def qattn_fwd(q8, q_scale, k8, k_scale, v8=None, v_scale=None, vh_bits=None, *, blkq=128, blkk=64,
               qk_mult=1.0, pv_mode=0, causal=False, q_offset=0, kv_valid=None, is_fp16=False, heads=None,
               qrows_limit=0, want_lse=False, tiles_per_split=0, lazy_tau=-1.0, lsum_rounded=False, q_gran=1,
-              k_gran=1, tile_mask=None, v_mean=None, pv_f16_tile=False):
+              k_gran=1, tile_mask=None, v_mean=None, pv_f16_tile=False, p_linear=False):
     """Quantized attention in the reference's tile order.  q8/k8 NHD int8; returns fp32 O NHD
     (and log2-domain LSE [B, Hq, Lq] when want_lse).  lazy_tau >= 0 / tiles_per_split > 0 restate the
     device kernel's lazy running-max rule / KV-split schedule and lsum_rounded its row sum over the
@@ -178,7 +178,9 @@ def qattn_fwd(q8, q_scale, k8, k_scale, v8=None, v_scale=None, vh_bits=None, *, 
     (1 per block, 2 per warp, 3 per thread) - see oq_qattn_fwd.  tile_mask: int8 [B, Hkv, ceil(Lq/128),
     ceil(Lk/64)] block-sparse mask (0 = skip the key tile for that query block).  v_mean: fp32 [B, Hkv, D]
     added to the output (smoothed V).  pv_f16_tile: each tile's P.V summed as two 32-key fp16 MMAs before it
-    joins the fp32 O (the reference's "fp32+fp16" accumulation)."""
+    joins the fp32 O (the reference's "fp32+fp16" accumulation).  p_linear (FP8 P.V only): P formed as the device
+    kernels form it, the e4m3 byte RNE(8 (s - m - 0.057539) + 56) clamped to [0, 255], instead of e4m3(exp2(s - m))
+    (see oq_qattn_fwd)."""
     q8 = np.ascontiguousarray(q8)
     k8 = np.ascontiguousarray(k8)
     B, Lq, Hq, D = q8.shape
@@ -208,7 +210,7 @@ def qattn_fwd(q8, q_scale, k8, k_scale, v8=None, v_scale=None, vh_bits=None, *, 
                        h1, int(qrows_limit), int(tiles_per_split), float(lazy_tau), int(lsum_rounded), int(q_gran),
                        int(k_gran), _p(tm), tm_s1, tm_s2,
                        _p(None if v_mean is None else np.ascontiguousarray(v_mean, dtype=np.float32)),
-                       int(bool(pv_f16_tile)), _p(out), _p(lse))
+                       int(bool(pv_f16_tile)), int(bool(p_linear)), _p(out), _p(lse))
     return (out, lse) if want_lse else out
 
 

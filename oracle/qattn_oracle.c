@@ -455,12 +455,27 @@ void oq_per_channel_fp8(const uint16_t* in, int is_fp16, int64_t B, int64_t L, i
  * lazy_tau < 0 is the reference rule m = max(m, rowmax(s) - offset) of update_mdo.
  * lsum_rounded != 0 sums the rounded P (what the device kernel's MFMA row sum computes) instead of
  * the unrounded p the reference's accumulate_d sums.
+ * p_linear != 0 (pv_mode 0) restates the device kernels' P: oq_p_linear_byte(s - m) read as e4m3, no exp2.
  * tiles_per_split > 0 restates the KV-split schedule: every run of tiles_per_split key tiles keeps its
  * own (m, d, O) and the partials are merged at the end with weights exp2(m_s - max m).
  *
  * Loop order: (b, h, 128-row query block) x key tile, with the tile's V decoded once into floats, so the
  * same code doubles as the timed CPU baseline.
  */
+/*
+ * The FP8 P of the device kernels (attn.hip p_e4m3_x4): the byte k = RNE(8 (x - 0.057539) + 56), clamped to
+ * [0, 255] (v_cvt_pk_u8_f32), taken as an e4m3 encoding.  For y = x - 0.057539 the byte holds exponent
+ * field floor(y) + 7 and mantissa round(8 frac(y)): 2^floor(y) (1 + frac(y)) on the e4m3 grid, the linear
+ * interpolation of 2^y between powers of two (Schraudolph, Neural Computation 11, 1999).  0.057539 =
+ * log2(1.040685), the mean of (1 + f) / 2^f over f in [0, 1).
+ */
+static uint8_t oq_p_linear_byte(double x) {
+  const double u = 8.0 * (x - 0.057539) + 56.0;
+  if (!(u > 0.0)) return 0;
+  if (u >= 255.0) return 255;
+  return (uint8_t)nearbyint(u); /* default rounding mode: ties to even */
+}
+
 void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const float* q_scale, int64_t blkq,
                   const int8_t* k8, int64_t ksb, int64_t ksl, int64_t ksh, const float* k_scale, int64_t blkk,
                   const uint8_t* v8, int64_t Lpad, const float* v_scale, const uint16_t* vh, int is_fp16,
@@ -468,7 +483,7 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
                   int64_t Hkv, int64_t D, double qk_mult, int pv_mode, int causal, int64_t q_offset,
                   const int32_t* kv_valid, int64_t h_begin, int64_t h_end, int64_t qrows_limit, int64_t tiles_per_split,
                   double lazy_tau, int lsum_rounded, int q_gran, int k_gran, const int8_t* tile_mask, int64_t tm_s1,
-                  int64_t tm_s2, const float* v_mean, int pv_f16_tile, float* out, float* lse2) {
+                  int64_t tm_s2, const float* v_mean, int pv_f16_tile, int p_linear, float* out, float* lse2) {
   const int64_t RB = 128; /* query rows per work item */
   int64_t nQB = (Lq + blkq - 1) / blkq;
   int64_t nKB = (Lk + blkk - 1) / blkk;
@@ -570,6 +585,7 @@ void oq_qattn_fwd(const int8_t* q8, int64_t qsb, int64_t qsl, int64_t qsh, const
                 double pr = pv_mode == 0 ? oq_e4m3_to_f32(oq_f32_to_e4m3((float)p))
                             : is_fp16   ? oq_f16_to_f32(oq_f32_to_f16((float)p))
                                         : oq_bf16_to_f32(oq_f32_to_bf16((float)p));
+                if (pv_mode == 0 && p_linear) pr = oq_e4m3_to_f32(oq_p_linear_byte(s[j - k0] - m_new));
                 dsum[r] += lsum_rounded ? pr : p;
                 const double* vr = vt + (j - k0) * D;
                 if (pv_f16_tile) {

@@ -19,6 +19,9 @@ LOG2E = 1.44269504
 KERNEL_LAZY_TAU = 3.0  # lazy running-max threshold of the FP8 / half attention kernels (kLazyTau in attn.hip)
 # FP8 P.V kernels sum the e4m3-rounded P on the matrix pipe (row_sum_mfma in attn.hip); the oracle restates it
 KERNEL_LSUM_ROUNDED = True
+# FP8 P.V kernels form P without exp2: the e4m3 byte RNE(8 (s - m - 0.057539) + 56) (p_e4m3_x4 in attn.hip);
+# the kernel-schedule oracle restates it (p_linear), the reference-schedule oracle keeps e4m3(exp2(s - m))
+KERNEL_P_LINEAR = True
 LSE_ROUNDED_SUM_BOUND = 0.0931  # log2(16/15): bound of the rounded-vs-unrounded row-sum LSE difference
 
 
@@ -76,7 +79,8 @@ def _run_and_check(oracle, q, k, v, *, layout="NHD", causal=False, kv_valid=None
                                     ks.cpu().numpy(), **vargs, causal=causal, q_offset=q_offset,
                                     kv_valid=kv_valid, want_lse=True, tiles_per_split=tps,
                                     lazy_tau=KERNEL_LAZY_TAU, qk_mult=qk_mult, q_gran=gcode,
-                                    k_gran=gcode, lsum_rounded=KERNEL_LSUM_ROUNDED and pv == "fp8")
+                                    k_gran=gcode, lsum_rounded=KERNEL_LSUM_ROUNDED and pv == "fp8",
+                                    p_linear=KERNEL_P_LINEAR)
     c = cosine(og, ref)
     err = float(np.abs(og - ref).max())
     og_bhld = og.transpose(0, 2, 1, 3)  # rows in the LSE's [B, H, Lq] order
@@ -576,7 +580,8 @@ def test_multi_block_workgroups(oracle, case):
     ref, ref_lse = oracle.qattn_fwd(pick(q8), qs[:1, 7:8].cpu().numpy(), pick(k8), ks[:1, 7:8].cpu().numpy(),
                                     v8=untile_v(v8[:1, 7:8]), v_scale=vs[:1, 7:8].cpu().numpy(),
                                     kv_valid=kv_valid[:1], want_lse=True, lazy_tau=KERNEL_LAZY_TAU, qk_mult=qk_mult,
-                                    q_gran=GRAN_CODE[gran], k_gran=GRAN_CODE[gran], lsum_rounded=KERNEL_LSUM_ROUNDED)
+                                    q_gran=GRAN_CODE[gran], k_gran=GRAN_CODE[gran], lsum_rounded=KERNEL_LSUM_ROUNDED,
+                                    p_linear=KERNEL_P_LINEAR)
     og = pick(o.float())
     c = cosine(og, ref)
     log(f"  head 7 vs quantized oracle: cosine={c:.6f} max_abs={float(np.abs(og - ref).max()):.4g}")
@@ -656,7 +661,7 @@ def test_resident_kernel_matches(oracle, case):
     if case == "padding":
         ref = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
                                ks.cpu().numpy(), v8=untile_v(v8), v_scale=vs.cpu().numpy(), kv_valid=kv_valid,
-                               lazy_tau=KERNEL_LAZY_TAU)
+                               lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED, p_linear=KERNEL_P_LINEAR)
         c = cosine(o1.float().cpu().numpy(), ref)
         log(f"  resident padding cos_oracle={c:.6f}")
         assert c >= COS_KERNEL
@@ -753,7 +758,8 @@ def test_pingpong_kernel_matches(oracle, case):
                                         v_mean=None if vm is None else vm.cpu().numpy(), qk_mult=qk_mult,
                                         q_gran=GRAN_CODE[gran], k_gran=GRAN_CODE[gran],
                                         tiles_per_split=(nkb + ns - 1) // ns if ns > 1 else 0,
-                                        lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED)
+                                        lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED,
+                               p_linear=KERNEL_P_LINEAR)
         og = o1.float().cpu().numpy()
         c = cosine(og, ref)
         lerr = lse_max_err(l1.cpu().numpy(), ref_lse, og.transpose(0, 2, 1, 3))
@@ -763,7 +769,8 @@ def test_pingpong_kernel_matches(oracle, case):
     if case == "long":
         ref = oracle.qattn_fwd(q8.contiguous().cpu().numpy(), qs.cpu().numpy(), k8.contiguous().cpu().numpy(),
                                ks.cpu().numpy(), v8=untile_v(v8), v_scale=vs.cpu().numpy(),
-                               lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED)
+                               lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED,
+                               p_linear=KERNEL_P_LINEAR)
         c = cosine(o1.float().cpu().numpy(), ref)
         log(f"  ping-pong kernel vs quantized oracle: cosine={c:.6f}")
         assert c >= COS_KERNEL
@@ -822,7 +829,8 @@ def test_full_size_configs(oracle, name, call):
         qsh = qs[:, h:h + 1].cpu().numpy()
         nqb = qsh.shape[-1] // qpb
         kw = dict(v8=np.ascontiguousarray(v8_plain[:, h:h + 1]), v_scale=vs[:, h:h + 1].cpu().numpy(),
-                  kv_valid=kvv, lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED, tiles_per_split=tps,
+                  kv_valid=kvv, lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED, p_linear=KERNEL_P_LINEAR,
+                  tiles_per_split=tps,
                   qk_mult=qk_mult, q_gran=gran, k_gran=gran)
         k8h, ksh = k8[:, :, h:h + 1].contiguous().cpu().numpy(), ks[:, h:h + 1].cpu().numpy()
         ref_first = oracle.qattn_fwd(q8h[:, :128].contiguous().numpy(), qsh[..., :qpb].copy(), k8h, ksh, **kw)
@@ -873,7 +881,8 @@ def test_pv_accum_modes_and_smooth_v(oracle, mode):
     args = (q8.cpu().numpy(), qs.cpu().numpy(), k8.cpu().numpy(), ks.cpu().numpy())
     kw = dict(v8=untile_v(v8), v_scale=vs.cpu().numpy(), qk_mult=128 ** -0.5 * LOG2E, q_gran=3, k_gran=3,
               v_mean=None if vm is None else vm.cpu().numpy())
-    ref_k = oracle.qattn_fwd(*args, **kw, lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED)
+    ref_k = oracle.qattn_fwd(*args, **kw, lazy_tau=KERNEL_LAZY_TAU, lsum_rounded=KERNEL_LSUM_ROUNDED,
+                               p_linear=KERNEL_P_LINEAR)
     ref_r = oracle.qattn_fwd(*args, **kw, pv_f16_tile=pv == "fp32+fp16")
     truth = oracle.attn_fp64(bf16_bits(q), bf16_bits(k), bf16_bits(v), 128 ** -0.5)
     ck, cr, ct = cosine(og, ref_k), cosine(og, ref_r), cosine(og, truth)

@@ -77,7 +77,8 @@ def test_cache_state_and_output(oracle, size, sink, n, local_attn, repeats):
             tps = ((size + 63) // 64 + ns - 1) // ns if ns > 1 else 0
             ref = oracle.qattn_fwd(q8.cpu().numpy(), qs.cpu().numpy(), cache.k8.cpu().numpy(),
                                    cache.k_scale.cpu().numpy(), v8=untile_v(cache.v8), v_scale=cache.v_scale.cpu().numpy(),
-                                   kv_valid=kv_valid, tiles_per_split=tps, lazy_tau=3.0, lsum_rounded=True)
+                                   kv_valid=kv_valid, tiles_per_split=tps, lazy_tau=3.0, lsum_rounded=True,
+                                   p_linear=True)
             ck = cosine(og, ref)
             log(f"  local_end={le} head={cache.head} cos_truth={ct:.6f} cos_oracle={ck:.6f}")
             assert ct >= COS_E2E

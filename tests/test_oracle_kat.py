@@ -464,6 +464,63 @@ def test_rounded_row_sum_mode(oracle):
     assert np.abs(o_ref[0, :, 0] - exact_v[None]).max() > 1e-4  # the reference's normaliser differs
 
 
+def _one_row_operands(acc, qk_mult=1.0):
+    """One query row whose logits are exactly acc[j] * qk_mult (q = e0, k_j = acc[j] e0, unit scales) and
+    a V that puts key j on channel j alone (e4m3 1.0), so O[j] = P_j / sum(P)."""
+    n = len(acc)
+    q8 = np.zeros((1, 1, 1, 128), np.int8)
+    q8[0, 0, 0, 0] = 1
+    k8 = np.zeros((1, n, 1, 128), np.int8)
+    k8[0, :, 0, 0] = acc
+    qs = np.ones((1, 1, 1), np.float32)
+    ks = np.ones((1, 1, (n + 63) // 64), np.float32)
+    v8 = np.zeros((1, 1, 128, 64 * ((n + 63) // 64)), np.uint8)
+    for j in range(n):
+        v8[0, 0, j, j] = 0x38  # e4m3 1.0
+    vs = np.ones((1, 1, 128), np.float32)
+    return q8, qs, k8, ks, v8, vs
+
+
+def test_p_linear_known_answers(oracle):
+    """p_linear: P is the e4m3 byte RNE(8 (x - 0.057539) + 56), x = s - m.  With the reference's max rule the
+    top logit sits at x = 8.807: byte 126 = 448; one below, 118 = 224; 14 below, 8 * (-5.193 - 0.057539) + 56
+    = 13.996 -> 14 = 2^-6 * 1.75 (the smallest normal octave); 30 below, a negative byte clamps to 0."""
+    q8, qs, k8, ks, v8, vs = _one_row_operands([100, 99, 86, 70])
+    o = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, lsum_rounded=True, p_linear=True)
+    p = np.array([448.0, 224.0, 2.0 ** -6 * 1.75, 0.0])
+    assert np.array_equal(o[0, 0, 0, :4], (p / p.sum()).astype(np.float32))
+    # without p_linear the same logits give e4m3(exp2(x)): 2^8.807 = 447.9 -> 448, 2^7.807 = 223.96 -> 224,
+    # 2^-5.193 = 0.02732 -> 2^-6 * 1.75 as well: the two agree on these logits
+    o_ref = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, lsum_rounded=True)
+    assert np.array_equal(o_ref[0, 0, 0, :4], o[0, 0, 0, :4])
+    # a logit 0.5 below the top: exp2 gives 2^8.307 = 316.7 -> e4m3 320; the linear form 8 * (8.307 -
+    # 0.057539) + 56 = 121.996 -> byte 122 = 2^8 * 1.25 = 320 too; 0.25 below: 2^8.557 = 376.6 -> 384,
+    # linear 124 = 384
+    q8, qs, k8, ks, v8, vs = _one_row_operands([100, 98, 99])
+    o = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, qk_mult=0.25, lsum_rounded=True, p_linear=True)
+    p = np.array([448.0, 320.0, 384.0])
+    assert np.allclose(o[0, 0, 0, :3], p / p.sum(), rtol=0, atol=1e-7)
+
+
+def test_p_linear_is_unbiased_and_close_to_exp2(oracle):
+    """Over logits whose fractional parts cover [0, 1) evenly the linear P is exp2(x) on average within 1 %
+    (the shift 0.057539 = log2(1.040685) removes the mean of (1 + f) / 2^f), its sum (weighted toward the top
+    of the octave) within 2 %, and no single P leaves [-8.3 %, +8.7 %] of exp2(x) (linear interpolation error
+    -4.0 / +4.4 % and the e4m3 half step of up to 6.25 %)."""
+    acc = np.arange(64)  # one key tile (one running max), x spanning one octave in 1/64 steps
+    q8, qs, k8, ks, v8, vs = _one_row_operands(acc)
+    o, lse = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, qk_mult=1.0 / 64, lsum_rounded=True, p_linear=True,
+                              want_lse=True)
+    _, lse_exp = oracle.qattn_fwd(q8, qs, k8, ks, v8, vs, qk_mult=1.0 / 64, want_lse=True)  # unrounded exp2
+    assert abs(float(lse[0, 0, 0]) - float(lse_exp[0, 0, 0])) < np.log2(1.02)
+    s_log = acc / 64.0
+    m = s_log.max() - 8.807                      # the reference's running max
+    p = o[0, 0, 0, :64].astype(np.float64) * 2.0 ** (float(lse[0, 0, 0]) - m)  # O_j * sum(P)
+    rel = p / 2.0 ** (s_log - m)
+    assert rel.min() > 1 - 0.083 and rel.max() < 1 + 0.087
+    assert abs(rel.mean() - 1) < 0.01
+
+
 # ------------------------------------------------------------------------------------------------
 # per-thread quantizer (triton/quant_per_thread.py) and scale granularities of the attention oracle
 # ------------------------------------------------------------------------------------------------
