@@ -222,7 +222,8 @@ int qattn_v_tile_half(qattn_seq v, int dtype, int64_t B, int64_t L, int64_t H, i
  * statistics (K sum when smooth_k; V max |v|, or sum / max / min when smooth_v), one finalize (k_mean
  * [B, Hkv, D] in the input dtype, v_scale, v_mean), V to FP8 tiles (as qattn_per_channel_fp8_ex), and K then
  * Q to INT8 in one launch (qk_quant_gran 1: per block, Q times q_sm_scale = sm_scale * log2(e), CUDA
- * rounding; 2: per warp; 3: per thread, as qattn_quant_qk_per_warp_int8 / _per_thread_int8).  Outputs are
+ * rounding; 2: per warp; 3: per thread, as qattn_quant_qk_per_warp_int8 / _per_thread_int8; 4 / 5: per warp /
+ * per thread with the sm90 tables, as the *_ex quantizers with QATTN_SCALES_SM90).  Outputs are
  * bit-identical to qattn_seq_mean + the quantizer + qattn_per_channel_fp8_ex.  Replaces the quantization
  * block of sageattn_qk_int8_pv_fp8_cuda (tf-kernel/tf_kernel/sageattn2.py:1334-1383), which the reference
  * runs as separate kernels.  workspace: qattn_sage_quant_workspace_size bytes.

@@ -1315,9 +1315,13 @@ extern "C" int qattn_sage_quant(qattn_seq q, qattn_seq k, qattn_seq v, int dtype
                                 float* v_mean, void* workspace, size_t workspace_bytes, qattn_stream_t stream) {
   int rc;
   if ((rc = check_common(dtype, D, QATTN_QUANT_CUDA, 64))) return rc;
-  QATTN_REQUIRE(qk_quant_gran == 1 || qk_quant_gran == 2 || qk_quant_gran == 3, QATTN_ERR_ARG,
-                "qk_quant_gran must be 1 (per block), 2 (per warp) or 3 (per thread), got %d", qk_quant_gran);
+  QATTN_REQUIRE(qk_quant_gran >= 1 && qk_quant_gran <= 5, QATTN_ERR_ARG,
+                "qk_quant_gran must be 1 (per block), 2 (per warp), 3 (per thread), 4 (per warp, sm90 tables) or "
+                "5 (per thread, sm90 tables), got %d", qk_quant_gran);
   QATTN_REQUIRE(B > 0 && Lq > 0 && Lk > 0 && Hq > 0 && Hkv > 0, QATTN_ERR_SHAPE, "sage_quant needs non-empty input");
+  // the sm90 tables: 64-row Q blocks of 16-row warps, 128-row K blocks (as the *_ex quantizers)
+  const bool sm90 = qk_quant_gran >= 4;
+  if (sm90) qk_quant_gran -= 2;
   if ((rc = check_seq("q", q, 2)) || (rc = check_seq("k", k, 2)) || (rc = check_seq("v", v, 2)) ||
       (rc = check_seq("q_out", q_out, 1)) || (rc = check_seq("k_out", k_out, 1)))
     return rc;
@@ -1376,7 +1380,7 @@ extern "C" int qattn_sage_quant(qattn_seq q, qattn_seq k, qattn_seq v, int dtype
   const void* kmean_in = smooth_k ? k_mean : nullptr;
   {
     QuantJob& J = a.job[a.njobs++];
-    fill_job(J, k, k_out, B, Lk, Hkv, kmean_in, k_scale, 1.0f, 0, 64);
+    fill_job(J, k, k_out, B, Lk, Hkv, kmean_in, k_scale, 1.0f, 0, sm90 ? 128 : 64);
     if (qk_quant_gran == 3) {
       J.ncls = 4;
       J.cls_shift = 1;
@@ -1388,7 +1392,7 @@ extern "C" int qattn_sage_quant(qattn_seq q, qattn_seq k, qattn_seq v, int dtype
       fill_job(J, q, q_out, B, Lq, Hq, nullptr, q_scale, q_sm_scale, 1, 128);
     } else {
       fill_job(J, q, q_out, B, Lq, Hq, nullptr, q_scale, 1.0f, 0, 32);
-      warp_block_job(J, B);
+      warp_block_job(J, B, sm90 ? 16 : 32);
       if (qk_quant_gran == 3) {
         J.ncls = 8;
         J.cls_shift = 0;

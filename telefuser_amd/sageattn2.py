@@ -185,10 +185,12 @@ def per_channel_fp8(v: torch.Tensor, tensor_layout: str = "HND", scale_max: floa
 
 def sage_quant(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str = "HND",
                qk_quant_gran: str = "per_block", sm_scale: Optional[float] = None, smooth_k: bool = True,
-               scale_max: float = 448.0, smooth_v: bool = False):
+               scale_max: float = 448.0, smooth_v: bool = False, scale_layout: str = "sm89"):
     """The whole prologue of the INT8-QK / FP8-PV path in four launches (column passes of K and V,
     their finalize, V to FP8, K and Q to INT8): the same outputs, bit for bit, as k_mean + the
     per_block / per_warp / per_thread quantizer + per_channel_fp8 (CUDA quantizer variant).
+    ``scale_layout="sm90"`` (per_warp / per_thread only) gives the sm90 entry's tables, as per_warp_int8 /
+    per_thread_int8 with BLKQ=64, WARPQ=16, BLKK=128.
     Returns (q_int8, q_scale, k_int8, k_scale, km or None, v_fp8, v_scale, vm or None)."""
     L = _lib.load()
     if not (q.dtype == k.dtype == v.dtype):
@@ -196,17 +198,22 @@ def sage_quant(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout:
     gran = {"per_block": 1, "per_warp": 2, "per_thread": 3}.get(qk_quant_gran)
     if gran is None:
         raise ValueError(f"unknown qk_quant_gran {qk_quant_gran!r}")
+    if scale_layout not in ("sm89", "sm90"):
+        raise ValueError(f"scale_layout must be 'sm89' or 'sm90', got {scale_layout!r}")
+    sm90 = scale_layout == "sm90"
+    if sm90 and gran == 1:
+        raise ValueError("scale_layout='sm90' needs qk_quant_gran 'per_warp' or 'per_thread'")
     b, lq, hq, d = _dims(q, tensor_layout)
     _, lk, hkv, _ = _dims(k, tensor_layout)
     dev = q.device
-    nqb, nkb = (lq + 127) // 128, (lk + 63) // 64
+    nqb, nkb = _scale_blocks(lq, lk, sm90)
     q_int8 = torch.empty(q.shape, dtype=torch.int8, device=dev)
     k_int8 = torch.empty(k.shape, dtype=torch.int8, device=dev)
     q_per = {1: 1, 2: 4, 3: 32}[gran]
     q_scale = torch.empty((b, hq, nqb * q_per), dtype=torch.float32, device=dev)
     k_scale = torch.empty((b, hkv, nkb * (4 if gran == 3 else 1)), dtype=torch.float32, device=dev)
     km = torch.empty((b, hkv, d), dtype=k.dtype, device=dev) if smooth_k else None
-    lpad = nkb * 64
+    lpad = (lk + 63) // 64 * 64
     v_fp8 = torch.empty((b, hkv, d, lpad), dtype=torch.float8_e4m3fn, device=dev)
     v_scale = torch.empty((b, hkv, d), dtype=torch.float32, device=dev)
     vm = torch.empty((b, hkv, d), dtype=torch.float32, device=dev) if smooth_v else None
@@ -215,7 +222,7 @@ def sage_quant(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout:
         sm_scale = d ** -0.5
     _lib.check(L.qattn_sage_quant(
         _lib.seq(q, tensor_layout), _lib.seq(k, tensor_layout), _lib.seq(v, tensor_layout), _lib.dtype_code(q.dtype),
-        b, lq, lk, hq, hkv, d, gran, float(sm_scale * LOG2E), int(bool(smooth_k)), float(scale_max),
+        b, lq, lk, hq, hkv, d, gran + (2 if sm90 else 0), float(sm_scale * LOG2E), int(bool(smooth_k)), float(scale_max),
         int(bool(smooth_v)), _lib.seq(q_int8, tensor_layout), _lib.ptr(q_scale), _lib.seq(k_int8, tensor_layout),
         _lib.ptr(k_scale), _lib.ptr(km), _lib.ptr(v_fp8), lpad, _lib.ptr(v_scale), _lib.ptr(vm), _lib.ptr(ws),
         ws.numel(), _lib.stream_of(q)))
@@ -379,15 +386,11 @@ def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv
             smooth_v = False
         scale_max = 2.25 if pv_accum_dtype == "fp32+fp16" else 448.0
     if sm90:
-        # the sm90 entry's quantizers and tables (sageattn2.py:1579-1660): V without smoothing
-        km = k_mean(k, tensor_layout) if smooth_k else None
-        if qk_quant_gran == "per_thread":
-            q_int8, q_scale, k_int8, k_scale = per_thread_int8(q, k, km, BLKQ=64, WARPQ=16, BLKK=128, WARPK=128,
-                                                               tensor_layout=tensor_layout)
-        else:
-            q_int8, q_scale, k_int8, k_scale = per_warp_int8(q, k, km, BLKQ=64, WARPQ=16, BLKK=128,
-                                                             tensor_layout=tensor_layout)
-        v_fp8, v_scale, vm = per_channel_fp8(v, tensor_layout=tensor_layout, smooth_v=False)
+        # the sm90 entry's quantizers and tables (sageattn2.py:1579-1660, V without smoothing), fused as
+        # below: the same bits as k_mean + per_*_int8(BLKQ=64, WARPQ=16, BLKK=128) + per_channel_fp8
+        q_int8, q_scale, k_int8, k_scale, km, v_fp8, v_scale, vm = sage_quant(
+            q, k, v, tensor_layout=tensor_layout, qk_quant_gran=qk_quant_gran, sm_scale=sm_scale, smooth_k=smooth_k,
+            scale_max=448.0, smooth_v=False, scale_layout="sm90")
     elif pv == "fp8" and quant_variant == "cuda":
         # K mean, Q/K INT8 and V FP8 in one fused prologue (four launches)
         q_int8, q_scale, k_int8, k_scale, km, v_fp8, v_scale, vm = sage_quant(

@@ -267,6 +267,9 @@ def test_v_fp8_smooth_bit_exact(oracle, B, L, H, layout, dtype, scale_max):
     ("per_warp", True, False, 448.0, "NHD", torch.bfloat16, (1, 517, 333, 2, 1)),
     ("per_thread", True, False, 448.0, "HND", torch.bfloat16, (2, 700, 515, 2, 2)),
     ("per_thread", False, True, 2.25, "NHD", torch.float16, (1, 129, 65, 2, 2)),
+    ("per_warp_sm90", True, False, 448.0, "NHD", torch.bfloat16, (2, 1000, 777, 4, 2)),
+    ("per_thread_sm90", True, False, 448.0, "HND", torch.bfloat16, (1, 517, 333, 2, 1)),
+    ("per_thread_sm90", False, False, 448.0, "NHD", torch.float16, (1, 40, 130, 3, 3)),
 ])
 def test_sage_quant_matches_separate_calls(gran, smooth_k, smooth_v, scale_max, layout, dtype, shape):
     """The fused prologue (column passes of K and V in one launch, one finalize, V FP8, K then Q INT8 in one
@@ -282,15 +285,18 @@ def test_sage_quant_matches_separate_calls(gran, smooth_k, smooth_v, scale_max, 
     if layout == "HND":
         qd, kd, vd = (t.transpose(1, 2).contiguous() for t in (qd, kd, vd))
     sm = 128 ** -0.5
+    sm90 = gran.endswith("_sm90")
+    gran = gran.replace("_sm90", "")
     got = sa.sage_quant(qd, kd, vd, tensor_layout=layout, qk_quant_gran=gran, sm_scale=sm, smooth_k=smooth_k,
-                        scale_max=scale_max, smooth_v=smooth_v)
+                        scale_max=scale_max, smooth_v=smooth_v, scale_layout="sm90" if sm90 else "sm89")
     km = sa.k_mean(kd, layout) if smooth_k else None
+    shapes = dict(BLKQ=64, WARPQ=16, BLKK=128) if sm90 else {}
     if gran == "per_block":
         ref_qk = sa.per_block_int8(qd, kd, km, sm_scale=sm, tensor_layout=layout)
     elif gran == "per_warp":
-        ref_qk = sa.per_warp_int8(qd, kd, km, tensor_layout=layout)
+        ref_qk = sa.per_warp_int8(qd, kd, km, tensor_layout=layout, **shapes)
     else:
-        ref_qk = sa.per_thread_int8(qd, kd, km, tensor_layout=layout)
+        ref_qk = sa.per_thread_int8(qd, kd, km, tensor_layout=layout, **(dict(shapes, WARPK=128) if sm90 else {}))
     v8, vs, vm = sa.per_channel_fp8(vd, tensor_layout=layout, scale_max=scale_max, smooth_v=smooth_v)
     torch.cuda.synchronize()
     for name, a, b in zip(("q_int8", "q_scale", "k_int8", "k_scale"), got[:4], ref_qk):
