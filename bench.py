@@ -265,6 +265,24 @@ def _config_bench(name: str, calls: int = 5, warmup: int = 2) -> dict:
         res["algorithmic_bytes_per_launch"] = byts
     else:
         res["bound"] = "mfma"
+    # the same config through the entry TeleFuser's attention() calls for SAGE_ATTN_2_8_8 (per-thread scales,
+    # "fp32+fp32"; attention_impl.py:249-258): for key ranges of at most 512 it quantizes Q inside the
+    # resident kernel (qattn_fwd_q16)
+    def tf_call():
+        return sa.sageattn_qk_int8_pv_fp8_cuda(q, k, v, tensor_layout="NHD", qk_quant_gran="per_thread",
+                                               pv_accum_dtype="fp32+fp32", kv_valid_len=kvv)
+
+    for _ in range(warmup):
+        tf_call()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(calls):
+        tf_call()
+    torch.cuda.synchronize()
+    ms_tf = (time.perf_counter() - t0) * 1e3 / calls
+    res["telefuser_path"] = {"entry": "sageattn_qk_int8_pv_fp8_cuda(per_thread, fp32+fp32)",
+                             "ms_per_call": round(ms_tf, 4), "call_TOPS": round(ops / (ms_tf * 1e-3) / 1e12, 2),
+                             "q_quantized_in_attention": bool(L.qattn_fwd_q16_supported(cfg.Lk, cfg.D, 0))}
     del q, k, v
     torch.cuda.empty_cache()
     return res

@@ -107,6 +107,9 @@ def load() -> ctypes.CDLL:
                                            sz, vp]
     L.qattn_quant_qk_per_warp_int8.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, vp]
     L.qattn_quant_qk_per_thread_int8.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, vp]
+    L.qattn_fwd_q16_supported.argtypes = [i64, i64, i32]
+    L.qattn_fwd_q16_supported.restype = i32
+    L.qattn_fwd_q16.argtypes = [S, S, vp, vp, i64, vp, vp, S, i32, i64, i64, i64, i64, i64, i64, f32, i32, vp, vp, vp]
     L.qattn_quant_qk_per_warp_int8_ex.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, i32, vp]
     L.qattn_quant_qk_per_thread_int8_ex.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, i32,
                                                     vp]
@@ -155,7 +158,7 @@ def load() -> ctypes.CDLL:
                  "qattn_fwd_varlen"):
         getattr(L, name).restype = i32
     for name in ("qattn_row_rstd", "qattn_norm_rope_seq_mean", "qattn_norm_rope_quant_qk", "qattn_fwd_block_sparse", "qattn_quant_qk_per_warp_int8", "qattn_quant_qk_per_thread_int8", "qattn_fwd_ex",
-                 "qattn_quant_qk_per_warp_int8_ex", "qattn_quant_qk_per_thread_int8_ex",
+                 "qattn_quant_qk_per_warp_int8_ex", "qattn_quant_qk_per_thread_int8_ex", "qattn_fwd_q16",
                  "qattn_v_fp8_cache_update", "qattn_quant_per_block_int8", "qattn_quant_qk_per_block_int8", "qattn_seq_mean",
                  "qattn_per_channel_fp8", "qattn_fwd", "qattn_v_tile_half", "qattn_fwd_pv16"):
         getattr(L, name).restype = i32

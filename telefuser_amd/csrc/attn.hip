@@ -1228,7 +1228,13 @@ constexpr int kResMaxTiles = 8;
 constexpr int kResThreads = 768;
 constexpr int kResWaves = kResThreads / 64;
 
-template <bool IS_FP16_OUT, bool KT>
+// QF: Q as int8 with its scale table (0), or Q in the output's half type quantized by each wave for its own
+// 32 rows: with the per-thread classes of the Triton quantizer (QF_THREAD: rows with equal row % 8 share a
+// scale, round half away from x / scale) or the per-warp blocks of the CUDA one (QF_WARP: the 32 rows share
+// a scale, RNE of x * 127 / amax) -- the codes and scales of per_thread_int8 / per_warp_int8 bit for bit,
+// without writing int8 Q out and reading it back.
+constexpr int QF_INT8 = 0, QF_THREAD = 1, QF_WARP = 2;
+template <bool IS_FP16_OUT, bool KT, int QF = QF_INT8>
 __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p) {
   constexpr int KS = ks_per_tile(KT);
   constexpr int NW = kResThreads / 64;
@@ -1295,6 +1301,52 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
     for (int m = 0; m < 4; m++)
       qf[m] = row < p.Lq ? *reinterpret_cast<const v4i*>(qhead + row * p.qsl + m * 32 + hf * 16) : v4i{0, 0, 0, 0};
   };
+  // QF != 0: the half Q row's 64 values this lane holds (bytes 32 m + 16 hf .. + 16 of the int8 row), their
+  // |x| maximum over the lane's scale group (class: lanes lq ^ 8, ^ 16 and the other half-row; warp: all 64
+  // lanes), the group's scale and the int8 codes.  Returns the scale.
+  const uint16_t* qhead16 = reinterpret_cast<const uint16_t*>(p.q8) + b * p.qsb + h * p.qsh;
+  auto quant_q = [&](int64_t wb, v4i (&qf)[4]) {
+    const int64_t row = wb * 32 + lq;
+    float x[4][16];
+    float am = QF == QF_WARP ? 0.0000001f : 0.f;  // the CUDA quantizer's amax floor
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      v4u r0 = v4u{0, 0, 0, 0}, r1 = v4u{0, 0, 0, 0};
+      if (row < p.Lq) {
+        r0 = *reinterpret_cast<const v4u*>(qhead16 + row * p.qsl + m * 32 + hf * 16);
+        r1 = *reinterpret_cast<const v4u*>(qhead16 + row * p.qsl + m * 32 + hf * 16 + 8);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        x[m][2 * e] = half_to_f32<IS_FP16_OUT>((uint16_t)(r0[e] & 0xffffu));
+        x[m][2 * e + 1] = half_to_f32<IS_FP16_OUT>((uint16_t)(r0[e] >> 16));
+        x[m][8 + 2 * e] = half_to_f32<IS_FP16_OUT>((uint16_t)(r1[e] & 0xffffu));
+        x[m][8 + 2 * e + 1] = half_to_f32<IS_FP16_OUT>((uint16_t)(r1[e] >> 16));
+      }
+#pragma unroll
+      for (int e = 0; e < 16; e++) am = fmaxf(am, fabsf(x[m][e]));
+    }
+    if constexpr (QF == QF_WARP) {
+      am = fmaxf(am, __shfl_xor(am, 1, 64));
+      am = fmaxf(am, __shfl_xor(am, 2, 64));
+      am = fmaxf(am, __shfl_xor(am, 4, 64));
+    }
+    am = fmaxf(am, __shfl_xor(am, 8, 64));
+    am = fmaxf(am, __shfl_xor(am, 16, 64));
+    am = fmaxf(am, __shfl_xor(am, 32, 64));
+    const float sc = QF == QF_WARP ? quant_scale_cuda(am) : quant_scale_triton(am);
+    const float iv = QF == QF_WARP ? quant_recip_cuda(am) : refined_rcp(sc);
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+      int c[16];
+#pragma unroll
+      for (int e = 0; e < 16; e++) c[e] = QF == QF_WARP ? quant_code_cuda(x[m][e], iv) : quant_code_triton(x[m][e], sc, iv);
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+        qf[m][g] = (c[4 * g] & 0xff) | ((c[4 * g + 1] & 0xff) << 8) | ((c[4 * g + 2] & 0xff) << 16) | (c[4 * g + 3] << 24);
+    }
+    return sc;
+  };
   v4i qf[4];
   int64_t wb = wb0 + w;
   v16i kbias;
@@ -1307,9 +1359,14 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
   __syncthreads();  // every wave's share of the key range has landed
 
   for (; wb < wb_end; wb += NW) {
-    load_q(wb, qf);
+    float qs;
+    if constexpr (QF == QF_INT8) {
+      load_q(wb, qf);
+      qs = qs_tab[q_scale_index(p, wb * 32 + lq)] * p.qk_mult;
+    } else {
+      qs = quant_q(wb, qf) * p.qk_mult;
+    }
     const int64_t wrow0 = wb * 32, qrow = wrow0 + lq;
-    const float qs = qs_tab[q_scale_index(p, wb * 32 + lq)] * p.qk_mult;
 
     v16f o[4];
     v4f lacc;
@@ -1898,6 +1955,47 @@ extern "C" int qattn_fwd_ex2(qattn_seq q8, const float* q_scale, qattn_seq k8, c
   p.v_scale = nullptr;
   if (pv == PV_BF16) return launch_gran<PV_BF16>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D, kernel);
   return launch_gran<PV_FP16>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D, kernel);
+}
+
+// ---- half Q quantized inside the resident kernel ----
+extern "C" int qattn_fwd_q16_supported(int64_t Lk, int64_t D, int causal) {
+  return D == kD && !causal && Lk > 0 && (Lk + kBK - 1) / kBK <= kResMaxTiles ? 1 : 0;
+}
+
+extern "C" int qattn_fwd_q16(qattn_seq q, qattn_seq k8, const float* k_scale, const uint8_t* v8, int64_t Lpad,
+                             const float* v_scale, const float* v_mean, qattn_seq o, int dtype, int64_t B,
+                             int64_t Lq, int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult,
+                             int qk_quant_gran, const int32_t* kv_valid, float* lse, qattn_stream_t stream) {
+  QATTN_REQUIRE(qk_quant_gran == QATTN_GRAN_WARP || qk_quant_gran == QATTN_GRAN_THREAD, QATTN_ERR_ARG,
+                "qattn_fwd_q16 quantizes Q per warp (2) or per thread (3), got %d", qk_quant_gran);
+  QATTN_REQUIRE(qattn_fwd_q16_supported(Lk, D, 0), QATTN_ERR_SHAPE,
+                "qattn_fwd_q16 needs head_dim 128 and at most %d keys (got %lld, %lld)", kResMaxTiles * kBK,
+                (long long)D, (long long)Lk);
+  QATTN_REQUIRE(v8 && v_scale, QATTN_ERR_ARG, "null V or v_scale");
+  AttnParams p;
+  int ns = 1, kernel = QATTN_KERNEL_AUTO;
+  // (q's scale table is formed inside the kernel: k_scale stands in for the pointer setup_fwd checks)
+  const int rc = setup_fwd(p, ns, q, k_scale, k8, k_scale, v8, Lpad, o, dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult, 0, 0,
+                           kv_valid, lse, 1, PV_FP8, qk_quant_gran, kernel);
+  if (rc < 0) return QATTN_OK;
+  if (rc) return rc;
+  p.v_scale = v_scale;
+  p.v_mean = v_mean;
+  p.nsplit = 1;
+  p.tiles_per_split = (int)p.nKB;
+  resident_layout(p.B * p.Hq, (p.Lq + 31) / 32, p.wb_per_wg, p.n_chunk);
+  const int64_t g = p.B * p.Hq * p.n_chunk;
+  QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
+  hipStream_t st = (hipStream_t)stream;
+  t_last_kernel = QATTN_KERNEL_RESIDENT;
+  if (qk_quant_gran == QATTN_GRAN_THREAD) {
+    if (dtype == QATTN_BF16) qattn_fwd_res_kernel<false, true, QF_THREAD><<<g, kResThreads, 0, st>>>(p);
+    else qattn_fwd_res_kernel<true, true, QF_THREAD><<<g, kResThreads, 0, st>>>(p);
+  } else {
+    if (dtype == QATTN_BF16) qattn_fwd_res_kernel<false, false, QF_WARP><<<g, kResThreads, 0, st>>>(p);
+    else qattn_fwd_res_kernel<true, false, QF_WARP><<<g, kResThreads, 0, st>>>(p);
+  }
+  return check_launch("qattn_fwd_q16");
 }
 
 // ---- packed variable-length batches ----

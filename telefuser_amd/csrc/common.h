@@ -71,6 +71,43 @@ __device__ __forceinline__ uint16_t f32_to_half(float f) {
   else return f32_to_bf16(f);
 }
 
+// ------------------------------------------------------------------------------------------------
+// device: the quantizers' rounding (shared by the quantizer kernels and the attention kernels that
+// quantize Q themselves)
+// ------------------------------------------------------------------------------------------------
+// v_cvt_i32_f32: truncate toward zero, saturate to the int32 range, NaN -> 0 (the hardware conversion; a C
+// cast leaves NaN and out-of-range values undefined)
+__device__ __forceinline__ int cvt_i32_trunc_sat(float t) {
+  int r;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(t));
+  return r;
+}
+
+// a / b, correctly rounded, from y1 = refined_rcp(b): the fma corrections of the IEEE division sequence
+// without its range scaling (div_scale / div_fixup).  Exact wherever the residuals do not underflow: the
+// quantizers divide |a| <= 127 b with b >= 1e-7, where only quotients below 2^-80 (which quantize to 0
+// either way) can differ.
+__device__ __forceinline__ float refined_rcp(float b) {
+  const float y0 = __builtin_amdgcn_rcpf(b);
+  return fmaf(fmaf(-b, y0, 1.0f), y0, y0);
+}
+__device__ __forceinline__ float div_by(float a, float b, float y1) {
+  const float q0 = a * y1;
+  const float q1 = fmaf(fmaf(-b, q0, a), y1, q0);
+  return fmaf(fmaf(-b, q1, a), y1, q1);
+}
+
+// Scales of the per-block / per-warp (CUDA QuantInt8Kernel: amax / 127, codes RNE(x * 127 / amax)) and
+// per-thread (Triton: amax / 127 + 1e-7, codes round-half-away(x / scale)) quantizers from the |x| maximum
+__device__ __forceinline__ float quant_scale_cuda(float amax) { return amax / 127.0f; }
+__device__ __forceinline__ float quant_recip_cuda(float amax) { return 127.0f / amax; }
+__device__ __forceinline__ float quant_scale_triton(float amax) { return amax / 127.0f + 0.0000001f; }
+__device__ __forceinline__ int quant_code_cuda(float x, float recip) { return cvt_i32_trunc_sat(__builtin_rintf(x * recip)); }
+__device__ __forceinline__ int quant_code_triton(float x, float scale, float rcp_scale) {
+  const float t = div_by(x, scale, rcp_scale);
+  return cvt_i32_trunc_sat(t + __builtin_copysignf(0.5f, t));
+}
+
 // Rows [start, start + len) of sequence b of a packed variable-length batch: cu[b] .. cu[b + 1] clamped to
 // the packed tensor's `total` rows and to `maxlen`, so that a malformed sequence table cannot address
 // memory outside the packed tensors (every varlen kernel and the block-offset kernel use this).

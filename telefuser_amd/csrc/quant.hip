@@ -105,28 +105,6 @@ __device__ __forceinline__ float round_to_half(float v) {
   }
 }
 
-// v_cvt_i32_f32: truncate toward zero, saturate to the int32 range, NaN -> 0 (the hardware conversion; a C
-// cast leaves NaN and out-of-range values undefined)
-__device__ __forceinline__ int cvt_i32_trunc_sat(float t) {
-  int r;
-  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(t));
-  return r;
-}
-
-// a / b, correctly rounded, from y1 = refined_rcp(b): the fma corrections of the IEEE division sequence
-// without its range scaling (div_scale / div_fixup).  Exact wherever the residuals do not underflow: the
-// quantizers divide |a| <= 127 b with b >= 1e-7, where only quotients below 2^-80 (which quantize to 0
-// either way) can differ.
-__device__ __forceinline__ float refined_rcp(float b) {
-  const float y0 = __builtin_amdgcn_rcpf(b);
-  return fmaf(fmaf(-b, y0, 1.0f), y0, y0);
-}
-__device__ __forceinline__ float div_by(float a, float b, float y1) {
-  const float q0 = a * y1;
-  const float q1 = fmaf(fmaf(-b, q0, a), y1, q0);
-  return fmaf(fmaf(-b, q1, a), y1, q1);
-}
-
 // One workgroup per block of one (batch entry, head) of a job; a launch covers up to two jobs (Q and K)
 // of equal cell layout (cr): workgroups [0, job[0].nwg) take job 0, the rest job 1.  Two passes over registers: |x|
 // maxima, then the scales and the quantized bytes.  GROUPED (CR = 32 or 16 rows per cell, nsub = blk / CR
@@ -235,8 +213,8 @@ void quant_per_block_kernel(QuantArgs args) {
 
   // IEEE division (hipcc default: correctly rounded)
   auto scale_of = [](float a) {
-    if constexpr (VARIANT == QATTN_QUANT_TRITON_THREAD) return a / 127.0f + 0.0000001f;
-    else return a / 127.0f;
+    if constexpr (VARIANT == QATTN_QUANT_TRITON_THREAD) return quant_scale_triton(a);
+    else return quant_scale_cuda(a);
   };
   // per chunk (GROUPED) or per thread: the scale (Triton rounding) or 127 / amax (CUDA rounding)
   float sc[NA];
@@ -299,7 +277,7 @@ void quant_per_block_kernel(QuantArgs args) {
         for (int c = 1; c < NCELL; c++)
           if (idx == c) a = cell[c];
       }
-      sc[i] = VARIANT == QATTN_QUANT_CUDA ? 127.0f / a : scale_of(a);
+      sc[i] = VARIANT == QATTN_QUANT_CUDA ? quant_recip_cuda(a) : scale_of(a);
     }
 #pragma unroll
     for (int c = 0; c < NCELL; c++)
@@ -320,11 +298,10 @@ void quant_per_block_kernel(QuantArgs args) {
         // NaN converts to 0
         if constexpr (VARIANT == QATTN_QUANT_CUDA) {
           // cvt.rni.sat.s8.f32: round to nearest even
-          qv[e] = (int8_t)cvt_i32_trunc_sat(__builtin_rintf(x[i][e] * iv));
+          qv[e] = (int8_t)quant_code_cuda(x[i][e], iv);
         } else {
           // Triton: t + 0.5 * sign(t) in fp32, truncate toward zero
-          const float t = div_by(x[i][e], s, iv);
-          qv[e] = (int8_t)cvt_i32_trunc_sat(t + __builtin_copysignf(0.5f, t));
+          qv[e] = (int8_t)quant_code_triton(x[i][e], s, iv);
         }
       }
       v2u packed;
@@ -1318,14 +1295,16 @@ extern "C" int qattn_sage_quant(qattn_seq q, qattn_seq k, qattn_seq v, int dtype
   QATTN_REQUIRE(qk_quant_gran >= 1 && qk_quant_gran <= 5, QATTN_ERR_ARG,
                 "qk_quant_gran must be 1 (per block), 2 (per warp), 3 (per thread), 4 (per warp, sm90 tables) or "
                 "5 (per thread, sm90 tables), got %d", qk_quant_gran);
-  QATTN_REQUIRE(B > 0 && Lq > 0 && Lk > 0 && Hq > 0 && Hkv > 0, QATTN_ERR_SHAPE, "sage_quant needs non-empty input");
+  // Lq = 0: K and V only (Q is quantized by the attention kernel, qattn_fwd_q16)
+  QATTN_REQUIRE(B > 0 && Lq >= 0 && Lk > 0 && Hq > 0 && Hkv > 0, QATTN_ERR_SHAPE, "sage_quant needs non-empty K / V");
   // the sm90 tables: 64-row Q blocks of 16-row warps, 128-row K blocks (as the *_ex quantizers)
   const bool sm90 = qk_quant_gran >= 4;
   if (sm90) qk_quant_gran -= 2;
-  if ((rc = check_seq("q", q, 2)) || (rc = check_seq("k", k, 2)) || (rc = check_seq("v", v, 2)) ||
-      (rc = check_seq("q_out", q_out, 1)) || (rc = check_seq("k_out", k_out, 1)))
+  if ((Lq > 0 && ((rc = check_seq("q", q, 2)) || (rc = check_seq("q_out", q_out, 1)))) ||
+      (rc = check_seq("k", k, 2)) || (rc = check_seq("v", v, 2)) || (rc = check_seq("k_out", k_out, 1)))
     return rc;
-  QATTN_REQUIRE(q_scale && k_scale && v_scale && v8 && aligned16(v8), QATTN_ERR_ARG, "null or misaligned output");
+  QATTN_REQUIRE((Lq == 0 || q_scale) && k_scale && v_scale && v8 && aligned16(v8), QATTN_ERR_ARG,
+                "null or misaligned output");
   QATTN_REQUIRE(!smooth_k || (k_mean && aligned16(k_mean)), QATTN_ERR_ALIGN, "smooth_k needs an aligned k_mean output");
   QATTN_REQUIRE(!smooth_v || v_mean, QATTN_ERR_ARG, "smooth_v needs a v_mean output");
   QATTN_REQUIRE(Lpad >= (Lk + 63) / 64 * 64 && Lpad % 64 == 0, QATTN_ERR_SHAPE,
@@ -1376,7 +1355,8 @@ extern "C" int qattn_sage_quant(qattn_seq q, qattn_seq k, qattn_seq v, int dtype
   // 4. K then Q to INT8 in one launch (K first: its rows were read by step 1 as well)
   QuantArgs a{};
   a.njobs = 0;
-  int variant = QATTN_QUANT_CUDA;
+  // per-thread scales: the Triton rounding for K (and Q); otherwise the CUDA rounding
+  const int variant = qk_quant_gran == 3 ? QATTN_QUANT_TRITON_THREAD : QATTN_QUANT_CUDA;
   const void* kmean_in = smooth_k ? k_mean : nullptr;
   {
     QuantJob& J = a.job[a.njobs++];
@@ -1386,7 +1366,7 @@ extern "C" int qattn_sage_quant(qattn_seq q, qattn_seq k, qattn_seq v, int dtype
       J.cls_shift = 1;
     }
   }
-  {
+  if (Lq > 0) {
     QuantJob& J = a.job[a.njobs++];
     if (qk_quant_gran == 1) {
       fill_job(J, q, q_out, B, Lq, Hq, nullptr, q_scale, q_sm_scale, 1, 128);
@@ -1396,7 +1376,6 @@ extern "C" int qattn_sage_quant(qattn_seq q, qattn_seq k, qattn_seq v, int dtype
       if (qk_quant_gran == 3) {
         J.ncls = 8;
         J.cls_shift = 0;
-        variant = QATTN_QUANT_TRITON_THREAD;
       }
     }
   }

@@ -185,12 +185,13 @@ def per_channel_fp8(v: torch.Tensor, tensor_layout: str = "HND", scale_max: floa
 
 def sage_quant(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout: str = "HND",
                qk_quant_gran: str = "per_block", sm_scale: Optional[float] = None, smooth_k: bool = True,
-               scale_max: float = 448.0, smooth_v: bool = False, scale_layout: str = "sm89"):
+               scale_max: float = 448.0, smooth_v: bool = False, scale_layout: str = "sm89", quantize_q: bool = True):
     """The whole prologue of the INT8-QK / FP8-PV path in four launches (column passes of K and V,
     their finalize, V to FP8, K and Q to INT8): the same outputs, bit for bit, as k_mean + the
     per_block / per_warp / per_thread quantizer + per_channel_fp8 (CUDA quantizer variant).
     ``scale_layout="sm90"`` (per_warp / per_thread only) gives the sm90 entry's tables, as per_warp_int8 /
-    per_thread_int8 with BLKQ=64, WARPQ=16, BLKK=128.
+    per_thread_int8 with BLKQ=64, WARPQ=16, BLKK=128.  ``quantize_q=False`` leaves Q out (for qattn_fwd_q16,
+    which quantizes it inside the attention kernel): q_int8 and q_scale are then None.
     Returns (q_int8, q_scale, k_int8, k_scale, km or None, v_fp8, v_scale, vm or None)."""
     L = _lib.load()
     if not (q.dtype == k.dtype == v.dtype):
@@ -207,10 +208,13 @@ def sage_quant(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout:
     _, lk, hkv, _ = _dims(k, tensor_layout)
     dev = q.device
     nqb, nkb = _scale_blocks(lq, lk, sm90)
-    q_int8 = torch.empty(q.shape, dtype=torch.int8, device=dev)
-    k_int8 = torch.empty(k.shape, dtype=torch.int8, device=dev)
     q_per = {1: 1, 2: 4, 3: 32}[gran]
-    q_scale = torch.empty((b, hq, nqb * q_per), dtype=torch.float32, device=dev)
+    if quantize_q:
+        q_int8 = torch.empty(q.shape, dtype=torch.int8, device=dev)
+        q_scale = torch.empty((b, hq, nqb * q_per), dtype=torch.float32, device=dev)
+    else:
+        q_int8 = q_scale = None
+    k_int8 = torch.empty(k.shape, dtype=torch.int8, device=dev)
     k_scale = torch.empty((b, hkv, nkb * (4 if gran == 3 else 1)), dtype=torch.float32, device=dev)
     km = torch.empty((b, hkv, d), dtype=k.dtype, device=dev) if smooth_k else None
     lpad = (lk + 63) // 64 * 64
@@ -222,8 +226,9 @@ def sage_quant(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, tensor_layout:
         sm_scale = d ** -0.5
     _lib.check(L.qattn_sage_quant(
         _lib.seq(q, tensor_layout), _lib.seq(k, tensor_layout), _lib.seq(v, tensor_layout), _lib.dtype_code(q.dtype),
-        b, lq, lk, hq, hkv, d, gran + (2 if sm90 else 0), float(sm_scale * LOG2E), int(bool(smooth_k)), float(scale_max),
-        int(bool(smooth_v)), _lib.seq(q_int8, tensor_layout), _lib.ptr(q_scale), _lib.seq(k_int8, tensor_layout),
+        b, lq if quantize_q else 0, lk, hq, hkv, d, gran + (2 if sm90 else 0), float(sm_scale * LOG2E),
+        int(bool(smooth_k)), float(scale_max), int(bool(smooth_v)),
+        _lib.seq(q_int8 if quantize_q else q, tensor_layout), _lib.ptr(q_scale), _lib.seq(k_int8, tensor_layout),
         _lib.ptr(k_scale), _lib.ptr(km), _lib.ptr(v_fp8), lpad, _lib.ptr(v_scale), _lib.ptr(vm), _lib.ptr(ws),
         ws.numel(), _lib.stream_of(q)))
     return q_int8, q_scale, k_int8, k_scale, km, v_fp8, v_scale, vm
@@ -257,14 +262,17 @@ _GRAN = {"per_block": _lib.QATTN_GRAN_BLOCK, "per_warp": _lib.QATTN_GRAN_WARP, "
 def _check_attn_operands(q_int8, q_scale, k_int8, k_scale, v, v_scale, b, lq, lk, hq, hkv, d, gran, out, out_dtype,
                          sm90=False):
     """Shapes, dtypes and devices of qattn_fwd's operands: a scale tensor of another granularity or a V
-    tile of the wrong size would make the kernel read outside them."""
+    tile of the wrong size would make the kernel read outside them.  q_scale None: Q is half precision and
+    quantized by the kernel (qattn_fwd_q16)."""
     nqb, nkb = _scale_blocks(lq, lk, sm90)
     q_per = {"per_block": 1, "per_warp": 4, "per_thread": 32}[gran]
     k_per = 4 if gran == "per_thread" else 1
     dev = q_int8.device
-    if q_int8.dtype != torch.int8 or k_int8.dtype != torch.int8:
-        raise ValueError("q_int8 and k_int8 must be int8")
-    for name, t, shape in (("q_scale", q_scale, (b, hq, nqb * q_per)), ("k_scale", k_scale, (b, hkv, nkb * k_per))):
+    q_dtypes = (torch.int8,) if q_scale is not None else (torch.bfloat16, torch.float16)
+    if q_int8.dtype not in q_dtypes or k_int8.dtype != torch.int8:
+        raise ValueError(f"q must be {' or '.join(str(t) for t in q_dtypes)} and k_int8 int8")
+    scales = (("q_scale", q_scale, (b, hq, nqb * q_per)),) if q_scale is not None else ()
+    for name, t, shape in scales + (("k_scale", k_scale, (b, hkv, nkb * k_per)),):
         if t.dtype != torch.float32 or tuple(t.shape) != shape or not t.is_contiguous():
             raise ValueError(f"{name} must be a contiguous float32 tensor of shape {shape} for qk_quant_gran="
                              f"{gran!r}, got {t.dtype} {tuple(t.shape)}")
@@ -336,6 +344,42 @@ def qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout
     return (o, lse) if return_lse else o
 
 
+def qattn_fwd_q16(q, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout="HND", qk_mult=1.0, kv_valid_len=None,
+                  return_lse=False, qk_quant_gran="per_thread", out: Optional[torch.Tensor] = None,
+                  v_mean: Optional[torch.Tensor] = None):
+    """Attention on half-precision Q for short key ranges (qattn_fwd_q16 in the C ABI): Q is quantized per
+    thread (Triton rounding) or per warp (CUDA rounding) inside the resident-K/V kernel, bit-identical to
+    per_thread_int8 / per_warp_int8 followed by qattn_fwd, without the int8 Q round trip through memory.
+    Non-causal, head_dim 128, at most 512 keys (qattn_fwd_q16_supported).  Returns o (and the log2-domain
+    LSE)."""
+    L = _lib.load()
+    b, lq, hq, d = _dims(q, tensor_layout)
+    _, lk, hkv, _ = _dims(k_int8, tensor_layout)
+    if hq % hkv != 0:
+        raise ValueError(f"num_qo_heads ({hq}) must be divisible by num_kv_heads ({hkv})")
+    if qk_quant_gran not in ("per_warp", "per_thread"):
+        raise ValueError(f"qk_quant_gran must be 'per_warp' or 'per_thread', got {qk_quant_gran!r}")
+    if q.dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError("q must be bf16 or fp16")
+    if not L.qattn_fwd_q16_supported(lk, d, 0):
+        raise ValueError(f"qattn_fwd_q16 needs head_dim 128 and at most 512 keys, got {d} and {lk}")
+    if v_scale is None:
+        raise ValueError("qattn_fwd_q16 takes the e4m3 V tile and its v_scale")
+    _check_attn_operands(q, None, k_int8, k_scale, v_fp8, v_scale, b, lq, lk, hq, hkv, d, qk_quant_gran, out, q.dtype)
+    if v_mean is not None and (v_mean.dtype != torch.float32 or tuple(v_mean.shape) != (b, hkv, d) or
+                               not v_mean.is_contiguous()):
+        raise ValueError(f"v_mean must be a contiguous float32 tensor of shape {(b, hkv, d)}")
+    o = out if out is not None else torch.empty(q.shape, dtype=q.dtype, device=q.device)
+    lse = torch.empty((b, hq, lq), dtype=torch.float32, device=q.device) if return_lse else None
+    kvv = _kv_valid_tensor(kv_valid_len, b, q.device)
+    gran = _GRAN[qk_quant_gran]
+    _lib.check(L.qattn_fwd_q16(
+        _lib.seq(q, tensor_layout), _lib.seq(k_int8, tensor_layout), _lib.ptr(k_scale), _lib.ptr(v_fp8),
+        v_fp8.shape[-1], _lib.ptr(v_scale), _lib.ptr(v_mean), _lib.seq(o, tensor_layout), _lib.dtype_code(q.dtype),
+        b, lq, lk, hq, hkv, d, float(qk_mult), gran, _lib.ptr(kvv), _lib.ptr(lse), _lib.stream_of(q)))
+    return (o, lse) if return_lse else o
+
+
 def _pad_head_dim(x: torch.Tensor, native64: bool = False) -> torch.Tensor:
     """Zero-pad the head dimension to what the kernels take.  With ``native64`` (the FP8 P.V path, whose
     kernel has a head_dim-64 form) heads of at most 64 are padded to 64 and larger ones to 128, as the
@@ -391,6 +435,16 @@ def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv
         q_int8, q_scale, k_int8, k_scale, km, v_fp8, v_scale, vm = sage_quant(
             q, k, v, tensor_layout=tensor_layout, qk_quant_gran=qk_quant_gran, sm_scale=sm_scale, smooth_k=smooth_k,
             scale_max=448.0, smooth_v=False, scale_layout="sm90")
+    elif (pv == "fp8" and quant_variant == "cuda" and qk_quant_gran != "per_block" and not is_causal and
+          _lib.load().qattn_fwd_q16_supported(lk, q.size(-1), 0)):
+        # short key ranges: K mean, K INT8 and V FP8 in the fused prologue, Q quantized inside the resident
+        # attention kernel (bit-identical to quantizing it first)
+        _, _, k_int8, k_scale, km, v_fp8, v_scale, vm = sage_quant(
+            q, k, v, tensor_layout=tensor_layout, qk_quant_gran=qk_quant_gran, sm_scale=sm_scale, smooth_k=smooth_k,
+            scale_max=scale_max, smooth_v=smooth_v, quantize_q=False)
+        res = qattn_fwd_q16(q, k_int8, k_scale, v_fp8, v_scale, tensor_layout=tensor_layout, qk_mult=qk_mult,
+                            kv_valid_len=kv_valid_len, return_lse=return_lse, qk_quant_gran=qk_quant_gran, v_mean=vm)
+        return _sage_finish(res, q, km, hq, hkv, head_dim_og, tensor_layout, sm_scale, smooth_k, return_lse)
     elif pv == "fp8" and quant_variant == "cuda":
         # K mean, Q/K INT8 and V FP8 in one fused prologue (four launches)
         q_int8, q_scale, k_int8, k_scale, km, v_fp8, v_scale, vm = sage_quant(
@@ -415,13 +469,18 @@ def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv
                     qk_mult=qk_mult, is_causal=is_causal, q_offset=q_offset, kv_valid_len=kv_valid_len,
                     return_lse=return_lse, qk_quant_gran=qk_quant_gran, v_mean=vm,
                     scale_layout="sm90" if sm90 else "sm89")
+    return _sage_finish(res, q, km, hq, hkv, head_dim_og, tensor_layout, sm_scale, smooth_k, return_lse)
+
+
+def _sage_finish(res, q, km, hq, hkv, head_dim_og, tensor_layout, sm_scale, smooth_k, return_lse):
+    """Unpad O; natural-log LSE with the K-smoothing correction (sageattn2.py:1334-1354,1450-1455)."""
     o, lse = res if return_lse else (res, None)
     o = o[..., :head_dim_og]
     if not return_lse:
         return o
     lse = lse / LOG2E
     if smooth_k:
-        # logits were computed against k - km: add back q.km * sm_scale (sageattn2.py:1334-1354,1450-1455)
+        # logits were computed against k - km: add back q.km * sm_scale
         qq = q if tensor_layout == "HND" else q.transpose(1, 2)
         kmb = km.repeat_interleave(hq // hkv, dim=1)  # [B, Hq, D]
         corr = torch.matmul(qq, kmb.unsqueeze(-1)).squeeze(-1).to(torch.float32)
@@ -600,6 +659,7 @@ __all__ = [
     "sageattn",
     "sageattn_qk_int8_pv_fp8_cuda",
     "sageattn_qk_int8_pv_fp8_cuda_sm90",
+    "qattn_fwd_q16",
     "sageattn_qk_int8_pv_fp16_cuda",
     "sageattn_qk_int8_pv_fp16_triton",
     "v_tile_half",

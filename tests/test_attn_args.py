@@ -122,3 +122,24 @@ def test_qattn_fwd_sm90_layout_checks(bad):
         kw["scale_layout"] = "sm100"
     with pytest.raises(ValueError):
         sa.qattn_fwd(q8, qs, k8, ks, v, vs, **kw)
+
+
+@pytest.mark.parametrize("bad", ["per_block", "too_many_keys", "int8_q", "k_scale_gran", "no_v_scale"])
+def test_fwd_q16_rejects(bad):
+    """qattn_fwd_q16 takes half Q, per-warp / per-thread K scales, the e4m3 V tile, at most 512 keys."""
+    from telefuser_amd import sageattn2 as sa
+
+    lk = 600 if bad == "too_many_keys" else 300
+    q8, qs, k8, ks, v, vs = _ops(Lk=lk, gran="per_thread")
+    q = torch.zeros(q8.shape, dtype=torch.bfloat16)
+    kw = dict(tensor_layout="NHD", qk_quant_gran="per_thread")
+    if bad == "per_block":
+        kw["qk_quant_gran"] = "per_block"
+    elif bad == "int8_q":
+        q = q8
+    elif bad == "k_scale_gran":
+        ks = ks[..., : ks.shape[-1] // 4].contiguous()
+    elif bad == "no_v_scale":
+        vs = None
+    with pytest.raises(ValueError):
+        sa.qattn_fwd_q16(q, k8, ks, v, vs, **kw)

@@ -891,3 +891,53 @@ def test_pv_accum_modes_and_smooth_v(oracle, mode):
     assert ck >= COS_KERNEL
     assert cr >= COS_E2E
     assert ct >= COS_E2E
+
+
+Q16_CASES = {
+    # name: (B, Lq, Lk, Hq, Hkv, layout, dtype, gran, kv_valid, smooth_v)
+    "thread_c4_like": (1, 1000, 512, 4, 4, "NHD", torch.bfloat16, "per_thread", [388], False),
+    "warp_ragged_gqa": (2, 333, 300, 4, 2, "NHD", torch.bfloat16, "per_warp", None, False),
+    "thread_hnd_fp16": (1, 517, 130, 3, 3, "HND", torch.float16, "per_thread", None, False),
+    "thread_smooth_v_short_q": (2, 40, 64, 2, 1, "NHD", torch.bfloat16, "per_thread", [64, 17], True),
+    "warp_fp16_keys_512": (1, 777, 512, 2, 2, "NHD", torch.float16, "per_warp", None, True),
+}
+
+
+@pytest.mark.parametrize("case", sorted(Q16_CASES))
+def test_fwd_q16_matches_quantize_then_attend(oracle, case):
+    """qattn_fwd_q16 quantizes Q inside the resident kernel: its output and LSE must be bit-identical to
+    per_thread_int8 / per_warp_int8 followed by qattn_fwd on the same K / V, and the drop-in (which takes
+    this route for non-causal launches over at most 512 keys) must give the same bits as well."""
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    B, Lq, Lk, Hq, Hkv, layout, dt, gran, kv_valid, smooth_v = Q16_CASES[case]
+    log(f"fwd_q16 {case}: B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} {layout} {dt} {gran} kv_valid={kv_valid}")
+    q, k, v = qkv(B, Lq, Lk, Hq, Hkv, seed=53, k_offset_std=0.5, dtype=dt)
+    qd, kd, vd = (t.to(dev) for t in (q, k, v))
+    if layout == "HND":
+        qd, kd, vd = (t.transpose(1, 2).contiguous() for t in (qd, kd, vd))
+    km = sa.k_mean(kd, layout)
+    quant = sa.per_thread_int8 if gran == "per_thread" else sa.per_warp_int8
+    q8, qs, k8, ks = quant(qd, kd, km, tensor_layout=layout)
+    v8, vs, vm = sa.per_channel_fp8(vd, tensor_layout=layout, smooth_v=smooth_v)
+    qk_mult = 128 ** -0.5 * LOG2E
+    o_ref, l_ref = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout=layout, out_dtype=dt, qk_mult=qk_mult,
+                                kv_valid_len=kv_valid, return_lse=True, qk_quant_gran=gran, v_mean=vm)
+    o, l = sa.qattn_fwd_q16(qd, k8, ks, v8, vs, tensor_layout=layout, qk_mult=qk_mult, kv_valid_len=kv_valid,
+                            return_lse=True, qk_quant_gran=gran, v_mean=vm)
+    torch.cuda.synchronize()
+    assert torch.equal(o, o_ref), f"max diff {float((o.float() - o_ref.float()).abs().max())}"
+    assert torch.equal(l, l_ref)
+    # the drop-in on the same inputs: identical to its quantize-then-attend steps
+    kw = dict(tensor_layout=layout, qk_quant_gran=gran, pv_accum_dtype="fp32" if smooth_v else "fp32+fp32",
+              smooth_v=smooth_v, kv_valid_len=kv_valid, return_lse=True)
+    od, ld = sa.sageattn_qk_int8_pv_fp8_cuda(qd, kd, vd, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(od, o)
+    # and within the end-to-end bound of float64 attention (rows with keys)
+    if layout == "HND":
+        od = od.transpose(1, 2)
+    bits = (lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)) if dt == torch.float16 else bf16_bits
+    truth = oracle.attn_fp64(bits(q), bits(k), bits(v), 128 ** -0.5, kv_valid=kv_valid, is_fp16=dt == torch.float16)
+    assert cosine(od.float().cpu().numpy(), truth) >= COS_E2E
