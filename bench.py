@@ -282,7 +282,8 @@ def _config_bench(name: str, calls: int = 5, warmup: int = 2) -> dict:
     ms_tf = (time.perf_counter() - t0) * 1e3 / calls
     res["telefuser_path"] = {"entry": "sageattn_qk_int8_pv_fp8_cuda(per_thread, fp32+fp32)",
                              "ms_per_call": round(ms_tf, 4), "call_TOPS": round(ops / (ms_tf * 1e-3) / 1e12, 2),
-                             "q_quantized_in_attention": bool(L.qattn_fwd_q16_supported(cfg.Lk, cfg.D, 0))}
+                             "q_quantized_in_attention": sa.q16_supported(cfg.B, cfg.Lq, cfg.Lk, cfg.Hq, cfg.D,
+                                                                          "per_thread")}
     del q, k, v
     torch.cuda.empty_cache()
     return res

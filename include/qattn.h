@@ -310,21 +310,24 @@ int qattn_v_fp8_cache_update(qattn_seq v, int dtype, int64_t B, int64_t fill, in
                              qattn_stream_t stream);
 
 /*
- * Attention on half-precision Q (bf16 / fp16, the output's dtype) for short key ranges: each wave quantizes
- * its own 32 query rows as the reference's per_thread_int8 (qk_quant_gran QATTN_GRAN_THREAD, Triton
- * rounding, quant_per_thread.py:22-158) or per_warp_int8 (QATTN_GRAN_WARP, QuantInt8Kernel rounding,
- * fused.cu:698-780) would -- bit-identical codes and scales, no sm_scale in Q -- and feeds them to the
- * resident-K/V kernel, so int8 Q is never written out and read back.  K and V are prepared as for qattn_fwd_ex
- * with the same granularity (k_scale per 64-key block, or 4 lane-pair classes per block for per-thread).
- * Replaces the quantize-then-attend sequence of sageattn_qk_int8_pv_fp8_cuda (sageattn2.py:1334-1446) for
- * non-causal launches with head_dim 128 and at most 512 keys (qattn_fwd_q16_supported); no counterpart
- * op in the reference.  qk_mult = sm_scale * 1.44269504.
+ * Attention on half-precision Q (bf16 / fp16, the output's dtype): each wave quantizes its own 32 query rows
+ * as the reference's per_thread_int8 (qk_quant_gran QATTN_GRAN_THREAD, Triton rounding,
+ * quant_per_thread.py:22-158) or per_warp_int8 (QATTN_GRAN_WARP, QuantInt8Kernel rounding, fused.cu:698-780)
+ * would -- bit-identical codes and scales, no sm_scale in Q -- inside the resident-K/V or the ping-pong
+ * kernel, so int8 Q is never written out and read back.  K and V are prepared as for qattn_fwd_ex with the
+ * same granularity (k_scale per 64-key block, or 4 lane-pair classes per block for per-thread).  Arguments
+ * as qattn_fwd_ex (causal, q_offset, kv_valid, lse, num_splits with its workspace sized by
+ * qattn_fwd_ex_num_splits / qattn_fwd_workspace_size); qk_mult = sm_scale * 1.44269504.  Runs when the
+ * automatic kernel rule gives one of those two kernels for the launch and head_dim is 128
+ * (qattn_fwd_q16_supported), else returns QATTN_ERR_SHAPE.  Replaces the quantize-then-attend sequence of
+ * sageattn_qk_int8_pv_fp8_cuda (sageattn2.py:1334-1446); no counterpart op in the reference.
  */
-int qattn_fwd_q16_supported(int64_t Lk, int64_t D, int causal);
+int qattn_fwd_q16_supported(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t D, int qk_quant_gran, int causal);
 int qattn_fwd_q16(qattn_seq q, qattn_seq k8, const float* k_scale, const uint8_t* v8, int64_t Lpad,
                   const float* v_scale, const float* v_mean, qattn_seq o, int dtype, int64_t B, int64_t Lq, int64_t Lk,
-                  int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int qk_quant_gran, const int32_t* kv_valid,
-                  float* lse, qattn_stream_t stream);
+                  int64_t Hq, int64_t Hkv, int64_t D, float qk_mult, int qk_quant_gran, int causal, int64_t q_offset,
+                  const int32_t* kv_valid, float* lse, int num_splits, void* workspace, size_t workspace_bytes,
+                  qattn_stream_t stream);
 
 /*
  * General form of qattn_fwd / qattn_fwd_pv16 with the Q/K scale granularity of the reference's kernels

@@ -107,9 +107,10 @@ def load() -> ctypes.CDLL:
                                            sz, vp]
     L.qattn_quant_qk_per_warp_int8.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, vp]
     L.qattn_quant_qk_per_thread_int8.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, vp]
-    L.qattn_fwd_q16_supported.argtypes = [i64, i64, i32]
+    L.qattn_fwd_q16_supported.argtypes = [i64, i64, i64, i64, i64, i32, i32]
     L.qattn_fwd_q16_supported.restype = i32
-    L.qattn_fwd_q16.argtypes = [S, S, vp, vp, i64, vp, vp, S, i32, i64, i64, i64, i64, i64, i64, f32, i32, vp, vp, vp]
+    L.qattn_fwd_q16.argtypes = [S, S, vp, vp, i64, vp, vp, S, i32, i64, i64, i64, i64, i64, i64, f32, i32, i32, i64, vp,
+                                vp, i32, vp, sz, vp]
     L.qattn_quant_qk_per_warp_int8_ex.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, i32, vp]
     L.qattn_quant_qk_per_thread_int8_ex.argtypes = [S, S, i32, i64, i64, i64, i64, i64, i64, vp, S, S, vp, vp, i32,
                                                     vp]

@@ -836,6 +836,60 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
 constexpr int kPPThreads = 512;
 constexpr int kPPNBuf = 4;
 
+// QF: Q as int8 with its scale table (0), or Q in the output's half type quantized by each wave for its own
+// 32 rows: with the per-thread classes of the Triton quantizer (QF_THREAD: rows with equal row % 8 share a
+// scale, round half away from x / scale) or the per-warp blocks of the CUDA one (QF_WARP: the 32 rows share
+// a scale, RNE of x * 127 / amax) -- the codes and scales of per_thread_int8 / per_warp_int8 bit for bit,
+// without writing int8 Q out and reading it back.
+constexpr int QF_INT8 = 0, QF_THREAD = 1, QF_WARP = 2;
+
+// Lane (lq, hf) of a wave whose 32 query rows are lq = lane % 32: the 16 NQF values of its row (row pointer
+// rowp, half type; zeros when !valid) at 32 m + 16 hf .. + 16, their |x| maximum over the lane's scale group
+// (per-thread class: lanes lq ^ 8, lq ^ 16 and the other half-row; per-warp: all 64 lanes, with the CUDA
+// quantizer's 1e-7 floor), the group's scale (returned) and the int8 codes as the MFMA B fragments qf.
+template <bool IS_FP16, int QF, int NQF>
+__device__ __forceinline__ float quant_q_rows(const uint16_t* rowp, bool valid, int hf, v4i (&qf)[NQF]) {
+  float x[NQF][16];
+  float am = QF == QF_WARP ? 0.0000001f : 0.f;
+#pragma unroll
+  for (int m = 0; m < NQF; m++) {
+    v4u r0 = v4u{0, 0, 0, 0}, r1 = v4u{0, 0, 0, 0};
+    if (valid) {
+      r0 = *reinterpret_cast<const v4u*>(rowp + m * 32 + hf * 16);
+      r1 = *reinterpret_cast<const v4u*>(rowp + m * 32 + hf * 16 + 8);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      x[m][2 * e] = half_to_f32<IS_FP16>((uint16_t)(r0[e] & 0xffffu));
+      x[m][2 * e + 1] = half_to_f32<IS_FP16>((uint16_t)(r0[e] >> 16));
+      x[m][8 + 2 * e] = half_to_f32<IS_FP16>((uint16_t)(r1[e] & 0xffffu));
+      x[m][8 + 2 * e + 1] = half_to_f32<IS_FP16>((uint16_t)(r1[e] >> 16));
+    }
+#pragma unroll
+    for (int e = 0; e < 16; e++) am = fmaxf(am, fabsf(x[m][e]));
+  }
+  if constexpr (QF == QF_WARP) {
+    am = fmaxf(am, __shfl_xor(am, 1, 64));
+    am = fmaxf(am, __shfl_xor(am, 2, 64));
+    am = fmaxf(am, __shfl_xor(am, 4, 64));
+  }
+  am = fmaxf(am, __shfl_xor(am, 8, 64));
+  am = fmaxf(am, __shfl_xor(am, 16, 64));
+  am = fmaxf(am, __shfl_xor(am, 32, 64));
+  const float sc = QF == QF_WARP ? quant_scale_cuda(am) : quant_scale_triton(am);
+  const float iv = QF == QF_WARP ? quant_recip_cuda(am) : refined_rcp(sc);
+#pragma unroll
+  for (int m = 0; m < NQF; m++) {
+    int c[16];
+#pragma unroll
+    for (int e = 0; e < 16; e++) c[e] = QF == QF_WARP ? quant_code_cuda(x[m][e], iv) : quant_code_triton(x[m][e], sc, iv);
+#pragma unroll
+    for (int g = 0; g < 4; g++)
+      qf[m][g] = (c[4 * g] & 0xff) | ((c[4 * g + 1] & 0xff) << 8) | ((c[4 * g + 2] & 0xff) << 16) | (c[4 * g + 3] << 24);
+  }
+  return sc;
+}
+
 // workgroup barrier that the compiler neither crosses with memory operations nor schedules around
 __device__ __forceinline__ void pp_barrier() {
   __builtin_amdgcn_sched_barrier(0);
@@ -843,7 +897,7 @@ __device__ __forceinline__ void pp_barrier() {
   __builtin_amdgcn_sched_barrier(0);
 }
 
-template <bool IS_FP16_OUT, bool KT, bool SPLIT, int HD>
+template <bool IS_FP16_OUT, bool KT, bool SPLIT, int HD, int QF = QF_INT8>
 __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   // HD: head dimension, 128 or 64.  Per 64-key tile a wave runs HD / 16 Q.K^T MFMAs (two key blocks x HD / 32
   // k-steps) and HD / 32 P.V MFMAs; K and V tiles are HD / 16 fragments of 1 KiB each.
@@ -907,7 +961,12 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   constexpr int QC = ROWB / 16;  // 16-byte chunks per Q row
   uint8_t* stage = &lds_k[0][0] + w * 4096;
   v4i qf[NQF];
-  {
+  float qs;
+  if constexpr (QF != QF_INT8) {
+    // half Q quantized by the wave itself (see quant_q_rows)
+    const uint16_t* qh16 = reinterpret_cast<const uint16_t*>(p.q8) + b * p.qsb + h * p.qsh;
+    qs = quant_q_rows<IS_FP16_OUT, QF, NQF>(qh16 + qrow * p.qsl, qrow < p.Lq, hf, qf) * p.qk_mult;
+  } else {
     const int8_t* qbase = p.q8 + b * p.qsb + h * p.qsh;
 #pragma unroll
     for (int i = 0; i < 32 * QC / 64; i++) {
@@ -924,10 +983,10 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     }
 #pragma unroll
     for (int m = 0; m < NQF; m++) asm volatile("" ::"v"(qf[m]));
+    const int64_t qbs = min(qb, p.nQB - 1);
+    const int64_t qsi = q_scale_index(p, qbs * kBQ + wl * 32 + lq);
+    qs = p.q_scale[(b * p.Hq + h) * p.nQS + qsi] * p.qk_mult;
   }
-  const int64_t qbs = min(qb, p.nQB - 1);
-  const int64_t qsi = q_scale_index(p, qbs * kBQ + wl * 32 + lq);
-  const float qs = p.q_scale[(b * p.Hq + h) * p.nQS + qsi] * p.qk_mult;
   const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
 
   // K/V tiles in LDS, fragment-major: 1 KiB block j holds MFMA operand fragment j of all 64 lanes (lane l
@@ -1207,9 +1266,9 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
 }
 
-template <bool IS_FP16_OUT, bool KT, bool SPLIT, int HD = kD>
+template <bool IS_FP16_OUT, bool KT, bool SPLIT, int HD = kD, int QF = QF_INT8>
 __global__ __launch_bounds__(kPPThreads) void qattn_fwd_pp_kernel(AttnParams p) {
-  qattn_fwd_pp<IS_FP16_OUT, KT, SPLIT, HD>(p);
+  qattn_fwd_pp<IS_FP16_OUT, KT, SPLIT, HD, QF>(p);
 }
 
 // ---- resident K/V: short key ranges (at most kResMaxTiles tiles, e.g. text cross-attention) ----
@@ -1228,12 +1287,6 @@ constexpr int kResMaxTiles = 8;
 constexpr int kResThreads = 768;
 constexpr int kResWaves = kResThreads / 64;
 
-// QF: Q as int8 with its scale table (0), or Q in the output's half type quantized by each wave for its own
-// 32 rows: with the per-thread classes of the Triton quantizer (QF_THREAD: rows with equal row % 8 share a
-// scale, round half away from x / scale) or the per-warp blocks of the CUDA one (QF_WARP: the 32 rows share
-// a scale, RNE of x * 127 / amax) -- the codes and scales of per_thread_int8 / per_warp_int8 bit for bit,
-// without writing int8 Q out and reading it back.
-constexpr int QF_INT8 = 0, QF_THREAD = 1, QF_WARP = 2;
 template <bool IS_FP16_OUT, bool KT, int QF = QF_INT8>
 __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p) {
   constexpr int KS = ks_per_tile(KT);
@@ -1301,52 +1354,7 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
     for (int m = 0; m < 4; m++)
       qf[m] = row < p.Lq ? *reinterpret_cast<const v4i*>(qhead + row * p.qsl + m * 32 + hf * 16) : v4i{0, 0, 0, 0};
   };
-  // QF != 0: the half Q row's 64 values this lane holds (bytes 32 m + 16 hf .. + 16 of the int8 row), their
-  // |x| maximum over the lane's scale group (class: lanes lq ^ 8, ^ 16 and the other half-row; warp: all 64
-  // lanes), the group's scale and the int8 codes.  Returns the scale.
   const uint16_t* qhead16 = reinterpret_cast<const uint16_t*>(p.q8) + b * p.qsb + h * p.qsh;
-  auto quant_q = [&](int64_t wb, v4i (&qf)[4]) {
-    const int64_t row = wb * 32 + lq;
-    float x[4][16];
-    float am = QF == QF_WARP ? 0.0000001f : 0.f;  // the CUDA quantizer's amax floor
-#pragma unroll
-    for (int m = 0; m < 4; m++) {
-      v4u r0 = v4u{0, 0, 0, 0}, r1 = v4u{0, 0, 0, 0};
-      if (row < p.Lq) {
-        r0 = *reinterpret_cast<const v4u*>(qhead16 + row * p.qsl + m * 32 + hf * 16);
-        r1 = *reinterpret_cast<const v4u*>(qhead16 + row * p.qsl + m * 32 + hf * 16 + 8);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        x[m][2 * e] = half_to_f32<IS_FP16_OUT>((uint16_t)(r0[e] & 0xffffu));
-        x[m][2 * e + 1] = half_to_f32<IS_FP16_OUT>((uint16_t)(r0[e] >> 16));
-        x[m][8 + 2 * e] = half_to_f32<IS_FP16_OUT>((uint16_t)(r1[e] & 0xffffu));
-        x[m][8 + 2 * e + 1] = half_to_f32<IS_FP16_OUT>((uint16_t)(r1[e] >> 16));
-      }
-#pragma unroll
-      for (int e = 0; e < 16; e++) am = fmaxf(am, fabsf(x[m][e]));
-    }
-    if constexpr (QF == QF_WARP) {
-      am = fmaxf(am, __shfl_xor(am, 1, 64));
-      am = fmaxf(am, __shfl_xor(am, 2, 64));
-      am = fmaxf(am, __shfl_xor(am, 4, 64));
-    }
-    am = fmaxf(am, __shfl_xor(am, 8, 64));
-    am = fmaxf(am, __shfl_xor(am, 16, 64));
-    am = fmaxf(am, __shfl_xor(am, 32, 64));
-    const float sc = QF == QF_WARP ? quant_scale_cuda(am) : quant_scale_triton(am);
-    const float iv = QF == QF_WARP ? quant_recip_cuda(am) : refined_rcp(sc);
-#pragma unroll
-    for (int m = 0; m < 4; m++) {
-      int c[16];
-#pragma unroll
-      for (int e = 0; e < 16; e++) c[e] = QF == QF_WARP ? quant_code_cuda(x[m][e], iv) : quant_code_triton(x[m][e], sc, iv);
-#pragma unroll
-      for (int g = 0; g < 4; g++)
-        qf[m][g] = (c[4 * g] & 0xff) | ((c[4 * g + 1] & 0xff) << 8) | ((c[4 * g + 2] & 0xff) << 16) | (c[4 * g + 3] << 24);
-    }
-    return sc;
-  };
   v4i qf[4];
   int64_t wb = wb0 + w;
   v16i kbias;
@@ -1364,7 +1372,8 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
       load_q(wb, qf);
       qs = qs_tab[q_scale_index(p, wb * 32 + lq)] * p.qk_mult;
     } else {
-      qs = quant_q(wb, qf) * p.qk_mult;
+      const int64_t row = wb * 32 + lq;
+      qs = quant_q_rows<IS_FP16_OUT, QF, 4>(qhead16 + row * p.qsl, row < p.Lq, hf, qf) * p.qk_mult;
     }
     const int64_t wrow0 = wb * 32, qrow = wrow0 + lq;
 
@@ -1957,44 +1966,91 @@ extern "C" int qattn_fwd_ex2(qattn_seq q8, const float* q_scale, qattn_seq k8, c
   return launch_gran<PV_FP16>(p, qk_quant_gran, out_dtype, ns, workspace, workspace_bytes, st, D, kernel);
 }
 
-// ---- half Q quantized inside the resident kernel ----
-extern "C" int qattn_fwd_q16_supported(int64_t Lk, int64_t D, int causal) {
-  return D == kD && !causal && Lk > 0 && (Lk + kBK - 1) / kBK <= kResMaxTiles ? 1 : 0;
+// ---- half Q quantized inside the attention kernel (resident or ping-pong) ----
+// the kernel a qattn_fwd_q16 launch runs: the automatic rule's, when it is one of the two with a fused-Q form
+static int q16_kernel(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t D, int gran, int causal) {
+  if (D != kD || B <= 0 || Lq <= 0 || Lk <= 0 || Hq <= 0) return QATTN_KERNEL_AUTO;
+  int ns, qpw, kernel;
+  plan_fwd(B, Lq, Lk, Hq, PV_FP8, gran, causal, false, 0, ns, qpw, kernel);
+  return kernel == QATTN_KERNEL_RESIDENT || kernel == QATTN_KERNEL_PINGPONG ? kernel : QATTN_KERNEL_AUTO;
+}
+
+extern "C" int qattn_fwd_q16_supported(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t D, int qk_quant_gran,
+                                       int causal) {
+  if (qk_quant_gran != QATTN_GRAN_WARP && qk_quant_gran != QATTN_GRAN_THREAD) return 0;
+  return q16_kernel(B, Lq, Lk, Hq, D, qk_quant_gran, causal) != QATTN_KERNEL_AUTO ? 1 : 0;
+}
+
+template <int QF>
+static void launch_pp_q16(AttnParams& p, int dtype, int ns, hipStream_t st) {
+  constexpr bool KT = QF == QF_THREAD;
+  const int64_t g = p.B * p.Hq * ((p.nQB + 1) / 2) * ns;
+  if (ns > 1) {
+    const int64_t rows = p.B * p.Hq * p.Lq;
+    if (dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT, true, kD, QF><<<g, kPPThreads, 0, st>>>(p);
+    else qattn_fwd_pp_kernel<true, KT, true, kD, QF><<<g, kPPThreads, 0, st>>>(p);
+    if (dtype == QATTN_BF16) qattn_combine_kernel<false><<<(rows + 3) / 4, 256, 0, st>>>(p);
+    else qattn_combine_kernel<true><<<(rows + 3) / 4, 256, 0, st>>>(p);
+  } else {
+    if (dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT, false, kD, QF><<<g, kPPThreads, 0, st>>>(p);
+    else qattn_fwd_pp_kernel<true, KT, false, kD, QF><<<g, kPPThreads, 0, st>>>(p);
+  }
 }
 
 extern "C" int qattn_fwd_q16(qattn_seq q, qattn_seq k8, const float* k_scale, const uint8_t* v8, int64_t Lpad,
                              const float* v_scale, const float* v_mean, qattn_seq o, int dtype, int64_t B,
                              int64_t Lq, int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult,
-                             int qk_quant_gran, const int32_t* kv_valid, float* lse, qattn_stream_t stream) {
+                             int qk_quant_gran, int causal, int64_t q_offset, const int32_t* kv_valid, float* lse,
+                             int num_splits, void* workspace, size_t workspace_bytes, qattn_stream_t stream) {
   QATTN_REQUIRE(qk_quant_gran == QATTN_GRAN_WARP || qk_quant_gran == QATTN_GRAN_THREAD, QATTN_ERR_ARG,
                 "qattn_fwd_q16 quantizes Q per warp (2) or per thread (3), got %d", qk_quant_gran);
-  QATTN_REQUIRE(qattn_fwd_q16_supported(Lk, D, 0), QATTN_ERR_SHAPE,
-                "qattn_fwd_q16 needs head_dim 128 and at most %d keys (got %lld, %lld)", kResMaxTiles * kBK,
-                (long long)D, (long long)Lk);
   QATTN_REQUIRE(v8 && v_scale, QATTN_ERR_ARG, "null V or v_scale");
+  if (B * Lq == 0) return QATTN_OK;
+  const int kernel = q16_kernel(B, Lq, Lk, Hq, D, qk_quant_gran, causal);
+  QATTN_REQUIRE(kernel != QATTN_KERNEL_AUTO, QATTN_ERR_SHAPE,
+                "qattn_fwd_q16 runs the resident or ping-pong kernel: head_dim 128 and a launch the automatic rule "
+                "gives one of them (see qattn_fwd_q16_supported)");
   AttnParams p;
-  int ns = 1, kernel = QATTN_KERNEL_AUTO;
+  int ns = 1, kplan = QATTN_KERNEL_AUTO;
   // (q's scale table is formed inside the kernel: k_scale stands in for the pointer setup_fwd checks)
-  const int rc = setup_fwd(p, ns, q, k_scale, k8, k_scale, v8, Lpad, o, dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult, 0, 0,
-                           kv_valid, lse, 1, PV_FP8, qk_quant_gran, kernel);
+  const int rc = setup_fwd(p, ns, q, k_scale, k8, k_scale, v8, Lpad, o, dtype, B, Lq, Lk, Hq, Hkv, D, qk_mult, causal,
+                           q_offset, kv_valid, lse, num_splits, PV_FP8, qk_quant_gran, kplan);
   if (rc < 0) return QATTN_OK;
   if (rc) return rc;
+  QATTN_REQUIRE(kplan == kernel, QATTN_ERR_ARG, "qattn_fwd_q16: num_splits %d moves the launch off its kernel",
+                num_splits);
   p.v_scale = v_scale;
   p.v_mean = v_mean;
-  p.nsplit = 1;
-  p.tiles_per_split = (int)p.nKB;
-  resident_layout(p.B * p.Hq, (p.Lq + 31) / 32, p.wb_per_wg, p.n_chunk);
-  const int64_t g = p.B * p.Hq * p.n_chunk;
-  QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
   hipStream_t st = (hipStream_t)stream;
-  t_last_kernel = QATTN_KERNEL_RESIDENT;
-  if (qk_quant_gran == QATTN_GRAN_THREAD) {
-    if (dtype == QATTN_BF16) qattn_fwd_res_kernel<false, true, QF_THREAD><<<g, kResThreads, 0, st>>>(p);
-    else qattn_fwd_res_kernel<true, true, QF_THREAD><<<g, kResThreads, 0, st>>>(p);
-  } else {
-    if (dtype == QATTN_BF16) qattn_fwd_res_kernel<false, false, QF_WARP><<<g, kResThreads, 0, st>>>(p);
-    else qattn_fwd_res_kernel<true, false, QF_WARP><<<g, kResThreads, 0, st>>>(p);
+  t_last_kernel = kernel;
+  if (kernel == QATTN_KERNEL_RESIDENT) {
+    p.nsplit = 1;
+    p.tiles_per_split = (int)p.nKB;
+    resident_layout(p.B * p.Hq, (p.Lq + 31) / 32, p.wb_per_wg, p.n_chunk);
+    const int64_t g = p.B * p.Hq * p.n_chunk;
+    QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
+    if (qk_quant_gran == QATTN_GRAN_THREAD) {
+      if (dtype == QATTN_BF16) qattn_fwd_res_kernel<false, true, QF_THREAD><<<g, kResThreads, 0, st>>>(p);
+      else qattn_fwd_res_kernel<true, true, QF_THREAD><<<g, kResThreads, 0, st>>>(p);
+    } else {
+      if (dtype == QATTN_BF16) qattn_fwd_res_kernel<false, false, QF_WARP><<<g, kResThreads, 0, st>>>(p);
+      else qattn_fwd_res_kernel<true, false, QF_WARP><<<g, kResThreads, 0, st>>>(p);
+    }
+    return check_launch("qattn_fwd_q16");
   }
+  const int64_t g = p.B * p.Hq * ((p.nQB + 1) / 2) * ns;
+  QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
+  p.nsplit = ns;
+  p.tiles_per_split = (int)((p.nKB + ns - 1) / ns);
+  if (ns > 1) {
+    QATTN_REQUIRE(workspace && workspace_bytes >= qattn_fwd_workspace_size(p.B, p.Lq, p.Hq, D, ns),
+                  QATTN_ERR_WORKSPACE, "qattn_fwd_q16 with %d KV splits needs %zu workspace bytes", ns,
+                  qattn_fwd_workspace_size(p.B, p.Lq, p.Hq, D, ns));
+    p.ws_o = static_cast<float*>(workspace);
+    p.ws_ml = p.ws_o + (int64_t)ns * p.B * p.Hq * p.Lq * D;
+  }
+  if (qk_quant_gran == QATTN_GRAN_THREAD) launch_pp_q16<QF_THREAD>(p, dtype, ns, st);
+  else launch_pp_q16<QF_WARP>(p, dtype, ns, st);
   return check_launch("qattn_fwd_q16");
 }
 

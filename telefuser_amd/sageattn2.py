@@ -344,14 +344,14 @@ def qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout
     return (o, lse) if return_lse else o
 
 
-def qattn_fwd_q16(q, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout="HND", qk_mult=1.0, kv_valid_len=None,
-                  return_lse=False, qk_quant_gran="per_thread", out: Optional[torch.Tensor] = None,
-                  v_mean: Optional[torch.Tensor] = None):
-    """Attention on half-precision Q for short key ranges (qattn_fwd_q16 in the C ABI): Q is quantized per
-    thread (Triton rounding) or per warp (CUDA rounding) inside the resident-K/V kernel, bit-identical to
+def qattn_fwd_q16(q, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout="HND", qk_mult=1.0, is_causal=False,
+                  q_offset=0, kv_valid_len=None, return_lse=False, num_splits=0, qk_quant_gran="per_thread",
+                  out: Optional[torch.Tensor] = None, v_mean: Optional[torch.Tensor] = None):
+    """Attention on half-precision Q (qattn_fwd_q16 in the C ABI): Q is quantized per thread (Triton rounding)
+    or per warp (CUDA rounding) inside the resident-K/V or ping-pong kernel, bit-identical to
     per_thread_int8 / per_warp_int8 followed by qattn_fwd, without the int8 Q round trip through memory.
-    Non-causal, head_dim 128, at most 512 keys (qattn_fwd_q16_supported).  Returns o (and the log2-domain
-    LSE)."""
+    head_dim 128, launches whose automatic kernel is one of those two (q16_supported).  Returns o (and the
+    log2-domain LSE)."""
     L = _lib.load()
     b, lq, hq, d = _dims(q, tensor_layout)
     _, lk, hkv, _ = _dims(k_int8, tensor_layout)
@@ -361,8 +361,9 @@ def qattn_fwd_q16(q, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout="HND", qk
         raise ValueError(f"qk_quant_gran must be 'per_warp' or 'per_thread', got {qk_quant_gran!r}")
     if q.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("q must be bf16 or fp16")
-    if not L.qattn_fwd_q16_supported(lk, d, 0):
-        raise ValueError(f"qattn_fwd_q16 needs head_dim 128 and at most 512 keys, got {d} and {lk}")
+    gran = _GRAN[qk_quant_gran]
+    if not q16_supported(b, lq, lk, hq, d, qk_quant_gran, is_causal):
+        raise ValueError(f"qattn_fwd_q16 does not cover this launch (head_dim {d}, {lq} x {lk}, causal={is_causal})")
     if v_scale is None:
         raise ValueError("qattn_fwd_q16 takes the e4m3 V tile and its v_scale")
     _check_attn_operands(q, None, k_int8, k_scale, v_fp8, v_scale, b, lq, lk, hq, hkv, d, qk_quant_gran, out, q.dtype)
@@ -372,12 +373,22 @@ def qattn_fwd_q16(q, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout="HND", qk
     o = out if out is not None else torch.empty(q.shape, dtype=q.dtype, device=q.device)
     lse = torch.empty((b, hq, lq), dtype=torch.float32, device=q.device) if return_lse else None
     kvv = _kv_valid_tensor(kv_valid_len, b, q.device)
-    gran = _GRAN[qk_quant_gran]
+    ns = num_splits if num_splits > 0 else L.qattn_fwd_ex_num_splits(b, lq, lk, hq, _lib.QATTN_V_FP8, gran)
+    wsb = L.qattn_fwd_workspace_size(b, lq, hq, d, ns)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=q.device) if wsb else None
     _lib.check(L.qattn_fwd_q16(
         _lib.seq(q, tensor_layout), _lib.seq(k_int8, tensor_layout), _lib.ptr(k_scale), _lib.ptr(v_fp8),
         v_fp8.shape[-1], _lib.ptr(v_scale), _lib.ptr(v_mean), _lib.seq(o, tensor_layout), _lib.dtype_code(q.dtype),
-        b, lq, lk, hq, hkv, d, float(qk_mult), gran, _lib.ptr(kvv), _lib.ptr(lse), _lib.stream_of(q)))
+        b, lq, lk, hq, hkv, d, float(qk_mult), gran, int(bool(is_causal)), int(q_offset), _lib.ptr(kvv), _lib.ptr(lse),
+        ns, _lib.ptr(ws), wsb, _lib.stream_of(q)))
     return (o, lse) if return_lse else o
+
+
+def q16_supported(b, lq, lk, hq, d, qk_quant_gran, is_causal=False) -> bool:
+    """Whether qattn_fwd_q16 (Q quantized inside the attention kernel) covers a launch of these sizes."""
+    if qk_quant_gran not in ("per_warp", "per_thread"):
+        return False
+    return bool(_lib.load().qattn_fwd_q16_supported(b, lq, lk, hq, d, _GRAN[qk_quant_gran], int(bool(is_causal))))
 
 
 def _pad_head_dim(x: torch.Tensor, native64: bool = False) -> torch.Tensor:
@@ -435,15 +446,16 @@ def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv
         q_int8, q_scale, k_int8, k_scale, km, v_fp8, v_scale, vm = sage_quant(
             q, k, v, tensor_layout=tensor_layout, qk_quant_gran=qk_quant_gran, sm_scale=sm_scale, smooth_k=smooth_k,
             scale_max=448.0, smooth_v=False, scale_layout="sm90")
-    elif (pv == "fp8" and quant_variant == "cuda" and qk_quant_gran != "per_block" and not is_causal and
-          _lib.load().qattn_fwd_q16_supported(lk, q.size(-1), 0)):
-        # short key ranges: K mean, K INT8 and V FP8 in the fused prologue, Q quantized inside the resident
+    elif (pv == "fp8" and quant_variant == "cuda" and
+          q16_supported(b, lq, lk, hq, q.size(-1), qk_quant_gran, is_causal)):
+        # per-thread / per-warp scales: K mean, K INT8 and V FP8 in the fused prologue, Q quantized inside the
         # attention kernel (bit-identical to quantizing it first)
         _, _, k_int8, k_scale, km, v_fp8, v_scale, vm = sage_quant(
             q, k, v, tensor_layout=tensor_layout, qk_quant_gran=qk_quant_gran, sm_scale=sm_scale, smooth_k=smooth_k,
             scale_max=scale_max, smooth_v=smooth_v, quantize_q=False)
         res = qattn_fwd_q16(q, k_int8, k_scale, v_fp8, v_scale, tensor_layout=tensor_layout, qk_mult=qk_mult,
-                            kv_valid_len=kv_valid_len, return_lse=return_lse, qk_quant_gran=qk_quant_gran, v_mean=vm)
+                            is_causal=is_causal, q_offset=q_offset, kv_valid_len=kv_valid_len, return_lse=return_lse,
+                            qk_quant_gran=qk_quant_gran, v_mean=vm)
         return _sage_finish(res, q, km, hq, hkv, head_dim_og, tensor_layout, sm_scale, smooth_k, return_lse)
     elif pv == "fp8" and quant_variant == "cuda":
         # K mean, Q/K INT8 and V FP8 in one fused prologue (four launches)
@@ -660,6 +672,7 @@ __all__ = [
     "sageattn_qk_int8_pv_fp8_cuda",
     "sageattn_qk_int8_pv_fp8_cuda_sm90",
     "qattn_fwd_q16",
+    "q16_supported",
     "sageattn_qk_int8_pv_fp16_cuda",
     "sageattn_qk_int8_pv_fp16_triton",
     "v_tile_half",

@@ -124,12 +124,13 @@ def test_qattn_fwd_sm90_layout_checks(bad):
         sa.qattn_fwd(q8, qs, k8, ks, v, vs, **kw)
 
 
-@pytest.mark.parametrize("bad", ["per_block", "too_many_keys", "int8_q", "k_scale_gran", "no_v_scale"])
+@pytest.mark.parametrize("bad", ["per_block", "small_grid_long_keys", "int8_q", "k_scale_gran", "no_v_scale"])
 def test_fwd_q16_rejects(bad):
-    """qattn_fwd_q16 takes half Q, per-warp / per-thread K scales, the e4m3 V tile, at most 512 keys."""
+    """qattn_fwd_q16 takes half Q, per-warp / per-thread K scales and the e4m3 V tile, for launches the resident
+    or ping-pong kernel runs (300 queries of 4 heads over 600 keys run the one-block kernel)."""
     from telefuser_amd import sageattn2 as sa
 
-    lk = 600 if bad == "too_many_keys" else 300
+    lk = 600 if bad == "small_grid_long_keys" else 300
     q8, qs, k8, ks, v, vs = _ops(Lk=lk, gran="per_thread")
     q = torch.zeros(q8.shape, dtype=torch.bfloat16)
     kw = dict(tensor_layout="NHD", qk_quant_gran="per_thread")

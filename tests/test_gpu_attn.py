@@ -894,12 +894,16 @@ def test_pv_accum_modes_and_smooth_v(oracle, mode):
 
 
 Q16_CASES = {
-    # name: (B, Lq, Lk, Hq, Hkv, layout, dtype, gran, kv_valid, smooth_v)
-    "thread_c4_like": (1, 1000, 512, 4, 4, "NHD", torch.bfloat16, "per_thread", [388], False),
-    "warp_ragged_gqa": (2, 333, 300, 4, 2, "NHD", torch.bfloat16, "per_warp", None, False),
-    "thread_hnd_fp16": (1, 517, 130, 3, 3, "HND", torch.float16, "per_thread", None, False),
-    "thread_smooth_v_short_q": (2, 40, 64, 2, 1, "NHD", torch.bfloat16, "per_thread", [64, 17], True),
-    "warp_fp16_keys_512": (1, 777, 512, 2, 2, "NHD", torch.float16, "per_warp", None, True),
+    # name: (B, Lq, Lk, Hq, Hkv, layout, dtype, gran, kv_valid, smooth_v, causal); the first five run the
+    # resident kernel (at most 512 keys), the others the ping-pong kernel (unsplit, KV split, causal)
+    "thread_c4_like": (1, 1000, 512, 4, 4, "NHD", torch.bfloat16, "per_thread", [388], False, False),
+    "warp_ragged_gqa": (2, 333, 300, 4, 2, "NHD", torch.bfloat16, "per_warp", None, False, False),
+    "thread_hnd_fp16": (1, 517, 130, 3, 3, "HND", torch.float16, "per_thread", None, False, False),
+    "thread_smooth_v_short_q": (2, 40, 64, 2, 1, "NHD", torch.bfloat16, "per_thread", [64, 17], True, False),
+    "warp_fp16_keys_512": (1, 777, 512, 2, 2, "NHD", torch.float16, "per_warp", None, True, False),
+    "pp_thread_unsplit": (1, 4680, 6000, 12, 12, "NHD", torch.bfloat16, "per_thread", None, False, False),
+    "pp_warp_split_gqa": (1, 2000, 20000, 8, 4, "NHD", torch.bfloat16, "per_warp", [19000], False, False),
+    "pp_thread_causal_fp16": (2, 1500, 3000, 8, 8, "HND", torch.float16, "per_thread", None, False, True),
 }
 
 
@@ -911,8 +915,10 @@ def test_fwd_q16_matches_quantize_then_attend(oracle, case):
     dev = require_gpu()
     from telefuser_amd import sageattn2 as sa
 
-    B, Lq, Lk, Hq, Hkv, layout, dt, gran, kv_valid, smooth_v = Q16_CASES[case]
-    log(f"fwd_q16 {case}: B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} {layout} {dt} {gran} kv_valid={kv_valid}")
+    B, Lq, Lk, Hq, Hkv, layout, dt, gran, kv_valid, smooth_v, causal = Q16_CASES[case]
+    log(f"fwd_q16 {case}: B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} {layout} {dt} {gran} kv_valid={kv_valid} "
+        f"causal={causal}")
+    assert sa.q16_supported(B, Lq, Lk, Hq, 128, gran, causal)
     q, k, v = qkv(B, Lq, Lk, Hq, Hkv, seed=53, k_offset_std=0.5, dtype=dt)
     qd, kd, vd = (t.to(dev) for t in (q, k, v))
     if layout == "HND":
@@ -923,15 +929,16 @@ def test_fwd_q16_matches_quantize_then_attend(oracle, case):
     v8, vs, vm = sa.per_channel_fp8(vd, tensor_layout=layout, smooth_v=smooth_v)
     qk_mult = 128 ** -0.5 * LOG2E
     o_ref, l_ref = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout=layout, out_dtype=dt, qk_mult=qk_mult,
-                                kv_valid_len=kv_valid, return_lse=True, qk_quant_gran=gran, v_mean=vm)
-    o, l = sa.qattn_fwd_q16(qd, k8, ks, v8, vs, tensor_layout=layout, qk_mult=qk_mult, kv_valid_len=kv_valid,
-                            return_lse=True, qk_quant_gran=gran, v_mean=vm)
+                                is_causal=causal, kv_valid_len=kv_valid, return_lse=True, qk_quant_gran=gran,
+                                v_mean=vm)
+    o, l = sa.qattn_fwd_q16(qd, k8, ks, v8, vs, tensor_layout=layout, qk_mult=qk_mult, is_causal=causal,
+                            kv_valid_len=kv_valid, return_lse=True, qk_quant_gran=gran, v_mean=vm)
     torch.cuda.synchronize()
     assert torch.equal(o, o_ref), f"max diff {float((o.float() - o_ref.float()).abs().max())}"
     assert torch.equal(l, l_ref)
     # the drop-in on the same inputs: identical to its quantize-then-attend steps
     kw = dict(tensor_layout=layout, qk_quant_gran=gran, pv_accum_dtype="fp32" if smooth_v else "fp32+fp32",
-              smooth_v=smooth_v, kv_valid_len=kv_valid, return_lse=True)
+              smooth_v=smooth_v, kv_valid_len=kv_valid, return_lse=True, is_causal=causal)
     od, ld = sa.sageattn_qk_int8_pv_fp8_cuda(qd, kd, vd, **kw)
     torch.cuda.synchronize()
     assert torch.equal(od, o)
@@ -939,5 +946,8 @@ def test_fwd_q16_matches_quantize_then_attend(oracle, case):
     if layout == "HND":
         od = od.transpose(1, 2)
     bits = (lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)) if dt == torch.float16 else bf16_bits
-    truth = oracle.attn_fp64(bits(q), bits(k), bits(v), 128 ** -0.5, kv_valid=kv_valid, is_fp16=dt == torch.float16)
-    assert cosine(od.float().cpu().numpy(), truth) >= COS_E2E
+    # float64 truth on the first 256 rows of heads 0 and 1 (and their KV heads)
+    rows, nkv = slice(0, min(Lq, 256)), max(1, 2 * Hkv // Hq)
+    truth = oracle.attn_fp64(bits(q[:, rows, :2]), bits(k[:, :, :nkv]), bits(v[:, :, :nkv]), 128 ** -0.5,
+                             kv_valid=kv_valid, is_fp16=dt == torch.float16, causal=causal)
+    assert cosine(od[:, rows, :2].float().cpu().numpy(), truth) >= COS_E2E
