@@ -208,7 +208,8 @@ def _prologue_bench(reps: int = 10) -> dict:
 
 def _config_bench(name: str, calls: int = 5, warmup: int = 2) -> dict:
     """One BASELINE config through the same drop-in sequence as the headline step (the fused prologue:
-    K mean, per-block Q/K quantizer, V fp8; then the attention), inputs resident in HBM: ms per call, the attention launch alone (HIP
+    K mean, per-block K (and Q) quantizer, V fp8; then the attention, which quantizes Q itself where
+    qattn_fwd_q16 covers the launch), inputs resident in HBM: ms per call, the attention launch alone (HIP
     events on the launch stream) and its roofline fraction.  C4's attention launch is bounded by HBM
     (int8 Q + K + e4m3 V read once, bf16 O written), the others by the dense INT8/FP8 MFMA peak."""
     import torch
@@ -224,12 +225,18 @@ def _config_bench(name: str, calls: int = 5, warmup: int = 2) -> dict:
     L = _lib.load()
     t_attn = []
 
+    q16 = sa.q16_supported(cfg.B, cfg.Lq, cfg.Lk, cfg.Hq, cfg.D, "per_block")
+
     def call(record):
-        q8, qs, k8, ks, _, v8, vs, _ = sa.sage_quant(q, k, v, tensor_layout="NHD", sm_scale=sm)
+        q8, qs, k8, ks, _, v8, vs, _ = sa.sage_quant(q, k, v, tensor_layout="NHD", sm_scale=sm, quantize_q=not q16)
         s = torch.cuda.current_stream()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record(s)
-        o = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout="NHD", out_dtype=q.dtype, kv_valid_len=kvv)
+        if q16:
+            o = sa.qattn_fwd_q16(q, k8, ks, v8, vs, tensor_layout="NHD", qk_mult=sm * sa.LOG2E, kv_valid_len=kvv,
+                                 qk_quant_gran="per_block")
+        else:
+            o = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout="NHD", out_dtype=q.dtype, kv_valid_len=kvv)
         e1.record(s)
         if record:
             t_attn.append((e0, e1))
@@ -252,13 +259,15 @@ def _config_bench(name: str, calls: int = 5, warmup: int = 2) -> dict:
     ms_attn = sum(a.elapsed_time(b) for a, b in t_attn) / len(t_attn)
     ops = cfg.ops()
     res = {"workload": cfg.name, "calls": calls, "ms_per_call": round(ms_call, 4), "attn_ms": round(ms_attn, 4),
+           "q_quantized_in_attention": q16,
            "attn_kernel": kernel + (f" + qattn_combine_kernel ({splits} KV splits)" if splits > 1 else ""),
            "attn_TOPS": round(ops / (ms_attn * 1e-3) / 1e12, 2),
            "call_TOPS": round(ops / (ms_call * 1e-3) / 1e12, 2),
            "mfma_frac": round(ops / (ms_attn * 1e-3) / peak_ops("fp8"), 4)}
     if name == "c4":
-        # algorithmic HBM bytes of the attention launch: int8 Q + int8 K + e4m3 V read once, bf16 O written
-        byts = cfg.B * cfg.Hq * cfg.Lq * cfg.D * (1 + 2) + 2 * cfg.B * cfg.Hkv * cfg.Lk * cfg.D
+        # algorithmic HBM bytes of the attention launch: Q (int8, or bf16 when the kernel quantizes it) + int8 K
+        # + e4m3 V read once, bf16 O written
+        byts = cfg.B * cfg.Hq * cfg.Lq * cfg.D * ((2 if q16 else 1) + 2) + 2 * cfg.B * cfg.Hkv * cfg.Lk * cfg.D
         res["bound"] = "hbm"
         res["attn_GB/s"] = round(byts / (ms_attn * 1e-3) / 1e9, 1)
         res["hbm_frac"] = round(byts / (ms_attn * 1e-3) / 8e12, 4)
@@ -366,18 +375,26 @@ def main() -> int:
     layout = "NHD"
 
     ev = {n: [] for n in ("attn", "quant")}
+    # the drop-in's route for per-block scales: Q quantized inside the attention kernel where qattn_fwd_q16
+    # covers the launch (the prologue then quantizes K and V only)
+    q16 = sa.q16_supported(cfg.B, cfg.Lq, cfg.Lk, cfg.Hq, cfg.D, "per_block")
 
     def step(i: int, record: bool):
         q, k, v, kvv = inputs[i % n_inputs]
         if record:
             e0 = torch.cuda.Event(enable_timing=True)
             e0.record()
-        q8, qs, k8, ks, _, v8, vs, _ = sa.sage_quant(q, k, v, tensor_layout=layout, sm_scale=sm_scale)
+        q8, qs, k8, ks, _, v8, vs, _ = sa.sage_quant(q, k, v, tensor_layout=layout, sm_scale=sm_scale,
+                                                     quantize_q=not q16)
         if record:
             e1 = torch.cuda.Event(enable_timing=True)
             e1.record()
             e2 = e1
-        o = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout=layout, out_dtype=q.dtype, kv_valid_len=kvv)
+        if q16:
+            o = sa.qattn_fwd_q16(q, k8, ks, v8, vs, tensor_layout=layout, qk_mult=sm_scale * sa.LOG2E,
+                                 kv_valid_len=kvv, qk_quant_gran="per_block")
+        else:
+            o = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout=layout, out_dtype=q.dtype, kv_valid_len=kvv)
         if record:
             e3 = torch.cuda.Event(enable_timing=True)
             e3.record()
@@ -404,8 +421,9 @@ def main() -> int:
     attn_tops = ops / (attn_ms * 1e-3) / 1e12
     q_elems = cfg.B * cfg.Lq * cfg.Hq * cfg.D
     k_elems = cfg.B * cfg.Lk * cfg.Hkv * cfg.D
-    # single-pass bytes of the prologue: bf16 Q, K, V read once, int8 Q/K and e4m3 V written once
-    quant_bytes = 3 * (q_elems + 2 * k_elems)
+    # single-pass bytes of the prologue: bf16 K, V (and Q, unless the attention kernel quantizes it) read
+    # once, int8 K (Q) and e4m3 V written once
+    quant_bytes = 3 * ((0 if q16 else q_elems) + 2 * k_elems)
 
     sdpa_ms = None
     if not args.no_sdpa:
@@ -453,7 +471,9 @@ def main() -> int:
                      "frac": round(attn_tops / peak, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "kernel": kernel_ran, "kernel_ms": round(attn_ms, 4),
                      "algorithmic_ops_per_launch": ops},
-        "pre_attention": {"entry": "qattn_sage_quant (K mean, Q/K INT8 per block, V FP8)",
+        "pre_attention": {"entry": ("qattn_sage_quant (K mean, K INT8 per block, V FP8; Q quantized inside the "
+                                    "attention kernel, qattn_fwd_q16)") if q16 else
+                                   "qattn_sage_quant (K mean, Q/K INT8 per block, V FP8)",
                           "kernels": "prep_col_kernel, prep_finalize_kernel, v_fp8_kernel, quant_per_block_kernel",
                           "ms": round(quant_ms, 4), "single_pass_bytes": quant_bytes,
                           "GB/s_vs_single_pass": round(quant_bytes / (quant_ms * 1e-3) / 1e9, 1), "peak_GB/s": 8000},

@@ -97,6 +97,7 @@ struct AttnParams {
   int64_t B, Lq, Lk, Hq, Hkv, nQB, nKB;
   int64_t nQS, nKS;  // scale entries per (b, h)
   int qgran;         // QATTN_GRAN_BLOCK / _WARP / _THREAD (q_scale indexing)
+  float q_sm_scale;  // Q quantized per block inside the kernel: the factor multiplied into Q first
   int qrs;           // log2 of the rows of a warp cell of q_scale: 5 (sm89 tables) or 4 (sm90 tables)
   int kts;           // key tiles (64 keys) per k_scale block, as a shift: 0 (64-key blocks) or 1 (128)
   int64_t q_offset;
@@ -836,21 +837,22 @@ __global__ __launch_bounds__(kThreads, kWavesPerSimd) void qattn_fwd_kernel(Attn
 constexpr int kPPThreads = 512;
 constexpr int kPPNBuf = 4;
 
-// QF: Q as int8 with its scale table (0), or Q in the output's half type quantized by each wave for its own
-// 32 rows: with the per-thread classes of the Triton quantizer (QF_THREAD: rows with equal row % 8 share a
-// scale, round half away from x / scale) or the per-warp blocks of the CUDA one (QF_WARP: the 32 rows share
-// a scale, RNE of x * 127 / amax) -- the codes and scales of per_thread_int8 / per_warp_int8 bit for bit,
-// without writing int8 Q out and reading it back.
-constexpr int QF_INT8 = 0, QF_THREAD = 1, QF_WARP = 2;
+// QF: Q as int8 with its scale table (0), or Q in the output's half type quantized inside the attention
+// kernel: with the per-thread classes of the Triton quantizer (QF_THREAD: rows with equal row % 8 of a wave's
+// 32 share a scale, round half away from x / scale), the per-warp blocks of the CUDA one (QF_WARP: a wave's
+// 32 rows share a scale, RNE of x * 127 / amax), or its per-block form (QF_BLOCK, ping-pong kernel only:
+// the 128 rows of a wave group share a scale, x multiplied by sm_scale * log2(e) first) -- the codes and
+// scales of per_thread_int8 / per_warp_int8 / per_block_int8 bit for bit, without writing int8 Q out and
+// reading it back.
+constexpr int QF_INT8 = 0, QF_THREAD = 1, QF_WARP = 2, QF_BLOCK = 3;
 
 // Lane (lq, hf) of a wave whose 32 query rows are lq = lane % 32: the 16 NQF values of its row (row pointer
-// rowp, half type; zeros when !valid) at 32 m + 16 hf .. + 16, their |x| maximum over the lane's scale group
-// (per-thread class: lanes lq ^ 8, lq ^ 16 and the other half-row; per-warp: all 64 lanes, with the CUDA
-// quantizer's 1e-7 floor), the group's scale (returned) and the int8 codes as the MFMA B fragments qf.
-template <bool IS_FP16, int QF, int NQF>
-__device__ __forceinline__ float quant_q_rows(const uint16_t* rowp, bool valid, int hf, v4i (&qf)[NQF]) {
-  float x[NQF][16];
-  float am = QF == QF_WARP ? 0.0000001f : 0.f;
+// rowp, half type; zeros when !valid) at 32 m + 16 hf .. + 16, times mul when MUL (fp32), and their |x|
+// maximum over the lane's scale group within the wave (per-thread class: lanes lq ^ 8, lq ^ 16 and the other
+// half-row; per-warp / per-block: all 64 lanes, from the CUDA quantizer's 1e-7 floor).
+template <bool IS_FP16, int QF, int NQF, bool MUL = false>
+__device__ __forceinline__ float quant_q_load(const uint16_t* rowp, bool valid, int hf, float mul, float (&x)[NQF][16]) {
+  float am = QF == QF_THREAD ? 0.f : 0.0000001f;
 #pragma unroll
   for (int m = 0; m < NQF; m++) {
     v4u r0 = v4u{0, 0, 0, 0}, r1 = v4u{0, 0, 0, 0};
@@ -866,9 +868,12 @@ __device__ __forceinline__ float quant_q_rows(const uint16_t* rowp, bool valid, 
       x[m][8 + 2 * e + 1] = half_to_f32<IS_FP16>((uint16_t)(r1[e] >> 16));
     }
 #pragma unroll
-    for (int e = 0; e < 16; e++) am = fmaxf(am, fabsf(x[m][e]));
+    for (int e = 0; e < 16; e++) {
+      if constexpr (MUL) x[m][e] = x[m][e] * mul;
+      am = fmaxf(am, fabsf(x[m][e]));
+    }
   }
-  if constexpr (QF == QF_WARP) {
+  if constexpr (QF != QF_THREAD) {
     am = fmaxf(am, __shfl_xor(am, 1, 64));
     am = fmaxf(am, __shfl_xor(am, 2, 64));
     am = fmaxf(am, __shfl_xor(am, 4, 64));
@@ -876,18 +881,34 @@ __device__ __forceinline__ float quant_q_rows(const uint16_t* rowp, bool valid, 
   am = fmaxf(am, __shfl_xor(am, 8, 64));
   am = fmaxf(am, __shfl_xor(am, 16, 64));
   am = fmaxf(am, __shfl_xor(am, 32, 64));
-  const float sc = QF == QF_WARP ? quant_scale_cuda(am) : quant_scale_triton(am);
-  const float iv = QF == QF_WARP ? quant_recip_cuda(am) : refined_rcp(sc);
+  return am;
+}
+
+// The scale of a group with |x| maximum am (returned) and the int8 codes as the MFMA B fragments qf.
+template <int QF, int NQF>
+__device__ __forceinline__ float quant_q_codes(const float (&x)[NQF][16], float am, v4i (&qf)[NQF]) {
+  constexpr bool TRITON = QF == QF_THREAD;
+  const float sc = TRITON ? quant_scale_triton(am) : quant_scale_cuda(am);
+  const float iv = TRITON ? refined_rcp(sc) : quant_recip_cuda(am);
 #pragma unroll
   for (int m = 0; m < NQF; m++) {
     int c[16];
 #pragma unroll
-    for (int e = 0; e < 16; e++) c[e] = QF == QF_WARP ? quant_code_cuda(x[m][e], iv) : quant_code_triton(x[m][e], sc, iv);
+    for (int e = 0; e < 16; e++) c[e] = TRITON ? quant_code_triton(x[m][e], sc, iv) : quant_code_cuda(x[m][e], iv);
 #pragma unroll
     for (int g = 0; g < 4; g++)
       qf[m][g] = (c[4 * g] & 0xff) | ((c[4 * g + 1] & 0xff) << 8) | ((c[4 * g + 2] & 0xff) << 16) | (c[4 * g + 3] << 24);
   }
   return sc;
+}
+
+// per-thread / per-warp: both steps within the wave
+template <bool IS_FP16, int QF, int NQF>
+__device__ __forceinline__ float quant_q_rows(const uint16_t* rowp, bool valid, int hf, v4i (&qf)[NQF]) {
+  static_assert(QF == QF_THREAD || QF == QF_WARP, "wave-local scale groups");
+  float x[NQF][16];
+  const float am = quant_q_load<IS_FP16, QF, NQF>(rowp, valid, hf, 1.f, x);
+  return quant_q_codes<QF, NQF>(x, am, qf);
 }
 
 // workgroup barrier that the compiler neither crosses with memory operations nor schedules around
@@ -962,7 +983,18 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   uint8_t* stage = &lds_k[0][0] + w * 4096;
   v4i qf[NQF];
   float qs;
-  if constexpr (QF != QF_INT8) {
+  if constexpr (QF == QF_BLOCK) {
+    // half Q quantized per 128-row block: the four waves of a group exchange their maxima through LDS
+    // (q_sm_scale = sm_scale * log2(e) multiplied in first; the logits then take qk_mult = 1)
+    __shared__ float lds_qam[8];
+    const uint16_t* qh16 = reinterpret_cast<const uint16_t*>(p.q8) + b * p.qsb + h * p.qsh;
+    float x[NQF][16];
+    const float am_w = quant_q_load<IS_FP16_OUT, QF, NQF, true>(qh16 + qrow * p.qsl, qrow < p.Lq, hf, p.q_sm_scale, x);
+    if (lane == 0) lds_qam[w] = am_w;
+    __syncthreads();
+    const float am = fmaxf(fmaxf(lds_qam[grp * 4], lds_qam[grp * 4 + 1]), fmaxf(lds_qam[grp * 4 + 2], lds_qam[grp * 4 + 3]));
+    qs = quant_q_codes<QF, NQF>(x, am, qf) * p.qk_mult;
+  } else if constexpr (QF != QF_INT8) {
     // half Q quantized by the wave itself (see quant_q_rows)
     const uint16_t* qh16 = reinterpret_cast<const uint16_t*>(p.q8) + b * p.qsb + h * p.qsh;
     qs = quant_q_rows<IS_FP16_OUT, QF, NQF>(qh16 + qrow * p.qsl, qrow < p.Lq, hf, qf) * p.qk_mult;
@@ -1972,12 +2004,14 @@ static int q16_kernel(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t D, 
   if (D != kD || B <= 0 || Lq <= 0 || Lk <= 0 || Hq <= 0) return QATTN_KERNEL_AUTO;
   int ns, qpw, kernel;
   plan_fwd(B, Lq, Lk, Hq, PV_FP8, gran, causal, false, 0, ns, qpw, kernel);
-  return kernel == QATTN_KERNEL_RESIDENT || kernel == QATTN_KERNEL_PINGPONG ? kernel : QATTN_KERNEL_AUTO;
+  // (per-block scales need the ping-pong kernel's workgroup-wide exchange of the wave maxima)
+  if (kernel == QATTN_KERNEL_RESIDENT && gran != QATTN_GRAN_BLOCK) return kernel;
+  return kernel == QATTN_KERNEL_PINGPONG ? kernel : QATTN_KERNEL_AUTO;
 }
 
 extern "C" int qattn_fwd_q16_supported(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t D, int qk_quant_gran,
                                        int causal) {
-  if (qk_quant_gran != QATTN_GRAN_WARP && qk_quant_gran != QATTN_GRAN_THREAD) return 0;
+  if (qk_quant_gran < QATTN_GRAN_BLOCK || qk_quant_gran > QATTN_GRAN_THREAD) return 0;
   return q16_kernel(B, Lq, Lk, Hq, D, qk_quant_gran, causal) != QATTN_KERNEL_AUTO ? 1 : 0;
 }
 
@@ -2002,8 +2036,8 @@ extern "C" int qattn_fwd_q16(qattn_seq q, qattn_seq k8, const float* k_scale, co
                              int64_t Lq, int64_t Lk, int64_t Hq, int64_t Hkv, int64_t D, float qk_mult,
                              int qk_quant_gran, int causal, int64_t q_offset, const int32_t* kv_valid, float* lse,
                              int num_splits, void* workspace, size_t workspace_bytes, qattn_stream_t stream) {
-  QATTN_REQUIRE(qk_quant_gran == QATTN_GRAN_WARP || qk_quant_gran == QATTN_GRAN_THREAD, QATTN_ERR_ARG,
-                "qattn_fwd_q16 quantizes Q per warp (2) or per thread (3), got %d", qk_quant_gran);
+  QATTN_REQUIRE(qk_quant_gran >= QATTN_GRAN_BLOCK && qk_quant_gran <= QATTN_GRAN_THREAD, QATTN_ERR_ARG,
+                "qattn_fwd_q16 quantizes Q per block (1), per warp (2) or per thread (3), got %d", qk_quant_gran);
   QATTN_REQUIRE(v8 && v_scale, QATTN_ERR_ARG, "null V or v_scale");
   if (B * Lq == 0) return QATTN_OK;
   const int kernel = q16_kernel(B, Lq, Lk, Hq, D, qk_quant_gran, causal);
@@ -2021,6 +2055,11 @@ extern "C" int qattn_fwd_q16(qattn_seq q, qattn_seq k8, const float* k_scale, co
                 num_splits);
   p.v_scale = v_scale;
   p.v_mean = v_mean;
+  if (qk_quant_gran == QATTN_GRAN_BLOCK) {
+    // per-block scales carry sm_scale * log2(e): it is multiplied into Q, the logits take 1
+    p.q_sm_scale = qk_mult;
+    p.qk_mult = 1.0f;
+  }
   hipStream_t st = (hipStream_t)stream;
   t_last_kernel = kernel;
   if (kernel == QATTN_KERNEL_RESIDENT) {
@@ -2050,7 +2089,8 @@ extern "C" int qattn_fwd_q16(qattn_seq q, qattn_seq k8, const float* k_scale, co
     p.ws_ml = p.ws_o + (int64_t)ns * p.B * p.Hq * p.Lq * D;
   }
   if (qk_quant_gran == QATTN_GRAN_THREAD) launch_pp_q16<QF_THREAD>(p, dtype, ns, st);
-  else launch_pp_q16<QF_WARP>(p, dtype, ns, st);
+  else if (qk_quant_gran == QATTN_GRAN_WARP) launch_pp_q16<QF_WARP>(p, dtype, ns, st);
+  else launch_pp_q16<QF_BLOCK>(p, dtype, ns, st);
   return check_launch("qattn_fwd_q16");
 }
 

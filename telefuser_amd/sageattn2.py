@@ -347,18 +347,20 @@ def qattn_fwd(q_int8, q_scale, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout
 def qattn_fwd_q16(q, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout="HND", qk_mult=1.0, is_causal=False,
                   q_offset=0, kv_valid_len=None, return_lse=False, num_splits=0, qk_quant_gran="per_thread",
                   out: Optional[torch.Tensor] = None, v_mean: Optional[torch.Tensor] = None):
-    """Attention on half-precision Q (qattn_fwd_q16 in the C ABI): Q is quantized per thread (Triton rounding)
-    or per warp (CUDA rounding) inside the resident-K/V or ping-pong kernel, bit-identical to
-    per_thread_int8 / per_warp_int8 followed by qattn_fwd, without the int8 Q round trip through memory.
-    head_dim 128, launches whose automatic kernel is one of those two (q16_supported).  Returns o (and the
-    log2-domain LSE)."""
+    """Attention on half-precision Q (qattn_fwd_q16 in the C ABI): Q is quantized per thread (Triton rounding),
+    per warp or per block (CUDA rounding) inside the attention kernel (the resident-K/V or the ping-pong
+    kernel; per block: the ping-pong kernel), bit-identical to per_thread_int8 / per_warp_int8 /
+    per_block_int8 followed by qattn_fwd, without the int8 Q round trip through memory.  qk_mult is
+    sm_scale * 1.44269504 for every granularity (per block it is multiplied into Q before quantization, as
+    per_block_int8's sm_scale).  head_dim 128, launches whose automatic kernel is one of those two
+    (q16_supported).  Returns o (and the log2-domain LSE)."""
     L = _lib.load()
     b, lq, hq, d = _dims(q, tensor_layout)
     _, lk, hkv, _ = _dims(k_int8, tensor_layout)
     if hq % hkv != 0:
         raise ValueError(f"num_qo_heads ({hq}) must be divisible by num_kv_heads ({hkv})")
-    if qk_quant_gran not in ("per_warp", "per_thread"):
-        raise ValueError(f"qk_quant_gran must be 'per_warp' or 'per_thread', got {qk_quant_gran!r}")
+    if qk_quant_gran not in _GRAN:
+        raise ValueError(f"qk_quant_gran must be one of {sorted(_GRAN)}, got {qk_quant_gran!r}")
     if q.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("q must be bf16 or fp16")
     gran = _GRAN[qk_quant_gran]
@@ -386,7 +388,7 @@ def qattn_fwd_q16(q, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout="HND", qk
 
 def q16_supported(b, lq, lk, hq, d, qk_quant_gran, is_causal=False) -> bool:
     """Whether qattn_fwd_q16 (Q quantized inside the attention kernel) covers a launch of these sizes."""
-    if qk_quant_gran not in ("per_warp", "per_thread"):
+    if qk_quant_gran not in _GRAN:
         return False
     return bool(_lib.load().qattn_fwd_q16_supported(b, lq, lk, hq, d, _GRAN[qk_quant_gran], int(bool(is_causal))))
 
@@ -448,14 +450,14 @@ def _sage_forward(q, k, v, tensor_layout, is_causal, qk_quant_gran, sm_scale, pv
             scale_max=448.0, smooth_v=False, scale_layout="sm90")
     elif (pv == "fp8" and quant_variant == "cuda" and
           q16_supported(b, lq, lk, hq, q.size(-1), qk_quant_gran, is_causal)):
-        # per-thread / per-warp scales: K mean, K INT8 and V FP8 in the fused prologue, Q quantized inside the
-        # attention kernel (bit-identical to quantizing it first)
+        # K mean, K INT8 and V FP8 in the fused prologue, Q quantized inside the attention kernel
+        # (bit-identical to quantizing it first)
         _, _, k_int8, k_scale, km, v_fp8, v_scale, vm = sage_quant(
             q, k, v, tensor_layout=tensor_layout, qk_quant_gran=qk_quant_gran, sm_scale=sm_scale, smooth_k=smooth_k,
             scale_max=scale_max, smooth_v=smooth_v, quantize_q=False)
-        res = qattn_fwd_q16(q, k_int8, k_scale, v_fp8, v_scale, tensor_layout=tensor_layout, qk_mult=qk_mult,
-                            is_causal=is_causal, q_offset=q_offset, kv_valid_len=kv_valid_len, return_lse=return_lse,
-                            qk_quant_gran=qk_quant_gran, v_mean=vm)
+        res = qattn_fwd_q16(q, k_int8, k_scale, v_fp8, v_scale, tensor_layout=tensor_layout,
+                            qk_mult=sm_scale * LOG2E, is_causal=is_causal, q_offset=q_offset, kv_valid_len=kv_valid_len,
+                            return_lse=return_lse, qk_quant_gran=qk_quant_gran, v_mean=vm)
         return _sage_finish(res, q, km, hq, hkv, head_dim_og, tensor_layout, sm_scale, smooth_k, return_lse)
     elif pv == "fp8" and quant_variant == "cuda":
         # K mean, Q/K INT8 and V FP8 in one fused prologue (four launches)

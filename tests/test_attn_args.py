@@ -124,7 +124,7 @@ def test_qattn_fwd_sm90_layout_checks(bad):
         sa.qattn_fwd(q8, qs, k8, ks, v, vs, **kw)
 
 
-@pytest.mark.parametrize("bad", ["per_block", "small_grid_long_keys", "int8_q", "k_scale_gran", "no_v_scale"])
+@pytest.mark.parametrize("bad", ["per_block_resident", "small_grid_long_keys", "int8_q", "k_scale_gran", "no_v_scale"])
 def test_fwd_q16_rejects(bad):
     """qattn_fwd_q16 takes half Q, per-warp / per-thread K scales and the e4m3 V tile, for launches the resident
     or ping-pong kernel runs (300 queries of 4 heads over 600 keys run the one-block kernel)."""
@@ -134,7 +134,8 @@ def test_fwd_q16_rejects(bad):
     q8, qs, k8, ks, v, vs = _ops(Lk=lk, gran="per_thread")
     q = torch.zeros(q8.shape, dtype=torch.bfloat16)
     kw = dict(tensor_layout="NHD", qk_quant_gran="per_thread")
-    if bad == "per_block":
+    if bad == "per_block_resident":  # 300 keys run the resident kernel, which has no per-block form
+        q8, qs, k8, ks, v, vs = _ops(Lk=lk, gran="per_block")
         kw["qk_quant_gran"] = "per_block"
     elif bad == "int8_q":
         q = q8

@@ -904,14 +904,17 @@ Q16_CASES = {
     "pp_thread_unsplit": (1, 4680, 6000, 12, 12, "NHD", torch.bfloat16, "per_thread", None, False, False),
     "pp_warp_split_gqa": (1, 2000, 20000, 8, 4, "NHD", torch.bfloat16, "per_warp", [19000], False, False),
     "pp_thread_causal_fp16": (2, 1500, 3000, 8, 8, "HND", torch.float16, "per_thread", None, False, True),
+    "pp_block_unsplit": (1, 4680, 6000, 12, 12, "NHD", torch.bfloat16, "per_block", None, False, False),
+    "pp_block_split_kv_valid": (1, 2000, 20000, 8, 4, "NHD", torch.bfloat16, "per_block", [19000], True, False),
+    "pp_block_causal_fp16": (2, 1500, 3000, 8, 8, "HND", torch.float16, "per_block", None, False, True),
 }
 
 
 @pytest.mark.parametrize("case", sorted(Q16_CASES))
 def test_fwd_q16_matches_quantize_then_attend(oracle, case):
-    """qattn_fwd_q16 quantizes Q inside the resident kernel: its output and LSE must be bit-identical to
-    per_thread_int8 / per_warp_int8 followed by qattn_fwd on the same K / V, and the drop-in (which takes
-    this route for non-causal launches over at most 512 keys) must give the same bits as well."""
+    """qattn_fwd_q16 quantizes Q inside the attention kernel: its output and LSE must be bit-identical to
+    per_thread_int8 / per_warp_int8 / per_block_int8 followed by qattn_fwd on the same K / V, and the drop-in
+    (which takes this route where qattn_fwd_q16 covers the launch) must give the same bits as well."""
     dev = require_gpu()
     from telefuser_amd import sageattn2 as sa
 
@@ -924,13 +927,16 @@ def test_fwd_q16_matches_quantize_then_attend(oracle, case):
     if layout == "HND":
         qd, kd, vd = (t.transpose(1, 2).contiguous() for t in (qd, kd, vd))
     km = sa.k_mean(kd, layout)
-    quant = sa.per_thread_int8 if gran == "per_thread" else sa.per_warp_int8
-    q8, qs, k8, ks = quant(qd, kd, km, tensor_layout=layout)
-    v8, vs, vm = sa.per_channel_fp8(vd, tensor_layout=layout, smooth_v=smooth_v)
     qk_mult = 128 ** -0.5 * LOG2E
-    o_ref, l_ref = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout=layout, out_dtype=dt, qk_mult=qk_mult,
-                                is_causal=causal, kv_valid_len=kv_valid, return_lse=True, qk_quant_gran=gran,
-                                v_mean=vm)
+    if gran == "per_block":  # sm_scale * log2(e) folded into Q's scales
+        q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=128 ** -0.5, tensor_layout=layout)
+    else:
+        quant = sa.per_thread_int8 if gran == "per_thread" else sa.per_warp_int8
+        q8, qs, k8, ks = quant(qd, kd, km, tensor_layout=layout)
+    v8, vs, vm = sa.per_channel_fp8(vd, tensor_layout=layout, smooth_v=smooth_v)
+    o_ref, l_ref = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout=layout, out_dtype=dt,
+                                qk_mult=1.0 if gran == "per_block" else qk_mult, is_causal=causal,
+                                kv_valid_len=kv_valid, return_lse=True, qk_quant_gran=gran, v_mean=vm)
     o, l = sa.qattn_fwd_q16(qd, k8, ks, v8, vs, tensor_layout=layout, qk_mult=qk_mult, is_causal=causal,
                             kv_valid_len=kv_valid, return_lse=True, qk_quant_gran=gran, v_mean=vm)
     torch.cuda.synchronize()
@@ -942,12 +948,24 @@ def test_fwd_q16_matches_quantize_then_attend(oracle, case):
     od, ld = sa.sageattn_qk_int8_pv_fp8_cuda(qd, kd, vd, **kw)
     torch.cuda.synchronize()
     assert torch.equal(od, o)
-    # and within the end-to-end bound of float64 attention (rows with keys)
+    # and within the north star's bound of the reference's quantized math (its own schedule, e4m3(exp2) P) on
+    # the same int8 / e4m3 operands: batch entry 0, the first 256 rows of heads 0 and 1 and their KV heads
+    # (float64 attention on the half inputs is printed: with smoothed V over 19000 keys of flat random
+    # attention the reference's math itself lands at 0.99897 from it, so it is not a gate here)
     if layout == "HND":
-        od = od.transpose(1, 2)
-    bits = (lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)) if dt == torch.float16 else bf16_bits
-    # float64 truth on the first 256 rows of heads 0 and 1 (and their KV heads)
+        od, q8, k8 = od.transpose(1, 2), q8.transpose(1, 2), k8.transpose(1, 2)
     rows, nkv = slice(0, min(Lq, 256)), max(1, 2 * Hkv // Hq)
-    truth = oracle.attn_fp64(bits(q[:, rows, :2]), bits(k[:, :, :nkv]), bits(v[:, :, :nkv]), 128 ** -0.5,
-                             kv_valid=kv_valid, is_fp16=dt == torch.float16, causal=causal)
-    assert cosine(od[:, rows, :2].float().cpu().numpy(), truth) >= COS_E2E
+    q_per = {"per_block": 1, "per_warp": 4, "per_thread": 32}[gran]
+    kvv0 = None if kv_valid is None else kv_valid[:1]
+    ref = oracle.qattn_fwd(q8[:1, rows, :2].contiguous().cpu().numpy(), qs[:1, :2, :2 * q_per].cpu().numpy(),
+                           k8[:1, :, :nkv].contiguous().cpu().numpy(), ks[:1, :nkv].cpu().numpy(),
+                           v8=untile_v(v8[:1, :nkv]), v_scale=vs[:1, :nkv].cpu().numpy(), causal=causal,
+                           kv_valid=kvv0, q_gran=GRAN_CODE[gran], k_gran=GRAN_CODE[gran],
+                           qk_mult=1.0 if gran == "per_block" else qk_mult,
+                           v_mean=None if vm is None else vm[:1, :nkv].cpu().numpy())
+    got = od[:1, rows, :2].float().cpu().numpy()
+    bits = (lambda t: t.contiguous().view(torch.int16).numpy().view(np.uint16)) if dt == torch.float16 else bf16_bits
+    truth = oracle.attn_fp64(bits(q[:1, rows, :2]), bits(k[:1, :, :nkv]), bits(v[:1, :, :nkv]), 128 ** -0.5,
+                             kv_valid=kvv0, is_fp16=dt == torch.float16, causal=causal)
+    log(f"  vs reference-schedule quantized math: cosine={cosine(got, ref):.6f}; vs float64: {cosine(got, truth):.6f}")
+    assert cosine(got, ref) >= COS_E2E
