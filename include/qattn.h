@@ -314,9 +314,9 @@ int qattn_v_fp8_cache_update(qattn_seq v, int dtype, int64_t B, int64_t fill, in
  * the reference's per_thread_int8 (qk_quant_gran QATTN_GRAN_THREAD, Triton rounding,
  * quant_per_thread.py:22-158), per_warp_int8 (QATTN_GRAN_WARP, QuantInt8Kernel rounding, fused.cu:698-780) or
  * per_block_int8 (QATTN_GRAN_BLOCK, QuantInt8Kernel rounding with sm_scale folded in, fused.cu:59-194) would
- * -- bit-identical codes and scales -- by the resident-K/V or the ping-pong kernel (per block: the ping-pong
- * kernel, whose four waves of a query block exchange their maxima), so int8 Q is never written out and read
- * back.  K and V are prepared as for qattn_fwd_ex with the
+ * -- bit-identical codes and scales -- by the resident-K/V or the ping-pong kernel (per block, the four
+ * waves that hold a 128-row query block exchange their maxima through LDS), so int8 Q is never written out
+ * and read back.  K and V are prepared as for qattn_fwd_ex with the
  * same granularity (k_scale per 64-key block, or 4 lane-pair classes per block for per-thread).  Arguments
  * as qattn_fwd_ex (causal, q_offset, kv_valid, lse, num_splits with its workspace sized by
  * qattn_fwd_ex_num_splits / qattn_fwd_workspace_size); qk_mult = sm_scale * 1.44269504 (per block it is the

@@ -172,6 +172,17 @@ __device__ __forceinline__ void lds_dma16(uint32_t voff, v4u rsrc, uint32_t soff
       : "memory", "m0");
 }
 
+// The 4-byte form (buffer_load_dword ... lds): lane j's dword lands at lds + 4 j.
+__device__ __forceinline__ void lds_dma4(uint32_t voff, v4u rsrc, uint32_t soff, uint32_t lds) {
+  asm volatile(
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dword %0, %1, %2 offen lds"
+      :
+      : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds)
+      : "memory", "m0");
+}
+
 // two floats -> two round-to-nearest-even halves (bf16: v_cvt_pk_bf16_f32), low word first
 template <bool IS_FP16>
 __device__ __forceinline__ uint32_t pack_half2(float a, float b) {
@@ -840,8 +851,9 @@ constexpr int kPPNBuf = 4;
 // QF: Q as int8 with its scale table (0), or Q in the output's half type quantized inside the attention
 // kernel: with the per-thread classes of the Triton quantizer (QF_THREAD: rows with equal row % 8 of a wave's
 // 32 share a scale, round half away from x / scale), the per-warp blocks of the CUDA one (QF_WARP: a wave's
-// 32 rows share a scale, RNE of x * 127 / amax), or its per-block form (QF_BLOCK, ping-pong kernel only:
-// the 128 rows of a wave group share a scale, x multiplied by sm_scale * log2(e) first) -- the codes and
+// 32 rows share a scale, RNE of x * 127 / amax), or its per-block form (QF_BLOCK: the
+// 128 rows of a query block, held by four waves of one workgroup, share a scale, x multiplied by
+// sm_scale * log2(e) first) -- the codes and
 // scales of per_thread_int8 / per_warp_int8 / per_block_int8 bit for bit, without writing int8 Q out and
 // reading it back.
 constexpr int QF_INT8 = 0, QF_THREAD = 1, QF_WARP = 2, QF_BLOCK = 3;
@@ -983,6 +995,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
   uint8_t* stage = &lds_k[0][0] + w * 4096;
   v4i qf[NQF];
   float qs;
+  auto load_q = [&]() {
   if constexpr (QF == QF_BLOCK) {
     // half Q quantized per 128-row block: the four waves of a group exchange their maxima through LDS
     // (q_sm_scale = sm_scale * log2(e) multiplied in first; the logits then take qk_mult = 1)
@@ -1019,6 +1032,10 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     const int64_t qsi = q_scale_index(p, qbs * kBQ + wl * 32 + lq);
     qs = p.q_scale[(b * p.Hq + h) * p.nQS + qsi] * p.qk_mult;
   }
+  };
+  // int8 Q goes through the LDS stage, which the first DMAs overwrite: it is loaded first.  Half Q is
+  // quantized in registers, so its loads are issued behind the first DMAs and their latencies overlap.
+  if constexpr (QF == QF_INT8) load_q();
   const float* ks_ptr = p.k_scale + (b * p.Hkv + hk) * p.nKS;
 
   // K/V tiles in LDS, fragment-major: 1 KiB block j holds MFMA operand fragment j of all 64 lanes (lane l
@@ -1067,7 +1084,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
 #pragma unroll
   for (int r = 0; r < 16; r++) kbias[r] = kAccBiasBits;
 
-  __syncthreads();  // Q fragments are out of the LDS stage before the DMA reuses it
+  if constexpr (QF == QF_INT8) __syncthreads();  // Q fragments are out of the LDS stage before the DMA reuses it
   // the key scales of tiles t_lo .. t_end - 1, from lds_ks[0]
   for (int i = tid; i < (t_end - t_lo) * KS; i += kPPThreads) lds_ks[i] = ks_ptr[k_scale_index(p, t_lo + i / KS, i % KS, KS)];
   if (tid < HD) {
@@ -1075,6 +1092,7 @@ __device__ __forceinline__ void qattn_fwd_pp(const AttnParams& p) {
     lds_vm[tid] = p.v_mean ? p.v_mean[(b * p.Hkv + hk) * HD + tid] : 0.f;
   }
   for (int t = t_lo; t < min(t_end, t_lo + 2); t++) dma_tile(t);
+  if constexpr (QF != QF_INT8) load_q();
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
 
@@ -1326,6 +1344,7 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
   __shared__ __align__(16) uint8_t lds_k[kResMaxTiles][kBK * kD];
   __shared__ __align__(16) uint8_t lds_v[kResMaxTiles][kD * kBK];
   __shared__ __align__(16) uint8_t lds_o[NW][32 * 64];
+  __shared__ __align__(16) uint8_t lds_pf[QF == QF_BLOCK ? NW : 1][256];  // landing slots of the Q prefetch, never read
   __shared__ float lds_ks[kResMaxTiles * 4];
   __shared__ __align__(16) float lds_vs[kD];
   __shared__ __align__(16) float lds_vm[kD];
@@ -1398,16 +1417,49 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();  // every wave's share of the key range has landed
 
-  for (; wb < wb_end; wb += NW) {
+  // per-block Q (QF_BLOCK): the layout starts every chunk on a 128-row block, so in each round waves 4 g ..
+  // 4 g + 3 hold the four 32-row blocks of one Q block and exchange their maxima through LDS; every wave
+  // runs all rounds of the chunk (a wave past the chunk's end contributes 0 and joins the barrier)
+  const int64_t n_rounds = (wb_end - wb0 + NW - 1) / NW;
+  for (int64_t rnd = 0; QF == QF_BLOCK ? rnd < n_rounds : wb < wb_end; rnd++, wb += NW) {
     float qs;
     if constexpr (QF == QF_INT8) {
       load_q(wb, qf);
       qs = qs_tab[q_scale_index(p, wb * 32 + lq)] * p.qk_mult;
+    } else if constexpr (QF == QF_BLOCK) {
+      // (double-buffered by round: a wave writes round r + 2's maximum only after the barrier of round r + 1,
+      // which every wave reaches after reading round r's)
+      __shared__ float lds_qam[2][NW];
+      const int64_t row = wb * 32 + lq;
+      float x[4][16];
+      const float am_w =
+          quant_q_load<IS_FP16_OUT, QF, 4, true>(qhead16 + row * p.qsl, row < p.Lq && wb < wb_end, hf, p.q_sm_scale, x);
+      if (lane == 0) lds_qam[rnd & 1][w] = am_w;
+      __syncthreads();
+      const float* g4 = &lds_qam[rnd & 1][w & ~3];
+      const float am = fmaxf(fmaxf(g4[0], g4[1]), fmaxf(g4[2], g4[3]));
+      if (wb >= wb_end) continue;
+      qs = quant_q_codes<QF, 4>(x, am, qf) * p.qk_mult;
     } else {
       const int64_t row = wb * 32 + lq;
       qs = quant_q_rows<IS_FP16_OUT, QF, 4>(qhead16 + row * p.qsl, row < p.Lq, hf, qf) * p.qk_mult;
     }
     const int64_t wrow0 = wb * 32, qrow = wrow0 + lq;
+    // Per block, the round barrier lines the waves up, so all of them would load their next Q rows at once
+    // and wait out the HBM latency together: the wave's next 32 rows go into L2 while this block runs, one
+    // dword of every 128-byte line (lane (lq, hf): row lq, line hf) DMA'd into the wave's landing slot so
+    // that no register waits for it.  (The free-running forms stagger their loads by themselves: the
+    // prefetch measured no gain there.)
+    if constexpr (QF == QF_BLOCK) {
+      if (wb + NW < wb_end) {
+        constexpr int kQB = 2;  // bytes per Q element
+        const int64_t nrow0 = (wb + NW) * 32;
+        const uint8_t* nbase = reinterpret_cast<const uint8_t*>(p.q8) + (b * p.qsb + h * p.qsh + nrow0 * p.qsl) * kQB;
+        const int64_t rem = ((p.Lq - 1 - nrow0) * p.qsl + kD) * kQB;  // bytes to the end of the last row
+        lds_dma4((uint32_t)((lq * p.qsl + hf * 64) * kQB), make_rsrc(nbase, (uint32_t)min(rem, (int64_t)UINT32_MAX)), 0,
+                 lds_addr(&lds_pf[w][0]));
+      }
+    }
 
     v16f o[4];
     v4f lacc;
@@ -1571,6 +1623,7 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
     if (p.lse && hf == 0 && qrow < p.Lq)
       p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
   }
+  if constexpr (QF == QF_BLOCK) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no prefetch left in flight
 }
 
 // Merge the KV-split partials: one wave per query row, 2 channels per lane.
@@ -1732,12 +1785,12 @@ static int pick_kernel(int pv, bool sparse, int ns, int causal, int64_t B, int64
 // of wb_per_wg blocks.  One workgroup runs per CU (its LDS holds the key range), its kResWaves waves each
 // taking every kResWaves-th block; the cut minimises full rounds of 256 workgroups x (wave rounds per
 // workgroup + one round of start-up for the key-range load).
-static void resident_layout(int64_t bh, int64_t n_wb, int64_t& wb_per_wg, int64_t& n_chunk) {
+static void resident_layout(int64_t bh, int64_t n_wb, int64_t& wb_per_wg, int64_t& n_chunk, int64_t align = 1) {
   double best = 1e300;
-  wb_per_wg = n_wb;
+  wb_per_wg = (n_wb + align - 1) / align * align;
   n_chunk = 1;
   for (int64_t c = 1; c <= std::max<int64_t>(1, (n_wb + kResWaves - 1) / kResWaves); c++) {
-    const int64_t per = (n_wb + c - 1) / c;
+    const int64_t per = ((n_wb + c - 1) / c + align - 1) / align * align;
     const int64_t chunks = (n_wb + per - 1) / per;
     const int64_t rounds = (bh * chunks + 255) / 256;
     const double cost = (double)rounds * (double)((per + kResWaves - 1) / kResWaves + 1);
@@ -2004,9 +2057,7 @@ static int q16_kernel(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t D, 
   if (D != kD || B <= 0 || Lq <= 0 || Lk <= 0 || Hq <= 0) return QATTN_KERNEL_AUTO;
   int ns, qpw, kernel;
   plan_fwd(B, Lq, Lk, Hq, PV_FP8, gran, causal, false, 0, ns, qpw, kernel);
-  // (per-block scales need the ping-pong kernel's workgroup-wide exchange of the wave maxima)
-  if (kernel == QATTN_KERNEL_RESIDENT && gran != QATTN_GRAN_BLOCK) return kernel;
-  return kernel == QATTN_KERNEL_PINGPONG ? kernel : QATTN_KERNEL_AUTO;
+  return kernel == QATTN_KERNEL_RESIDENT || kernel == QATTN_KERNEL_PINGPONG ? kernel : QATTN_KERNEL_AUTO;
 }
 
 extern "C" int qattn_fwd_q16_supported(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t D, int qk_quant_gran,
@@ -2065,10 +2116,14 @@ extern "C" int qattn_fwd_q16(qattn_seq q, qattn_seq k8, const float* k_scale, co
   if (kernel == QATTN_KERNEL_RESIDENT) {
     p.nsplit = 1;
     p.tiles_per_split = (int)p.nKB;
-    resident_layout(p.B * p.Hq, (p.Lq + 31) / 32, p.wb_per_wg, p.n_chunk);
+    // (chunks of whole 128-row Q blocks for per-block scales)
+    resident_layout(p.B * p.Hq, (p.Lq + 31) / 32, p.wb_per_wg, p.n_chunk, qk_quant_gran == QATTN_GRAN_BLOCK ? 4 : 1);
     const int64_t g = p.B * p.Hq * p.n_chunk;
     QATTN_REQUIRE(g < (1ll << 31), QATTN_ERR_SHAPE, "grid too large");
-    if (qk_quant_gran == QATTN_GRAN_THREAD) {
+    if (qk_quant_gran == QATTN_GRAN_BLOCK) {
+      if (dtype == QATTN_BF16) qattn_fwd_res_kernel<false, false, QF_BLOCK><<<g, kResThreads, 0, st>>>(p);
+      else qattn_fwd_res_kernel<true, false, QF_BLOCK><<<g, kResThreads, 0, st>>>(p);
+    } else if (qk_quant_gran == QATTN_GRAN_THREAD) {
       if (dtype == QATTN_BF16) qattn_fwd_res_kernel<false, true, QF_THREAD><<<g, kResThreads, 0, st>>>(p);
       else qattn_fwd_res_kernel<true, true, QF_THREAD><<<g, kResThreads, 0, st>>>(p);
     } else {

@@ -349,7 +349,7 @@ def qattn_fwd_q16(q, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout="HND", qk
                   out: Optional[torch.Tensor] = None, v_mean: Optional[torch.Tensor] = None):
     """Attention on half-precision Q (qattn_fwd_q16 in the C ABI): Q is quantized per thread (Triton rounding),
     per warp or per block (CUDA rounding) inside the attention kernel (the resident-K/V or the ping-pong
-    kernel; per block: the ping-pong kernel), bit-identical to per_thread_int8 / per_warp_int8 /
+    kernel), bit-identical to per_thread_int8 / per_warp_int8 /
     per_block_int8 followed by qattn_fwd, without the int8 Q round trip through memory.  qk_mult is
     sm_scale * 1.44269504 for every granularity (per block it is multiplied into Q before quantization, as
     per_block_int8's sm_scale).  head_dim 128, launches whose automatic kernel is one of those two

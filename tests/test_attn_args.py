@@ -124,9 +124,9 @@ def test_qattn_fwd_sm90_layout_checks(bad):
         sa.qattn_fwd(q8, qs, k8, ks, v, vs, **kw)
 
 
-@pytest.mark.parametrize("bad", ["per_block_resident", "small_grid_long_keys", "int8_q", "k_scale_gran", "no_v_scale"])
+@pytest.mark.parametrize("bad", ["small_grid_long_keys", "int8_q", "k_scale_gran", "no_v_scale"])
 def test_fwd_q16_rejects(bad):
-    """qattn_fwd_q16 takes half Q, per-warp / per-thread K scales and the e4m3 V tile, for launches the resident
+    """qattn_fwd_q16 takes half Q, K scales of its granularity and the e4m3 V tile, for launches the resident
     or ping-pong kernel runs (300 queries of 4 heads over 600 keys run the one-block kernel)."""
     from telefuser_amd import sageattn2 as sa
 
@@ -134,10 +134,7 @@ def test_fwd_q16_rejects(bad):
     q8, qs, k8, ks, v, vs = _ops(Lk=lk, gran="per_thread")
     q = torch.zeros(q8.shape, dtype=torch.bfloat16)
     kw = dict(tensor_layout="NHD", qk_quant_gran="per_thread")
-    if bad == "per_block_resident":  # 300 keys run the resident kernel, which has no per-block form
-        q8, qs, k8, ks, v, vs = _ops(Lk=lk, gran="per_block")
-        kw["qk_quant_gran"] = "per_block"
-    elif bad == "int8_q":
+    if bad == "int8_q":
         q = q8
     elif bad == "k_scale_gran":
         ks = ks[..., : ks.shape[-1] // 4].contiguous()
@@ -145,3 +142,15 @@ def test_fwd_q16_rejects(bad):
         vs = None
     with pytest.raises(ValueError):
         sa.qattn_fwd_q16(q, k8, ks, v, vs, **kw)
+
+
+def test_q16_supported_rule():
+    """The host rule behind the drop-in's route: every granularity on the resident kernel (at most 512 keys)
+    and on the ping-pong kernel, nothing on the one-block kernel, head_dim 128 only."""
+    from telefuser_amd import sageattn2 as sa
+
+    for gran in ("per_block", "per_warp", "per_thread"):
+        assert sa.q16_supported(1, 1000, 512, 4, 128, gran, False)  # resident
+        assert sa.q16_supported(1, 32760, 32760, 12, 128, gran, False)  # ping-pong (C2)
+        assert not sa.q16_supported(1, 300, 600, 4, 128, gran, False)  # one-block
+        assert not sa.q16_supported(1, 1000, 512, 4, 64, gran, False)

@@ -894,13 +894,18 @@ def test_pv_accum_modes_and_smooth_v(oracle, mode):
 
 
 Q16_CASES = {
-    # name: (B, Lq, Lk, Hq, Hkv, layout, dtype, gran, kv_valid, smooth_v, causal); the first five run the
+    # name: (B, Lq, Lk, Hq, Hkv, layout, dtype, gran, kv_valid, smooth_v, causal); the first eight run the
     # resident kernel (at most 512 keys), the others the ping-pong kernel (unsplit, KV split, causal)
     "thread_c4_like": (1, 1000, 512, 4, 4, "NHD", torch.bfloat16, "per_thread", [388], False, False),
     "warp_ragged_gqa": (2, 333, 300, 4, 2, "NHD", torch.bfloat16, "per_warp", None, False, False),
     "thread_hnd_fp16": (1, 517, 130, 3, 3, "HND", torch.float16, "per_thread", None, False, False),
     "thread_smooth_v_short_q": (2, 40, 64, 2, 1, "NHD", torch.bfloat16, "per_thread", [64, 17], True, False),
     "warp_fp16_keys_512": (1, 777, 512, 2, 2, "NHD", torch.float16, "per_warp", None, True, False),
+    # per block on the resident kernel: chunks of whole 128-row blocks (12 rows of 32 in three chunks; a ragged
+    # last block; 200 heads in one chunk each, so three rounds per wave with a partial last group)
+    "block_res_chunks": (1, 1000, 512, 4, 4, "NHD", torch.bfloat16, "per_block", [388], False, False),
+    "block_res_hnd_fp16": (2, 333, 300, 4, 2, "HND", torch.float16, "per_block", [300, 17], True, False),
+    "block_res_rounds_gqa": (5, 900, 200, 40, 8, "NHD", torch.bfloat16, "per_block", None, False, False),
     "pp_thread_unsplit": (1, 4680, 6000, 12, 12, "NHD", torch.bfloat16, "per_thread", None, False, False),
     "pp_warp_split_gqa": (1, 2000, 20000, 8, 4, "NHD", torch.bfloat16, "per_warp", [19000], False, False),
     "pp_thread_causal_fp16": (2, 1500, 3000, 8, 8, "HND", torch.float16, "per_thread", None, False, True),
