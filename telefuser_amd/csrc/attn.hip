@@ -858,33 +858,48 @@ constexpr int kPPNBuf = 4;
 // reading it back.
 constexpr int QF_INT8 = 0, QF_THREAD = 1, QF_WARP = 2, QF_BLOCK = 3;
 
-// Lane (lq, hf) of a wave whose 32 query rows are lq = lane % 32: the 16 NQF values of its row (row pointer
-// rowp, half type; zeros when !valid) at 32 m + 16 hf .. + 16, times mul when MUL (fp32), and their |x|
-// maximum over the lane's scale group within the wave (per-thread class: lanes lq ^ 8, lq ^ 16 and the other
-// half-row; per-warp / per-block: all 64 lanes, from the CUDA quantizer's 1e-7 floor).
-template <bool IS_FP16, int QF, int NQF, bool MUL = false>
-__device__ __forceinline__ float quant_q_load(const uint16_t* rowp, bool valid, int hf, float mul, float (&x)[NQF][16]) {
-  float am = QF == QF_THREAD ? 0.f : 0.0000001f;
+// Lane (lq, hf) of a wave whose 32 query rows are lq = lane % 32: the raw half words of its row (row
+// pointer rowp; zeros when !valid) at 32 m + 16 hf .. + 16, m < NQF.
+template <int NQF>
+__device__ __forceinline__ void quant_q_raw(const uint16_t* rowp, bool valid, int hf, v4u (&r)[NQF][2]) {
 #pragma unroll
   for (int m = 0; m < NQF; m++) {
-    v4u r0 = v4u{0, 0, 0, 0}, r1 = v4u{0, 0, 0, 0};
+    r[m][0] = r[m][1] = v4u{0, 0, 0, 0};
     if (valid) {
-      r0 = *reinterpret_cast<const v4u*>(rowp + m * 32 + hf * 16);
-      r1 = *reinterpret_cast<const v4u*>(rowp + m * 32 + hf * 16 + 8);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-      x[m][2 * e] = half_to_f32<IS_FP16>((uint16_t)(r0[e] & 0xffffu));
-      x[m][2 * e + 1] = half_to_f32<IS_FP16>((uint16_t)(r0[e] >> 16));
-      x[m][8 + 2 * e] = half_to_f32<IS_FP16>((uint16_t)(r1[e] & 0xffffu));
-      x[m][8 + 2 * e + 1] = half_to_f32<IS_FP16>((uint16_t)(r1[e] >> 16));
-    }
-#pragma unroll
-    for (int e = 0; e < 16; e++) {
-      if constexpr (MUL) x[m][e] = x[m][e] * mul;
-      am = fmaxf(am, fabsf(x[m][e]));
+      r[m][0] = *reinterpret_cast<const v4u*>(rowp + m * 32 + hf * 16);
+      r[m][1] = *reinterpret_cast<const v4u*>(rowp + m * 32 + hf * 16 + 8);
     }
   }
+}
+
+// Those values as fp32, times mul when MUL.
+template <bool IS_FP16, int NQF, bool MUL>
+__device__ __forceinline__ void quant_q_unpack(const v4u (&r)[NQF][2], float mul, float (&x)[NQF][16]) {
+#pragma unroll
+  for (int m = 0; m < NQF; m++) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      x[m][2 * e] = half_to_f32<IS_FP16>((uint16_t)(r[m][0][e] & 0xffffu));
+      x[m][2 * e + 1] = half_to_f32<IS_FP16>((uint16_t)(r[m][0][e] >> 16));
+      x[m][8 + 2 * e] = half_to_f32<IS_FP16>((uint16_t)(r[m][1][e] & 0xffffu));
+      x[m][8 + 2 * e + 1] = half_to_f32<IS_FP16>((uint16_t)(r[m][1][e] >> 16));
+    }
+    if constexpr (MUL) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) x[m][e] = x[m][e] * mul;
+    }
+  }
+}
+
+// The |x| maximum over the lane's scale group within the wave (per-thread class: lanes lq ^ 8, lq ^ 16 and
+// the other half-row; per-warp / per-block: all 64 lanes, from the CUDA quantizer's 1e-7 floor).
+template <int QF, int NQF>
+__device__ __forceinline__ float quant_q_amax(const float (&x)[NQF][16]) {
+  float am = QF == QF_THREAD ? 0.f : 0.0000001f;
+#pragma unroll
+  for (int m = 0; m < NQF; m++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) am = fmaxf(am, fabsf(x[m][e]));
   if constexpr (QF != QF_THREAD) {
     am = fmaxf(am, __shfl_xor(am, 1, 64));
     am = fmaxf(am, __shfl_xor(am, 2, 64));
@@ -894,6 +909,15 @@ __device__ __forceinline__ float quant_q_load(const uint16_t* rowp, bool valid, 
   am = fmaxf(am, __shfl_xor(am, 16, 64));
   am = fmaxf(am, __shfl_xor(am, 32, 64));
   return am;
+}
+
+// The three steps at once: the lane's values x (times mul when MUL) and their group maximum.
+template <bool IS_FP16, int QF, int NQF, bool MUL = false>
+__device__ __forceinline__ float quant_q_load(const uint16_t* rowp, bool valid, int hf, float mul, float (&x)[NQF][16]) {
+  v4u r[NQF][2];
+  quant_q_raw<NQF>(rowp, valid, hf, r);
+  quant_q_unpack<IS_FP16, NQF, MUL>(r, mul, x);
+  return quant_q_amax<QF, NQF>(x);
 }
 
 // The scale of a group with |x| maximum am (returned) and the int8 codes as the MFMA B fragments qf.
@@ -1419,9 +1443,11 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
 
   // per-block Q (QF_BLOCK): the layout starts every chunk on a 128-row block, so in each round waves 4 g ..
   // 4 g + 3 hold the four 32-row blocks of one Q block and exchange their maxima through LDS; every wave
-  // runs all rounds of the chunk (a wave past the chunk's end contributes 0 and joins the barrier)
-  const int64_t n_rounds = (wb_end - wb0 + NW - 1) / NW;
-  for (int64_t rnd = 0; QF == QF_BLOCK ? rnd < n_rounds : wb < wb_end; rnd++, wb += NW) {
+  // runs all rounds of the chunk (a wave past the chunk's end takes zero rows, contributes 0 to the maxima,
+  // joins the barrier and stores nothing)
+  const int64_t wb_lim = QF == QF_BLOCK ? wb0 + (wb_end - wb0 + NW - 1) / NW * NW : wb_end;
+  for (int rnd = 0; wb < wb_lim; rnd++, wb += NW) {
+    const bool live = QF != QF_BLOCK || wb < wb_end;
     float qs;
     if constexpr (QF == QF_INT8) {
       load_q(wb, qf);
@@ -1429,16 +1455,26 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
     } else if constexpr (QF == QF_BLOCK) {
       // (double-buffered by round: a wave writes round r + 2's maximum only after the barrier of round r + 1,
       // which every wave reaches after reading round r's)
+      // (only the raw half words stay live across the barrier, and the values are formed again after it:
+      // 64 fp32 values per lane would not fit beside the kernel's other registers)
       __shared__ float lds_qam[2][NW];
       const int64_t row = wb * 32 + lq;
-      float x[4][16];
-      const float am_w =
-          quant_q_load<IS_FP16_OUT, QF, 4, true>(qhead16 + row * p.qsl, row < p.Lq && wb < wb_end, hf, p.q_sm_scale, x);
+      v4u raw[4][2];
+      quant_q_raw<4>(qhead16 + row * p.qsl, live && row < p.Lq, hf, raw);
+      float am_w;
+      {
+        float x[4][16];
+        quant_q_unpack<IS_FP16_OUT, 4, true>(raw, p.q_sm_scale, x);
+        am_w = quant_q_amax<QF, 4>(x);
+      }
       if (lane == 0) lds_qam[rnd & 1][w] = am_w;
       __syncthreads();
       const float* g4 = &lds_qam[rnd & 1][w & ~3];
       const float am = fmaxf(fmaxf(g4[0], g4[1]), fmaxf(g4[2], g4[3]));
-      if (wb >= wb_end) continue;
+#pragma unroll
+      for (int m = 0; m < 4; m++) asm volatile("" : "+v"(raw[m][0]), "+v"(raw[m][1]));  // (no reuse of the first unpack)
+      float x[4][16];
+      quant_q_unpack<IS_FP16_OUT, 4, true>(raw, p.q_sm_scale, x);
       qs = quant_q_codes<QF, 4>(x, am, qf) * p.qk_mult;
     } else {
       const int64_t row = wb * 32 + lq;
@@ -1498,7 +1534,8 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
       if (masked) {
         select_mask = !__all(cs_a > 0.f && cs_b > 0.f);
         const int mval = select_mask ? INT32_MIN : kMaskedLogitBits;
-        const int lim = (int)min(kv_end - k0, (int64_t)kBK) - hf * 4;
+        int lim = (int)min(kv_end - k0, (int64_t)kBK) - hf * 4;
+        asm volatile("" : "+v"(lim));  // (compared here, not as 32 lane masks kept in registers across the loops)
 #pragma unroll
         for (int kb = 0; kb < 2; kb++)
 #pragma unroll
@@ -1613,14 +1650,14 @@ __global__ __launch_bounds__(kResThreads) void qattn_fwd_res_kernel(AttnParams p
         const int id = i * 64 + lane, r = id >> 2, c = id & 3;
         const v4u val = *reinterpret_cast<const v4u*>(stage + r * 64 + ((c ^ (r & 3)) << 4));
         const int64_t row = wrow0 + r;
-        if (row < p.Lq) *reinterpret_cast<v4u*>(obase + row * p.osl + dblk * 32 + c * 8) = val;
+        if (live && row < p.Lq) *reinterpret_cast<v4u*>(obase + row * p.osl + dblk * 32 + c * 8) = val;
       }
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     }
     };
     if (p.v_mean) store(std::true_type{});
     else store(std::false_type{});
-    if (p.lse && hf == 0 && qrow < p.Lq)
+    if (p.lse && hf == 0 && live && qrow < p.Lq)
       p.lse[(b * p.Hq + h) * p.Lq + qrow] = l_tot > 0.f ? __builtin_log2f(l_tot) + m_run : -INFINITY;
   }
   if constexpr (QF == QF_BLOCK) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no prefetch left in flight
