@@ -894,7 +894,7 @@ def test_pv_accum_modes_and_smooth_v(oracle, mode):
 
 
 Q16_CASES = {
-    # name: (B, Lq, Lk, Hq, Hkv, layout, dtype, gran, kv_valid, smooth_v, causal); the first eight run the
+    # name: (B, Lq, Lk, Hq, Hkv, layout, dtype, gran, kv_valid, smooth_v, causal); the first nine run the
     # resident kernel (at most 512 keys), the others the ping-pong kernel (unsplit, KV split, causal)
     "thread_c4_like": (1, 1000, 512, 4, 4, "NHD", torch.bfloat16, "per_thread", [388], False, False),
     "warp_ragged_gqa": (2, 333, 300, 4, 2, "NHD", torch.bfloat16, "per_warp", None, False, False),
@@ -906,6 +906,7 @@ Q16_CASES = {
     "block_res_chunks": (1, 1000, 512, 4, 4, "NHD", torch.bfloat16, "per_block", [388], False, False),
     "block_res_hnd_fp16": (2, 333, 300, 4, 2, "HND", torch.float16, "per_block", [300, 17], True, False),
     "block_res_rounds_gqa": (5, 900, 200, 40, 8, "NHD", torch.bfloat16, "per_block", None, False, False),
+    "block_res_tiny": (1, 20, 100, 2, 1, "NHD", torch.bfloat16, "per_block", [37], False, False),
     "pp_thread_unsplit": (1, 4680, 6000, 12, 12, "NHD", torch.bfloat16, "per_thread", None, False, False),
     "pp_warp_split_gqa": (1, 2000, 20000, 8, 4, "NHD", torch.bfloat16, "per_warp", [19000], False, False),
     "pp_thread_causal_fp16": (2, 1500, 3000, 8, 8, "HND", torch.float16, "per_thread", None, False, True),
