@@ -916,6 +916,40 @@ Q16_CASES = {
 }
 
 
+@pytest.mark.parametrize("gran", ["per_block", "per_warp", "per_thread"])
+def test_fwd_q16_causal_query_offset(gran):
+    """A streaming chunk through qattn_fwd_q16: 1536 causal queries placed after 2560 earlier keys (q_offset),
+    bit-identical to the quantize-then-attend sequence (48 query-block pairs: the automatic rule splits the
+    key range of the ping-pong launch)."""
+    dev = require_gpu()
+    from telefuser_amd import _lib
+    from telefuser_amd import sageattn2 as sa
+
+    B, Lq, Lk, Hq, Hkv = 1, 1536, 4096, 8, 4
+    log(f"fwd_q16 causal q_offset: {gran} B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} q_offset={Lk - Lq}")
+    q, k, v = qkv(B, Lq, Lk, Hq, Hkv, seed=57, k_offset_std=0.5)
+    qd, kd, vd = (t.to(dev) for t in (q, k, v))
+    km = sa.k_mean(kd, "NHD")
+    qk_mult = 128 ** -0.5 * LOG2E
+    if gran == "per_block":
+        q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=128 ** -0.5, tensor_layout="NHD")
+    else:
+        quant = sa.per_thread_int8 if gran == "per_thread" else sa.per_warp_int8
+        q8, qs, k8, ks = quant(qd, kd, km, tensor_layout="NHD")
+    v8, vs, _ = sa.per_channel_fp8(vd, tensor_layout="NHD")
+    assert sa.q16_supported(B, Lq, Lk, Hq, 128, gran, True)
+    L = _lib.load()
+    log(f"  automatic splits: {L.qattn_fwd_ex_num_splits(B, Lq, Lk, Hq, _lib.QATTN_V_FP8, GRAN_CODE[gran])}")
+    kw = dict(tensor_layout="NHD", is_causal=True, q_offset=Lk - Lq, return_lse=True, qk_quant_gran=gran)
+    o_ref, l_ref = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, out_dtype=q.dtype,
+                                qk_mult=1.0 if gran == "per_block" else qk_mult, **kw)
+    o, l = sa.qattn_fwd_q16(qd, k8, ks, v8, vs, qk_mult=qk_mult, **kw)
+    torch.cuda.synchronize()
+    assert L.qattn_last_kernel() == _lib.QATTN_KERNEL_PINGPONG
+    assert torch.equal(o, o_ref), f"max diff {float((o.float() - o_ref.float()).abs().max())}"
+    assert torch.equal(l, l_ref)
+
+
 @pytest.mark.parametrize("case", sorted(Q16_CASES))
 def test_fwd_q16_matches_quantize_then_attend(oracle, case):
     """qattn_fwd_q16 quantizes Q inside the attention kernel: its output and LSE must be bit-identical to
