@@ -783,8 +783,9 @@ def test_full_size_configs(oracle, name, call):
     inputs and calls): the Wan2.1-1.3B 480p self attention of the headline number (L = 32760, H = 12, q and
     k after RMSNorm + 3-D RoPE), 14B 720p self attention (L = 75600, H = 40, K mean offset), the 14B text
     cross attention (Lk = 512 with zero-padded, masked keys) and the streaming chunk over a 32760-key
-    window (KV split, restated by the oracle).  call="qattn" is the per-block quantizers + qattn_fwd (the
-    benchmark's step); call="telefuser" is TeleFuser's own call (attention_impl.py:249-258):
+    window (KV split, restated by the oracle).  call="qattn" is the per-block quantizers + qattn_fwd, and
+    the benchmark's step (the fused K/V prologue + qattn_fwd_q16, Q quantized inside the attention kernel)
+    must give the same bits; call="telefuser" is TeleFuser's own call (attention_impl.py:249-258):
     sageattn_qk_int8_pv_fp8_cuda with per-thread scales and "fp32+fp32" accumulation, checked against the
     oracle on the per-thread operands that the module's quantizers produce for the same inputs.
     Checked on a subset that the CPU finishes in seconds: 192 query rows (the first 128 and the last 64) of
@@ -810,6 +811,13 @@ def test_full_size_configs(oracle, name, call):
     v8, vs, _ = sa.per_channel_fp8(v, tensor_layout="NHD", smooth_v=False)
     if call == "qattn":
         o = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, tensor_layout="NHD", out_dtype=q.dtype, kv_valid_len=kvv)
+        if sa.q16_supported(cfg.B, cfg.Lq, cfg.Lk, cfg.Hq, cfg.D, "per_block"):
+            _, _, k8b, ksb, _, v8b, vsb, _ = sa.sage_quant(q, k, v, tensor_layout="NHD", sm_scale=sm, quantize_q=False)
+            o16 = sa.qattn_fwd_q16(q, k8b, ksb, v8b, vsb, tensor_layout="NHD", qk_mult=sm * LOG2E, kv_valid_len=kvv,
+                                   qk_quant_gran="per_block")
+            torch.cuda.synchronize()
+            assert torch.equal(o16, o), f"bench route differs: {float((o16.float() - o.float()).abs().max())}"
+            del o16, k8b, v8b
     torch.cuda.synchronize()
     assert bool(torch.isfinite(o.float()).all())
     rows = torch.cat([torch.arange(0, 128), torch.arange(cfg.Lq - 64, cfg.Lq)])
