@@ -1017,3 +1017,27 @@ def test_fwd_q16_matches_quantize_then_attend(oracle, case):
                              kv_valid=kvv0, is_fp16=dt == torch.float16, causal=causal)
     log(f"  vs reference-schedule quantized math: cosine={cosine(got, ref):.6f}; vs float64: {cosine(got, truth):.6f}")
     assert cosine(got, ref) >= COS_E2E
+
+
+@pytest.mark.parametrize("gran,lk", [("per_block", 3000), ("per_thread", 3000), ("per_block", 300),
+                                     ("per_thread", 300)])
+def test_dropin_strided_views_of_packed_qkv(gran, lk):
+    """q, k and v as views of one packed [B, L, 3, H, D] projection output (row strides 3 H D, last dim
+    contiguous), through the drop-in, whose Q goes straight into the attention kernel (qattn_fwd_q16 on the
+    ping-pong kernel for 3000 keys, on the resident kernel for 300): the same bits as contiguous copies."""
+    dev = require_gpu()
+    from telefuser_amd import sageattn2 as sa
+
+    B, L, H, D = 1, lk, 4, 128
+    log(f"strided packed qkv: {gran} B={B} L={L} H={H}")
+    g = torch.Generator().manual_seed(61)
+    qkv_packed = torch.randn(B, L, 3, H, D, generator=g).to(torch.bfloat16).to(dev)
+    q, k, v = qkv_packed[:, :, 0], qkv_packed[:, :, 1], qkv_packed[:, :, 2]
+    assert not q.is_contiguous() and q.stride(1) == 3 * H * D
+    assert sa.q16_supported(B, L, L, H, D, gran, False)
+    kw = dict(tensor_layout="NHD", qk_quant_gran=gran, pv_accum_dtype="fp32+fp32", return_lse=True)
+    o, lse = sa.sageattn_qk_int8_pv_fp8_cuda(q, k, v, **kw)
+    oc, lsec = sa.sageattn_qk_int8_pv_fp8_cuda(q.contiguous(), k.contiguous(), v.contiguous(), **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o, oc), f"max diff {float((o.float() - oc.float()).abs().max())}"
+    assert torch.equal(lse, lsec)
