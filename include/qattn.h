@@ -321,8 +321,9 @@ int qattn_v_fp8_cache_update(qattn_seq v, int dtype, int64_t B, int64_t fill, in
  * as qattn_fwd_ex (causal, q_offset, kv_valid, lse, num_splits with its workspace sized by
  * qattn_fwd_ex_num_splits / qattn_fwd_workspace_size); qk_mult = sm_scale * 1.44269504 (per block it is the
  * factor multiplied into Q before quantization, and the logits take 1).  Runs when the
- * automatic kernel rule gives one of those two kernels for the launch and head_dim is 128
- * (qattn_fwd_q16_supported), else returns QATTN_ERR_SHAPE.  Replaces the quantize-then-attend sequence of
+ * automatic kernel rule gives one of those two kernels for the launch and head_dim is 128, or for
+ * any launch with head_dim 64 (the ping-pong kernel's D = 64 form) (qattn_fwd_q16_supported), else returns
+ * QATTN_ERR_SHAPE.  Replaces the quantize-then-attend sequence of
  * sageattn_qk_int8_pv_fp8_cuda (sageattn2.py:1334-1446); no counterpart op in the reference.
  */
 int qattn_fwd_q16_supported(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t D, int qk_quant_gran, int causal);

@@ -2091,7 +2091,8 @@ extern "C" int qattn_fwd_ex2(qattn_seq q8, const float* q_scale, qattn_seq k8, c
 // ---- half Q quantized inside the attention kernel (resident or ping-pong) ----
 // the kernel a qattn_fwd_q16 launch runs: the automatic rule's, when it is one of the two with a fused-Q form
 static int q16_kernel(int64_t B, int64_t Lq, int64_t Lk, int64_t Hq, int64_t D, int gran, int causal) {
-  if (D != kD || B <= 0 || Lq <= 0 || Lk <= 0 || Hq <= 0) return QATTN_KERNEL_AUTO;
+  if ((D != kD && D != 64) || B <= 0 || Lq <= 0 || Lk <= 0 || Hq <= 0) return QATTN_KERNEL_AUTO;
+  if (D == 64) return QATTN_KERNEL_PINGPONG;  // (head_dim 64 runs the ping-pong kernel only)
   int ns, qpw, kernel;
   plan_fwd(B, Lq, Lk, Hq, PV_FP8, gran, causal, false, 0, ns, qpw, kernel);
   return kernel == QATTN_KERNEL_RESIDENT || kernel == QATTN_KERNEL_PINGPONG ? kernel : QATTN_KERNEL_AUTO;
@@ -2103,20 +2104,25 @@ extern "C" int qattn_fwd_q16_supported(int64_t B, int64_t Lq, int64_t Lk, int64_
   return q16_kernel(B, Lq, Lk, Hq, D, qk_quant_gran, causal) != QATTN_KERNEL_AUTO ? 1 : 0;
 }
 
-template <int QF>
+template <int QF, int HD>
 static void launch_pp_q16(AttnParams& p, int dtype, int ns, hipStream_t st) {
   constexpr bool KT = QF == QF_THREAD;
   const int64_t g = p.B * p.Hq * ((p.nQB + 1) / 2) * ns;
   if (ns > 1) {
     const int64_t rows = p.B * p.Hq * p.Lq;
-    if (dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT, true, kD, QF><<<g, kPPThreads, 0, st>>>(p);
-    else qattn_fwd_pp_kernel<true, KT, true, kD, QF><<<g, kPPThreads, 0, st>>>(p);
-    if (dtype == QATTN_BF16) qattn_combine_kernel<false><<<(rows + 3) / 4, 256, 0, st>>>(p);
-    else qattn_combine_kernel<true><<<(rows + 3) / 4, 256, 0, st>>>(p);
+    if (dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT, true, HD, QF><<<g, kPPThreads, 0, st>>>(p);
+    else qattn_fwd_pp_kernel<true, KT, true, HD, QF><<<g, kPPThreads, 0, st>>>(p);
+    if (dtype == QATTN_BF16) qattn_combine_kernel<false, HD><<<(rows + 3) / 4, 256, 0, st>>>(p);
+    else qattn_combine_kernel<true, HD><<<(rows + 3) / 4, 256, 0, st>>>(p);
   } else {
-    if (dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT, false, kD, QF><<<g, kPPThreads, 0, st>>>(p);
-    else qattn_fwd_pp_kernel<true, KT, false, kD, QF><<<g, kPPThreads, 0, st>>>(p);
+    if (dtype == QATTN_BF16) qattn_fwd_pp_kernel<false, KT, false, HD, QF><<<g, kPPThreads, 0, st>>>(p);
+    else qattn_fwd_pp_kernel<true, KT, false, HD, QF><<<g, kPPThreads, 0, st>>>(p);
   }
+}
+template <int QF>
+static void launch_pp_q16(AttnParams& p, int dtype, int ns, hipStream_t st, int64_t D) {
+  if (D == 64) launch_pp_q16<QF, 64>(p, dtype, ns, st);
+  else launch_pp_q16<QF, kD>(p, dtype, ns, st);
 }
 
 extern "C" int qattn_fwd_q16(qattn_seq q, qattn_seq k8, const float* k_scale, const uint8_t* v8, int64_t Lpad,
@@ -2130,8 +2136,8 @@ extern "C" int qattn_fwd_q16(qattn_seq q, qattn_seq k8, const float* k_scale, co
   if (B * Lq == 0) return QATTN_OK;
   const int kernel = q16_kernel(B, Lq, Lk, Hq, D, qk_quant_gran, causal);
   QATTN_REQUIRE(kernel != QATTN_KERNEL_AUTO, QATTN_ERR_SHAPE,
-                "qattn_fwd_q16 runs the resident or ping-pong kernel: head_dim 128 and a launch the automatic rule "
-                "gives one of them (see qattn_fwd_q16_supported)");
+                "qattn_fwd_q16 runs the resident or ping-pong kernel: head_dim 64, or 128 and a launch the automatic "
+                "rule gives one of them (see qattn_fwd_q16_supported)");
   AttnParams p;
   int ns = 1, kplan = QATTN_KERNEL_AUTO;
   // (q's scale table is formed inside the kernel: k_scale stands in for the pointer setup_fwd checks)
@@ -2180,9 +2186,9 @@ extern "C" int qattn_fwd_q16(qattn_seq q, qattn_seq k8, const float* k_scale, co
     p.ws_o = static_cast<float*>(workspace);
     p.ws_ml = p.ws_o + (int64_t)ns * p.B * p.Hq * p.Lq * D;
   }
-  if (qk_quant_gran == QATTN_GRAN_THREAD) launch_pp_q16<QF_THREAD>(p, dtype, ns, st);
-  else if (qk_quant_gran == QATTN_GRAN_WARP) launch_pp_q16<QF_WARP>(p, dtype, ns, st);
-  else launch_pp_q16<QF_BLOCK>(p, dtype, ns, st);
+  if (qk_quant_gran == QATTN_GRAN_THREAD) launch_pp_q16<QF_THREAD>(p, dtype, ns, st, D);
+  else if (qk_quant_gran == QATTN_GRAN_WARP) launch_pp_q16<QF_WARP>(p, dtype, ns, st, D);
+  else launch_pp_q16<QF_BLOCK>(p, dtype, ns, st, D);
   return check_launch("qattn_fwd_q16");
 }
 

@@ -352,8 +352,8 @@ def qattn_fwd_q16(q, k_int8, k_scale, v_fp8, v_scale, *, tensor_layout="HND", qk
     kernel), bit-identical to per_thread_int8 / per_warp_int8 /
     per_block_int8 followed by qattn_fwd, without the int8 Q round trip through memory.  qk_mult is
     sm_scale * 1.44269504 for every granularity (per block it is multiplied into Q before quantization, as
-    per_block_int8's sm_scale).  head_dim 128, launches whose automatic kernel is one of those two
-    (q16_supported).  Returns o (and the log2-domain LSE)."""
+    per_block_int8's sm_scale).  head_dim 128 for launches whose automatic kernel is one of those two, any
+    launch with head_dim 64 (the ping-pong kernel's D = 64 form) (q16_supported).  Returns o (and the log2-domain LSE)."""
     L = _lib.load()
     b, lq, hq, d = _dims(q, tensor_layout)
     _, lk, hkv, _ = _dims(k_int8, tensor_layout)

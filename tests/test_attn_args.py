@@ -146,11 +146,13 @@ def test_fwd_q16_rejects(bad):
 
 def test_q16_supported_rule():
     """The host rule behind the drop-in's route: every granularity on the resident kernel (at most 512 keys)
-    and on the ping-pong kernel, nothing on the one-block kernel, head_dim 128 only."""
+    and on the ping-pong kernel, nothing on the one-block kernel; head_dim 128, or 64 (always the ping-pong
+    kernel)."""
     from telefuser_amd import sageattn2 as sa
 
     for gran in ("per_block", "per_warp", "per_thread"):
         assert sa.q16_supported(1, 1000, 512, 4, 128, gran, False)  # resident
         assert sa.q16_supported(1, 32760, 32760, 12, 128, gran, False)  # ping-pong (C2)
         assert not sa.q16_supported(1, 300, 600, 4, 128, gran, False)  # one-block
-        assert not sa.q16_supported(1, 1000, 512, 4, 64, gran, False)
+        assert sa.q16_supported(1, 1000, 512, 4, 64, gran, False)  # head_dim 64: the ping-pong kernel's form
+        assert not sa.q16_supported(1, 1000, 512, 4, 96, gran, False)

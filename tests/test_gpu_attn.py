@@ -263,6 +263,38 @@ def test_head_dim_64_native(oracle, case):
     assert _lib.load().qattn_last_kernel() == KERNEL_PINGPONG
 
 
+@pytest.mark.parametrize("gran,causal,split", [("per_block", False, False), ("per_warp", True, False),
+                                                ("per_thread", False, True), ("per_block", False, True)])
+def test_fwd_q16_head_dim_64(gran, causal, split):
+    """qattn_fwd_q16 on the head-dim-64 form of the ping-pong kernel (Q quantized inside it, NQF = 2 fragment
+    columns per lane), unsplit and KV-split, bit-identical to the quantizer + qattn_fwd on the same K / V."""
+    dev = require_gpu()
+    from telefuser_amd import _lib
+    from telefuser_amd import sageattn2 as sa
+
+    B, Lq, Lk, Hq, Hkv = 1, 1000, 2400, 4, 2
+    log(f"fwd_q16 head_dim 64: {gran} causal={causal} split={split}")
+    q, k, v = qkv(B, Lq, Lk, Hq, Hkv, D=64, seed=66, k_offset_std=0.5)
+    qd, kd, vd = (t.to(dev) for t in (q, k, v))
+    km = sa.k_mean(kd, "NHD")
+    qk_mult = 64 ** -0.5 * LOG2E
+    if gran == "per_block":
+        q8, qs, k8, ks = sa.per_block_int8(qd, kd, km, sm_scale=64 ** -0.5, tensor_layout="NHD")
+    else:
+        quant = sa.per_thread_int8 if gran == "per_thread" else sa.per_warp_int8
+        q8, qs, k8, ks = quant(qd, kd, km, tensor_layout="NHD")
+    v8, vs, _ = sa.per_channel_fp8(vd, tensor_layout="NHD")
+    assert sa.q16_supported(B, Lq, Lk, Hq, 64, gran, causal)
+    kw = dict(tensor_layout="NHD", is_causal=causal, return_lse=True, qk_quant_gran=gran, num_splits=3 if split else 1)
+    o_ref, l_ref = sa.qattn_fwd(q8, qs, k8, ks, v8, vs, out_dtype=q.dtype,
+                                qk_mult=1.0 if gran == "per_block" else qk_mult, **kw)
+    o, l = sa.qattn_fwd_q16(qd, k8, ks, v8, vs, qk_mult=qk_mult, **kw)
+    torch.cuda.synchronize()
+    assert _lib.load().qattn_last_kernel() == KERNEL_PINGPONG
+    assert torch.equal(o, o_ref), f"max diff {float((o.float() - o_ref.float()).abs().max())}"
+    assert torch.equal(l, l_ref)
+
+
 @pytest.mark.parametrize("d", [48, 64, 96])
 def test_small_head_dims_through_the_drop_in(oracle, d):
     """sageattn_qk_int8_pv_fp8_cuda pads head_dim <= 64 to 64 (native kernel form) and 64 < D < 128 to 128, as
