@@ -253,10 +253,17 @@ class QuantizedKVCache:
         d = q.shape[-1]
         if sm_scale is None:
             sm_scale = d ** -0.5
-        q8, qs = sa.quant_per_block_int8(q, sa.BLKQ, sm_scale=sm_scale * sa.LOG2E, tensor_layout="NHD")
         kv_valid = n_valid if n_valid < self.size else None
-        res = sa.qattn_fwd(q8, qs, self.k8, self.k_scale, self.v8, self.v_scale, tensor_layout="NHD",
-                           out_dtype=q.dtype, kv_valid_len=kv_valid, return_lse=return_lse)
+        b, lq, hq, _ = q.shape
+        if sa.q16_supported(b, lq, self.k8.shape[1], hq, d, "per_block"):
+            # the chunk's Q quantized per block inside the attention kernel (same bits as the quantizer below)
+            res = sa.qattn_fwd_q16(q, self.k8, self.k_scale, self.v8, self.v_scale, tensor_layout="NHD",
+                                   qk_mult=sm_scale * sa.LOG2E, kv_valid_len=kv_valid, return_lse=return_lse,
+                                   qk_quant_gran="per_block")
+        else:
+            q8, qs = sa.quant_per_block_int8(q, sa.BLKQ, sm_scale=sm_scale * sa.LOG2E, tensor_layout="NHD")
+            res = sa.qattn_fwd(q8, qs, self.k8, self.k_scale, self.v8, self.v_scale, tensor_layout="NHD",
+                               out_dtype=q.dtype, kv_valid_len=kv_valid, return_lse=return_lse)
         if not return_lse:
             return res
         o, lse = res
